@@ -1,0 +1,105 @@
+/* ct_launch.h — C-callable launchers for the gfx950 kernels.
+ *
+ * Plain pointers, sizes and a hipStream_t: the C glue (abi.c) and the decode
+ * engine call these; no C++ or device types cross this header.
+ */
+#ifndef CT_LAUNCH_H
+#define CT_LAUNCH_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------- GEMM: Y = epi(A W^T + b) ---------------- */
+enum {
+    CT_EPI_STORE = 0,   /* Y = s                                   */
+    CT_EPI_SILU  = 1,   /* Y = s * sigmoid(s)                      */
+    CT_EPI_RELU  = 2,   /* Y = max(s, 0)                           */
+    CT_EPI_FMADD = 3,   /* Y += scale * s                          */
+    CT_EPI_GLU   = 4    /* Y[:, j] = s_j * sigmoid(s_{j+glu_half}) */
+};
+
+typedef struct {
+    const float    *A;        /* [M][lda] fp32 activations                 */
+    long            lda;
+    const uint16_t *W;        /* [N][K] bf16 weights, row-major            */
+    const uint16_t *bias;     /* [N] bf16 or NULL                          */
+    float          *Y;        /* output rows of ldy floats                 */
+    long            ldy;
+    int M, N, K;
+    int epi;
+    float scale;              /* CT_EPI_FMADD                              */
+    /* Row scatter (KV-cache append): when row_len != NULL, result row m is
+     * written to Y row m*row_stride + row_len[m*row_len_step] - 1.          */
+    const int      *row_len;
+    int             row_len_step;
+    long            row_stride;
+    int             glu_half; /* CT_EPI_GLU: N == 2*glu_half               */
+    const int      *row_mask; /* rows m with row_mask[m] == 0 are not written */
+} CtGemm;
+
+void ctk_gemm(const CtGemm *g, hipStream_t s);
+
+/* ---------------- row-wise ops ---------------- */
+void ctk_layernorm(float *dst, const float *src, const uint16_t *w, const uint16_t *b,
+                   int T, int D, hipStream_t s);
+void ctk_add(float *dst, const float *src, long n, hipStream_t s);
+void ctk_causal_mask(float *mask, int S, hipStream_t s);
+/* pe rows p = 0..2T-2 hold relative position T-1-p; inv_freq[k] (ENC_D/2
+ * entries) is exp(-2k ln(1e4)/ENC_D), computed on the host. */
+void ctk_rel_pos_emb(float *pe, int T, const float *inv_freq, hipStream_t s);
+/* h[r] = LN(etw[tok] + epw[pos]) for r in [0, R): tok = tokens[r]; pos =
+ * pos_len ? pos_len[r] - 1 : pos_start + r; rows with active[r] == 0 are
+ * skipped when active != NULL. */
+void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, const int *pos_len,
+                  const int *active, const uint16_t *etw, const uint16_t *epw,
+                  const uint16_t *lnw, const uint16_t *lnb, hipStream_t s);
+/* out[r] = first index of the maximum of logits[r][0..n) (rows with
+ * active[r] == 0 untouched). */
+void ctk_argmax(int *out, const float *logits, int R, int n, const int *active, hipStream_t s);
+void ctk_inc(int *p, hipStream_t s);
+
+/* ---------------- attention ---------------- */
+typedef struct {
+    float       *out;         /* out[b][qi][h*dk + d]                                  */
+    const float *Q;
+    long q_sb, q_st;          /* Q/out strides (floats) per item and per query row     */
+    const void  *K, *V;       /* fp32 or bf16 (kv_bf16)                                */
+    int   kv_bf16;
+    long  kv_sb, kv_st, kv_sh;/* K/V element strides per item, per key row, per head   */
+    const int *lens;          /* keys per item: lens[b*lens_step] (device) ...         */
+    int   lens_step;
+    int   len_const;          /* ... or this when lens == NULL                          */
+    const float *mask;        /* optional additive [T_q][T_k] mask (B == 1)            */
+    int   T_q, B, H;
+    float scale;
+} CtAttn;
+/* Head dim fixed at DEC_DK (128). */
+void ctk_attn(const CtAttn *a, hipStream_t s);
+
+/* ---------------- encoder ---------------- */
+/* Relative-position MHSA core for one clip: O = softmax(((Q+u)K^T +
+ * rel_shift((Q+v)P^T)) * scale) V, per head; P has 2T-1 rows. */
+void ctk_relpos_attn(float *O, const float *Q, const float *K, const float *V,
+                     const float *P, const uint16_t *pbu, const uint16_t *pbv,
+                     int T, hipStream_t s);
+/* Depthwise conv k=9 (zero pad 4 inside the sequence) + BN + SiLU. */
+void ctk_dwconv_bn_silu(float *out, const float *in, int T,
+                        const uint16_t *dww, const uint16_t *dwb,
+                        const uint16_t *bnw, const uint16_t *bnb,
+                        const uint16_t *bnm, const uint16_t *bnv, hipStream_t s);
+/* Subsampling stages (position-major [t][f][ch] activations). */
+void ctk_sub_conv0(float *out, const float *mel, int T_mel, int stride,
+                   const uint16_t *w, const uint16_t *b, hipStream_t s);
+void ctk_sub_dwconv(float *out, const float *in, int H, int Wd,
+                    const uint16_t *w, const uint16_t *b, hipStream_t s);
+/* [T][16][256] -> [T][256*16] (channel-major flatten per frame). */
+void ctk_sub_flatten(float *out, const float *in, int T, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,198 @@
+// k_rows.hip — row-wise kernels: layernorm, embedding+LN, argmax, small
+// elementwise helpers.  One wavefront per row; rows are independent, so
+// results never depend on how many rows a launch covers.
+#include "ct_dev.h"
+#include "ct_launch.h"
+#include "../../include/model_types.h"
+#include <limits.h>
+
+namespace {
+
+constexpr int LN_MAXV = 32;   // register-cached elements per lane (D <= 2048)
+
+// LayerNorm of one row held in registers: mean, then the mean of squared
+// deviations, 1/sqrt(var + 1e-5), scale and shift
+// (backends/cpu/backend.c:109-122).
+__device__ __forceinline__ void ln_row(float (&v)[LN_MAXV], int D, int lane,
+                                       const uint16_t *w, const uint16_t *b, float *dst) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < LN_MAXV; i++) {
+        const int d = lane + i * 64;
+        if (d < D) s += v[i];
+    }
+    const float mu = wave_sum(s) / (float)D;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < LN_MAXV; i++) {
+        const int d = lane + i * 64;
+        if (d < D) { const float c = v[i] - mu; q += c * c; }
+    }
+    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < LN_MAXV; i++) {
+        const int d = lane + i * 64;
+        if (d < D) dst[d] = (v[i] - mu) * rs * bf2f(w[d]) + bf2f(b[d]);
+    }
+}
+
+__global__ __launch_bounds__(256) void layernorm_kernel(float *dst, const float *src,
+                                                        const uint16_t *w, const uint16_t *b,
+                                                        int T, int D) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= T) return;
+    const float *x = src + (long)row * D;
+    float v[LN_MAXV];
+#pragma unroll
+    for (int i = 0; i < LN_MAXV; i++) {
+        const int d = lane + i * 64;
+        v[i] = d < D ? x[d] : 0.0f;
+    }
+    ln_row(v, D, lane, w, b, dst + (long)row * D);
+}
+
+// Rows longer than 2048: three passes over the (cache-resident) row.
+__global__ __launch_bounds__(64) void layernorm_long_kernel(float *dst, const float *src,
+                                                            const uint16_t *w, const uint16_t *b,
+                                                            int T, int D) {
+    const int row = blockIdx.x, lane = threadIdx.x;
+    if (row >= T) return;
+    const float *x = src + (long)row * D;
+    float *y = dst + (long)row * D;
+    float s = 0.0f;
+    for (int d = lane; d < D; d += 64) s += x[d];
+    const float mu = wave_sum(s) / (float)D;
+    float q = 0.0f;
+    for (int d = lane; d < D; d += 64) { const float c = x[d] - mu; q += c * c; }
+    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
+    for (int d = lane; d < D; d += 64) y[d] = (x[d] - mu) * rs * bf2f(w[d]) + bf2f(b[d]);
+}
+
+// h[r] = LN(etw[tok] + epw[pos]) (backends/cpu/backend.c:362-371, 425-435).
+__global__ __launch_bounds__(256) void embed_ln_kernel(float *h, const int *tokens, int R,
+                                                       int pos_start, const int *pos_len,
+                                                       const int *active,
+                                                       const uint16_t *etw, const uint16_t *epw,
+                                                       const uint16_t *lnw, const uint16_t *lnb) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= R) return;
+    if (active && !active[r]) return;
+    const long tok = tokens[r];
+    const long pos = pos_len ? (long)pos_len[r] - 1 : (long)pos_start + r;
+    float v[LN_MAXV];
+#pragma unroll
+    for (int i = 0; i < LN_MAXV; i++) {
+        const int d = lane + i * 64;
+        v[i] = d < DEC_D ? bf2f(etw[tok * DEC_D + d]) + bf2f(epw[pos * DEC_D + d]) : 0.0f;
+    }
+    ln_row(v, DEC_D, lane, lnw, lnb, h + (long)r * DEC_D);
+}
+
+// First index of the maximum with the sequential scan's rules
+// (backends/cpu/backend.c:446-456): strict '>', so ties keep the lowest index
+// and NaN never wins; a NaN at index 0 stays the answer.
+__device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(int *out, const float *logits, int n,
+                                                     const int *active) {
+    const int r = blockIdx.x;
+    if (active && !active[r]) return;
+    const float *x = logits + (long)r * n;
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int i = threadIdx.x; i < n; i += 256) better(bv, bi, x[i], i);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        better(bv, bi, ov, oi);
+    }
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[wv] = bv; si[wv] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; k++) better(bv, bi, sv[k], si[k]);
+        out[r] = (x[0] != x[0] || bi == INT_MAX) ? 0 : bi;
+    }
+}
+
+__global__ void add_kernel(float *dst, const float *src, long n) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] += src[i];
+}
+
+__global__ void causal_mask_kernel(float *mask, int S) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)S * S) return;
+    const int q = (int)(i / S), k = (int)(i % S);
+    mask[i] = k > q ? -1e9f : 0.0f;
+}
+
+// pe[p][2k] = sin(pos w_k), pe[p][2k+1] = cos(pos w_k), pos = T-1-p
+// (backends/cpu/backend.c:231-242); w_k comes from the host (glibc expf).
+__global__ void rel_pos_emb_kernel(float *pe, int T, const float *inv_freq) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long L = 2L * T - 1;
+    if (i >= L * (ENC_D / 2)) return;
+    const int p = (int)(i / (ENC_D / 2)), k = (int)(i % (ENC_D / 2));
+    const float arg = (float)(T - 1 - p) * inv_freq[k];
+    pe[(long)p * ENC_D + 2 * k] = sinf(arg);
+    pe[(long)p * ENC_D + 2 * k + 1] = cosf(arg);
+}
+
+__global__ void inc_kernel(int *p) {
+    if (threadIdx.x == 0) *p += 1;
+}
+
+}  // namespace
+
+extern "C" void ctk_layernorm(float *dst, const float *src, const uint16_t *w, const uint16_t *b,
+                              int T, int D, hipStream_t s) {
+    if (T <= 0) return;
+    if (D <= 64 * LN_MAXV)
+        hipLaunchKernelGGL(layernorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, dst, src, w, b, T, D);
+    else
+        hipLaunchKernelGGL(layernorm_long_kernel, dim3(T), dim3(64), 0, s, dst, src, w, b, T, D);
+}
+
+extern "C" void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, const int *pos_len,
+                             const int *active, const uint16_t *etw, const uint16_t *epw,
+                             const uint16_t *lnw, const uint16_t *lnb, hipStream_t s) {
+    if (R <= 0) return;
+    hipLaunchKernelGGL(embed_ln_kernel, dim3((R + 3) / 4), dim3(256), 0, s, h, tokens, R, pos_start,
+                       pos_len, active, etw, epw, lnw, lnb);
+}
+
+extern "C" void ctk_argmax(int *out, const float *logits, int R, int n, const int *active,
+                           hipStream_t s) {
+    if (R <= 0) return;
+    hipLaunchKernelGGL(argmax_kernel, dim3(R), dim3(256), 0, s, out, logits, n, active);
+}
+
+extern "C" void ctk_add(float *dst, const float *src, long n, hipStream_t s) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst, src, n);
+}
+
+extern "C" void ctk_causal_mask(float *mask, int S, hipStream_t s) {
+    const long n = (long)S * S;
+    if (n <= 0) return;
+    hipLaunchKernelGGL(causal_mask_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, mask, S);
+}
+
+extern "C" void ctk_rel_pos_emb(float *pe, int T, const float *inv_freq, hipStream_t s) {
+    const long n = (2L * T - 1) * (ENC_D / 2);
+    if (n <= 0) return;
+    hipLaunchKernelGGL(rel_pos_emb_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, pe, T,
+                       inv_freq);
+}
+
+extern "C" void ctk_inc(int *p, hipStream_t s) {
+    hipLaunchKernelGGL(inc_kernel, dim3(1), dim3(64), 0, s, p);
+}

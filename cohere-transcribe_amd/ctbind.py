@@ -1,0 +1,206 @@
+"""ctypes bindings for the MI355X backend libraries built in this directory.
+
+libct_hip.so exports the 40-function backend ABI (include/backend.h) and the
+hipb_* decode engine (include/hipb.h); libct_host.so holds the seeded
+synthetic workload (weights in the converter's safetensors layout, audio).
+
+Nothing here falls back to a CPU path: if a library is missing the loader
+raises, so a test or benchmark that runs has run the HIP code.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+HOST_LIB = os.path.join(PKG_DIR, "libct_host.so")
+HIP_LIB = os.path.join(PKG_DIR, "libct_hip.so")
+
+# Model constants (include/model_types.h).
+ENC_D, ENC_FF, ENC_H, ENC_DK, ENC_N, ENC_CK, SUB_CH = 1280, 5120, 8, 160, 48, 9, 256
+DEC_D, DEC_FF, DEC_H, DEC_DK, DEC_N = 1024, 4096, 8, 128, 8
+VOCAB, MAX_SEQ = 16384, 1024
+N_MELS, HOP_LEN, SR = 128, 160, 16000
+EOS = 3
+# Prompt built by transcribe.c:1320-1330 with pnc/itn/timestamps/diarize off;
+# the language id is a fixed placeholder (the vocabulary is not available).
+PROMPT = [13764, 7, 4, 16, 62, 62, 6, 9, 11, 13]
+
+# Field order of the Weights struct (include/model_types.h), flattened.
+_FIXED_A = ["s0w", "s0b", "s2w", "s2b", "s3w", "s3b", "s5w", "s5b", "s6w", "s6b", "sow", "sob"]
+ELAYER_FIELDS = ["ff1_lnw", "ff1_lnb", "ff1_w1", "ff1_b1", "ff1_w2", "ff1_b2",
+                 "sa_lnw", "sa_lnb", "sa_qw", "sa_qb", "sa_kw", "sa_kb",
+                 "sa_vw", "sa_vb", "sa_pw", "sa_ow", "sa_ob", "sa_pbu", "sa_pbv",
+                 "cv_lnw", "cv_lnb", "cv_pw1w", "cv_pw1b", "cv_dww", "cv_dwb",
+                 "cv_bnw", "cv_bnb", "cv_bnmean", "cv_bnvar", "cv_pw2w", "cv_pw2b",
+                 "ff2_lnw", "ff2_lnb", "ff2_w1", "ff2_b1", "ff2_w2", "ff2_b2",
+                 "out_lnw", "out_lnb"]
+DLAYER_FIELDS = ["sa_lnw", "sa_lnb", "sa_qw", "sa_qb", "sa_kw", "sa_kb",
+                 "sa_vw", "sa_vb", "sa_ow", "sa_ob",
+                 "ca_lnw", "ca_lnb", "ca_qw", "ca_qb", "ca_kw", "ca_kb",
+                 "ca_vw", "ca_vb", "ca_ow", "ca_ob",
+                 "ffn_lnw", "ffn_lnb", "ffn_w1", "ffn_b1", "ffn_w2", "ffn_b2"]
+FIELDS = (_FIXED_A
+          + [f"enc{i}.{f}" for i in range(ENC_N) for f in ELAYER_FIELDS]
+          + ["prw", "prb", "etw", "epw", "elnw", "elnb"]
+          + [f"dec{i}.{f}" for i in range(DEC_N) for f in DLAYER_FIELDS]
+          + ["dlnw", "dlnb", "hdb"])
+FIELD_INDEX = {n: i for i, n in enumerate(FIELDS)}
+N_PTRS = len(FIELDS)                     # 2101
+WeightsT = C.c_void_p * N_PTRS
+ELAYER_BYTES = len(ELAYER_FIELDS) * 8
+DLAYER_BYTES = len(DLAYER_FIELDS) * 8
+ENC_OFF = len(_FIXED_A)                  # index of enc[0] inside Weights
+
+
+def t_mel(n_samples):
+    return 1 + n_samples // HOP_LEN
+
+
+def t_enc(T_mel):
+    a = (T_mel + 1) // 2
+    b = (a + 1) // 2
+    return (b + 1) // 2
+
+
+_host = None
+
+
+def host():
+    """libct_host.so (synthetic workload)."""
+    global _host
+    if _host is None:
+        if not os.path.exists(HOST_LIB):
+            raise RuntimeError(f"{HOST_LIB} is not built (run __graft_entry__.build())")
+        L = C.CDLL(HOST_LIB)
+        L.ct_synth_file_bytes.restype = C.c_size_t
+        L.ct_synth_weights.argtypes = [C.c_void_p, C.c_size_t, C.c_uint64, C.c_int, C.c_int]
+        L.ct_synth_weights.restype = C.c_int
+        L.ct_weights_bind.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p,
+                                      C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]
+        L.ct_weights_bind.restype = C.c_int
+        L.ct_synth_audio.argtypes = [C.c_void_p, C.c_int, C.c_uint64]
+        L.ct_hash64.argtypes = [C.c_uint64, C.c_uint64]
+        L.ct_hash64.restype = C.c_uint64
+        L.ct_normal16.argtypes = [C.c_uint64]
+        L.ct_normal16.restype = C.c_float
+        _host = L
+    return _host
+
+
+class SynthModel:
+    """Seeded synthetic weights at model dimensions, bound to a Weights struct.
+
+    `image` is the full safetensors file image; `data_ptr`/`data_bytes` is its
+    data section (what the host hands to backend_weights_upload_blob)."""
+
+    def __init__(self, seed=1234, variant=0, nthreads=0):
+        L = host()
+        n = L.ct_synth_file_bytes()
+        self.image = np.empty(n, dtype=np.uint8)
+        rc = L.ct_synth_weights(self.image.ctypes.data, n, seed, variant, nthreads)
+        if rc != 0:
+            raise RuntimeError("ct_synth_weights failed")
+        self.W = WeightsT()
+        data = C.c_void_p()
+        nbytes = C.c_size_t()
+        rc = L.ct_weights_bind(self.image.ctypes.data, n, C.byref(self.W),
+                               C.byref(data), C.byref(nbytes))
+        if rc != 0:
+            raise RuntimeError("ct_weights_bind failed")
+        self.data_ptr = data.value
+        self.data_bytes = nbytes.value
+        self.seed, self.variant = seed, variant
+
+    def ptr(self, field):
+        return self.W[FIELD_INDEX[field]]
+
+    def tensor(self, field, n):
+        """First n bf16 values of a tensor, widened to float32."""
+        raw = np.ctypeslib.as_array(C.cast(self.ptr(field), C.POINTER(C.c_uint16)), shape=(n,))
+        return (raw.astype(np.uint32) << 16).view(np.float32)
+
+    def weights_ref(self):
+        return C.byref(self.W)
+
+    def elayer_ptr(self, i):
+        return C.addressof(self.W) + (ENC_OFF + i * len(ELAYER_FIELDS)) * 8
+
+
+def synth_audio(n_samples, seed):
+    out = np.empty(n_samples, dtype=np.float32)
+    host().ct_synth_audio(out.ctypes.data, n_samples, seed)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# The 40-function backend ABI (include/backend.h).  Any library exporting it
+# (this backend, or the reference CPU backend when it is built for fixtures)
+# can be bound with bind_abi().
+# ---------------------------------------------------------------------------
+_P, _I, _F, _Z = C.c_void_p, C.c_int, C.c_float, C.c_size_t
+ABI_SIGS = {
+    "backend_init": ([_I], None),
+    "backend_destroy": ([], None),
+    "backend_num_devices": ([], _I),
+    "backend_thread_cleanup": ([], None),
+    "backend_weights_upload_blob": ([_P, _Z], None),
+    "backend_device_ptr": ([_P], _P),
+    "backend_arena_alloc": ([_Z], _P),
+    "backend_arena_free": ([_P], None),
+    "backend_htod": ([_P, _P, _Z], None),
+    "backend_dtoh": ([_P, _P, _Z], None),
+    "backend_layernorm": ([_P, _P, _P, _P, _I, _I], None),
+    "backend_linear": ([_P, _P, _P, _P, _I, _I, _I], None),
+    "backend_linear_silu": ([_P, _P, _P, _P, _I, _I, _I], None),
+    "backend_linear_relu": ([_P, _P, _P, _P, _I, _I, _I], None),
+    "backend_linear_fmadd": ([_P, _F, _P, _P, _P, _I, _I, _I], None),
+    "backend_add_inplace": ([_P, _P, _I], None),
+    "backend_encoder_subsampling": ([_P, _I, _I, _P, _I, _P, _P], None),
+    "backend_make_rel_pos_emb": ([_P, _I], None),
+    "backend_rel_pos_mhsa": ([_P, _P, _I, _P, _P], None),
+    "backend_conformer_conv": ([_P, _I, _P, _P], None),
+    "backend_sdp_attn": ([_P, _P, _P, _P, _P, _I, _I, _P], None),
+    "backend_embed": ([_P, _P, _I, _I, _P, _P, _P, _P], None),
+    "backend_fill_causal_mask": ([_P, _I], None),
+    "backend_lm_head": ([_P, _P, _P, _P], None),
+    "backend_upload_tokens": ([_P, _I], None),
+    "backend_graph_replay": ([_I, _I, _I, _I], _I),
+    "backend_graph_begin_capture": ([_I], None),
+    "backend_graph_end_capture": ([_I, _I, _I, _I], None),
+    "backend_decode_set_S": ([_I], None),
+    "backend_decode_inc_S": ([], None),
+    "backend_linear_to_kvcache": ([_P, _P, _P, _P, _I, _I], None),
+    "backend_sdp_attn_devS": ([_P, _P, _P, _P, _P], None),
+    "backend_embed_decode": ([_P, _P, _P, _P, _P], None),
+    "backend_embed_decode_batch": ([_P, _P, _P, _P, _I, _P, _P, _P, _P], None),
+    "backend_lm_head_batch": ([_P, _P, _P, _P, _P, _I], None),
+    "backend_argmax_batch": ([_P, _P, _P, _I], None),
+    "backend_upload_T_enc": ([_P, _I], None),
+    "backend_linear_to_kvcache_batch": ([_P, _P, _P, _P, _I, _I, _I, _I], None),
+    "backend_sdp_attn_batch_decode_sa": ([_P, _P, _P, _P, _I, _I, _P], None),
+    "backend_sdp_attn_batch_decode_ca": ([_P, _P, _P, _P, _I, _I, _P], None),
+}
+assert len(ABI_SIGS) == 40
+
+
+def bind_abi(lib):
+    for name, (args, ret) in ABI_SIGS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = ret
+    return lib
+
+
+_hip = None
+
+
+def hip():
+    """libct_hip.so with the ABI bound.  Raises if the library is missing:
+    there is no CPU fallback behind this binding."""
+    global _hip
+    if _hip is None:
+        if not os.path.exists(HIP_LIB):
+            raise RuntimeError(f"{HIP_LIB} is not built (run __graft_entry__.build())")
+        _hip = bind_abi(C.CDLL(HIP_LIB))
+    return _hip
