@@ -1,0 +1,47 @@
+/* ct_engine.h — device-resident decode state of the engine (C and HIP). */
+#ifndef CT_ENGINE_H
+#define CT_ENGINE_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CT_PROMPT_MAX 16
+
+/* All pointers are device memory.  Slot-major arrays have `slots` entries,
+ * request-major arrays `max_req`. */
+typedef struct {
+    int slots, max_req, smax, tmax;
+    /* slot table */
+    int  *slot_req;    /* request in the slot, -1 when free                    */
+    int  *slot_S;      /* tokens already in the slot's self cache              */
+    int  *act;         /* 1 if the slot decodes this step                      */
+    int  *tok;         /* token embedded this step                             */
+    int  *pos_len;     /* self length after this step's append (0 when idle)   */
+    int  *cross_len;   /* encoder frames of the slot's request (0 when idle)   */
+    int  *cross_idx;   /* request whose cross K/V the slot reads               */
+    long *kv_rowoff;   /* element offset of this step's self K/V row, -1 idle  */
+    /* requests */
+    int  *req_T, *req_limit, *req_flags, *req_np, *req_ngen;
+    int  *req_prompt;  /* [max_req][CT_PROMPT_MAX]                             */
+    int  *req_out;     /* [max_req][smax] generated tokens                     */
+    /* queue: q[0] next request to admit, q[1] requests ready (encoded),
+     * q[2] requests finished */
+    int  *q;
+} CtEngDev;
+
+/* Admission + per-slot step inputs (one workgroup; admission is sequential
+ * over slots in slot order, so scheduling is deterministic). */
+void ctk_eng_begin(const CtEngDev *d, hipStream_t s);
+/* Argmax with the request's policy, token append, retirement. */
+void ctk_eng_end(const CtEngDev *d, const float *logits, hipStream_t s);
+/* Seeded fill of n elements (N(0,1)*scale approx.), bf16 or fp32. */
+void ctk_fill_random(void *p, long n, int bf16, float scale, uint64_t seed, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

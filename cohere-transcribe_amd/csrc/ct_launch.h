@@ -22,6 +22,16 @@ enum {
     CT_EPI_GLU   = 4    /* Y[:, j] = s_j * sigmoid(s_{j+glu_half}) */
 };
 
+/* Output segment of a GEMM: columns [i*seg_w, (i+1)*seg_w) go to seg[i]. */
+enum { CT_OUT_DENSE = 0, CT_OUT_HEADS_F32 = 1, CT_OUT_HEADS_BF16 = 2 };
+typedef struct {
+    int         mode;
+    void       *base;
+    long        ld;           /* DENSE: row stride in floats                     */
+    const long *rowoff;       /* HEADS: per-row element offset (< 0: skip row);  */
+    long        hstride;      /* column c -> base + rowoff[m] + (c/128)*hstride + c%128 */
+} CtSeg;
+
 typedef struct {
     const float    *A;        /* [M][lda] fp32 activations                 */
     long            lda;
@@ -39,6 +49,9 @@ typedef struct {
     long            row_stride;
     int             glu_half; /* CT_EPI_GLU: N == 2*glu_half               */
     const int      *row_mask; /* rows m with row_mask[m] == 0 are not written */
+    int             nseg;     /* > 0: segmented output (epi must be STORE)  */
+    int             seg_w;
+    CtSeg           seg[3];
 } CtGemm;
 
 void ctk_gemm(const CtGemm *g, hipStream_t s);
@@ -73,6 +86,7 @@ typedef struct {
     const int *lens;          /* keys per item: lens[b*lens_step] (device) ...         */
     int   lens_step;
     int   len_const;          /* ... or this when lens == NULL                          */
+    const int   *kv_index;    /* optional: item b reads K/V block kv_index[b]          */
     const float *mask;        /* optional additive [T_q][T_k] mask (B == 1)            */
     int   T_q, B, H;
     float scale;
@@ -86,11 +100,26 @@ void ctk_attn(const CtAttn *a, hipStream_t s);
 void ctk_relpos_attn(float *O, const float *Q, const float *K, const float *V,
                      const float *P, const uint16_t *pbu, const uint16_t *pbv,
                      int T, hipStream_t s);
-/* Depthwise conv k=9 (zero pad 4 inside the sequence) + BN + SiLU. */
+/* Packed clips: sequence i has T = seq_T[i] rows starting at row seq_off[i]
+ * of Q/K/V/O; its P rows are the window of a table built for T_max, shifted
+ * by T_max - T (model.h:586-592).  Work items (clip, 16-query block) are
+ * listed in blk_seq/blk_q0 (n_blk entries, built by ctk_relpos_plan). */
+int  ctk_relpos_plan(int *blk_seq, int *blk_q0, const int *seq_T, int n_seq);
+void ctk_relpos_attn_packed(float *O, const float *Q, const float *K, const float *V,
+                            const float *P, int T_max, const uint16_t *pbu, const uint16_t *pbv,
+                            const int *seq_off, const int *seq_T, const int *blk_seq,
+                            const int *blk_q0, int n_blk, int max_T, hipStream_t s);
+/* Depthwise conv k=9 (zero pad 4 inside the sequence) + BN + SiLU.  With
+ * row_start/row_len (per row: first row and length of its sequence) the rows
+ * are packed sequences; otherwise one sequence of T rows. */
 void ctk_dwconv_bn_silu(float *out, const float *in, int T,
                         const uint16_t *dww, const uint16_t *dwb,
                         const uint16_t *bnw, const uint16_t *bnb,
                         const uint16_t *bnm, const uint16_t *bnv, hipStream_t s);
+void ctk_dwconv_bn_silu_packed(float *out, const float *in, int M, const int *row_start,
+                               const int *row_len, const uint16_t *dww, const uint16_t *dwb,
+                               const uint16_t *bnw, const uint16_t *bnb,
+                               const uint16_t *bnm, const uint16_t *bnv, hipStream_t s);
 /* Subsampling stages (position-major [t][f][ch] activations). */
 void ctk_sub_conv0(float *out, const float *mel, int T_mel, int stride,
                    const uint16_t *w, const uint16_t *b, hipStream_t s);

@@ -1,0 +1,595 @@
+/* engine.c — the hipb_* decode engine (include/hipb.h), host side.
+ *
+ * Owns the device state of a continuous-batching transcription run: the
+ * request pool (encoder output, cross-attention K/V per request), the slot
+ * table and self-attention KV caches per slot, activations for one step over
+ * all slots, and a captured hipGraph of that step.  A step is
+ *   eng_begin -> embed+LN -> 8 x [LN, QKV GEMM (+KV append), self attention,
+ *   out-proj (+residual), LN, Q GEMM, cross attention, out-proj (+residual),
+ *   LN, FFN up (ReLU), FFN down (+residual)] -> LN -> LM head -> eng_end,
+ * the per-item loop of model.h:666-744 with every slot processed at once.
+ * The encoder runs packed: all frames of a batch of requests form the rows
+ * of one GEMM (model.h:573-635 per item, here M = sum of frames).
+ */
+#include "../../include/backend.h"
+#include "../../include/hipb.h"
+#include "ct_abi_state.h"
+#include "ct_engine.h"
+#include "ct_launch.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef struct {
+    float *mel;          /* host copy until encoded */
+    int T_mel, T_enc;
+} HostReq;
+
+struct HipbEngine {
+    HipbConfig cfg;
+    Weights W;
+    hipStream_t s;
+    int dev;
+    int esz;             /* KV element size */
+    CtEngDev d;
+    /* repacked weights: [Wq;Wk;Wv] per layer, [Wk;Wv] cross per layer */
+    uint16_t *wqkv, *bqkv, *wckv, *bckv;
+    /* caches */
+    void *kself, *vself;       /* [L][slots][H][smax][128] */
+    void *kcross, *vcross;     /* [L][max_req][H][tmax][128] */
+    float *enc_pool;           /* [max_req][tmax][DEC_D] */
+    /* step activations */
+    float *h, *ln, *q, *att, *mid, *logits;
+    /* encoder workspace (lazy) */
+    int enc_cap;               /* frames */
+    int sub_cap;               /* subsampling scratch floats */
+    float *ex, *eln, *emid, *eq, *ek, *ev, *eo, *eg, *edw, *epe, *ep, *eh, *esub, *emel;
+    size_t emel_cap;
+    int *e_row_start, *e_row_len, *e_seq_off, *e_seq_T, *e_blk_seq, *e_blk_q0;
+    long *e_rowoff;
+    /* requests */
+    HostReq *req;
+    int n_req, n_enc;
+    int *h_tmp;                /* pinned staging */
+    /* graph */
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    int have_graph;
+    int bench_mode;
+};
+
+#define ECHK(x) ct_hip_check((x), #x, __FILE__, __LINE__)
+
+static void *dmalloc(size_t bytes) {
+    void *p = NULL;
+    ECHK(hipMalloc(&p, bytes ? bytes : 16));
+    return p;
+}
+
+static const uint16_t *DW(const void *p) { return (const uint16_t *)ct_dev_w(p); }
+
+static void gemm(HipbEngine *e, const float *A, int M, int K, const uint16_t *Wh, const uint16_t *bh,
+                 float *Y, int N, int epi, float scale, const int *row_mask) {
+    CtGemm g;
+    memset(&g, 0, sizeof g);
+    g.A = A; g.lda = K; g.W = DW(Wh); g.bias = DW(bh);
+    g.Y = Y; g.ldy = N; g.M = M; g.N = N; g.K = K; g.epi = epi; g.scale = scale;
+    g.row_mask = row_mask;
+    ctk_gemm(&g, e->s);
+}
+
+HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
+    if (ct_t.dev < 0) CT_FATAL("hipb_create: call backend_init first");
+    if (cfg->slots < 1 || cfg->slots > CT_MAX_BATCH) CT_FATAL("hipb_create: slots outside [1, 256]");
+    if (cfg->max_frames < 1 || cfg->max_frames > 2048) CT_FATAL("hipb_create: max_frames outside [1, 2048]");
+    if (cfg->max_requests < 1) CT_FATAL("hipb_create: max_requests < 1");
+    HipbEngine *e = calloc(1, sizeof *e);
+    if (!e) CT_FATAL("out of host memory");
+    e->cfg = *cfg;
+    e->W = *W;
+    e->s = ct_t.stream;
+    e->dev = ct_t.dev;
+    e->esz = cfg->kv_bf16 ? 2 : 4;
+    const int S = cfg->slots, R = cfg->max_requests;
+    const int tmax = (cfg->max_frames + 7) / 8 * 8;
+    CtEngDev *d = &e->d;
+    d->slots = S; d->max_req = R; d->smax = MAX_SEQ; d->tmax = tmax;
+    d->slot_req = dmalloc(S * sizeof(int));
+    d->slot_S = dmalloc(S * sizeof(int));
+    d->act = dmalloc(S * sizeof(int));
+    d->tok = dmalloc(S * sizeof(int));
+    d->pos_len = dmalloc(S * sizeof(int));
+    d->cross_len = dmalloc(S * sizeof(int));
+    d->cross_idx = dmalloc(S * sizeof(int));
+    d->kv_rowoff = dmalloc(S * sizeof(long));
+    d->req_T = dmalloc(R * sizeof(int));
+    d->req_limit = dmalloc(R * sizeof(int));
+    d->req_flags = dmalloc(R * sizeof(int));
+    d->req_np = dmalloc(R * sizeof(int));
+    d->req_ngen = dmalloc(R * sizeof(int));
+    d->req_prompt = dmalloc((size_t)R * CT_PROMPT_MAX * sizeof(int));
+    d->req_out = dmalloc((size_t)R * MAX_SEQ * sizeof(int));
+    d->q = dmalloc(4 * sizeof(int));
+    ECHK(hipMemsetAsync(d->slot_req, 0xff, S * sizeof(int), e->s));   /* -1: free */
+    ECHK(hipMemsetAsync(d->slot_S, 0, S * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->req_ngen, 0, R * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->q, 0, 4 * sizeof(int), e->s));
+
+    /* repack [Wq;Wk;Wv] and cross [Wk;Wv] contiguously (device to device) */
+    const size_t wsz = (size_t)DEC_D * DEC_D * 2, bsz = (size_t)DEC_D * 2;
+    e->wqkv = dmalloc(DEC_N * 3 * wsz);
+    e->bqkv = dmalloc(DEC_N * 3 * bsz);
+    e->wckv = dmalloc(DEC_N * 2 * wsz);
+    e->bckv = dmalloc(DEC_N * 2 * bsz);
+    for (int l = 0; l < DEC_N; l++) {
+        const DLayer *L = &W->dec[l];
+        const uint16_t *ws[3] = {L->sa_qw, L->sa_kw, L->sa_vw}, *bs[3] = {L->sa_qb, L->sa_kb, L->sa_vb};
+        for (int i = 0; i < 3; i++) {
+            ECHK(hipMemcpyAsync((char *)e->wqkv + (3 * l + i) * wsz, DW(ws[i]), wsz, hipMemcpyDeviceToDevice, e->s));
+            ECHK(hipMemcpyAsync((char *)e->bqkv + (3 * l + i) * bsz, DW(bs[i]), bsz, hipMemcpyDeviceToDevice, e->s));
+        }
+        ECHK(hipMemcpyAsync((char *)e->wckv + (2 * l) * wsz, DW(L->ca_kw), wsz, hipMemcpyDeviceToDevice, e->s));
+        ECHK(hipMemcpyAsync((char *)e->wckv + (2 * l + 1) * wsz, DW(L->ca_vw), wsz, hipMemcpyDeviceToDevice, e->s));
+        ECHK(hipMemcpyAsync((char *)e->bckv + (2 * l) * bsz, DW(L->ca_kb), bsz, hipMemcpyDeviceToDevice, e->s));
+        ECHK(hipMemcpyAsync((char *)e->bckv + (2 * l + 1) * bsz, DW(L->ca_vb), bsz, hipMemcpyDeviceToDevice, e->s));
+    }
+    const size_t self_el = (size_t)DEC_N * S * DEC_H * MAX_SEQ * DEC_DK;
+    const size_t cross_el = (size_t)DEC_N * R * DEC_H * tmax * DEC_DK;
+    e->kself = dmalloc(self_el * e->esz);
+    e->vself = dmalloc(self_el * e->esz);
+    e->kcross = dmalloc(cross_el * e->esz);
+    e->vcross = dmalloc(cross_el * e->esz);
+    e->enc_pool = dmalloc((size_t)R * tmax * DEC_D * sizeof(float));
+    e->h = dmalloc((size_t)S * DEC_D * 4);
+    e->ln = dmalloc((size_t)S * DEC_D * 4);
+    e->q = dmalloc((size_t)S * DEC_D * 4);
+    e->att = dmalloc((size_t)S * DEC_D * 4);
+    e->mid = dmalloc((size_t)S * DEC_FF * 4);
+    e->logits = dmalloc((size_t)S * VOCAB * 4);
+    ECHK(hipMemsetAsync(e->h, 0, (size_t)S * DEC_D * 4, e->s));
+    e->req = calloc(R, sizeof(HostReq));
+    ECHK(hipHostMalloc((void **)&e->h_tmp, (size_t)(R + 8) * (MAX_SEQ + 8) * sizeof(int), 0));
+    ECHK(hipStreamSynchronize(e->s));
+    return e;
+}
+
+void hipb_destroy(HipbEngine *e) {
+    if (!e) return;
+    ECHK(hipStreamSynchronize(e->s));
+    if (e->have_graph) { hipGraphExecDestroy(e->exec); hipGraphDestroy(e->graph); }
+    void *ptrs[] = {e->d.slot_req, e->d.slot_S, e->d.act, e->d.tok, e->d.pos_len, e->d.cross_len,
+                    e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
+                    e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
+                    e->wqkv, e->bqkv, e->wckv, e->bckv, e->kself, e->vself, e->kcross, e->vcross,
+                    e->enc_pool, e->h, e->ln, e->q, e->att, e->mid, e->logits,
+                    e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
+                    e->eh, e->esub, e->emel, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
+                    e->e_blk_seq, e->e_blk_q0, e->e_rowoff};
+    for (size_t i = 0; i < sizeof ptrs / sizeof ptrs[0]; i++)
+        if (ptrs[i]) ECHK(hipFree(ptrs[i]));
+    for (int r = 0; r < e->n_req; r++) free(e->req[r].mel);
+    free(e->req);
+    ECHK(hipHostFree(e->h_tmp));
+    free(e);
+}
+
+void *hipb_stream(HipbEngine *e) { return (void *)e->s; }
+
+/* ------------------------------------------------------------------ */
+/* Requests and the packed encoder                                     */
+/* ------------------------------------------------------------------ */
+static int t_enc_of(int T_mel) {
+    const int a = (T_mel + 1) / 2, b = (a + 1) / 2;
+    return (b + 1) / 2;
+}
+
+int hipb_submit(HipbEngine *e, const float *mel, int T_mel, const int *prompt, int n_prompt,
+                int limit, int flags) {
+    if (e->bench_mode) CT_FATAL("hipb_submit: engine is in microbenchmark mode");
+    if (e->n_req >= e->cfg.max_requests) CT_FATAL("hipb_submit: request pool full");
+    if (n_prompt < 1 || n_prompt > CT_PROMPT_MAX) CT_FATAL("hipb_submit: prompt length outside [1, 16]");
+    if (limit < 1) CT_FATAL("hipb_submit: limit < 1");
+    const int Te = t_enc_of(T_mel);
+    if (T_mel < 1 || Te > e->d.tmax || Te > e->cfg.max_frames) CT_FATAL("hipb_submit: clip longer than max_frames");
+    const int r = e->n_req++;
+    HostReq *q = &e->req[r];
+    q->T_mel = T_mel;
+    q->T_enc = Te;
+    q->mel = malloc((size_t)N_MELS * T_mel * sizeof(float));
+    if (!q->mel) CT_FATAL("out of host memory");
+    memcpy(q->mel, mel, (size_t)N_MELS * T_mel * sizeof(float));
+    int meta[4 + CT_PROMPT_MAX];
+    meta[0] = Te; meta[1] = limit; meta[2] = flags; meta[3] = n_prompt;
+    memset(meta + 4, 0, sizeof(int) * CT_PROMPT_MAX);
+    memcpy(meta + 4, prompt, (size_t)n_prompt * sizeof(int));
+    ECHK(hipMemcpy(e->d.req_T + r, &meta[0], sizeof(int), hipMemcpyHostToDevice));
+    ECHK(hipMemcpy(e->d.req_limit + r, &meta[1], sizeof(int), hipMemcpyHostToDevice));
+    ECHK(hipMemcpy(e->d.req_flags + r, &meta[2], sizeof(int), hipMemcpyHostToDevice));
+    ECHK(hipMemcpy(e->d.req_np + r, &meta[3], sizeof(int), hipMemcpyHostToDevice));
+    ECHK(hipMemcpy(e->d.req_prompt + (size_t)r * CT_PROMPT_MAX, meta + 4, CT_PROMPT_MAX * sizeof(int),
+                   hipMemcpyHostToDevice));
+    return r;
+}
+
+int hipb_req_frames(HipbEngine *e, int req) {
+    return (req >= 0 && req < e->n_req) ? e->req[req].T_enc : 0;
+}
+
+static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
+    const int T1 = (max_tmel + 1) / 2, T2 = (T1 + 1) / 2;
+    const int sub = SUB_CH * (T1 * 64 + T2 * 32);
+    if (frames <= e->enc_cap && sub <= e->sub_cap) return;
+    ECHK(hipStreamSynchronize(e->s));
+    float **bufs[] = {&e->ex, &e->eln, &e->emid, &e->eq, &e->ek, &e->ev, &e->eo, &e->eg, &e->edw, &e->eh};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
+        if (*bufs[i]) { ECHK(hipFree(*bufs[i])); *bufs[i] = NULL; }
+    int **ib[] = {&e->e_row_start, &e->e_row_len, &e->e_seq_off, &e->e_seq_T, &e->e_blk_seq, &e->e_blk_q0};
+    for (size_t i = 0; i < sizeof ib / sizeof ib[0]; i++)
+        if (*ib[i]) { ECHK(hipFree(*ib[i])); *ib[i] = NULL; }
+    if (e->e_rowoff) ECHK(hipFree(e->e_rowoff));
+    if (e->esub) ECHK(hipFree(e->esub));
+    if (!e->epe) {
+        e->epe = dmalloc((size_t)(2 * e->d.tmax - 1) * ENC_D * 4);
+        e->ep = dmalloc((size_t)(2 * e->d.tmax - 1) * ENC_D * 4);
+    }
+    const int M = frames > e->enc_cap ? frames : e->enc_cap;
+    const size_t rows = (size_t)M;
+    e->ex = dmalloc(rows * ENC_D * 4);
+    e->eln = dmalloc(rows * ENC_D * 4);
+    e->emid = dmalloc(rows * ENC_FF * 4);
+    e->eq = dmalloc(rows * ENC_D * 4);
+    e->ek = dmalloc(rows * ENC_D * 4);
+    e->ev = dmalloc(rows * ENC_D * 4);
+    e->eo = dmalloc(rows * ENC_D * 4);
+    e->eg = dmalloc(rows * ENC_D * 4);
+    e->edw = dmalloc(rows * ENC_D * 4);
+    e->eh = dmalloc(rows * DEC_D * 4);
+    e->e_row_start = dmalloc(rows * sizeof(int));
+    e->e_row_len = dmalloc(rows * sizeof(int));
+    e->e_rowoff = dmalloc(rows * sizeof(long));
+    /* at most M sequences (one frame each) and M query blocks */
+    e->e_seq_off = dmalloc(rows * sizeof(int));
+    e->e_seq_T = dmalloc(rows * sizeof(int));
+    e->e_blk_seq = dmalloc(rows * sizeof(int));
+    e->e_blk_q0 = dmalloc(rows * sizeof(int));
+    const int sc = sub > e->sub_cap ? sub : e->sub_cap;
+    e->esub = dmalloc((size_t)sc * 4);
+    e->enc_cap = M;
+    e->sub_cap = sc;
+}
+
+/* Encodes requests [r0, r1) as one packed batch. */
+static void encode_batch(HipbEngine *e, int r0, int r1) {
+    const int n = r1 - r0;
+    int M = 0, tmel_max = 0, T_max = 0;
+    for (int r = r0; r < r1; r++) {
+        M += e->req[r].T_enc;
+        if (e->req[r].T_mel > tmel_max) tmel_max = e->req[r].T_mel;
+        if (e->req[r].T_enc > T_max) T_max = e->req[r].T_enc;
+    }
+    enc_reserve(e, M, tmel_max);
+    hipStream_t s = e->s;
+    /* host-side row tables */
+    int *row_start = malloc(M * sizeof(int)), *row_len = malloc(M * sizeof(int));
+    long *rowoff = malloc(M * sizeof(long));
+    int *seq_off = malloc(n * sizeof(int)), *seq_T = malloc(n * sizeof(int));
+    int off = 0;
+    for (int i = 0; i < n; i++) {
+        const int r = r0 + i, T = e->req[r].T_enc;
+        seq_off[i] = off;
+        seq_T[i] = T;
+        for (int t = 0; t < T; t++) {
+            row_start[off + t] = off;
+            row_len[off + t] = T;
+            rowoff[off + t] = ((long)r * DEC_H * e->d.tmax + t) * DEC_DK;
+        }
+        off += T;
+    }
+    const int nblk = ctk_relpos_plan(NULL, NULL, seq_T, n);
+    int *blk_seq = malloc(nblk * sizeof(int)), *blk_q0 = malloc(nblk * sizeof(int));
+    ctk_relpos_plan(blk_seq, blk_q0, seq_T, n);
+    if (nblk > e->enc_cap) CT_FATAL("encode: query-block table larger than the workspace");
+    ECHK(hipMemcpyAsync(e->e_row_start, row_start, M * sizeof(int), hipMemcpyHostToDevice, s));
+    ECHK(hipMemcpyAsync(e->e_row_len, row_len, M * sizeof(int), hipMemcpyHostToDevice, s));
+    ECHK(hipMemcpyAsync(e->e_rowoff, rowoff, M * sizeof(long), hipMemcpyHostToDevice, s));
+    ECHK(hipMemcpyAsync(e->e_seq_off, seq_off, n * sizeof(int), hipMemcpyHostToDevice, s));
+    ECHK(hipMemcpyAsync(e->e_seq_T, seq_T, n * sizeof(int), hipMemcpyHostToDevice, s));
+    ECHK(hipMemcpyAsync(e->e_blk_seq, blk_seq, nblk * sizeof(int), hipMemcpyHostToDevice, s));
+    ECHK(hipMemcpyAsync(e->e_blk_q0, blk_q0, nblk * sizeof(int), hipMemcpyHostToDevice, s));
+
+    /* subsampling per request into packed rows (scratch as the ABI path) */
+    size_t mel_need = 0;
+    for (int r = r0; r < r1; r++) mel_need += (size_t)N_MELS * e->req[r].T_mel;
+    if (mel_need > e->emel_cap) {
+        if (e->emel) ECHK(hipFree(e->emel));
+        e->emel = dmalloc(mel_need * 4);
+        e->emel_cap = mel_need;
+    }
+    size_t moff = 0;
+    const Weights *W = &e->W;
+    for (int i = 0; i < n; i++) {
+        HostReq *q = &e->req[r0 + i];
+        float *mel = e->emel + moff;
+        moff += (size_t)N_MELS * q->T_mel;
+        ECHK(hipMemcpyAsync(mel, q->mel, (size_t)N_MELS * q->T_mel * 4, hipMemcpyHostToDevice, s));
+        const int T1 = (q->T_mel + 1) / 2, T2 = (T1 + 1) / 2;
+        float *ra = e->esub, *rb = e->esub + (size_t)SUB_CH * T1 * 64;
+        ctk_sub_conv0(ra, mel, q->T_mel, q->T_mel, DW(W->s0w), DW(W->s0b), s);
+        ctk_sub_dwconv(rb, ra, T1, 64, DW(W->s2w), DW(W->s2b), s);
+        gemm(e, rb, T2 * 32, SUB_CH, W->s3w, W->s3b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
+        ctk_sub_dwconv(rb, ra, T2, 32, DW(W->s5w), DW(W->s5b), s);
+        gemm(e, rb, q->T_enc * 16, SUB_CH, W->s6w, W->s6b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
+        ctk_sub_flatten(rb, ra, q->T_enc, s);
+        gemm(e, rb, q->T_enc, SUB_CH * 16, W->sow, W->sob, e->ex + (size_t)seq_off[i] * ENC_D, ENC_D,
+             CT_EPI_STORE, 0, NULL);
+    }
+    /* relative positions for T_max; each clip reads its shifted window */
+    ctk_rel_pos_emb(e->epe, T_max, ct_inv_freq(), s);
+    for (int l = 0; l < ENC_N; l++) {
+        const ELayer *L = &W->enc[l];
+        ctk_layernorm(e->eln, e->ex, DW(L->ff1_lnw), DW(L->ff1_lnb), M, ENC_D, s);
+        gemm(e, e->eln, M, ENC_D, L->ff1_w1, L->ff1_b1, e->emid, ENC_FF, CT_EPI_SILU, 0, NULL);
+        gemm(e, e->emid, M, ENC_FF, L->ff1_w2, L->ff1_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f, NULL);
+
+        ctk_layernorm(e->eln, e->ex, DW(L->sa_lnw), DW(L->sa_lnb), M, ENC_D, s);
+        gemm(e, e->eln, M, ENC_D, L->sa_qw, L->sa_qb, e->eq, ENC_D, CT_EPI_STORE, 0, NULL);
+        gemm(e, e->eln, M, ENC_D, L->sa_kw, L->sa_kb, e->ek, ENC_D, CT_EPI_STORE, 0, NULL);
+        gemm(e, e->eln, M, ENC_D, L->sa_vw, L->sa_vb, e->ev, ENC_D, CT_EPI_STORE, 0, NULL);
+        gemm(e, e->epe, 2 * T_max - 1, ENC_D, L->sa_pw, NULL, e->ep, ENC_D, CT_EPI_STORE, 0, NULL);
+        ctk_relpos_attn_packed(e->eo, e->eq, e->ek, e->ev, e->ep, T_max, DW(L->sa_pbu), DW(L->sa_pbv),
+                               e->e_seq_off, e->e_seq_T, e->e_blk_seq, e->e_blk_q0, nblk, T_max, s);
+        gemm(e, e->eo, M, ENC_D, L->sa_ow, L->sa_ob, e->ex, ENC_D, CT_EPI_FMADD, 1.0f, NULL);
+
+        ctk_layernorm(e->eln, e->ex, DW(L->cv_lnw), DW(L->cv_lnb), M, ENC_D, s);
+        {
+            CtGemm g;
+            memset(&g, 0, sizeof g);
+            g.A = e->eln; g.lda = ENC_D; g.W = DW(L->cv_pw1w); g.bias = DW(L->cv_pw1b);
+            g.Y = e->eg; g.ldy = ENC_D; g.M = M; g.N = 2 * ENC_D; g.K = ENC_D;
+            g.epi = CT_EPI_GLU; g.glu_half = ENC_D;
+            ctk_gemm(&g, s);
+        }
+        ctk_dwconv_bn_silu_packed(e->edw, e->eg, M, e->e_row_start, e->e_row_len, DW(L->cv_dww),
+                                  DW(L->cv_dwb), DW(L->cv_bnw), DW(L->cv_bnb), DW(L->cv_bnmean),
+                                  DW(L->cv_bnvar), s);
+        gemm(e, e->edw, M, ENC_D, L->cv_pw2w, L->cv_pw2b, e->ex, ENC_D, CT_EPI_FMADD, 1.0f, NULL);
+
+        ctk_layernorm(e->eln, e->ex, DW(L->ff2_lnw), DW(L->ff2_lnb), M, ENC_D, s);
+        gemm(e, e->eln, M, ENC_D, L->ff2_w1, L->ff2_b1, e->emid, ENC_FF, CT_EPI_SILU, 0, NULL);
+        gemm(e, e->emid, M, ENC_FF, L->ff2_w2, L->ff2_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f, NULL);
+        ctk_layernorm(e->ex, e->ex, DW(L->out_lnw), DW(L->out_lnb), M, ENC_D, s);
+    }
+    gemm(e, e->ex, M, ENC_D, W->prw, W->prb, e->eh, DEC_D, CT_EPI_STORE, 0, NULL);
+    /* keep enc_h per request; cross K/V straight into the head-major pool */
+    for (int i = 0; i < n; i++)
+        ECHK(hipMemcpyAsync(e->enc_pool + (size_t)(r0 + i) * e->d.tmax * DEC_D,
+                            e->eh + (size_t)seq_off[i] * DEC_D, (size_t)seq_T[i] * DEC_D * 4,
+                            hipMemcpyDeviceToDevice, s));
+    const size_t cross_l = (size_t)e->d.max_req * DEC_H * e->d.tmax * DEC_DK;
+    for (int l = 0; l < DEC_N; l++) {
+        CtGemm g;
+        memset(&g, 0, sizeof g);
+        g.A = e->eh; g.lda = DEC_D;
+        g.W = e->wckv + (size_t)2 * l * DEC_D * DEC_D; g.bias = e->bckv + (size_t)2 * l * DEC_D;
+        g.M = M; g.N = 2 * DEC_D; g.K = DEC_D; g.epi = CT_EPI_STORE;
+        g.nseg = 2; g.seg_w = DEC_D;
+        const int mode = e->esz == 2 ? CT_OUT_HEADS_BF16 : CT_OUT_HEADS_F32;
+        g.seg[0] = (CtSeg){mode, (char *)e->kcross + l * cross_l * e->esz, 0, e->e_rowoff,
+                           (long)e->d.tmax * DEC_DK};
+        g.seg[1] = (CtSeg){mode, (char *)e->vcross + l * cross_l * e->esz, 0, e->e_rowoff,
+                           (long)e->d.tmax * DEC_DK};
+        ctk_gemm(&g, s);
+    }
+    ECHK(hipStreamSynchronize(s));
+    free(row_start); free(row_len); free(rowoff); free(seq_off); free(seq_T); free(blk_seq); free(blk_q0);
+}
+
+void hipb_encode(HipbEngine *e, int max_batch_frames) {
+    if (max_batch_frames < e->d.tmax) max_batch_frames = e->d.tmax;
+    int r = e->n_enc;
+    while (r < e->n_req) {
+        int frames = 0, r1 = r;
+        while (r1 < e->n_req && (r1 == r || frames + e->req[r1].T_enc <= max_batch_frames)) {
+            frames += e->req[r1].T_enc;
+            r1++;
+        }
+        encode_batch(e, r, r1);
+        for (int i = r; i < r1; i++) { free(e->req[i].mel); e->req[i].mel = NULL; }
+        r = r1;
+    }
+    e->n_enc = r;
+    /* publish: requests [0, n_enc) may now be admitted */
+    ECHK(hipMemcpy(e->d.q + 1, &e->n_enc, sizeof(int), hipMemcpyHostToDevice));
+}
+
+/* ------------------------------------------------------------------ */
+/* The decode step                                                     */
+/* ------------------------------------------------------------------ */
+static void attn(HipbEngine *e, float *out, const float *Q, const void *K, const void *V,
+                 long item_stride, long head_stride, const int *lens, const int *kv_index) {
+    CtAttn a;
+    memset(&a, 0, sizeof a);
+    a.out = out; a.Q = Q; a.q_sb = DEC_D; a.q_st = DEC_D;
+    a.K = K; a.V = V; a.kv_bf16 = e->esz == 2;
+    a.kv_sb = item_stride; a.kv_st = DEC_DK; a.kv_sh = head_stride;
+    a.lens = lens; a.lens_step = 1; a.kv_index = kv_index;
+    a.T_q = 1; a.B = e->d.slots; a.H = DEC_H;
+    a.scale = 0.08838834764831845f;   /* 1/sqrt(128) */
+    ctk_attn(&a, e->s);
+}
+
+static void self_kv(HipbEngine *e, int l, void **k, void **v) {
+    const size_t per = (size_t)e->d.slots * DEC_H * MAX_SEQ * DEC_DK * e->esz;
+    *k = (char *)e->kself + l * per;
+    *v = (char *)e->vself + l * per;
+}
+
+static void cross_kv(HipbEngine *e, int l, void **k, void **v) {
+    const size_t per = (size_t)e->d.max_req * DEC_H * e->d.tmax * DEC_DK * e->esz;
+    *k = (char *)e->kcross + l * per;
+    *v = (char *)e->vcross + l * per;
+}
+
+static void step_attention(HipbEngine *e, int l, int cross) {
+    void *k, *v;
+    if (!cross) {
+        self_kv(e, l, &k, &v);
+        attn(e, e->att, e->q, k, v, (long)DEC_H * MAX_SEQ * DEC_DK, (long)MAX_SEQ * DEC_DK,
+             e->d.pos_len, NULL);
+    } else {
+        cross_kv(e, l, &k, &v);
+        attn(e, e->att, e->q, k, v, (long)DEC_H * e->d.tmax * DEC_DK, (long)e->d.tmax * DEC_DK,
+             e->d.cross_len, e->d.cross_idx);
+    }
+}
+
+static void step_launch(HipbEngine *e) {
+    const Weights *W = &e->W;
+    const int B = e->d.slots;
+    hipStream_t s = e->s;
+    ctk_eng_begin(&e->d, s);
+    ctk_embed_ln(e->h, e->d.tok, B, 0, e->d.pos_len, e->d.act, DW(W->etw), DW(W->epw),
+                 DW(W->elnw), DW(W->elnb), s);
+    for (int l = 0; l < DEC_N; l++) {
+        const DLayer *L = &W->dec[l];
+        void *ks, *vs;
+        self_kv(e, l, &ks, &vs);
+        ctk_layernorm(e->ln, e->h, DW(L->sa_lnw), DW(L->sa_lnb), B, DEC_D, s);
+        CtGemm g;
+        memset(&g, 0, sizeof g);
+        g.A = e->ln; g.lda = DEC_D;
+        g.W = e->wqkv + (size_t)3 * l * DEC_D * DEC_D; g.bias = e->bqkv + (size_t)3 * l * DEC_D;
+        g.M = B; g.N = 3 * DEC_D; g.K = DEC_D; g.epi = CT_EPI_STORE; g.row_mask = e->d.act;
+        g.nseg = 3; g.seg_w = DEC_D;
+        const int mode = e->esz == 2 ? CT_OUT_HEADS_BF16 : CT_OUT_HEADS_F32;
+        g.seg[0] = (CtSeg){CT_OUT_DENSE, e->q, DEC_D, NULL, 0};
+        g.seg[1] = (CtSeg){mode, ks, 0, e->d.kv_rowoff, (long)MAX_SEQ * DEC_DK};
+        g.seg[2] = (CtSeg){mode, vs, 0, e->d.kv_rowoff, (long)MAX_SEQ * DEC_DK};
+        ctk_gemm(&g, s);
+        step_attention(e, l, 0);
+        gemm(e, e->att, B, DEC_D, L->sa_ow, L->sa_ob, e->h, DEC_D, CT_EPI_FMADD, 1.0f, NULL);
+
+        ctk_layernorm(e->ln, e->h, DW(L->ca_lnw), DW(L->ca_lnb), B, DEC_D, s);
+        gemm(e, e->ln, B, DEC_D, L->ca_qw, L->ca_qb, e->q, DEC_D, CT_EPI_STORE, 0, NULL);
+        step_attention(e, l, 1);
+        gemm(e, e->att, B, DEC_D, L->ca_ow, L->ca_ob, e->h, DEC_D, CT_EPI_FMADD, 1.0f, NULL);
+
+        ctk_layernorm(e->ln, e->h, DW(L->ffn_lnw), DW(L->ffn_lnb), B, DEC_D, s);
+        gemm(e, e->ln, B, DEC_D, L->ffn_w1, L->ffn_b1, e->mid, DEC_FF, CT_EPI_RELU, 0, NULL);
+        gemm(e, e->mid, B, DEC_FF, L->ffn_w2, L->ffn_b2, e->h, DEC_D, CT_EPI_FMADD, 1.0f, NULL);
+    }
+    ctk_layernorm(e->ln, e->h, DW(W->dlnw), DW(W->dlnb), B, DEC_D, s);
+    gemm(e, e->ln, B, DEC_D, W->etw, W->hdb, e->logits, VOCAB, CT_EPI_STORE, 0, NULL);
+    ctk_eng_end(&e->d, e->logits, s);
+}
+
+void hipb_step(HipbEngine *e) { step_launch(e); }
+
+void hipb_attention_only(HipbEngine *e) {
+    for (int l = 0; l < DEC_N; l++) {
+        step_attention(e, l, 0);
+        step_attention(e, l, 1);
+    }
+}
+
+int hipb_finished(HipbEngine *e) {
+    int v = 0;
+    ECHK(hipMemcpyAsync(e->h_tmp, e->d.q + 2, sizeof(int), hipMemcpyDeviceToHost, e->s));
+    ECHK(hipStreamSynchronize(e->s));
+    v = e->h_tmp[0];
+    return v;
+}
+
+long hipb_run(HipbEngine *e, int chunk) {
+    if (chunk < 1) chunk = 1;
+    if (!e->have_graph) {
+        ECHK(hipStreamBeginCapture(e->s, hipStreamCaptureModeThreadLocal));
+        step_launch(e);
+        ECHK(hipStreamEndCapture(e->s, &e->graph));
+        ECHK(hipGraphInstantiate(&e->exec, e->graph, NULL, NULL, 0));
+        e->have_graph = 1;
+    }
+    long steps = 0;
+    for (;;) {
+        if (hipb_finished(e) >= e->n_enc) break;
+        for (int i = 0; i < chunk; i++) ECHK(hipGraphLaunch(e->exec, e->s));
+        steps += chunk;
+    }
+    return steps;
+}
+
+/* ------------------------------------------------------------------ */
+/* Results                                                             */
+/* ------------------------------------------------------------------ */
+int hipb_tokens(HipbEngine *e, int req, int *out, int cap) {
+    if (req < 0 || req >= e->n_req) return 0;
+    int n = 0;
+    ECHK(hipStreamSynchronize(e->s));
+    ECHK(hipMemcpy(&n, e->d.req_ngen + req, sizeof(int), hipMemcpyDeviceToHost));
+    if (n > cap) n = cap;
+    if (n > 0) ECHK(hipMemcpy(out, e->d.req_out + (size_t)req * MAX_SEQ, n * sizeof(int), hipMemcpyDeviceToHost));
+    return n;
+}
+
+int hipb_slot_of(HipbEngine *e, int req) {
+    ECHK(hipStreamSynchronize(e->s));
+    ECHK(hipMemcpy(e->h_tmp, e->d.slot_req, e->d.slots * sizeof(int), hipMemcpyDeviceToHost));
+    for (int s = 0; s < e->d.slots; s++)
+        if (e->h_tmp[s] == req) return s;
+    return -1;
+}
+
+void hipb_logits(HipbEngine *e, int slot, float *out) {
+    ECHK(hipStreamSynchronize(e->s));
+    ECHK(hipMemcpy(out, e->logits + (size_t)slot * VOCAB, VOCAB * sizeof(float), hipMemcpyDeviceToHost));
+}
+
+void hipb_enc_out(HipbEngine *e, int req, float *out) {
+    if (req < 0 || req >= e->n_enc) CT_FATAL("hipb_enc_out: request not encoded");
+    ECHK(hipStreamSynchronize(e->s));
+    ECHK(hipMemcpy(out, e->enc_pool + (size_t)req * e->d.tmax * DEC_D,
+                   (size_t)e->req[req].T_enc * DEC_D * sizeof(float), hipMemcpyDeviceToHost));
+}
+
+/* ------------------------------------------------------------------ */
+/* Microbenchmark state                                                */
+/* ------------------------------------------------------------------ */
+void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t seed) {
+    const int B = e->d.slots;
+    if (e->n_req) CT_FATAL("hipb_bench_fill: engine already has requests");
+    if (B > e->d.max_req) CT_FATAL("hipb_bench_fill: needs max_requests >= slots");
+    int *buf = e->h_tmp;
+    for (int s = 0; s < B; s++) {
+        if (S[s] < 1 || S[s] > MAX_SEQ - 64) CT_FATAL("hipb_bench_fill: S outside [1, MAX_SEQ-64]");
+        if (T_enc[s] < 1 || T_enc[s] > e->d.tmax) CT_FATAL("hipb_bench_fill: T_enc outside [1, max_frames]");
+    }
+    /* one synthetic request per slot: no prompt, one generated token, never
+     * finishes within the benchmark (limit MAX_SEQ, EOS suppressed) */
+    for (int s = 0; s < B; s++) buf[s] = s;
+    ECHK(hipMemcpy(e->d.slot_req, buf, B * sizeof(int), hipMemcpyHostToDevice));
+    for (int s = 0; s < B; s++) buf[s] = S[s] - 1;
+    ECHK(hipMemcpy(e->d.slot_S, buf, B * sizeof(int), hipMemcpyHostToDevice));
+    ECHK(hipMemcpy(e->d.req_T, T_enc, B * sizeof(int), hipMemcpyHostToDevice));
+    for (int s = 0; s < B; s++) buf[s] = MAX_SEQ;
+    ECHK(hipMemcpy(e->d.req_limit, buf, B * sizeof(int), hipMemcpyHostToDevice));
+    for (int s = 0; s < B; s++) buf[s] = HIPB_SUPPRESS_EOS;
+    ECHK(hipMemcpy(e->d.req_flags, buf, B * sizeof(int), hipMemcpyHostToDevice));
+    for (int s = 0; s < B; s++) buf[s] = 0;
+    ECHK(hipMemcpy(e->d.req_np, buf, B * sizeof(int), hipMemcpyHostToDevice));
+    for (int s = 0; s < B; s++) buf[s] = 1;
+    ECHK(hipMemcpy(e->d.req_ngen, buf, B * sizeof(int), hipMemcpyHostToDevice));
+    for (int s = 0; s < B; s++)
+        ECHK(hipMemcpy(e->d.req_out + (size_t)s * MAX_SEQ, &(int){100 + s}, sizeof(int), hipMemcpyHostToDevice));
+    int q[4] = {B, B, 0, 0};
+    ECHK(hipMemcpy(e->d.q, q, sizeof q, hipMemcpyHostToDevice));
+    const long self_el = (long)DEC_N * B * DEC_H * MAX_SEQ * DEC_DK;
+    const long cross_el = (long)DEC_N * e->d.max_req * DEC_H * e->d.tmax * DEC_DK;
+    ctk_fill_random(e->kself, self_el, e->esz == 2, 0.1f, seed, e->s);
+    ctk_fill_random(e->vself, self_el, e->esz == 2, 0.1f, seed + 1, e->s);
+    ctk_fill_random(e->kcross, cross_el, e->esz == 2, 0.1f, seed + 2, e->s);
+    ctk_fill_random(e->vcross, cross_el, e->esz == 2, 0.1f, seed + 3, e->s);
+    ECHK(hipStreamSynchronize(e->s));
+    e->n_enc = B;
+    e->bench_mode = 1;
+}

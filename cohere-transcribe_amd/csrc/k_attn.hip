@@ -52,7 +52,8 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
 #pragma unroll
     for (int i = 0; i < 8; i++) q[i] = qp[i];
     const float *mrow = a.mask ? a.mask + (long)qi * T : nullptr;
-    const long base = (long)b * a.kv_sb + (long)h * a.kv_sh + l16 * 8;
+    const long item = a.kv_index ? (long)a.kv_index[b] : (long)b;
+    const long base = item * a.kv_sb + (long)h * a.kv_sh + l16 * 8;
 
     float m = -INFINITY, l = 0.0f, o[8];
 #pragma unroll

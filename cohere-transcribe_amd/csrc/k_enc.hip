@@ -19,16 +19,31 @@ namespace {
 // Phase A walks keys, phase B walks the P window (T+QB-1 rows); each score
 // receives exactly one term from each phase.
 // ---------------------------------------------------------------------------
-template <int QB>
+template <int QB, bool PACKED>
 __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float *Q, const float *K,
                                                           const float *V, const float *P,
                                                           const uint16_t *pbu, const uint16_t *pbv,
-                                                          int T) {
+                                                          int T_arg, int T_max, const int *seq_off,
+                                                          const int *seq_T, const int *blk_seq,
+                                                          const int *blk_q0) {
     extern __shared__ float smem[];
+    int T, q0;
+    long off = 0;
+    if (PACKED) {
+        const int sq = blk_seq[blockIdx.x];
+        q0 = blk_q0[blockIdx.x];
+        T = seq_T[sq];
+        off = seq_off[sq];
+        P += (long)(T_max - T) * ENC_D;     // this clip's window of the T_max table
+    } else {
+        T = T_arg;
+        q0 = blockIdx.x * QB;
+    }
+    Q += off * ENC_D; K += off * ENC_D; V += off * ENC_D; O += off * ENC_D;
     float *qu = smem;                         // [QB][160]
     float *qv = qu + QB * ENC_DK;             // [QB][160]
     float *S = qv + QB * ENC_DK;              // [QB][T]
-    const int h = blockIdx.y, q0 = blockIdx.x * QB, tid = threadIdx.x;
+    const int h = blockIdx.y, tid = threadIdx.x;
     const int nq = min(QB, T - q0);
     const float sc = 1.0f / sqrtf((float)ENC_DK);
     for (int i = tid; i < QB * ENC_DK; i += 256) {
@@ -106,18 +121,22 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
 // Depthwise conv (k = 9, zero padding 4 inside the sequence) + inference
 // BatchNorm + SiLU (backends/cpu/backend.c:312-334).
 // ---------------------------------------------------------------------------
-__global__ void dwconv_bn_silu_kernel(float *out, const float *in, int T, const uint16_t *dww,
+__global__ void dwconv_bn_silu_kernel(float *out, const float *in, int M, const int *row_start,
+                                      const int *row_len, const uint16_t *dww,
                                       const uint16_t *dwb, const uint16_t *bnw, const uint16_t *bnb,
                                       const uint16_t *bnm, const uint16_t *bnv) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)T * ENC_D) return;
-    const int t = (int)(i / ENC_D), c = (int)(i % ENC_D);
+    if (i >= (long)M * ENC_D) return;
+    const int r = (int)(i / ENC_D), c = (int)(i % ENC_D);
+    const int st = row_start ? row_start[r] : 0;       // this row's sequence: [st, st + T)
+    const int T = row_len ? row_len[r] : M;
+    const int t = r - st;
     float s = bf2f(dwb[c]);
 #pragma unroll
     for (int k = 0; k < ENC_CK; k++) {
         const int ti = t - (ENC_CK - 1) / 2 + k;
         if (ti < 0 || ti >= T) continue;
-        s += bf2f(dww[c * ENC_CK + k]) * in[(long)ti * ENC_D + c];
+        s += bf2f(dww[c * ENC_CK + k]) * in[(long)(st + ti) * ENC_D + c];
     }
     const float v = (s - bf2f(bnm[c])) / sqrtf(bf2f(bnv[c]) + 1e-5f) * bf2f(bnw[c]) + bf2f(bnb[c]);
     out[i] = v / (1.0f + expf(-v));
@@ -189,22 +208,59 @@ inline unsigned nblk(long n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
 
+static int relpos_qb(int max_T) { return max_T <= 512 ? 16 : 4; }
+
 extern "C" void ctk_relpos_attn(float *O, const float *Q, const float *K, const float *V,
                                 const float *P, const uint16_t *pbu, const uint16_t *pbv,
                                 int T, hipStream_t s) {
     if (T <= 0) return;
-    if (T <= 512) {
-        const size_t lds = (2 * 16 * ENC_DK + 16 * (size_t)T) * sizeof(float);
-        hipLaunchKernelGGL(relpos_attn_kernel<16>, dim3((T + 15) / 16, ENC_H), dim3(256), lds, s,
-                           O, Q, K, V, P, pbu, pbv, T);
-    } else if (T <= 2048) {
-        const size_t lds = (2 * 4 * ENC_DK + 4 * (size_t)T) * sizeof(float);
-        hipLaunchKernelGGL(relpos_attn_kernel<4>, dim3((T + 3) / 4, ENC_H), dim3(256), lds, s,
-                           O, Q, K, V, P, pbu, pbv, T);
-    } else {
+    if (T > 2048) {
         fprintf(stderr, "ctk_relpos_attn: T=%d exceeds the supported 2048 frames\n", T);
         exit(1);
     }
+    const int qb = relpos_qb(T);
+    const size_t lds = (2 * qb * ENC_DK + qb * (size_t)T) * sizeof(float);
+    const dim3 grid((T + qb - 1) / qb, ENC_H);
+    if (qb == 16)
+        hipLaunchKernelGGL((relpos_attn_kernel<16, false>), grid, dim3(256), lds, s,
+                           O, Q, K, V, P, pbu, pbv, T, T, nullptr, nullptr, nullptr, nullptr);
+    else
+        hipLaunchKernelGGL((relpos_attn_kernel<4, false>), grid, dim3(256), lds, s,
+                           O, Q, K, V, P, pbu, pbv, T, T, nullptr, nullptr, nullptr, nullptr);
+}
+
+extern "C" int ctk_relpos_plan(int *blk_seq, int *blk_q0, const int *seq_T, int n_seq) {
+    int mx = 0;
+    for (int i = 0; i < n_seq; i++) mx = seq_T[i] > mx ? seq_T[i] : mx;
+    const int qb = relpos_qb(mx);
+    int n = 0;
+    for (int i = 0; i < n_seq; i++)
+        for (int q0 = 0; q0 < seq_T[i]; q0 += qb) {
+            if (blk_seq) { blk_seq[n] = i; blk_q0[n] = q0; }
+            n++;
+        }
+    return n;
+}
+
+extern "C" void ctk_relpos_attn_packed(float *O, const float *Q, const float *K, const float *V,
+                                       const float *P, int T_max, const uint16_t *pbu,
+                                       const uint16_t *pbv, const int *seq_off, const int *seq_T,
+                                       const int *blk_seq, const int *blk_q0, int n_blk, int max_T,
+                                       hipStream_t s) {
+    if (n_blk <= 0) return;
+    if (max_T > 2048) {
+        fprintf(stderr, "ctk_relpos_attn_packed: T=%d exceeds the supported 2048 frames\n", max_T);
+        exit(1);
+    }
+    const int qb = relpos_qb(max_T);
+    const size_t lds = (2 * qb * ENC_DK + qb * (size_t)max_T) * sizeof(float);
+    const dim3 grid(n_blk, ENC_H);
+    if (qb == 16)
+        hipLaunchKernelGGL((relpos_attn_kernel<16, true>), grid, dim3(256), lds, s,
+                           O, Q, K, V, P, pbu, pbv, 0, T_max, seq_off, seq_T, blk_seq, blk_q0);
+    else
+        hipLaunchKernelGGL((relpos_attn_kernel<4, true>), grid, dim3(256), lds, s,
+                           O, Q, K, V, P, pbu, pbv, 0, T_max, seq_off, seq_T, blk_seq, blk_q0);
 }
 
 extern "C" void ctk_dwconv_bn_silu(float *out, const float *in, int T, const uint16_t *dww,
@@ -212,7 +268,17 @@ extern "C" void ctk_dwconv_bn_silu(float *out, const float *in, int T, const uin
                                    const uint16_t *bnm, const uint16_t *bnv, hipStream_t s) {
     if (T <= 0) return;
     hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)T * ENC_D)), dim3(256), 0, s,
-                       out, in, T, dww, dwb, bnw, bnb, bnm, bnv);
+                       out, in, T, nullptr, nullptr, dww, dwb, bnw, bnb, bnm, bnv);
+}
+
+extern "C" void ctk_dwconv_bn_silu_packed(float *out, const float *in, int M, const int *row_start,
+                                          const int *row_len, const uint16_t *dww,
+                                          const uint16_t *dwb, const uint16_t *bnw,
+                                          const uint16_t *bnb, const uint16_t *bnm,
+                                          const uint16_t *bnv, hipStream_t s) {
+    if (M <= 0) return;
+    hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)M * ENC_D)), dim3(256), 0, s,
+                       out, in, M, row_start, row_len, dww, dwb, bnw, bnb, bnm, bnv);
 }
 
 extern "C" void ctk_sub_conv0(float *out, const float *mel, int T_mel, int stride,

@@ -1,0 +1,137 @@
+// k_engine.hip — slot-table kernels of the decode engine.
+//
+// eng_begin admits queued requests into free slots and prepares each slot's
+// step inputs (token, position, cache lengths, KV row offset); eng_end turns
+// each active slot's logits into its next token under the request's policy
+// and retires finished requests, freeing the slot for the next eng_begin.
+// Together they replace the host loop of transcribe.c:733-795 (gather
+// tokens, advance S, argmax, append, retire on EOS or MAX_SEQ) with no host
+// round trip.
+#include "ct_dev.h"
+#include "ct_engine.h"
+#include "../../include/model_types.h"
+#include <limits.h>
+
+#define EOS_ID 3   // model.h:24
+
+namespace {
+
+__global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d) {
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        int nxt = d.q[0];
+        const int ready = d.q[1];
+        for (int s = 0; s < d.slots; s++) {
+            if (d.slot_req[s] < 0 && nxt < ready) {
+                d.slot_req[s] = nxt++;
+                d.slot_S[s] = 0;
+            }
+        }
+        d.q[0] = nxt;
+    }
+    __syncthreads();
+    for (int s = tid; s < d.slots; s += 256) {
+        const int r = d.slot_req[s];
+        if (r >= 0) {
+            int S = d.slot_S[s];
+            const int np = d.req_np[r];
+            const int t = S < np ? d.req_prompt[r * CT_PROMPT_MAX + S]
+                                 : d.req_out[(long)r * d.smax + d.req_ngen[r] - 1];
+            S += 1;
+            d.slot_S[s] = S;
+            d.act[s] = 1;
+            d.tok[s] = t;
+            d.pos_len[s] = S;
+            d.cross_len[s] = d.req_T[r];
+            d.cross_idx[s] = r;
+            d.kv_rowoff[s] = ((long)s * DEC_H * d.smax + (S - 1)) * DEC_DK;
+        } else {
+            d.act[s] = 0;
+            d.tok[s] = 0;
+            d.pos_len[s] = 0;
+            d.cross_len[s] = 0;
+            d.cross_idx[s] = 0;
+            d.kv_rowoff[s] = -1;
+        }
+    }
+}
+
+__device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+// First maximum (ties -> lowest id, NaN never chosen unless at id 0, as the
+// sequential scan of backends/cpu/backend.c:446-456), optionally skipping EOS.
+__global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *logits) {
+    const int s = blockIdx.x;
+    if (!d.act[s]) return;
+    const int r = d.slot_req[s];
+    const int S = d.slot_S[s];
+    if (S < d.req_np[r]) return;                 // still feeding the prompt
+    const int flags = d.req_flags[r];
+    const int skip = (flags & 1) ? EOS_ID : -1;
+    const float *x = logits + (long)s * VOCAB;
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int i = threadIdx.x; i < VOCAB; i += 256)
+        if (i != skip) better(bv, bi, x[i], i);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        better(bv, bi, ov, oi);
+    }
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[wv] = bv; si[wv] = bi; }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int k = 1; k < 4; k++) better(bv, bi, sv[k], si[k]);
+    const int first = skip == 0 ? 1 : 0;
+    int best = (x[first] != x[first] || bi == INT_MAX) ? first : bi;
+    const int ng = d.req_ngen[r], lim = d.req_limit[r];
+    if ((flags & 2) && ng == lim - 1) best = EOS_ID;
+    d.req_out[(long)r * d.smax + ng] = best;
+    d.req_ngen[r] = ng + 1;
+    const bool fin = (best == EOS_ID && !(flags & 1)) || ng + 1 >= lim || S >= d.smax;
+    if (fin) {
+        d.slot_req[s] = -1;
+        atomicAdd(&d.q[2], 1);
+    }
+}
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+// Approximately normal: sum of four 16-bit uniforms, centred and scaled to
+// unit variance (Irwin-Hall).  Synthetic cache contents for the microbench.
+__global__ void fill_random_kernel(void *p, long n, int bf16, float scale, uint64_t seed) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint64_t h = mix64(seed + 0x9E3779B97F4A7C15ULL * (uint64_t)(i + 1));
+        const float u = (float)(h & 0xffff) + (float)((h >> 16) & 0xffff) +
+                        (float)((h >> 32) & 0xffff) + (float)(h >> 48);
+        const float z = (u / 65536.0f - 2.0f) * 1.7320508f;
+        if (bf16) reinterpret_cast<uint16_t *>(p)[i] = f2bf(z * scale);
+        else reinterpret_cast<float *>(p)[i] = z * scale;
+    }
+}
+
+}  // namespace
+
+extern "C" void ctk_eng_begin(const CtEngDev *d, hipStream_t s) {
+    hipLaunchKernelGGL(eng_begin_kernel, dim3(1), dim3(256), 0, s, *d);
+}
+
+extern "C" void ctk_eng_end(const CtEngDev *d, const float *logits, hipStream_t s) {
+    hipLaunchKernelGGL(eng_end_kernel, dim3(d->slots), dim3(256), 0, s, *d, logits);
+}
+
+extern "C" void ctk_fill_random(void *p, long n, int bf16, float scale, uint64_t seed, hipStream_t s) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(fill_random_kernel, dim3(4096), dim3(256), 0, s, p, n, bf16, scale, seed);
+}

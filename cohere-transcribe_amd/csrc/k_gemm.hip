@@ -142,8 +142,26 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(CtGemm g, int n_mt, in
                 if (m >= g.M) continue;
                 if (g.row_mask && !g.row_mask[m]) continue;
                 const float s = acc[rb][cb][j] + ba;
+                if (g.nseg > 0) {
+                    const int si = col / g.seg_w, c = col - si * g.seg_w;
+                    const CtSeg &sg = g.seg[si];
+                    if (sg.mode == CT_OUT_DENSE) {
+                        reinterpret_cast<float *>(sg.base)[(long)m * sg.ld + c] = s;
+                    } else {
+                        const long ro = sg.rowoff[m];
+                        if (ro < 0) continue;
+                        const long off = ro + (long)(c >> 7) * sg.hstride + (c & 127);
+                        if (sg.mode == CT_OUT_HEADS_BF16) reinterpret_cast<uint16_t *>(sg.base)[off] = f2bf(s);
+                        else reinterpret_cast<float *>(sg.base)[off] = s;
+                    }
+                    continue;
+                }
                 long yrow = m;
-                if (g.row_len) yrow = (long)m * g.row_stride + g.row_len[(long)m * g.row_len_step] - 1;
+                if (g.row_len) {
+                    const int len = g.row_len[(long)m * g.row_len_step];
+                    if (len <= 0) continue;          // no slot to write
+                    yrow = (long)m * g.row_stride + len - 1;
+                }
                 float *y = g.Y + yrow * g.ldy + col;
                 if (GLU) {
                     const float gt = acc[rb][cb + (GLU ? CO : 0)][j] + bg;
@@ -175,18 +193,18 @@ void launch(const CtGemm &g, hipStream_t s) {
 
 template <bool VEC, bool GLU>
 void dispatch(const CtGemm &g, hipStream_t s) {
-    if (GLU) {
+    if constexpr (GLU) {
         if (g.M <= 16) launch<1, 4, VEC, GLU, 1>(g, s);
         else if (g.M <= 64) launch<2, 4, VEC, GLU, 2>(g, s);
         else launch<4, 4, VEC, GLU, 4>(g, s);
-        return;
-    }
+    } else {
     // Small M (decode): one row-block group per wave, narrow columns, one
     // wave per workgroup so the weight stream spreads over many CUs.
     if (g.M <= 16) launch<1, 1, VEC, GLU, 1>(g, s);
     else if (g.M <= 32) launch<2, 1, VEC, GLU, 1>(g, s);
     else if (g.M <= 64) launch<4, 1, VEC, GLU, 1>(g, s);
     else launch<4, 4, VEC, GLU, 4>(g, s);
+    }
 }
 
 }  // namespace

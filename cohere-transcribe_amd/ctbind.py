@@ -204,3 +204,110 @@ def hip():
             raise RuntimeError(f"{HIP_LIB} is not built (run __graft_entry__.build())")
         _hip = bind_abi(C.CDLL(HIP_LIB))
     return _hip
+
+
+# ---------------------------------------------------------------------------
+# The decode engine (include/hipb.h)
+# ---------------------------------------------------------------------------
+HIPB_SUPPRESS_EOS = 1
+HIPB_FORCE_EOS = 2
+
+
+class HipbConfig(C.Structure):
+    _fields_ = [("slots", C.c_int), ("max_requests", C.c_int),
+                ("max_frames", C.c_int), ("kv_bf16", C.c_int)]
+
+
+_ENGINE_SIGS = {
+    "hipb_create": ([C.POINTER(HipbConfig), C.c_void_p], C.c_void_p),
+    "hipb_destroy": ([C.c_void_p], None),
+    "hipb_submit": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int], C.c_int),
+    "hipb_encode": ([C.c_void_p, C.c_int], None),
+    "hipb_step": ([C.c_void_p], None),
+    "hipb_run": ([C.c_void_p, C.c_int], C.c_long),
+    "hipb_finished": ([C.c_void_p], C.c_int),
+    "hipb_tokens": ([C.c_void_p, C.c_int, C.c_void_p, C.c_int], C.c_int),
+    "hipb_slot_of": ([C.c_void_p, C.c_int], C.c_int),
+    "hipb_logits": ([C.c_void_p, C.c_int, C.c_void_p], None),
+    "hipb_enc_out": ([C.c_void_p, C.c_int, C.c_void_p], None),
+    "hipb_req_frames": ([C.c_void_p, C.c_int], C.c_int),
+    "hipb_bench_fill": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64], None),
+    "hipb_attention_only": ([C.c_void_p], None),
+    "hipb_stream": ([C.c_void_p], C.c_void_p),
+}
+
+
+def engine_lib():
+    lib = hip()
+    if not getattr(lib, "_hipb_bound", False):
+        for n, (a, r) in _ENGINE_SIGS.items():
+            fn = getattr(lib, n)
+            fn.argtypes = a
+            fn.restype = r
+        lib._hipb_bound = True
+    return lib
+
+
+class Engine:
+    """Thin owner of a HipbEngine* (the calling thread must have run
+    backend_init and uploaded the model's blob)."""
+
+    def __init__(self, model, slots, max_requests, max_frames, kv_bf16=True):
+        self.L = engine_lib()
+        self.model = model
+        cfg = HipbConfig(slots, max_requests, max_frames, int(kv_bf16))
+        self.e = self.L.hipb_create(C.byref(cfg), model.weights_ref())
+        self.slots = slots
+
+    def submit(self, mel, limit, flags=HIPB_SUPPRESS_EOS, prompt=None):
+        mel = np.ascontiguousarray(mel, dtype=np.float32)
+        p = np.ascontiguousarray(prompt if prompt is not None else PROMPT, dtype=np.int32)
+        return self.L.hipb_submit(self.e, mel.ctypes.data, mel.shape[1], p.ctypes.data, len(p),
+                                  limit, flags)
+
+    def encode(self, max_batch_frames=32768):
+        self.L.hipb_encode(self.e, max_batch_frames)
+
+    def step(self):
+        self.L.hipb_step(self.e)
+
+    def run(self, chunk=8):
+        return self.L.hipb_run(self.e, chunk)
+
+    def finished(self):
+        return self.L.hipb_finished(self.e)
+
+    def tokens(self, req):
+        out = np.zeros(MAX_SEQ, np.int32)
+        n = self.L.hipb_tokens(self.e, req, out.ctypes.data, MAX_SEQ)
+        return out[:n].copy()
+
+    def slot_of(self, req):
+        return self.L.hipb_slot_of(self.e, req)
+
+    def logits(self, slot):
+        out = np.zeros(VOCAB, np.float32)
+        self.L.hipb_logits(self.e, slot, out.ctypes.data)
+        return out
+
+    def enc_out(self, req):
+        T = self.L.hipb_req_frames(self.e, req)
+        out = np.zeros((T, DEC_D), np.float32)
+        self.L.hipb_enc_out(self.e, req, out.ctypes.data)
+        return out
+
+    def bench_fill(self, S, T_enc, seed=1):
+        S = np.ascontiguousarray(S, np.int32)
+        T = np.ascontiguousarray(T_enc, np.int32)
+        self.L.hipb_bench_fill(self.e, S.ctypes.data, T.ctypes.data, seed)
+
+    def attention_only(self):
+        self.L.hipb_attention_only(self.e)
+
+    def stream(self):
+        return self.L.hipb_stream(self.e)
+
+    def close(self):
+        if self.e:
+            self.L.hipb_destroy(self.e)
+            self.e = None

@@ -1,0 +1,91 @@
+/* hipb.h — the MI355X decode engine behind the drop-in backend.
+ *
+ * The reference has no counterpart for these entry points: they extend the
+ * 40-function ABI (backend.h) with what the batched ragged decode needs and
+ * the ABI cannot express (backends/backend.h:181-228 covers one step with
+ * host-side active[]/S[] arrays, transcribe.c:733-795 drives it):
+ *
+ *  - a device-resident slot table: each of `slots` KV slots holds one request;
+ *    a finished request's slot is refilled from the request queue by a device
+ *    kernel at the start of the next step (continuous batching, no host
+ *    round trip);
+ *  - KV caches in HBM as [layer][slot][head][position][128] (self) and
+ *    [layer][request][head][frame][128] (cross), bf16 or fp32;
+ *  - the prompt is fed one token per step through the same kernels, so a
+ *    request's numbers never depend on its slot or on the other requests;
+ *  - the forced-length policy of the benchmark configurations on device:
+ *    EOS excluded from the argmax and/or EOS forced at token `limit`;
+ *  - the encoder on packed ragged batches (M = sum of frames).
+ *
+ * Threading: an engine belongs to the thread that created it, which must have
+ * called backend_init(dev) after backend_weights_upload_blob().  Errors print
+ * and exit(1) like the ABI.
+ */
+#ifndef CT_HIPB_H
+#define CT_HIPB_H
+
+#include "model_types.h"
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct HipbEngine HipbEngine;
+
+typedef struct {
+    int slots;          /* concurrent KV slots (decode batch), 1..256          */
+    int max_requests;   /* request pool capacity                                */
+    int max_frames;     /* largest encoder length a request may have (<= 2048) */
+    int kv_bf16;        /* 1: bf16 KV caches, 0: fp32                           */
+} HipbConfig;
+
+/* Request policy flags. */
+#define HIPB_SUPPRESS_EOS 1   /* EOS never chosen by the argmax              */
+#define HIPB_FORCE_EOS    2   /* token number `limit` is EOS                  */
+
+/* Creates an engine on the calling thread's device for the weights W (host
+ * pointers into the uploaded blob, as every ABI call takes them). */
+HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W);
+void hipb_destroy(HipbEngine *e);
+
+/* Queues a request: mel (N_MELS x T_mel, row stride T_mel, host memory),
+ * prompt ids, at most `limit` generated tokens.  Returns the request id
+ * (0, 1, 2, ... in submission order). */
+int  hipb_submit(HipbEngine *e, const float *mel, int T_mel, const int *prompt, int n_prompt,
+                 int limit, int flags);
+/* Runs the encoder and cross-attention K/V for every submitted request not yet
+ * encoded, in packed batches of at most max_batch_frames encoder frames. */
+void hipb_encode(HipbEngine *e, int max_batch_frames);
+/* One decode step over all slots (admission, embed, 8 layers, LM head,
+ * argmax/policy).  Returns nothing; state stays on the device. */
+void hipb_step(HipbEngine *e);
+/* Runs decode steps until every encoded request has finished; steps are
+ * replayed from one captured graph, chunk steps per host check.
+ * Returns the number of steps run. */
+long hipb_run(HipbEngine *e, int chunk);
+/* Number of requests finished so far (device counter, synchronises). */
+int  hipb_finished(HipbEngine *e);
+
+/* Results and inspection (synchronise the engine's stream). */
+int  hipb_tokens(HipbEngine *e, int req, int *out, int cap);        /* returns count */
+int  hipb_slot_of(HipbEngine *e, int req);                          /* -1 if none    */
+void hipb_logits(HipbEngine *e, int slot, float *out);              /* VOCAB floats  */
+void hipb_enc_out(HipbEngine *e, int req, float *out);              /* T_enc x DEC_D */
+int  hipb_req_frames(HipbEngine *e, int req);
+
+/* Microbenchmark support: fills the self and cross caches of every slot with
+ * seeded values (N(0,1)*0.1, bf16/fp32 as configured) at lengths S[slot] and
+ * T_enc[slot] and marks the slots active without a request queue, so
+ * hipb_step runs decode steps at exactly those lengths. */
+void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t seed);
+/* Launches only the 16 decode-attention kernels of one step (8 layers x self
+ * and cross) on the engine stream, for per-kernel timing. */
+void hipb_attention_only(HipbEngine *e);
+/* The engine's HIP stream (hipStream_t), for events and profiling. */
+void *hipb_stream(HipbEngine *e);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -17,3 +17,14 @@ def pytest_configure(config):
 def kernel_model():
     import ctbind as cb
     return cb.SynthModel(seed=11, variant=1)
+
+
+@pytest.fixture(scope="session")
+def hip():
+    """libct_hip.so with backend_init(0) done once for the test process."""
+    import ctbind as cb
+    lib = cb.hip()
+    if lib.backend_num_devices() < 1:
+        pytest.fail("no HIP device visible")
+    lib.backend_init(0)
+    return lib

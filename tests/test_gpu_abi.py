@@ -37,15 +37,6 @@ def bits_equal(a, b):
 
 
 @pytest.fixture(scope="module")
-def hip():
-    lib = cb.hip()
-    if lib.backend_num_devices() < 1:
-        pytest.fail("no HIP device visible")
-    lib.backend_init(0)
-    return lib
-
-
-@pytest.fixture(scope="module")
 def kmodel(hip, kernel_model):
     hip.backend_weights_upload_blob(kernel_model.data_ptr, kernel_model.data_bytes)
     return kernel_model
