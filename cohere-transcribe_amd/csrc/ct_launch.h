@@ -128,6 +128,27 @@ void ctk_sub_dwconv(float *out, const float *in, int H, int Wd,
 /* [T][16][256] -> [T][256*16] (channel-major flatten per frame). */
 void ctk_sub_flatten(float *out, const float *in, int T, hipStream_t s);
 
+/* ---------------- log-mel front-end ---------------- */
+typedef struct {
+    const float *pcm; /* the clip's samples (device memory)               */
+    int  n;        /* samples                                             */
+    long mel0;     /* first float of the clip's [N_MELS][T] mel block     */
+    int  T;        /* frames = 1 + n / HOP_LEN                            */
+    int  frame0;   /* global index of the clip's frame 0                  */
+} CtMelClip;
+
+typedef struct {
+    const float *hann;          /* [WIN_LEN]                          */
+    const float *twr, *twi;     /* [N_FFT/2] exp(-2 pi i k / N_FFT)   */
+    const float *fb;            /* [N_MELS][N_BINS] Slaney filterbank */
+    const int *fb_lo, *fb_hi;   /* non-zero bin range per filter      */
+} CtMelTables;
+
+/* mel for n_clips packed clips; frame_clip[f] names the clip of global
+ * frame f (n_frames = sum of T). */
+void ctk_mel(float *mel, const CtMelClip *clips, int n_clips,
+             const int *frame_clip, int n_frames, const CtMelTables *tab, hipStream_t s);
+
 #ifdef __cplusplus
 }
 #endif

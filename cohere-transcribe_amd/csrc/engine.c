@@ -17,12 +17,16 @@
 #include "ct_engine.h"
 #include "ct_launch.h"
 
+#include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
 typedef struct {
-    float *mel;          /* host copy until encoded */
+    float *mel;          /* host copy until encoded (mel requests) ...        */
+    float *pcm;          /* ... or the 16 kHz samples (PCM requests) ...      */
+    const float *dpcm;   /* ... or samples already in device memory          */
+    int n;               /* samples of a PCM request                          */
     int T_mel, T_enc;
 } HostReq;
 
@@ -57,6 +61,15 @@ struct HipbEngine {
     hipGraphExec_t exec;
     int have_graph;
     int bench_mode;
+    /* log-mel front-end */
+    CtMelTables mel_tab;
+    float *d_hann, *d_twr, *d_twi, *d_fb;
+    int *d_fb_lo, *d_fb_hi;
+    float *epcm;
+    size_t epcm_cap;
+    CtMelClip *e_clips;
+    int *e_frame_clip;
+    int clips_cap, frames_cap;
 };
 
 #define ECHK(x) ct_hip_check((x), #x, __FILE__, __LINE__)
@@ -77,6 +90,59 @@ static void gemm(HipbEngine *e, const float *A, int M, int K, const uint16_t *Wh
     g.Y = Y; g.ldy = N; g.M = M; g.N = N; g.K = K; g.epi = epi; g.scale = scale;
     g.row_mask = row_mask;
     ctk_gemm(&g, e->s);
+}
+
+/* Slaney mel scale and the librosa-style filterbank the reference builds in
+ * transcribe.c:51-93 (fmin 0, fmax 8 kHz, area-normalised triangles). */
+static double hz_mel(double f) {
+    const double sp = 200.0 / 3.0, brk = 1000.0, step = log(6.4) / 27.0;
+    return f < brk ? f / sp : brk / sp + log(f / brk) / step;
+}
+static double mel_hz(double m) {
+    const double sp = 200.0 / 3.0, brk = 1000.0, step = log(6.4) / 27.0;
+    return m < brk / sp ? sp * m : brk * exp(step * (m - brk / sp));
+}
+
+static void mel_tables_init(HipbEngine *e) {
+    float hann[WIN_LEN], twr[N_FFT / 2], twi[N_FFT / 2];
+    static float fb[N_MELS * N_BINS];
+    int lo[N_MELS], hi[N_MELS];
+    /* Hann window in the reference's fp32 expression (transcribe.c:47-49) */
+    for (int i = 0; i < WIN_LEN; i++)
+        hann[i] = 0.5f * (1.0f - cosf(2.0f * (float)M_PI * i / (WIN_LEN - 1)));
+    for (int k = 0; k < N_FFT / 2; k++) {
+        twr[k] = (float)cos(2.0 * M_PI * k / N_FFT);
+        twi[k] = (float)-sin(2.0 * M_PI * k / N_FFT);
+    }
+    double pts[N_MELS + 2];
+    const double m0 = hz_mel(0.0), m1 = hz_mel(SR / 2.0);
+    for (int i = 0; i < N_MELS + 2; i++) pts[i] = mel_hz(m0 + (m1 - m0) * i / (N_MELS + 1));
+    for (int m = 0; m < N_MELS; m++) {
+        const double norm = 2.0 / (pts[m + 2] - pts[m]);
+        lo[m] = N_BINS; hi[m] = 0;
+        for (int i = 0; i < N_BINS; i++) {
+            const double f = (SR / 2.0) * i / (N_BINS - 1);
+            const double up = (f - pts[m]) / (pts[m + 1] - pts[m]);
+            const double dn = (pts[m + 2] - f) / (pts[m + 2] - pts[m + 1]);
+            const double w = up < dn ? up : dn;
+            fb[m * N_BINS + i] = (float)(w > 0.0 ? w * norm : 0.0);
+            if (fb[m * N_BINS + i] != 0.0f) { if (i < lo[m]) lo[m] = i; hi[m] = i + 1; }
+        }
+        if (hi[m] < lo[m]) { lo[m] = 0; hi[m] = 0; }
+    }
+    e->d_hann = dmalloc(sizeof hann);
+    e->d_twr = dmalloc(sizeof twr);
+    e->d_twi = dmalloc(sizeof twi);
+    e->d_fb = dmalloc(sizeof fb);
+    e->d_fb_lo = dmalloc(sizeof lo);
+    e->d_fb_hi = dmalloc(sizeof hi);
+    ECHK(hipMemcpy(e->d_hann, hann, sizeof hann, hipMemcpyHostToDevice));
+    ECHK(hipMemcpy(e->d_twr, twr, sizeof twr, hipMemcpyHostToDevice));
+    ECHK(hipMemcpy(e->d_twi, twi, sizeof twi, hipMemcpyHostToDevice));
+    ECHK(hipMemcpy(e->d_fb, fb, sizeof fb, hipMemcpyHostToDevice));
+    ECHK(hipMemcpy(e->d_fb_lo, lo, sizeof lo, hipMemcpyHostToDevice));
+    ECHK(hipMemcpy(e->d_fb_hi, hi, sizeof hi, hipMemcpyHostToDevice));
+    e->mel_tab = (CtMelTables){e->d_hann, e->d_twr, e->d_twi, e->d_fb, e->d_fb_lo, e->d_fb_hi};
 }
 
 HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
@@ -149,6 +215,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->logits = dmalloc((size_t)S * VOCAB * 4);
     ECHK(hipMemsetAsync(e->h, 0, (size_t)S * DEC_D * 4, e->s));
     e->req = calloc(R, sizeof(HostReq));
+    mel_tables_init(e);
     ECHK(hipHostMalloc((void **)&e->h_tmp, (size_t)(R + 8) * (MAX_SEQ + 8) * sizeof(int), 0));
     ECHK(hipStreamSynchronize(e->s));
     return e;
@@ -165,16 +232,32 @@ void hipb_destroy(HipbEngine *e) {
                     e->enc_pool, e->h, e->ln, e->q, e->att, e->mid, e->logits,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
                     e->eh, e->esub, e->emel, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
-                    e->e_blk_seq, e->e_blk_q0, e->e_rowoff};
+                    e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
+                    e->d_fb_lo, e->d_fb_hi, e->epcm, e->e_clips, e->e_frame_clip};
     for (size_t i = 0; i < sizeof ptrs / sizeof ptrs[0]; i++)
         if (ptrs[i]) ECHK(hipFree(ptrs[i]));
-    for (int r = 0; r < e->n_req; r++) free(e->req[r].mel);
+    for (int r = 0; r < e->n_req; r++) { free(e->req[r].mel); free(e->req[r].pcm); }
     free(e->req);
     ECHK(hipHostFree(e->h_tmp));
     free(e);
 }
 
 void *hipb_stream(HipbEngine *e) { return (void *)e->s; }
+
+void hipb_reset(HipbEngine *e) {
+    ECHK(hipStreamSynchronize(e->s));
+    for (int r = 0; r < e->n_req; r++) {
+        free(e->req[r].mel); free(e->req[r].pcm);
+        memset(&e->req[r], 0, sizeof e->req[r]);
+    }
+    e->n_req = e->n_enc = 0;
+    e->bench_mode = 0;
+    ECHK(hipMemsetAsync(e->d.slot_req, 0xff, e->d.slots * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(e->d.slot_S, 0, e->d.slots * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(e->d.req_ngen, 0, e->d.max_req * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(e->d.q, 0, 4 * sizeof(int), e->s));
+    ECHK(hipStreamSynchronize(e->s));
+}
 
 /* ------------------------------------------------------------------ */
 /* Requests and the packed encoder                                     */
@@ -184,8 +267,42 @@ static int t_enc_of(int T_mel) {
     return (b + 1) / 2;
 }
 
+static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prompt, int limit,
+                         int flags);
+
 int hipb_submit(HipbEngine *e, const float *mel, int T_mel, const int *prompt, int n_prompt,
                 int limit, int flags) {
+    const int r = submit_common(e, T_mel, prompt, n_prompt, limit, flags);
+    HostReq *q = &e->req[r];
+    q->mel = malloc((size_t)N_MELS * T_mel * sizeof(float));
+    if (!q->mel) CT_FATAL("out of host memory");
+    memcpy(q->mel, mel, (size_t)N_MELS * T_mel * sizeof(float));
+    return r;
+}
+
+int hipb_submit_pcm(HipbEngine *e, const float *pcm, int n_samples, const int *prompt, int n_prompt,
+                    int limit, int flags) {
+    if (n_samples < HOP_LEN) CT_FATAL("hipb_submit_pcm: clip shorter than one hop (160 samples)");
+    const int r = submit_common(e, 1 + n_samples / HOP_LEN, prompt, n_prompt, limit, flags);
+    HostReq *q = &e->req[r];
+    q->pcm = malloc((size_t)n_samples * sizeof(float));
+    if (!q->pcm) CT_FATAL("out of host memory");
+    memcpy(q->pcm, pcm, (size_t)n_samples * sizeof(float));
+    q->n = n_samples;
+    return r;
+}
+
+int hipb_submit_pcm_device(HipbEngine *e, const float *dev_pcm, int n_samples, const int *prompt,
+                           int n_prompt, int limit, int flags) {
+    if (n_samples < HOP_LEN) CT_FATAL("hipb_submit_pcm_device: clip shorter than one hop (160 samples)");
+    const int r = submit_common(e, 1 + n_samples / HOP_LEN, prompt, n_prompt, limit, flags);
+    e->req[r].dpcm = dev_pcm;
+    e->req[r].n = n_samples;
+    return r;
+}
+
+static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prompt, int limit,
+                         int flags) {
     if (e->bench_mode) CT_FATAL("hipb_submit: engine is in microbenchmark mode");
     if (e->n_req >= e->cfg.max_requests) CT_FATAL("hipb_submit: request pool full");
     if (n_prompt < 1 || n_prompt > CT_PROMPT_MAX) CT_FATAL("hipb_submit: prompt length outside [1, 16]");
@@ -194,11 +311,9 @@ int hipb_submit(HipbEngine *e, const float *mel, int T_mel, const int *prompt, i
     if (T_mel < 1 || Te > e->d.tmax || Te > e->cfg.max_frames) CT_FATAL("hipb_submit: clip longer than max_frames");
     const int r = e->n_req++;
     HostReq *q = &e->req[r];
+    memset(q, 0, sizeof *q);
     q->T_mel = T_mel;
     q->T_enc = Te;
-    q->mel = malloc((size_t)N_MELS * T_mel * sizeof(float));
-    if (!q->mel) CT_FATAL("out of host memory");
-    memcpy(q->mel, mel, (size_t)N_MELS * T_mel * sizeof(float));
     int meta[4 + CT_PROMPT_MAX];
     meta[0] = Te; meta[1] = limit; meta[2] = flags; meta[3] = n_prompt;
     memset(meta + 4, 0, sizeof(int) * CT_PROMPT_MAX);
@@ -306,13 +421,66 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         e->emel = dmalloc(mel_need * 4);
         e->emel_cap = mel_need;
     }
+    /* log-mel on the GPU for PCM requests, uploaded mel otherwise */
+    {
+        size_t pcm_need = 0;
+        int nclip = 0, nfr = 0;
+        for (int r = r0; r < r1; r++)
+            if (e->req[r].pcm || e->req[r].dpcm) {
+                if (e->req[r].pcm) pcm_need += e->req[r].n;
+                nclip++;
+                nfr += e->req[r].T_mel;
+            }
+        if (nclip) {
+            if (pcm_need > e->epcm_cap) {
+                if (e->epcm) ECHK(hipFree(e->epcm));
+                e->epcm = dmalloc(pcm_need * 4);
+                e->epcm_cap = pcm_need;
+            }
+            if (nclip > e->clips_cap) {
+                if (e->e_clips) ECHK(hipFree(e->e_clips));
+                e->e_clips = dmalloc((size_t)nclip * sizeof(CtMelClip));
+                e->clips_cap = nclip;
+            }
+            if (nfr > e->frames_cap) {
+                if (e->e_frame_clip) ECHK(hipFree(e->e_frame_clip));
+                e->e_frame_clip = dmalloc((size_t)nfr * sizeof(int));
+                e->frames_cap = nfr;
+            }
+            CtMelClip *cl = malloc(nclip * sizeof *cl);
+            int *fc = malloc(nfr * sizeof(int));
+            size_t po = 0, mo = 0;
+            int ci = 0, fo = 0;
+            for (int r = r0; r < r1; r++) {
+                HostReq *q = &e->req[r];
+                if (q->pcm || q->dpcm) {
+                    const float *src = q->dpcm;
+                    if (q->pcm) {
+                        ECHK(hipMemcpyAsync(e->epcm + po, q->pcm, (size_t)q->n * 4, hipMemcpyHostToDevice, s));
+                        src = e->epcm + po;
+                        po += q->n;
+                    }
+                    cl[ci] = (CtMelClip){src, q->n, (long)mo, q->T_mel, fo};
+                    for (int t = 0; t < q->T_mel; t++) fc[fo + t] = ci;
+                    fo += q->T_mel; ci++;
+                }
+                mo += (size_t)N_MELS * q->T_mel;
+            }
+            ECHK(hipMemcpyAsync(e->e_clips, cl, nclip * sizeof *cl, hipMemcpyHostToDevice, s));
+            ECHK(hipMemcpyAsync(e->e_frame_clip, fc, nfr * sizeof(int), hipMemcpyHostToDevice, s));
+            ctk_mel(e->emel, e->e_clips, nclip, e->e_frame_clip, nfr, &e->mel_tab, s);
+            ECHK(hipStreamSynchronize(s));
+            free(cl); free(fc);
+        }
+    }
     size_t moff = 0;
     const Weights *W = &e->W;
     for (int i = 0; i < n; i++) {
         HostReq *q = &e->req[r0 + i];
         float *mel = e->emel + moff;
         moff += (size_t)N_MELS * q->T_mel;
-        ECHK(hipMemcpyAsync(mel, q->mel, (size_t)N_MELS * q->T_mel * 4, hipMemcpyHostToDevice, s));
+        if (q->mel)
+            ECHK(hipMemcpyAsync(mel, q->mel, (size_t)N_MELS * q->T_mel * 4, hipMemcpyHostToDevice, s));
         const int T1 = (q->T_mel + 1) / 2, T2 = (T1 + 1) / 2;
         float *ra = e->esub, *rb = e->esub + (size_t)SUB_CH * T1 * 64;
         ctk_sub_conv0(ra, mel, q->T_mel, q->T_mel, DW(W->s0w), DW(W->s0b), s);
@@ -395,7 +563,10 @@ void hipb_encode(HipbEngine *e, int max_batch_frames) {
             r1++;
         }
         encode_batch(e, r, r1);
-        for (int i = r; i < r1; i++) { free(e->req[i].mel); e->req[i].mel = NULL; }
+        for (int i = r; i < r1; i++) {
+            free(e->req[i].mel); e->req[i].mel = NULL;
+            free(e->req[i].pcm); e->req[i].pcm = NULL;
+        }
         r = r1;
     }
     e->n_enc = r;
@@ -511,8 +682,13 @@ long hipb_run(HipbEngine *e, int chunk) {
         e->have_graph = 1;
     }
     long steps = 0;
+    /* every admitted request finishes within prompt + limit <= prompt +
+     * MAX_SEQ steps of its admission, and some request is admitted whenever
+     * a slot frees up */
+    const long bound = (long)(e->n_enc / e->d.slots + 2) * (MAX_SEQ + CT_PROMPT_MAX + 1);
     for (;;) {
         if (hipb_finished(e) >= e->n_enc) break;
+        if (steps > bound) CT_FATAL("hipb_run: requests did not finish within the step bound");
         for (int i = 0; i < chunk; i++) ECHK(hipGraphLaunch(e->exec, e->s));
         steps += chunk;
     }
@@ -592,4 +768,20 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
     ECHK(hipStreamSynchronize(e->s));
     e->n_enc = B;
     e->bench_mode = 1;
+}
+
+void hipb_mel(HipbEngine *e, const float *pcm, int n_samples, float *mel_out) {
+    if (n_samples < HOP_LEN) CT_FATAL("hipb_mel: clip shorter than one hop (160 samples)");
+    const int T = 1 + n_samples / HOP_LEN;
+    float *dp = dmalloc((size_t)n_samples * 4), *dm = dmalloc((size_t)N_MELS * T * 4);
+    CtMelClip *dc = dmalloc(sizeof(CtMelClip));
+    int *fc = dmalloc((size_t)T * sizeof(int));
+    const CtMelClip c = {dp, n_samples, 0, T, 0};
+    ECHK(hipMemcpyAsync(dp, pcm, (size_t)n_samples * 4, hipMemcpyHostToDevice, e->s));
+    ECHK(hipMemcpyAsync(dc, &c, sizeof c, hipMemcpyHostToDevice, e->s));
+    ECHK(hipMemsetAsync(fc, 0, (size_t)T * sizeof(int), e->s));
+    ctk_mel(dm, dc, 1, fc, T, &e->mel_tab, e->s);
+    ECHK(hipMemcpyAsync(mel_out, dm, (size_t)N_MELS * T * 4, hipMemcpyDeviceToHost, e->s));
+    ECHK(hipStreamSynchronize(e->s));
+    ECHK(hipFree(dp)); ECHK(hipFree(dm)); ECHK(hipFree(dc)); ECHK(hipFree(fc));
 }

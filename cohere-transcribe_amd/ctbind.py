@@ -311,3 +311,61 @@ class Engine:
         if self.e:
             self.L.hipb_destroy(self.e)
             self.e = None
+
+
+_ENGINE_SIGS.update({
+    "hipb_submit_pcm": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int], C.c_int),
+    "hipb_mel": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p], None),
+    "hipb_reset": ([C.c_void_p], None),
+    "hipb_submit_pcm_device": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int], C.c_int),
+})
+
+
+def _engine_extra(self, pcm, limit, flags=HIPB_SUPPRESS_EOS, prompt=None):
+    pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+    p = np.ascontiguousarray(prompt if prompt is not None else PROMPT, dtype=np.int32)
+    return self.L.hipb_submit_pcm(self.e, pcm.ctypes.data, len(pcm), p.ctypes.data, len(p), limit, flags)
+
+
+def _engine_mel(self, pcm):
+    pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+    out = np.zeros((N_MELS, t_mel(len(pcm))), np.float32)
+    self.L.hipb_mel(self.e, pcm.ctypes.data, len(pcm), out.ctypes.data)
+    return out
+
+
+Engine.submit_pcm = _engine_extra
+Engine.mel = _engine_mel
+Engine.reset = lambda self: self.L.hipb_reset(self.e)
+
+
+class HipEvents:
+    """hipEvent timing on a given stream (libamdhip64 through ctypes)."""
+
+    def __init__(self):
+        self.rt = C.CDLL("libamdhip64.so")
+        self.rt.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.rt.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.rt.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.rt.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.rt.hipDeviceSynchronize.argtypes = []
+
+    def event(self):
+        ev = C.c_void_p()
+        if self.rt.hipEventCreate(C.byref(ev)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        return ev
+
+    def record(self, ev, stream):
+        if self.rt.hipEventRecord(ev, stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def ms(self, a, b):
+        self.rt.hipEventSynchronize(b)
+        out = C.c_float()
+        self.rt.hipEventElapsedTime(C.byref(out), a, b)
+        return out.value
+
+    def sync(self):
+        if self.rt.hipDeviceSynchronize() != 0:
+            raise RuntimeError("hipDeviceSynchronize failed")

@@ -54,6 +54,18 @@ void hipb_destroy(HipbEngine *e);
  * (0, 1, 2, ... in submission order). */
 int  hipb_submit(HipbEngine *e, const float *mel, int T_mel, const int *prompt, int n_prompt,
                  int limit, int flags);
+/* Queues a request given 16 kHz mono PCM (host memory); its log-mel
+ * spectrogram is computed on the GPU at encode time (transcribe.c:177-214). */
+int  hipb_submit_pcm(HipbEngine *e, const float *pcm, int n_samples, const int *prompt,
+                     int n_prompt, int limit, int flags);
+/* The same with the samples already in device memory (not copied; they must
+ * stay valid until hipb_encode returns). */
+int  hipb_submit_pcm_device(HipbEngine *e, const float *dev_pcm, int n_samples, const int *prompt,
+                            int n_prompt, int limit, int flags);
+/* Log-mel of one clip on the GPU, synchronously (N_MELS x (1 + n/160)). */
+void hipb_mel(HipbEngine *e, const float *pcm, int n_samples, float *mel_out);
+/* Drops every request and frees all slots (caches and weights stay). */
+void hipb_reset(HipbEngine *e);
 /* Runs the encoder and cross-attention K/V for every submitted request not yet
  * encoded, in packed batches of at most max_batch_frames encoder frames. */
 void hipb_encode(HipbEngine *e, int max_batch_frames);

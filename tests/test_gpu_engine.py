@@ -130,3 +130,34 @@ def test_engine_continuous_batching(hip, hot, mels, oracle_runs):
             assert np.array_equal(eng.tokens(r), oracle_runs[(True, i)][0]), (r, i)
     finally:
         eng.close()
+
+
+def test_gpu_mel_matches_oracle(hip, hot):
+    """GPU log-mel (exact twiddles, one FFT per workgroup) vs the oracle's
+    restatement of transcribe.c:177-214 (recurrence twiddles)."""
+    eng = cb.Engine(hot, slots=1, max_requests=2, max_frames=400, kv_bf16=True)
+    try:
+        for n, seed in ((16000 + 37, 9), (160 * 7, 10), (8 * 16000, 11)):
+            x = cb.synth_audio(n, seed)
+            got = eng.mel(x)
+            ref = ob.compute_mel(x)
+            print(f"case: mel n={n} max abs err {np.abs(got - ref).max():.2e}", flush=True)
+            assert got.shape == ref.shape
+            assert np.abs(got - ref).max() < 2e-3
+    finally:
+        eng.close()
+
+
+def test_engine_pcm_path(hip, hot, oracle_runs):
+    """PCM submitted (host and device-resident) -> GPU mel -> same tokens as
+    the oracle fed the oracle's mel."""
+    eng = cb.Engine(hot, slots=2, max_requests=4, max_frames=64, kv_bf16=True)
+    try:
+        for i, (n, s) in enumerate(CLIPS):
+            eng.submit_pcm(cb.synth_audio(n, s), LIMITS[i], FLAGS)
+        eng.encode()
+        eng.run(chunk=2)
+        for i in range(len(CLIPS)):
+            assert np.array_equal(eng.tokens(i), oracle_runs[(True, i)][0]), i
+    finally:
+        eng.close()
