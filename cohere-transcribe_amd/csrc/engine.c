@@ -60,6 +60,7 @@ struct HipbEngine {
     hipGraph_t graph;
     hipGraphExec_t exec;
     int have_graph;
+    int eager;           /* HIPB_EAGER=1: launch steps without a graph */
     int bench_mode;
     /* log-mel front-end */
     CtMelTables mel_tab;
@@ -215,6 +216,8 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->logits = dmalloc((size_t)S * VOCAB * 4);
     ECHK(hipMemsetAsync(e->h, 0, (size_t)S * DEC_D * 4, e->s));
     e->req = calloc(R, sizeof(HostReq));
+    const char *eg = getenv("HIPB_EAGER");
+    e->eager = eg && eg[0] == '1';
     mel_tables_init(e);
     ECHK(hipHostMalloc((void **)&e->h_tmp, (size_t)(R + 8) * (MAX_SEQ + 8) * sizeof(int), 0));
     ECHK(hipStreamSynchronize(e->s));
@@ -674,7 +677,7 @@ int hipb_finished(HipbEngine *e) {
 
 long hipb_run(HipbEngine *e, int chunk) {
     if (chunk < 1) chunk = 1;
-    if (!e->have_graph) {
+    if (!e->have_graph && !e->eager) {
         ECHK(hipStreamBeginCapture(e->s, hipStreamCaptureModeThreadLocal));
         step_launch(e);
         ECHK(hipStreamEndCapture(e->s, &e->graph));
@@ -689,7 +692,10 @@ long hipb_run(HipbEngine *e, int chunk) {
     for (;;) {
         if (hipb_finished(e) >= e->n_enc) break;
         if (steps > bound) CT_FATAL("hipb_run: requests did not finish within the step bound");
-        for (int i = 0; i < chunk; i++) ECHK(hipGraphLaunch(e->exec, e->s));
+        for (int i = 0; i < chunk; i++) {
+            if (e->eager) step_launch(e);
+            else ECHK(hipGraphLaunch(e->exec, e->s));
+        }
         steps += chunk;
     }
     return steps;

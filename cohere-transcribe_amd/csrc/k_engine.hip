@@ -73,8 +73,18 @@ __global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *l
     const float *x = logits + (long)s * VOCAB;
     float bv = -INFINITY;
     int bi = INT_MAX;
-    for (int i = threadIdx.x; i < VOCAB; i += 256)
-        if (i != skip) better(bv, bi, x[i], i);
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    float4 v[VOCAB / 1024];
+#pragma unroll
+    for (int k = 0; k < VOCAB / 1024; k++) v[k] = x4[threadIdx.x + 256 * k];
+#pragma unroll
+    for (int k = 0; k < VOCAB / 1024; k++) {
+        const int i = 4 * (threadIdx.x + 256 * k);
+        if (i != skip) better(bv, bi, v[k].x, i);
+        if (i + 1 != skip) better(bv, bi, v[k].y, i + 1);
+        if (i + 2 != skip) better(bv, bi, v[k].z, i + 2);
+        if (i + 3 != skip) better(bv, bi, v[k].w, i + 3);
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(bv, o, 64);

@@ -52,6 +52,43 @@ __global__ __launch_bounds__(256) void layernorm_kernel(float *dst, const float 
     ln_row(v, D, lane, w, b, dst + (long)row * D);
 }
 
+// D = 256*V (the model's 1024 and 1280): each lane holds V float4 of the row,
+// all loaded before any arithmetic.
+template <int V>
+__global__ __launch_bounds__(256) void layernorm_vec_kernel(float *dst, const float *src,
+                                                            const uint16_t *w, const uint16_t *b, int T) {
+    constexpr int D = 256 * V;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= T) return;
+    const float4 *x = reinterpret_cast<const float4 *>(src + (long)row * D);
+    float4 v[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) v[i] = x[lane + 64 * i];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    const float mu = wave_sum(s) / (float)D;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const float a = v[i].x - mu, bb = v[i].y - mu, c = v[i].z - mu, d = v[i].w - mu;
+        q += (a * a + bb * bb) + (c * c + d * d);
+    }
+    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
+    float4 *y = reinterpret_cast<float4 *>(dst + (long)row * D);
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int d0 = 4 * (lane + 64 * i);
+        float4 o;
+        o.x = (v[i].x - mu) * rs * bf2f(w[d0]) + bf2f(b[d0]);
+        o.y = (v[i].y - mu) * rs * bf2f(w[d0 + 1]) + bf2f(b[d0 + 1]);
+        o.z = (v[i].z - mu) * rs * bf2f(w[d0 + 2]) + bf2f(b[d0 + 2]);
+        o.w = (v[i].w - mu) * rs * bf2f(w[d0 + 3]) + bf2f(b[d0 + 3]);
+        y[lane + 64 * i] = o;
+    }
+}
+
 // Rows longer than 2048: three passes over the (cache-resident) row.
 __global__ __launch_bounds__(64) void layernorm_long_kernel(float *dst, const float *src,
                                                             const uint16_t *w, const uint16_t *b,
@@ -155,7 +192,12 @@ __global__ void inc_kernel(int *p) {
 extern "C" void ctk_layernorm(float *dst, const float *src, const uint16_t *w, const uint16_t *b,
                               int T, int D, hipStream_t s) {
     if (T <= 0) return;
-    if (D <= 64 * LN_MAXV)
+    const bool al = ((uintptr_t)dst % 16 == 0) && ((uintptr_t)src % 16 == 0);
+    if (al && D == 1024)
+        hipLaunchKernelGGL(layernorm_vec_kernel<4>, dim3((T + 3) / 4), dim3(256), 0, s, dst, src, w, b, T);
+    else if (al && D == 1280)
+        hipLaunchKernelGGL(layernorm_vec_kernel<5>, dim3((T + 3) / 4), dim3(256), 0, s, dst, src, w, b, T);
+    else if (D <= 64 * LN_MAXV)
         hipLaunchKernelGGL(layernorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, dst, src, w, b, T, D);
     else
         hipLaunchKernelGGL(layernorm_long_kernel, dim3(T), dim3(64), 0, s, dst, src, w, b, T, D);

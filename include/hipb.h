@@ -73,7 +73,9 @@ void hipb_encode(HipbEngine *e, int max_batch_frames);
  * argmax/policy).  Returns nothing; state stays on the device. */
 void hipb_step(HipbEngine *e);
 /* Runs decode steps until every encoded request has finished; steps are
- * replayed from one captured graph, chunk steps per host check.
+ * replayed from one captured graph (launched one by one instead when the
+ * environment sets HIPB_EAGER=1, e.g. under a tracing profiler), chunk steps
+ * per host check.
  * Returns the number of steps run. */
 long hipb_run(HipbEngine *e, int chunk);
 /* Number of requests finished so far (device counter, synchronises). */
