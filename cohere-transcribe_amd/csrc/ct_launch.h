@@ -23,11 +23,12 @@ enum {
 };
 
 /* Output segment of a GEMM: columns [i*seg_w, (i+1)*seg_w) go to seg[i]. */
-enum { CT_OUT_DENSE = 0, CT_OUT_HEADS_F32 = 1, CT_OUT_HEADS_BF16 = 2 };
+enum { CT_OUT_DENSE = 0, CT_OUT_HEADS_F32 = 1, CT_OUT_HEADS_BF16 = 2, CT_OUT_SPLIT = 3 };
 typedef struct {
     int         mode;
     void       *base;
-    long        ld;           /* DENSE: row stride in floats                     */
+    long        ld;           /* DENSE / SPLIT: row stride in elements           */
+    void       *base_lo;      /* SPLIT: lo plane (base is the hi plane)          */
     const long *rowoff;       /* HEADS: per-row element offset (< 0: skip row);  */
     long        hstride;      /* column c -> base + rowoff[m] + (c/128)*hstride + c%128 */
 } CtSeg;
@@ -35,6 +36,9 @@ typedef struct {
 typedef struct {
     const float    *A;        /* [M][lda] fp32 activations                 */
     long            lda;
+    /* Pre-split activations: when Ahi != NULL, A = Ahi + Alo (bf16 [M][lda]
+     * each, written by the producing kernel) and A is not read. */
+    const uint16_t *Ahi, *Alo;
     const uint16_t *W;        /* [N][K] bf16 weights, row-major            */
     const uint16_t *bias;     /* [N] bf16 or NULL                          */
     float          *Y;        /* output rows of ldy floats                 */
@@ -56,7 +60,13 @@ typedef struct {
 
 void ctk_gemm(const CtGemm *g, hipStream_t s);
 
+/* fp32 -> (hi, lo) bf16 pair, the split every GEMM applies to activations. */
+void ctk_split(uint16_t *hi, uint16_t *lo, const float *x, long n, hipStream_t s);
+
 /* ---------------- row-wise ops ---------------- */
+/* LayerNorm writing the normalised rows pre-split (hi, lo bf16). */
+void ctk_layernorm_split(uint16_t *hi, uint16_t *lo, const float *src, const uint16_t *w,
+                         const uint16_t *b, int T, int D, hipStream_t s);
 void ctk_layernorm(float *dst, const float *src, const uint16_t *w, const uint16_t *b,
                    int T, int D, hipStream_t s);
 void ctk_add(float *dst, const float *src, long n, hipStream_t s);
@@ -116,8 +126,10 @@ void ctk_dwconv_bn_silu(float *out, const float *in, int T,
                         const uint16_t *dww, const uint16_t *dwb,
                         const uint16_t *bnw, const uint16_t *bnb,
                         const uint16_t *bnm, const uint16_t *bnv, hipStream_t s);
-void ctk_dwconv_bn_silu_packed(float *out, const float *in, int M, const int *row_start,
-                               const int *row_len, const uint16_t *dww, const uint16_t *dwb,
+/* Packed form; writes its output pre-split (hi, lo bf16) for the next GEMM. */
+void ctk_dwconv_bn_silu_packed(uint16_t *out_hi, uint16_t *out_lo, const float *in, int M,
+                               const int *row_start, const int *row_len,
+                               const uint16_t *dww, const uint16_t *dwb,
                                const uint16_t *bnw, const uint16_t *bnb,
                                const uint16_t *bnm, const uint16_t *bnv, hipStream_t s);
 /* Subsampling stages (position-major [t][f][ch] activations). */

@@ -49,6 +49,7 @@ struct HipbEngine {
     int enc_cap;               /* frames */
     int sub_cap;               /* subsampling scratch floats */
     float *ex, *eln, *emid, *eq, *ek, *ev, *eo, *eg, *edw, *epe, *ep, *eh, *esub, *emel;
+    uint16_t *eln_h, *eln_l, *emid_h, *emid_l, *eo_h, *eo_l, *edw_h, *edw_l;  /* pre-split GEMM inputs */
     size_t emel_cap;
     int *e_row_start, *e_row_len, *e_seq_off, *e_seq_T, *e_blk_seq, *e_blk_q0;
     long *e_rowoff;
@@ -146,6 +147,28 @@ static void mel_tables_init(HipbEngine *e) {
     e->mel_tab = (CtMelTables){e->d_hann, e->d_twr, e->d_twi, e->d_fb, e->d_fb_lo, e->d_fb_hi};
 }
 
+/* GEMM whose activations come pre-split (hi, lo bf16 planes). */
+static void gemm_sp(HipbEngine *e, const uint16_t *Ah, const uint16_t *Al, int M, int K,
+                    const uint16_t *Wh, const uint16_t *bh, float *Y, int N, int epi, float scale) {
+    CtGemm g;
+    memset(&g, 0, sizeof g);
+    g.Ahi = Ah; g.Alo = Al; g.lda = K; g.W = DW(Wh); g.bias = DW(bh);
+    g.Y = Y; g.ldy = N; g.M = M; g.N = N; g.K = K; g.epi = epi; g.scale = scale;
+    ctk_gemm(&g, e->s);
+}
+
+/* FFN up projection with SiLU, written pre-split for the down projection. */
+static void gemm_sp_silu_split(HipbEngine *e, const uint16_t *Ah, const uint16_t *Al, int M,
+                               const uint16_t *Wh, const uint16_t *bh, uint16_t *Oh, uint16_t *Ol) {
+    CtGemm g;
+    memset(&g, 0, sizeof g);
+    g.Ahi = Ah; g.Alo = Al; g.lda = ENC_D; g.W = DW(Wh); g.bias = DW(bh);
+    g.M = M; g.N = ENC_FF; g.K = ENC_D; g.epi = CT_EPI_SILU;
+    g.nseg = 1; g.seg_w = ENC_FF;
+    g.seg[0].mode = CT_OUT_SPLIT; g.seg[0].base = Oh; g.seg[0].base_lo = Ol; g.seg[0].ld = ENC_FF;
+    ctk_gemm(&g, e->s);
+}
+
 HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     if (ct_t.dev < 0) CT_FATAL("hipb_create: call backend_init first");
     if (cfg->slots < 1 || cfg->slots > CT_MAX_BATCH) CT_FATAL("hipb_create: slots outside [1, 256]");
@@ -236,7 +259,8 @@ void hipb_destroy(HipbEngine *e) {
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
                     e->eh, e->esub, e->emel, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
                     e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
-                    e->d_fb_lo, e->d_fb_hi, e->epcm, e->e_clips, e->e_frame_clip};
+                    e->d_fb_lo, e->d_fb_hi, e->epcm, e->e_clips, e->e_frame_clip,
+                    e->eln_h, e->eln_l, e->emid_h, e->emid_l, e->eo_h, e->eo_l, e->edw_h, e->edw_l};
     for (size_t i = 0; i < sizeof ptrs / sizeof ptrs[0]; i++)
         if (ptrs[i]) ECHK(hipFree(ptrs[i]));
     for (int r = 0; r < e->n_req; r++) { free(e->req[r].mel); free(e->req[r].pcm); }
@@ -342,6 +366,9 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     float **bufs[] = {&e->ex, &e->eln, &e->emid, &e->eq, &e->ek, &e->ev, &e->eo, &e->eg, &e->edw, &e->eh};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
         if (*bufs[i]) { ECHK(hipFree(*bufs[i])); *bufs[i] = NULL; }
+    uint16_t **hb[] = {&e->eln_h, &e->eln_l, &e->emid_h, &e->emid_l, &e->eo_h, &e->eo_l, &e->edw_h, &e->edw_l};
+    for (size_t i = 0; i < sizeof hb / sizeof hb[0]; i++)
+        if (*hb[i]) { ECHK(hipFree(*hb[i])); *hb[i] = NULL; }
     int **ib[] = {&e->e_row_start, &e->e_row_len, &e->e_seq_off, &e->e_seq_T, &e->e_blk_seq, &e->e_blk_q0};
     for (size_t i = 0; i < sizeof ib / sizeof ib[0]; i++)
         if (*ib[i]) { ECHK(hipFree(*ib[i])); *ib[i] = NULL; }
@@ -354,14 +381,22 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     const int M = frames > e->enc_cap ? frames : e->enc_cap;
     const size_t rows = (size_t)M;
     e->ex = dmalloc(rows * ENC_D * 4);
-    e->eln = dmalloc(rows * ENC_D * 4);
-    e->emid = dmalloc(rows * ENC_FF * 4);
+    e->eln = NULL;
+    e->emid = NULL;
+    e->eln_h = dmalloc(rows * ENC_D * 2);
+    e->eln_l = dmalloc(rows * ENC_D * 2);
+    e->emid_h = dmalloc(rows * ENC_FF * 2);
+    e->emid_l = dmalloc(rows * ENC_FF * 2);
+    e->eo_h = dmalloc(rows * ENC_D * 2);
+    e->eo_l = dmalloc(rows * ENC_D * 2);
+    e->edw_h = dmalloc(rows * ENC_D * 2);
+    e->edw_l = dmalloc(rows * ENC_D * 2);
     e->eq = dmalloc(rows * ENC_D * 4);
     e->ek = dmalloc(rows * ENC_D * 4);
     e->ev = dmalloc(rows * ENC_D * 4);
     e->eo = dmalloc(rows * ENC_D * 4);
     e->eg = dmalloc(rows * ENC_D * 4);
-    e->edw = dmalloc(rows * ENC_D * 4);
+    e->edw = NULL;
     e->eh = dmalloc(rows * DEC_D * 4);
     e->e_row_start = dmalloc(rows * sizeof(int));
     e->e_row_len = dmalloc(rows * sizeof(int));
@@ -499,36 +534,38 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     ctk_rel_pos_emb(e->epe, T_max, ct_inv_freq(), s);
     for (int l = 0; l < ENC_N; l++) {
         const ELayer *L = &W->enc[l];
-        ctk_layernorm(e->eln, e->ex, DW(L->ff1_lnw), DW(L->ff1_lnb), M, ENC_D, s);
-        gemm(e, e->eln, M, ENC_D, L->ff1_w1, L->ff1_b1, e->emid, ENC_FF, CT_EPI_SILU, 0, NULL);
-        gemm(e, e->emid, M, ENC_FF, L->ff1_w2, L->ff1_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f, NULL);
-
-        ctk_layernorm(e->eln, e->ex, DW(L->sa_lnw), DW(L->sa_lnb), M, ENC_D, s);
-        gemm(e, e->eln, M, ENC_D, L->sa_qw, L->sa_qb, e->eq, ENC_D, CT_EPI_STORE, 0, NULL);
-        gemm(e, e->eln, M, ENC_D, L->sa_kw, L->sa_kb, e->ek, ENC_D, CT_EPI_STORE, 0, NULL);
-        gemm(e, e->eln, M, ENC_D, L->sa_vw, L->sa_vb, e->ev, ENC_D, CT_EPI_STORE, 0, NULL);
+        /* x += 0.5 FFN1(LN x) */
+        ctk_layernorm_split(e->eln_h, e->eln_l, e->ex, DW(L->ff1_lnw), DW(L->ff1_lnb), M, ENC_D, s);
+        gemm_sp_silu_split(e, e->eln_h, e->eln_l, M, L->ff1_w1, L->ff1_b1, e->emid_h, e->emid_l);
+        gemm_sp(e, e->emid_h, e->emid_l, M, ENC_FF, L->ff1_w2, L->ff1_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
+        /* x += MHSA(LN x) */
+        ctk_layernorm_split(e->eln_h, e->eln_l, e->ex, DW(L->sa_lnw), DW(L->sa_lnb), M, ENC_D, s);
+        gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_qw, L->sa_qb, e->eq, ENC_D, CT_EPI_STORE, 0);
+        gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_kw, L->sa_kb, e->ek, ENC_D, CT_EPI_STORE, 0);
+        gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_vw, L->sa_vb, e->ev, ENC_D, CT_EPI_STORE, 0);
         gemm(e, e->epe, 2 * T_max - 1, ENC_D, L->sa_pw, NULL, e->ep, ENC_D, CT_EPI_STORE, 0, NULL);
         ctk_relpos_attn_packed(e->eo, e->eq, e->ek, e->ev, e->ep, T_max, DW(L->sa_pbu), DW(L->sa_pbv),
                                e->e_seq_off, e->e_seq_T, e->e_blk_seq, e->e_blk_q0, nblk, T_max, s);
-        gemm(e, e->eo, M, ENC_D, L->sa_ow, L->sa_ob, e->ex, ENC_D, CT_EPI_FMADD, 1.0f, NULL);
-
-        ctk_layernorm(e->eln, e->ex, DW(L->cv_lnw), DW(L->cv_lnb), M, ENC_D, s);
+        ctk_split(e->eo_h, e->eo_l, e->eo, (long)M * ENC_D, s);
+        gemm_sp(e, e->eo_h, e->eo_l, M, ENC_D, L->sa_ow, L->sa_ob, e->ex, ENC_D, CT_EPI_FMADD, 1.0f);
+        /* x += Conv(LN x) */
+        ctk_layernorm_split(e->eln_h, e->eln_l, e->ex, DW(L->cv_lnw), DW(L->cv_lnb), M, ENC_D, s);
         {
             CtGemm g;
             memset(&g, 0, sizeof g);
-            g.A = e->eln; g.lda = ENC_D; g.W = DW(L->cv_pw1w); g.bias = DW(L->cv_pw1b);
+            g.Ahi = e->eln_h; g.Alo = e->eln_l; g.lda = ENC_D; g.W = DW(L->cv_pw1w); g.bias = DW(L->cv_pw1b);
             g.Y = e->eg; g.ldy = ENC_D; g.M = M; g.N = 2 * ENC_D; g.K = ENC_D;
             g.epi = CT_EPI_GLU; g.glu_half = ENC_D;
             ctk_gemm(&g, s);
         }
-        ctk_dwconv_bn_silu_packed(e->edw, e->eg, M, e->e_row_start, e->e_row_len, DW(L->cv_dww),
-                                  DW(L->cv_dwb), DW(L->cv_bnw), DW(L->cv_bnb), DW(L->cv_bnmean),
-                                  DW(L->cv_bnvar), s);
-        gemm(e, e->edw, M, ENC_D, L->cv_pw2w, L->cv_pw2b, e->ex, ENC_D, CT_EPI_FMADD, 1.0f, NULL);
-
-        ctk_layernorm(e->eln, e->ex, DW(L->ff2_lnw), DW(L->ff2_lnb), M, ENC_D, s);
-        gemm(e, e->eln, M, ENC_D, L->ff2_w1, L->ff2_b1, e->emid, ENC_FF, CT_EPI_SILU, 0, NULL);
-        gemm(e, e->emid, M, ENC_FF, L->ff2_w2, L->ff2_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f, NULL);
+        ctk_dwconv_bn_silu_packed(e->edw_h, e->edw_l, e->eg, M, e->e_row_start, e->e_row_len,
+                                  DW(L->cv_dww), DW(L->cv_dwb), DW(L->cv_bnw), DW(L->cv_bnb),
+                                  DW(L->cv_bnmean), DW(L->cv_bnvar), s);
+        gemm_sp(e, e->edw_h, e->edw_l, M, ENC_D, L->cv_pw2w, L->cv_pw2b, e->ex, ENC_D, CT_EPI_FMADD, 1.0f);
+        /* x += 0.5 FFN2(LN x); x = LN(x) */
+        ctk_layernorm_split(e->eln_h, e->eln_l, e->ex, DW(L->ff2_lnw), DW(L->ff2_lnb), M, ENC_D, s);
+        gemm_sp_silu_split(e, e->eln_h, e->eln_l, M, L->ff2_w1, L->ff2_b1, e->emid_h, e->emid_l);
+        gemm_sp(e, e->emid_h, e->emid_l, M, ENC_FF, L->ff2_w2, L->ff2_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
         ctk_layernorm(e->ex, e->ex, DW(L->out_lnw), DW(L->out_lnb), M, ENC_D, s);
     }
     gemm(e, e->ex, M, ENC_D, W->prw, W->prb, e->eh, DEC_D, CT_EPI_STORE, 0, NULL);
@@ -546,10 +583,10 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         g.M = M; g.N = 2 * DEC_D; g.K = DEC_D; g.epi = CT_EPI_STORE;
         g.nseg = 2; g.seg_w = DEC_D;
         const int mode = e->esz == 2 ? CT_OUT_HEADS_BF16 : CT_OUT_HEADS_F32;
-        g.seg[0] = (CtSeg){mode, (char *)e->kcross + l * cross_l * e->esz, 0, e->e_rowoff,
-                           (long)e->d.tmax * DEC_DK};
-        g.seg[1] = (CtSeg){mode, (char *)e->vcross + l * cross_l * e->esz, 0, e->e_rowoff,
-                           (long)e->d.tmax * DEC_DK};
+        g.seg[0] = (CtSeg){.mode = mode, .base = (char *)e->kcross + l * cross_l * e->esz,
+                           .rowoff = e->e_rowoff, .hstride = (long)e->d.tmax * DEC_DK};
+        g.seg[1] = (CtSeg){.mode = mode, .base = (char *)e->vcross + l * cross_l * e->esz,
+                           .rowoff = e->e_rowoff, .hstride = (long)e->d.tmax * DEC_DK};
         ctk_gemm(&g, s);
     }
     ECHK(hipStreamSynchronize(s));
@@ -637,9 +674,9 @@ static void step_launch(HipbEngine *e) {
         g.M = B; g.N = 3 * DEC_D; g.K = DEC_D; g.epi = CT_EPI_STORE; g.row_mask = e->d.act;
         g.nseg = 3; g.seg_w = DEC_D;
         const int mode = e->esz == 2 ? CT_OUT_HEADS_BF16 : CT_OUT_HEADS_F32;
-        g.seg[0] = (CtSeg){CT_OUT_DENSE, e->q, DEC_D, NULL, 0};
-        g.seg[1] = (CtSeg){mode, ks, 0, e->d.kv_rowoff, (long)MAX_SEQ * DEC_DK};
-        g.seg[2] = (CtSeg){mode, vs, 0, e->d.kv_rowoff, (long)MAX_SEQ * DEC_DK};
+        g.seg[0] = (CtSeg){.mode = CT_OUT_DENSE, .base = e->q, .ld = DEC_D};
+        g.seg[1] = (CtSeg){.mode = mode, .base = ks, .rowoff = e->d.kv_rowoff, .hstride = (long)MAX_SEQ * DEC_DK};
+        g.seg[2] = (CtSeg){.mode = mode, .base = vs, .rowoff = e->d.kv_rowoff, .hstride = (long)MAX_SEQ * DEC_DK};
         ctk_gemm(&g, s);
         step_attention(e, l, 0);
         gemm(e, e->att, B, DEC_D, L->sa_ow, L->sa_ob, e->h, DEC_D, CT_EPI_FMADD, 1.0f, NULL);

@@ -121,7 +121,8 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
 // Depthwise conv (k = 9, zero padding 4 inside the sequence) + inference
 // BatchNorm + SiLU (backends/cpu/backend.c:312-334).
 // ---------------------------------------------------------------------------
-__global__ void dwconv_bn_silu_kernel(float *out, const float *in, int M, const int *row_start,
+__global__ void dwconv_bn_silu_kernel(float *out, uint16_t *out_hi, uint16_t *out_lo,
+                                      const float *in, int M, const int *row_start,
                                       const int *row_len, const uint16_t *dww,
                                       const uint16_t *dwb, const uint16_t *bnw, const uint16_t *bnb,
                                       const uint16_t *bnm, const uint16_t *bnv) {
@@ -139,7 +140,15 @@ __global__ void dwconv_bn_silu_kernel(float *out, const float *in, int M, const 
         s += bf2f(dww[c * ENC_CK + k]) * in[(long)(st + ti) * ENC_D + c];
     }
     const float v = (s - bf2f(bnm[c])) / sqrtf(bf2f(bnv[c]) + 1e-5f) * bf2f(bnw[c]) + bf2f(bnb[c]);
-    out[i] = v / (1.0f + expf(-v));
+    const float o = v / (1.0f + expf(-v));
+    if (out_hi) {
+        uint16_t h, l;
+        split_bf16(o, h, l);
+        out_hi[i] = h;
+        out_lo[i] = l;
+    } else {
+        out[i] = o;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -268,17 +277,17 @@ extern "C" void ctk_dwconv_bn_silu(float *out, const float *in, int T, const uin
                                    const uint16_t *bnm, const uint16_t *bnv, hipStream_t s) {
     if (T <= 0) return;
     hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)T * ENC_D)), dim3(256), 0, s,
-                       out, in, T, nullptr, nullptr, dww, dwb, bnw, bnb, bnm, bnv);
+                       out, nullptr, nullptr, in, T, nullptr, nullptr, dww, dwb, bnw, bnb, bnm, bnv);
 }
 
-extern "C" void ctk_dwconv_bn_silu_packed(float *out, const float *in, int M, const int *row_start,
-                                          const int *row_len, const uint16_t *dww,
-                                          const uint16_t *dwb, const uint16_t *bnw,
-                                          const uint16_t *bnb, const uint16_t *bnm,
-                                          const uint16_t *bnv, hipStream_t s) {
+extern "C" void ctk_dwconv_bn_silu_packed(uint16_t *out_hi, uint16_t *out_lo, const float *in, int M,
+                                          const int *row_start, const int *row_len,
+                                          const uint16_t *dww, const uint16_t *dwb,
+                                          const uint16_t *bnw, const uint16_t *bnb,
+                                          const uint16_t *bnm, const uint16_t *bnv, hipStream_t s) {
     if (M <= 0) return;
     hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)M * ENC_D)), dim3(256), 0, s,
-                       out, in, M, row_start, row_len, dww, dwb, bnw, bnb, bnm, bnv);
+                       nullptr, out_hi, out_lo, in, M, row_start, row_len, dww, dwb, bnw, bnb, bnm, bnv);
 }
 
 extern "C" void ctk_sub_conv0(float *out, const float *mel, int T_mel, int stride,

@@ -64,6 +64,14 @@ __device__ __forceinline__ void store_out(const CtGemm &g, int m, int col, float
         const CtSeg &sg = g.seg[si];
         if (sg.mode == CT_OUT_DENSE) {
             reinterpret_cast<float *>(sg.base)[(long)m * sg.ld + c] = s;
+        } else if (sg.mode == CT_OUT_SPLIT) {
+            float v = s;
+            if (g.epi == CT_EPI_SILU) v = s / (1.0f + expf(-s));
+            else if (g.epi == CT_EPI_RELU) v = s > 0.0f ? s : 0.0f;
+            uint16_t h, l;
+            split_bf16(v, h, l);
+            reinterpret_cast<uint16_t *>(sg.base)[(long)m * sg.ld + c] = h;
+            reinterpret_cast<uint16_t *>(sg.base_lo)[(long)m * sg.ld + c] = l;
         } else {
             const long ro = sg.rowoff[m];
             if (ro < 0) return;
@@ -94,7 +102,10 @@ __device__ __forceinline__ void store_out(const CtGemm &g, int m, int col, float
 // LDS in wave order.  The split depends only on K, never on M, so a row's
 // result is the same for any number of rows.
 // ---------------------------------------------------------------------------
-constexpr int DSPLIT = 8;
+#ifndef CT_DEC_SPLIT
+#define CT_DEC_SPLIT 8
+#endif
+constexpr int DSPLIT = CT_DEC_SPLIT;
 
 template <int CB>
 __global__ __launch_bounds__(64 * DSPLIT) void gemm_dec_kernel(CtGemm g) {
@@ -188,6 +199,340 @@ __global__ __launch_bounds__(64 * DSPLIT) void gemm_dec_kernel(CtGemm g) {
         if (g.bias) s += bf2f(g.bias[col]);
         store_out(g, m, col, s);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Encoder-class GEMM (many rows): 128x128 output tile per 256-thread
+// workgroup, K in steps of 32, double-buffered LDS.  Each stage loads the A
+// tile (128x32 fp32, 64 contiguous bytes per thread), splits it to hi/lo
+// bf16 into LDS, and stages the W tile (128x32 bf16); every wave then runs a
+// 64x64 sub-tile as 4x4 MFMA 16x16x32 tiles, hi then lo, per K-step.  Tiles
+// are numbered so that consecutive workgroups of one XCD (blockIdx % 8) share
+// an A row block and read it from that XCD's L2.  Per element the sequence is
+// the same as the small-M kernels (K-steps in order, hi then lo), so results
+// do not depend on which of them ran.
+// ---------------------------------------------------------------------------
+constexpr int BT = 128, BK = 32, LDP = BK + 8;   // LDS row pitch 80 B (conflict-free b128 reads)
+
+template <bool GLU>
+__global__ __launch_bounds__(256) void gemm_big_kernel(CtGemm g, int n_mt, int n_nt) {
+    // one LDS block: [A hi x2][A lo x2][W x2] stage buffers; the GLU epilogue
+    // reuses its first 32 KB
+    __shared__ __attribute__((aligned(16))) uint16_t smem[6 * BT * LDP];
+    uint16_t (*sAh)[BT * LDP] = reinterpret_cast<uint16_t (*)[BT * LDP]>(smem);
+    uint16_t (*sAl)[BT * LDP] = reinterpret_cast<uint16_t (*)[BT * LDP]>(smem + 2 * BT * LDP);
+    uint16_t (*sW)[BT * LDP] = reinterpret_cast<uint16_t (*)[BT * LDP]>(smem + 4 * BT * LDP);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int r = lane & 15, kg = lane >> 4;
+    // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
+    // contiguous range of tiles, row-block major.
+    const int nt = n_mt * n_nt;
+    const int per = (nt + 7) / 8;
+    const int xcd = blockIdx.x % 8, loc = blockIdx.x / 8;
+    const int tile = xcd * per + loc;
+    if (tile >= nt) return;
+    const int tm = tile / n_nt, tn = tile % n_nt;
+    const int m0 = tm * BT;
+    const int c0 = tn * (GLU ? BT / 2 : BT);          // first output column
+    // loader mapping: thread -> row tid/2, 16 consecutive k at (tid%2)*16
+    const int lr = tid >> 1, lk = (tid & 1) * 16;
+    const int am = m0 + lr;
+    const float *arow = am < g.M ? g.A + (long)am * g.lda : nullptr;
+    int wn;
+    if (GLU) wn = lr < 64 ? c0 + lr : g.glu_half + c0 + (lr - 64);
+    else wn = c0 + lr;
+    const int nlim = GLU ? 2 * g.glu_half : g.N;
+    const uint16_t *wrow = wn < nlim ? g.W + (long)wn * g.K : nullptr;
+
+    float4 pa[4];
+    u16x8 pw[2];
+    auto gload = [&](int k0) {
+        if (arow) {
+            const float4 *p = reinterpret_cast<const float4 *>(arow + k0 + lk);
+            pa[0] = p[0]; pa[1] = p[1]; pa[2] = p[2]; pa[3] = p[3];
+        } else {
+            pa[0] = pa[1] = pa[2] = pa[3] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (wrow) {
+            const u16x8 *q = reinterpret_cast<const u16x8 *>(wrow + k0 + lk);
+            pw[0] = q[0]; pw[1] = q[1];
+        } else {
+            pw[0] = pw[1] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+        }
+    };
+    auto lstore = [&](int buf) {
+        const float x[16] = {pa[0].x, pa[0].y, pa[0].z, pa[0].w, pa[1].x, pa[1].y, pa[1].z, pa[1].w,
+                             pa[2].x, pa[2].y, pa[2].z, pa[2].w, pa[3].x, pa[3].y, pa[3].z, pa[3].w};
+        u16x8 h0, h1, l0, l1;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint16_t h, l;
+            split_bf16(x[j], h, l); h0[j] = h; l0[j] = l;
+            split_bf16(x[j + 8], h, l); h1[j] = h; l1[j] = l;
+        }
+        u16x8 *ah = reinterpret_cast<u16x8 *>(&sAh[buf][lr * LDP + lk]);
+        u16x8 *al = reinterpret_cast<u16x8 *>(&sAl[buf][lr * LDP + lk]);
+        u16x8 *ww = reinterpret_cast<u16x8 *>(&sW[buf][lr * LDP + lk]);
+        ah[0] = h0; ah[1] = h1; al[0] = l0; al[1] = l1; ww[0] = pw[0]; ww[1] = pw[1];
+    };
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const int wm = (wv >> 1) * 64, wnn = (wv & 1) * 64;   // wave sub-tile origin
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    const int nk = g.K / BK;
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload((kt + 1) * BK);
+        bf16x8 bfr[4];
+#pragma unroll
+        for (int cb = 0; cb < 4; cb++)
+            bfr[cb] = as_bf16x8(*reinterpret_cast<const u16x8 *>(&sW[cur][(wnn + cb * 16 + r) * LDP + kg * 8]));
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            const int row = (wm + rb * 16 + r) * LDP + kg * 8;
+            const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8 *>(&sAh[cur][row]));
+            const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(&sAl[cur][row]));
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) {
+                acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
+                acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
+            }
+        }
+        if (kt + 1 < nk) {
+            lstore(cur ^ 1);
+            __syncthreads();
+        }
+    }
+
+    // epilogue: wave sub-tile rows wm + rb*16 + 4*kg + j, columns wnn + cb*16 + r
+    if (GLU) {
+        // local columns [0,64) are the value half, [64,128) the gate half:
+        // waves with wnn == 0 hold values, wnn == 64 gates -> pair via LDS.
+        __syncthreads();
+        float *sx = reinterpret_cast<float *>(smem);   // 128 x 64 floats = 32 KB of the 60 KB block
+        if (wnn == 64) {
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                for (int cb = 0; cb < 4; cb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        sx[(wm + rb * 16 + kg * 4 + j) * 64 + cb * 16 + r] = acc[rb][cb][j];
+        }
+        __syncthreads();
+        if (wnn == 0) {
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) {
+                const int col = c0 + cb * 16 + r;
+                if (col >= g.glu_half) continue;
+                const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
+                const float bg = g.bias ? bf2f(g.bias[g.glu_half + col]) : 0.0f;
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int lrow = wm + rb * 16 + kg * 4 + j, m = m0 + lrow;
+                        if (m >= g.M) continue;
+                        const float a = acc[rb][cb][j] + ba;
+                        const float gt = sx[lrow * 64 + cb * 16 + r] + bg;
+                        g.Y[(long)m * g.ldy + col] = a / (1.0f + expf(-gt));
+                    }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int cb = 0; cb < 4; cb++) {
+        const int col = c0 + wnn + cb * 16 + r;
+        if (col >= g.N) continue;
+        const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int m = m0 + wm + rb * 16 + kg * 4 + j;
+                if (m >= g.M) continue;
+                if (g.row_mask && !g.row_mask[m]) continue;
+                store_out(g, m, col, acc[rb][cb][j] + ba);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Pre-split encoder GEMM: A arrives as two bf16 planes (hi, lo) written by the
+// producing kernel, so all three operands stream straight from HBM/L2 into
+// LDS with gfx950 global_load_lds_dwordx4 (no register staging), through a
+// ring of SST stages.  128x128 tile, BK = 64 (two MFMA K-steps) per stage,
+// 4 waves of 64x64.  LDS rows are 128 B; 16-B chunk c of row R is stored at
+// chunk c ^ (R & 7) so the fragment reads spread over the banks.
+// Per element: K-steps in order, hi then lo (as every other GEMM kernel).
+// ---------------------------------------------------------------------------
+constexpr int SBK = 64, SST = 3;
+constexpr int STAGE_ELEMS = 3 * 128 * SBK;            // Ahi, Alo, W tiles (bf16)
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+typedef const __attribute__((address_space(1))) void *glb_ptr_t;
+
+__device__ __forceinline__ void lds_dma16(const void *g, uint16_t *lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((glb_ptr_t)g, (lds_ptr_t)lds_wave_base, 16, 0, 0);
+}
+
+template <bool GLU>
+__global__ __launch_bounds__(256) void gemm_split_kernel(CtGemm g, int n_mt, int n_nt) {
+    __shared__ __attribute__((aligned(16))) uint16_t smem[SST * STAGE_ELEMS];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int r = lane & 15, kg = lane >> 4;
+    const int nt = n_mt * n_nt;
+    const int per = (nt + 7) / 8;
+    const int tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (tile >= nt) return;
+    const int tm = tile / n_nt, tn = tile % n_nt;
+    const int m0 = tm * 128;
+    const int c0 = tn * (GLU ? 64 : 128);
+    const int nlim = GLU ? 2 * g.glu_half : g.N;
+
+    // DMA plan: each of the 3 operand tiles is 128 rows x 128 B = 16 KB =
+    // 16 wave-instructions of 1 KB (8 rows each); wave wv issues
+    // instructions i = wv, wv+4, ... (12 per stage).  Within an instruction,
+    // lane L lands at LDS row 8*(i%16) + L/8, chunk L%8, and fetches global
+    // chunk (L%8) ^ (row & 7) of that row.
+    const uint16_t *src_row[12];
+    int src_chunk[12];
+#pragma unroll
+    for (int j = 0; j < 12; j++) {
+        const int i = wv + 4 * j;              // 0..47
+        const int op = i / 16, rr = (i % 16) * 8 + lane / 8;
+        const int ch = (lane % 8) ^ (rr & 7);
+        src_chunk[j] = ch;
+        if (op < 2) {
+            const int m = min(m0 + rr, g.M - 1);          // clamp: rows >= M are never stored
+            src_row[j] = (op == 0 ? g.Ahi : g.Alo) + (long)m * g.lda;
+        } else {
+            int n = GLU ? (rr < 64 ? c0 + rr : g.glu_half + c0 + rr - 64) : c0 + rr;
+            n = min(n, nlim - 1);
+            src_row[j] = g.W + (long)n * g.K;
+        }
+    }
+    auto issue = [&](int kt) {
+        uint16_t *stage = smem + (kt % SST) * STAGE_ELEMS;
+#pragma unroll
+        for (int j = 0; j < 12; j++) {
+            const int i = wv + 4 * j;
+            const uint16_t *gsrc = src_row[j] + kt * SBK + src_chunk[j] * 8;
+            lds_dma16(gsrc, stage + (i / 16) * 128 * SBK + (i % 16) * 8 * SBK);
+        }
+    };
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const int wm = (wv >> 1) * 64, wnn = (wv & 1) * 64;
+    const int nk = g.K / SBK;
+#pragma unroll
+    for (int p = 0; p < SST - 1; p++)
+        if (p < nk) issue(p);
+    for (int kt = 0; kt < nk; kt++) {
+        // stage kt complete for this wave: at most the younger stages in flight
+        if (kt + 1 < nk) __builtin_amdgcn_s_waitcnt((12 & 0xF) | ((12 >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+        else __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
+        __builtin_amdgcn_s_barrier();            // ... and for every wave
+        asm volatile("" ::: "memory");           // no LDS access moves across the barrier
+        if (kt + SST - 1 < nk) issue(kt + SST - 1);
+        const uint16_t *st = smem + (kt % SST) * STAGE_ELEMS;
+        const uint16_t *sAh = st, *sAl = st + 128 * SBK, *sW = st + 2 * 128 * SBK;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const int c = ks * 4 + kg;            // 16-B chunk of this lane's fragment
+            bf16x8 bfr[4];
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) {
+                const int R = wnn + cb * 16 + r;
+                bfr[cb] = as_bf16x8(*reinterpret_cast<const u16x8 *>(sW + R * SBK + ((c ^ (R & 7)) * 8)));
+            }
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++) {
+                const int R = wm + rb * 16 + r;
+                const int off = R * SBK + ((c ^ (R & 7)) * 8);
+                const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAh + off));
+                const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
+#pragma unroll
+                for (int cb = 0; cb < 4; cb++) {
+                    acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
+                    acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0): this wave's LDS reads done
+        __builtin_amdgcn_s_barrier();            // stage buffer free for the next issue
+        asm volatile("" ::: "memory");
+    }
+
+    if (GLU) {
+        float *sx = reinterpret_cast<float *>(smem);     // 128 x 64 floats
+        if (wnn == 64) {
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                for (int cb = 0; cb < 4; cb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        sx[(wm + rb * 16 + kg * 4 + j) * 64 + cb * 16 + r] = acc[rb][cb][j];
+        }
+        __syncthreads();
+        if (wnn == 0) {
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) {
+                const int col = c0 + cb * 16 + r;
+                if (col >= g.glu_half) continue;
+                const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
+                const float bg = g.bias ? bf2f(g.bias[g.glu_half + col]) : 0.0f;
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int lrow = wm + rb * 16 + kg * 4 + j, m = m0 + lrow;
+                        if (m >= g.M) continue;
+                        const float a = acc[rb][cb][j] + ba;
+                        const float gt = sx[lrow * 64 + cb * 16 + r] + bg;
+                        g.Y[(long)m * g.ldy + col] = a / (1.0f + expf(-gt));
+                    }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int cb = 0; cb < 4; cb++) {
+        const int col = c0 + wnn + cb * 16 + r;
+        if (col >= g.N) continue;
+        const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int m = m0 + wm + rb * 16 + kg * 4 + j;
+                if (m >= g.M) continue;
+                if (g.row_mask && !g.row_mask[m]) continue;
+                store_out(g, m, col, acc[rb][cb][j] + ba);
+            }
+    }
+}
+
+__global__ void split_kernel(uint16_t *hi, uint16_t *lo, const float *x, long n) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint16_t h, l;
+    split_bf16(x[i], h, l);
+    hi[i] = h;
+    lo[i] = l;
 }
 
 // One wavefront computes a (16*RB) x (16*CB) tile.  In GLU mode the first CB/2
@@ -329,6 +674,21 @@ extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
         fprintf(stderr, "ctk_gemm: GLU needs N == 2*glu_half\n");
         exit(1);
     }
+    if (g->Ahi) {
+        // pre-split activations: the DMA kernel (needs K % 64 == 0, 16-B aligned rows)
+        if (!(g->K % SBK == 0 && g->lda % 8 == 0 && ((uintptr_t)g->Ahi & 15) == 0 &&
+              ((uintptr_t)g->Alo & 15) == 0 && ((uintptr_t)g->W & 15) == 0)) {
+            fprintf(stderr, "ctk_gemm: pre-split A needs K %% 64 == 0 and 16-byte aligned rows\n");
+            exit(1);
+        }
+        const bool glu = g->epi == CT_EPI_GLU;
+        const int n_mt = (g->M + 127) / 128;
+        const int n_nt = glu ? (g->glu_half + 63) / 64 : (g->N + 127) / 128;
+        const int nt = n_mt * n_nt, per = (nt + 7) / 8;
+        if (glu) hipLaunchKernelGGL(gemm_split_kernel<true>, dim3(per * 8), dim3(256), 0, s, *g, n_mt, n_nt);
+        else hipLaunchKernelGGL(gemm_split_kernel<false>, dim3(per * 8), dim3(256), 0, s, *g, n_mt, n_nt);
+        return;
+    }
     const bool vec = (g->K % 8 == 0) && (g->lda % 4 == 0) &&
                      (((uintptr_t)g->A & 15) == 0) && (((uintptr_t)g->W & 15) == 0);
     const bool glu = g->epi == CT_EPI_GLU;
@@ -339,6 +699,21 @@ extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
         else hipLaunchKernelGGL(gemm_dec_kernel<1>, grid, dim3(64 * DSPLIT), 0, s, *g);
         return;
     }
+    if (vec && g->K % BK == 0 && g->M > 64) {
+        // same per-element MFMA sequence as the small-M kernels: bit-identical rows
+        const int n_mt = (g->M + BT - 1) / BT;
+        const int n_nt = glu ? (g->glu_half + BT / 2 - 1) / (BT / 2) : (g->N + BT - 1) / BT;
+        const int nt = n_mt * n_nt, per = (nt + 7) / 8;
+        const int blocks = per * 8;
+        if (glu) hipLaunchKernelGGL(gemm_big_kernel<true>, dim3(blocks), dim3(256), 0, s, *g, n_mt, n_nt);
+        else hipLaunchKernelGGL(gemm_big_kernel<false>, dim3(blocks), dim3(256), 0, s, *g, n_mt, n_nt);
+        return;
+    }
     if (vec) { if (glu) dispatch<true, true>(*g, s); else dispatch<true, false>(*g, s); }
     else     { if (glu) dispatch<false, true>(*g, s); else dispatch<false, false>(*g, s); }
+}
+
+extern "C" void ctk_split(uint16_t *hi, uint16_t *lo, const float *x, long n, hipStream_t s) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, hi, lo, x, n);
 }

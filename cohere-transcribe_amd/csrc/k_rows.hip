@@ -5,6 +5,8 @@
 #include "ct_launch.h"
 #include "../../include/model_types.h"
 #include <limits.h>
+#include <stdio.h>
+#include <stdlib.h>
 
 namespace {
 
@@ -86,6 +88,48 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(float *dst, const fl
         o.z = (v[i].z - mu) * rs * bf2f(w[d0 + 2]) + bf2f(b[d0 + 2]);
         o.w = (v[i].w - mu) * rs * bf2f(w[d0 + 3]) + bf2f(b[d0 + 3]);
         y[lane + 64 * i] = o;
+    }
+}
+
+// Same as layernorm_vec_kernel, writing each output as its hi/lo bf16 split.
+template <int V>
+__global__ __launch_bounds__(256) void layernorm_split_kernel(uint16_t *hi, uint16_t *lo,
+                                                              const float *src, const uint16_t *w,
+                                                              const uint16_t *b, int T) {
+    constexpr int D = 256 * V;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= T) return;
+    const float4 *x = reinterpret_cast<const float4 *>(src + (long)row * D);
+    float4 v[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) v[i] = x[lane + 64 * i];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    const float mu = wave_sum(s) / (float)D;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const float a = v[i].x - mu, bb = v[i].y - mu, c = v[i].z - mu, d = v[i].w - mu;
+        q += (a * a + bb * bb) + (c * c + d * d);
+    }
+    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int d0 = 4 * (lane + 64 * i);
+        const float o[4] = {(v[i].x - mu) * rs * bf2f(w[d0]) + bf2f(b[d0]),
+                            (v[i].y - mu) * rs * bf2f(w[d0 + 1]) + bf2f(b[d0 + 1]),
+                            (v[i].z - mu) * rs * bf2f(w[d0 + 2]) + bf2f(b[d0 + 2]),
+                            (v[i].w - mu) * rs * bf2f(w[d0 + 3]) + bf2f(b[d0 + 3])};
+        ushort4 h4, l4;
+        uint16_t hh[4], ll[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) split_bf16(o[j], hh[j], ll[j]);
+        h4.x = hh[0]; h4.y = hh[1]; h4.z = hh[2]; h4.w = hh[3];
+        l4.x = ll[0]; l4.y = ll[1]; l4.z = ll[2]; l4.w = ll[3];
+        reinterpret_cast<ushort4 *>(hi + (long)row * D)[lane + 64 * i] = h4;
+        reinterpret_cast<ushort4 *>(lo + (long)row * D)[lane + 64 * i] = l4;
     }
 }
 
@@ -201,6 +245,19 @@ extern "C" void ctk_layernorm(float *dst, const float *src, const uint16_t *w, c
         hipLaunchKernelGGL(layernorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, dst, src, w, b, T, D);
     else
         hipLaunchKernelGGL(layernorm_long_kernel, dim3(T), dim3(64), 0, s, dst, src, w, b, T, D);
+}
+
+extern "C" void ctk_layernorm_split(uint16_t *hi, uint16_t *lo, const float *src, const uint16_t *w,
+                                    const uint16_t *b, int T, int D, hipStream_t s) {
+    if (T <= 0) return;
+    if ((uintptr_t)src % 16 || (uintptr_t)hi % 8 || (uintptr_t)lo % 8 || (D != 1024 && D != 1280)) {
+        fprintf(stderr, "ctk_layernorm_split: needs D in {1024, 1280} and aligned rows\n");
+        exit(1);
+    }
+    if (D == 1024)
+        hipLaunchKernelGGL(layernorm_split_kernel<4>, dim3((T + 3) / 4), dim3(256), 0, s, hi, lo, src, w, b, T);
+    else
+        hipLaunchKernelGGL(layernorm_split_kernel<5>, dim3((T + 3) / 4), dim3(256), 0, s, hi, lo, src, w, b, T);
 }
 
 extern "C" void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, const int *pos_len,
