@@ -368,14 +368,22 @@ __global__ __launch_bounds__(256) void gemm_big_kernel(CtGemm g, int n_mt, int n
 // ---------------------------------------------------------------------------
 // Pre-split encoder GEMM: A arrives as two bf16 planes (hi, lo) written by the
 // producing kernel, so all three operands stream straight from HBM/L2 into
-// LDS with gfx950 global_load_lds_dwordx4 (no register staging), through a
-// ring of SST stages.  128x128 tile, BK = 64 (two MFMA K-steps) per stage,
-// 4 waves of 64x64.  LDS rows are 128 B; 16-B chunk c of row R is stored at
-// chunk c ^ (R & 7) so the fragment reads spread over the banks.
+// LDS with gfx950 global_load_lds_dwordx4 (no register staging) through a
+// ring of SST stages, one barrier per stage.  Tile 128 (rows) x 256 (weight
+// columns): A is the doubled operand, so the tile is wide in N.  BK = 32 (one
+// MFMA K-step) per stage; 8 waves, each a 64x64 sub-tile (4x4 MFMA 16x16x32,
+// hi then lo).  LDS rows are 64 B; 16-B chunk c of row R sits at chunk
+// c ^ ((R >> 2) & 3), which makes the 16-lane fragment reads conflict-free.
+// Tiles run in groups of SGM row blocks (all column tiles of a group before
+// the next), each XCD taking a contiguous range, so a group's A rows and the
+// W columns in use stay in that XCD's L2.
 // Per element: K-steps in order, hi then lo (as every other GEMM kernel).
 // ---------------------------------------------------------------------------
-constexpr int SBK = 64, SST = 3;
-constexpr int STAGE_ELEMS = 3 * 128 * SBK;            // Ahi, Alo, W tiles (bf16)
+constexpr int SBM = 128, SBN = 256, SBK = 32, SST = 4, SGM = 4;
+constexpr int S_A = SBM * SBK, S_W = SBN * SBK;       // elements per operand tile
+constexpr int STAGE_ELEMS = 2 * S_A + S_W;            // Ahi, Alo, W
+constexpr int S_INSTR = STAGE_ELEMS / 512;            // 1-KB DMA instructions per stage (32)
+constexpr int S_PER_WAVE = S_INSTR / 8;               // 4
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 typedef const __attribute__((address_space(1))) void *glb_ptr_t;
@@ -384,50 +392,53 @@ __device__ __forceinline__ void lds_dma16(const void *g, uint16_t *lds_wave_base
     __builtin_amdgcn_global_load_lds((glb_ptr_t)g, (lds_ptr_t)lds_wave_base, 16, 0, 0);
 }
 
+__device__ __forceinline__ int swz(int R, int c) { return c ^ ((R >> 2) & 3); }
+
 template <bool GLU>
-__global__ __launch_bounds__(256) void gemm_split_kernel(CtGemm g, int n_mt, int n_nt) {
+__global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int n_nt) {
     __shared__ __attribute__((aligned(16))) uint16_t smem[SST * STAGE_ELEMS];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r = lane & 15, kg = lane >> 4;
     const int nt = n_mt * n_nt;
     const int per = (nt + 7) / 8;
-    const int tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
-    if (tile >= nt) return;
-    const int tm = tile / n_nt, tn = tile % n_nt;
-    const int m0 = tm * 128;
-    const int c0 = tn * (GLU ? 64 : 128);
+    const int t = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (t >= nt) return;
+    // grouped order: SGM row blocks x all column tiles per group, row fastest
+    const int gsize = SGM * n_nt;
+    const int grp = t / gsize, rem = t % gsize;
+    const int gm = min(SGM, n_mt - grp * SGM);
+    const int tn = rem / gm, tm = grp * SGM + rem % gm;
+    const int m0 = tm * SBM;
+    const int c0 = tn * (GLU ? SBN / 2 : SBN);
     const int nlim = GLU ? 2 * g.glu_half : g.N;
 
-    // DMA plan: each of the 3 operand tiles is 128 rows x 128 B = 16 KB =
-    // 16 wave-instructions of 1 KB (8 rows each); wave wv issues
-    // instructions i = wv, wv+4, ... (12 per stage).  Within an instruction,
-    // lane L lands at LDS row 8*(i%16) + L/8, chunk L%8, and fetches global
-    // chunk (L%8) ^ (row & 7) of that row.
-    const uint16_t *src_row[12];
-    int src_chunk[12];
+    // DMA plan: instruction i (0..31) covers 16 rows x 64 B of one operand
+    // tile: i < 8 A-hi, i < 16 A-lo, else W.  Lane L lands at row
+    // 16*(i%8 or (i-16)) + L/4, chunk slot L%4, fetching global chunk
+    // swz(row, L%4).  Wave wv issues i = wv + 8*j.
+    const uint16_t *src[S_PER_WAVE];
+    int dst[S_PER_WAVE];
 #pragma unroll
-    for (int j = 0; j < 12; j++) {
-        const int i = wv + 4 * j;              // 0..47
-        const int op = i / 16, rr = (i % 16) * 8 + lane / 8;
-        const int ch = (lane % 8) ^ (rr & 7);
-        src_chunk[j] = ch;
-        if (op < 2) {
-            const int m = min(m0 + rr, g.M - 1);          // clamp: rows >= M are never stored
-            src_row[j] = (op == 0 ? g.Ahi : g.Alo) + (long)m * g.lda;
+    for (int j = 0; j < S_PER_WAVE; j++) {
+        const int i = wv + 8 * j;
+        const int Rl = lane >> 2, ch = lane & 3;
+        if (i < 16) {
+            const int R = (i & 7) * 16 + Rl;
+            const int m = min(m0 + R, g.M - 1);            // rows >= M are never stored
+            src[j] = (i < 8 ? g.Ahi : g.Alo) + (long)m * g.lda + swz(R, ch) * 8;
+            dst[j] = (i < 8 ? 0 : S_A) + (i & 7) * 16 * SBK;
         } else {
-            int n = GLU ? (rr < 64 ? c0 + rr : g.glu_half + c0 + rr - 64) : c0 + rr;
+            const int R = (i - 16) * 16 + Rl;
+            int n = GLU ? (R < SBN / 2 ? c0 + R : g.glu_half + c0 + R - SBN / 2) : c0 + R;
             n = min(n, nlim - 1);
-            src_row[j] = g.W + (long)n * g.K;
+            src[j] = g.W + (long)n * g.K + swz(R, ch) * 8;
+            dst[j] = 2 * S_A + (i - 16) * 16 * SBK;
         }
     }
     auto issue = [&](int kt) {
         uint16_t *stage = smem + (kt % SST) * STAGE_ELEMS;
 #pragma unroll
-        for (int j = 0; j < 12; j++) {
-            const int i = wv + 4 * j;
-            const uint16_t *gsrc = src_row[j] + kt * SBK + src_chunk[j] * 8;
-            lds_dma16(gsrc, stage + (i / 16) * 128 * SBK + (i % 16) * 8 * SBK);
-        }
+        for (int j = 0; j < S_PER_WAVE; j++) lds_dma16(src[j] + kt * SBK, stage + dst[j]);
     };
 
     f32x4 acc[4][4];
@@ -435,63 +446,62 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(CtGemm g, int n_mt, int
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    const int wm = (wv >> 1) * 64, wnn = (wv & 1) * 64;
+    const int wm = (wv >> 2) * 64, wn = (wv & 3) * 64;
     const int nk = g.K / SBK;
 #pragma unroll
     for (int p = 0; p < SST - 1; p++)
         if (p < nk) issue(p);
     for (int kt = 0; kt < nk; kt++) {
-        // stage kt complete for this wave: at most the younger stages in flight
-        if (kt + 1 < nk) __builtin_amdgcn_s_waitcnt((12 & 0xF) | ((12 >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+        // wait for this wave's part of stage kt; younger stages stay in flight
+        const int younger = min(nk - 1 - kt, SST - 2);
+        if (younger >= 2) __builtin_amdgcn_s_waitcnt((8 & 0xF) | (0x7 << 4) | (0xF << 8));
+        else if (younger == 1) __builtin_amdgcn_s_waitcnt((4 & 0xF) | (0x7 << 4) | (0xF << 8));
         else __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
-        __builtin_amdgcn_s_barrier();            // ... and for every wave
-        asm volatile("" ::: "memory");           // no LDS access moves across the barrier
+        __builtin_amdgcn_s_barrier();            // stage kt landed for every wave, and every
+        asm volatile("" ::: "memory");           // wave is done reading stage kt-1
         if (kt + SST - 1 < nk) issue(kt + SST - 1);
         const uint16_t *st = smem + (kt % SST) * STAGE_ELEMS;
-        const uint16_t *sAh = st, *sAl = st + 128 * SBK, *sW = st + 2 * 128 * SBK;
+        const uint16_t *sAh = st, *sAl = st + S_A, *sW = st + 2 * S_A;
+        bf16x8 bfr[4];
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            const int c = ks * 4 + kg;            // 16-B chunk of this lane's fragment
-            bf16x8 bfr[4];
+        for (int cb = 0; cb < 4; cb++) {
+            const int R = wn + cb * 16 + r;
+            bfr[cb] = as_bf16x8(*reinterpret_cast<const u16x8 *>(sW + R * SBK + swz(R, kg) * 8));
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            const int R = wm + rb * 16 + r;
+            const int off = R * SBK + swz(R, kg) * 8;
+            const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAh + off));
+            const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
 #pragma unroll
             for (int cb = 0; cb < 4; cb++) {
-                const int R = wnn + cb * 16 + r;
-                bfr[cb] = as_bf16x8(*reinterpret_cast<const u16x8 *>(sW + R * SBK + ((c ^ (R & 7)) * 8)));
-            }
-#pragma unroll
-            for (int rb = 0; rb < 4; rb++) {
-                const int R = wm + rb * 16 + r;
-                const int off = R * SBK + ((c ^ (R & 7)) * 8);
-                const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAh + off));
-                const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
-#pragma unroll
-                for (int cb = 0; cb < 4; cb++) {
-                    acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
-                    acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
-                }
+                acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
+                acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
             }
         }
-        __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0): this wave's LDS reads done
-        __builtin_amdgcn_s_barrier();            // stage buffer free for the next issue
-        asm volatile("" ::: "memory");
     }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 
     if (GLU) {
-        float *sx = reinterpret_cast<float *>(smem);     // 128 x 64 floats
-        if (wnn == 64) {
+        // local columns [0,128) are values (waves wn < 128), [128,256) gates
+        float *sx = reinterpret_cast<float *>(smem);     // 128 x 128 floats = 64 KB
+        if (wn >= 128) {
 #pragma unroll
             for (int rb = 0; rb < 4; rb++)
 #pragma unroll
                 for (int cb = 0; cb < 4; cb++)
 #pragma unroll
                     for (int j = 0; j < 4; j++)
-                        sx[(wm + rb * 16 + kg * 4 + j) * 64 + cb * 16 + r] = acc[rb][cb][j];
+                        sx[(wm + rb * 16 + kg * 4 + j) * 128 + (wn - 128) + cb * 16 + r] = acc[rb][cb][j];
         }
         __syncthreads();
-        if (wnn == 0) {
+        if (wn < 128) {
 #pragma unroll
             for (int cb = 0; cb < 4; cb++) {
-                const int col = c0 + cb * 16 + r;
+                const int lc = wn + cb * 16 + r, col = c0 + lc;
                 if (col >= g.glu_half) continue;
                 const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
                 const float bg = g.bias ? bf2f(g.bias[g.glu_half + col]) : 0.0f;
@@ -502,7 +512,7 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(CtGemm g, int n_mt, int
                         const int lrow = wm + rb * 16 + kg * 4 + j, m = m0 + lrow;
                         if (m >= g.M) continue;
                         const float a = acc[rb][cb][j] + ba;
-                        const float gt = sx[lrow * 64 + cb * 16 + r] + bg;
+                        const float gt = sx[lrow * 128 + lc] + bg;
                         g.Y[(long)m * g.ldy + col] = a / (1.0f + expf(-gt));
                     }
             }
@@ -511,7 +521,7 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(CtGemm g, int n_mt, int
     }
 #pragma unroll
     for (int cb = 0; cb < 4; cb++) {
-        const int col = c0 + wnn + cb * 16 + r;
+        const int col = c0 + wn + cb * 16 + r;
         if (col >= g.N) continue;
         const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
 #pragma unroll
@@ -675,18 +685,18 @@ extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
         exit(1);
     }
     if (g->Ahi) {
-        // pre-split activations: the DMA kernel (needs K % 64 == 0, 16-B aligned rows)
+        // pre-split activations: the DMA kernel (needs K % 32 == 0, 16-B aligned rows)
         if (!(g->K % SBK == 0 && g->lda % 8 == 0 && ((uintptr_t)g->Ahi & 15) == 0 &&
               ((uintptr_t)g->Alo & 15) == 0 && ((uintptr_t)g->W & 15) == 0)) {
-            fprintf(stderr, "ctk_gemm: pre-split A needs K %% 64 == 0 and 16-byte aligned rows\n");
+            fprintf(stderr, "ctk_gemm: pre-split A needs K %% 32 == 0 and 16-byte aligned rows\n");
             exit(1);
         }
         const bool glu = g->epi == CT_EPI_GLU;
-        const int n_mt = (g->M + 127) / 128;
-        const int n_nt = glu ? (g->glu_half + 63) / 64 : (g->N + 127) / 128;
+        const int n_mt = (g->M + SBM - 1) / SBM;
+        const int n_nt = glu ? (g->glu_half + SBN / 2 - 1) / (SBN / 2) : (g->N + SBN - 1) / SBN;
         const int nt = n_mt * n_nt, per = (nt + 7) / 8;
-        if (glu) hipLaunchKernelGGL(gemm_split_kernel<true>, dim3(per * 8), dim3(256), 0, s, *g, n_mt, n_nt);
-        else hipLaunchKernelGGL(gemm_split_kernel<false>, dim3(per * 8), dim3(256), 0, s, *g, n_mt, n_nt);
+        if (glu) hipLaunchKernelGGL(gemm_split_kernel<true>, dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt);
+        else hipLaunchKernelGGL(gemm_split_kernel<false>, dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt);
         return;
     }
     const bool vec = (g->K % 8 == 0) && (g->lda % 4 == 0) &&
