@@ -10,6 +10,7 @@ extern "C" {
 #endif
 
 #define CT_PROMPT_MAX 16
+#define CT_MAX_KSPLIT 8    /* largest ctk_gemv_ksplit() of a decoder weight */
 
 /* All pointers are device memory.  Slot-major arrays have `slots` entries,
  * request-major arrays `max_req`. */

@@ -60,6 +60,58 @@ typedef struct {
 
 void ctk_gemm(const CtGemm *g, hipStream_t s);
 
+/* ---------------- decode GEMM on fragment-ordered activations ----------------
+ * "Frag" layout of an activation matrix X[M][K] (K % 32 == 0), as the decode
+ * GEMM's MFMA lanes consume it: rows in blocks of 64, each block in K-steps of
+ * 32, each K-step in four 16-row groups; one group is 1024 uint16 = the hi
+ * plane (64 lanes x 8 bf16) then the lo plane.  Lane l of a group holds row
+ * 16*g + (l & 15), columns 8*(l >> 4) .. +7 of the K-step.  X = hi + lo.
+ * Element (m, k) of plane p sits at ct_frag_off(m, k, K) + 512*p. */
+#ifdef __HIPCC__
+#define CT_HD __host__ __device__
+#else
+#define CT_HD
+#endif
+static inline CT_HD long ct_frag_off(int m, int k, int K) {
+    return ((((long)(m >> 6) * (K >> 5) + (k >> 5)) * 4 + ((m >> 4) & 3)) << 10) +
+           ((long)((((k >> 3) & 3) << 4) + (m & 15)) << 3) + (k & 7);
+}
+/* uint16 elements of a frag buffer for M rows (rows padded to 64). */
+static inline long ct_frag_elems(int M, int K) { return (long)((M + 63) / 64) * 64 * K * 2; }
+
+enum {
+    CT_GV_PARTIAL = 0,  /* Y[(ks*M + m)*N + n] = partial sum over K-slice ks (no bias)  */
+    CT_GV_DENSE   = 1,  /* Y[m*ldy + n] = act(s + b)                                    */
+    CT_GV_FRAG    = 2,  /* F (frag layout, K' = N) = act(s + b), split hi/lo           */
+    CT_GV_QKV     = 3   /* n < 1024: Y[m*ldy + n] (query); n in [1024, 3072): key/value */
+                        /* rows of the head-major caches kc/vc at rowoff[m] (< 0: skip) */
+};
+typedef struct {
+    const uint16_t *A;        /* frag-ordered activations [M][K]                      */
+    const uint16_t *W;        /* [N][K] bf16                                           */
+    const uint16_t *bias;     /* [N] bf16 or NULL (ignored for CT_GV_PARTIAL)          */
+    int M, N, K;
+    int ksplit;               /* K-slices (workgroups along K); 1 unless PARTIAL       */
+    int out, relu;
+    float *Y;  long ldy;
+    uint16_t *F;
+    void *kc, *vc;            /* CT_GV_QKV caches, element offset rowoff[m] + (c/128)*hstride + c%128 */
+    const long *rowoff;
+    long hstride;
+    int kv_bf16;
+} CtGemv;
+/* Requires N % 16 == 0 (N % 64 == 0 when N >= 8192), K % (256 * steps) == 0. */
+void ctk_gemv(const CtGemv *g, hipStream_t s);
+/* K-slices the decode GEMM uses for an N x K weight (a function of the shape
+ * only, so every row's result is independent of M). */
+int  ctk_gemv_ksplit(int N, int K);
+
+/* Decoder residual + LayerNorm (D = DEC_D): h[m] += sum_{p<nparts} parts[p][m]
+ * + pbias (in that order; skipped when nparts == 0), then frag = LN(h[m]) in
+ * frag layout (K = DEC_D). */
+void ctk_ln_frag(float *h, uint16_t *frag, const float *parts, int nparts,
+                 const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M, hipStream_t s);
+
 /* fp32 -> (hi, lo) bf16 pair, the split every GEMM applies to activations. */
 void ctk_split(uint16_t *hi, uint16_t *lo, const float *x, long n, hipStream_t s);
 
@@ -100,6 +152,15 @@ typedef struct {
     const float *mask;        /* optional additive [T_q][T_k] mask (B == 1)            */
     int   T_q, B, H;
     float scale;
+    /* optional: the query is the sum of q_nparts partial rows q_parts[p][b]
+     * (p-major, q_pstride floats apart) plus q_bias, instead of Q */
+    const float    *q_parts;
+    int             q_nparts;
+    long            q_pstride;
+    const uint16_t *q_bias;
+    /* optional: write the output split hi/lo in frag layout (K = H*128),
+     * row b*T_q + qi, instead of out */
+    uint16_t       *out_frag;
 } CtAttn;
 /* Head dim fixed at DEC_DK (128). */
 void ctk_attn(const CtAttn *a, hipStream_t s);

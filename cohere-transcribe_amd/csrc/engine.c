@@ -43,8 +43,10 @@ struct HipbEngine {
     void *kself, *vself;       /* [L][slots][H][smax][128] */
     void *kcross, *vcross;     /* [L][max_req][H][tmax][128] */
     float *enc_pool;           /* [max_req][tmax][DEC_D] */
-    /* step activations */
-    float *h, *ln, *q, *att, *mid, *logits;
+    /* step activations: h residual rows (fp32); lnf/attf/midf the decode
+     * GEMMs' inputs in frag layout; parts K-slice partial sums */
+    float *h, *q, *parts, *logits;
+    uint16_t *lnf, *attf, *midf;
     /* encoder workspace (lazy) */
     int enc_cap;               /* frames */
     int sub_cap;               /* subsampling scratch floats */
@@ -232,10 +234,11 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->vcross = dmalloc(cross_el * e->esz);
     e->enc_pool = dmalloc((size_t)R * tmax * DEC_D * sizeof(float));
     e->h = dmalloc((size_t)S * DEC_D * 4);
-    e->ln = dmalloc((size_t)S * DEC_D * 4);
     e->q = dmalloc((size_t)S * DEC_D * 4);
-    e->att = dmalloc((size_t)S * DEC_D * 4);
-    e->mid = dmalloc((size_t)S * DEC_FF * 4);
+    e->parts = dmalloc((size_t)CT_MAX_KSPLIT * S * DEC_D * 4);
+    e->lnf = dmalloc(ct_frag_elems(S, DEC_D) * 2);
+    e->attf = dmalloc(ct_frag_elems(S, DEC_D) * 2);
+    e->midf = dmalloc(ct_frag_elems(S, DEC_FF) * 2);
     e->logits = dmalloc((size_t)S * VOCAB * 4);
     ECHK(hipMemsetAsync(e->h, 0, (size_t)S * DEC_D * 4, e->s));
     e->req = calloc(R, sizeof(HostReq));
@@ -255,7 +258,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->kself, e->vself, e->kcross, e->vcross,
-                    e->enc_pool, e->h, e->ln, e->q, e->att, e->mid, e->logits,
+                    e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
                     e->eh, e->esub, e->emel, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
                     e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
@@ -617,16 +620,26 @@ void hipb_encode(HipbEngine *e, int max_batch_frames) {
 /* ------------------------------------------------------------------ */
 /* The decode step                                                     */
 /* ------------------------------------------------------------------ */
-static void attn(HipbEngine *e, float *out, const float *Q, const void *K, const void *V,
-                 long item_stride, long head_stride, const int *lens, const int *kv_index) {
+/* Decode attention of every slot; the output goes split into attf (frag
+ * layout) for the out-projection.  The query is q (self) or the Q
+ * projection's K-slice partials plus bias (cross). */
+static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, long head_stride,
+                 const int *lens, const int *kv_index, const uint16_t *q_bias) {
     CtAttn a;
     memset(&a, 0, sizeof a);
-    a.out = out; a.Q = Q; a.q_sb = DEC_D; a.q_st = DEC_D;
+    a.Q = e->q; a.q_sb = DEC_D; a.q_st = DEC_D;
     a.K = K; a.V = V; a.kv_bf16 = e->esz == 2;
     a.kv_sb = item_stride; a.kv_st = DEC_DK; a.kv_sh = head_stride;
     a.lens = lens; a.lens_step = 1; a.kv_index = kv_index;
     a.T_q = 1; a.B = e->d.slots; a.H = DEC_H;
     a.scale = 0.08838834764831845f;   /* 1/sqrt(128) */
+    if (q_bias) {
+        a.q_parts = e->parts;
+        a.q_nparts = ctk_gemv_ksplit(DEC_D, DEC_D);
+        a.q_pstride = (long)e->d.slots * DEC_D;
+        a.q_bias = q_bias;
+    }
+    a.out_frag = e->attf;
     ctk_attn(&a, e->s);
 }
 
@@ -646,52 +659,69 @@ static void step_attention(HipbEngine *e, int l, int cross) {
     void *k, *v;
     if (!cross) {
         self_kv(e, l, &k, &v);
-        attn(e, e->att, e->q, k, v, (long)DEC_H * MAX_SEQ * DEC_DK, (long)MAX_SEQ * DEC_DK,
-             e->d.pos_len, NULL);
+        attn(e, k, v, (long)DEC_H * MAX_SEQ * DEC_DK, (long)MAX_SEQ * DEC_DK, e->d.pos_len, NULL, NULL);
     } else {
         cross_kv(e, l, &k, &v);
-        attn(e, e->att, e->q, k, v, (long)DEC_H * e->d.tmax * DEC_DK, (long)e->d.tmax * DEC_DK,
-             e->d.cross_len, e->d.cross_idx);
+        attn(e, k, v, (long)DEC_H * e->d.tmax * DEC_DK, (long)e->d.tmax * DEC_DK,
+             e->d.cross_len, e->d.cross_idx, DW(e->W.dec[l].ca_qb));
     }
+}
+
+/* Decode GEMM over all slots; CT_GV_PARTIAL outputs go to parts. */
+static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint16_t *bd, int N, int K,
+               int out, int relu, float *Y, long ldy, uint16_t *F) {
+    CtGemv g;
+    memset(&g, 0, sizeof g);
+    g.A = A; g.W = Wd; g.bias = bd;
+    g.M = e->d.slots; g.N = N; g.K = K;
+    g.out = out; g.relu = relu;
+    g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, K) : 1;
+    g.Y = out == CT_GV_PARTIAL ? e->parts : Y;
+    g.ldy = ldy; g.F = F;
+    ctk_gemv(&g, e->s);
 }
 
 static void step_launch(HipbEngine *e) {
     const Weights *W = &e->W;
     const int B = e->d.slots;
     hipStream_t s = e->s;
+    const int ks_o = ctk_gemv_ksplit(DEC_D, DEC_D), ks_ff = ctk_gemv_ksplit(DEC_D, DEC_FF);
     ctk_eng_begin(&e->d, s);
     ctk_embed_ln(e->h, e->d.tok, B, 0, e->d.pos_len, e->d.act, DW(W->etw), DW(W->epw),
                  DW(W->elnw), DW(W->elnb), s);
+    /* each LayerNorm first adds the previous projection's K-slices + bias to h */
+    int np = 0;
+    const uint16_t *pb = NULL;
     for (int l = 0; l < DEC_N; l++) {
         const DLayer *L = &W->dec[l];
         void *ks, *vs;
         self_kv(e, l, &ks, &vs);
-        ctk_layernorm(e->ln, e->h, DW(L->sa_lnw), DW(L->sa_lnb), B, DEC_D, s);
-        CtGemm g;
+        ctk_ln_frag(e->h, e->lnf, e->parts, np, pb, DW(L->sa_lnw), DW(L->sa_lnb), B, s);
+        CtGemv g;
         memset(&g, 0, sizeof g);
-        g.A = e->ln; g.lda = DEC_D;
+        g.A = e->lnf;
         g.W = e->wqkv + (size_t)3 * l * DEC_D * DEC_D; g.bias = e->bqkv + (size_t)3 * l * DEC_D;
-        g.M = B; g.N = 3 * DEC_D; g.K = DEC_D; g.epi = CT_EPI_STORE; g.row_mask = e->d.act;
-        g.nseg = 3; g.seg_w = DEC_D;
-        const int mode = e->esz == 2 ? CT_OUT_HEADS_BF16 : CT_OUT_HEADS_F32;
-        g.seg[0] = (CtSeg){.mode = CT_OUT_DENSE, .base = e->q, .ld = DEC_D};
-        g.seg[1] = (CtSeg){.mode = mode, .base = ks, .rowoff = e->d.kv_rowoff, .hstride = (long)MAX_SEQ * DEC_DK};
-        g.seg[2] = (CtSeg){.mode = mode, .base = vs, .rowoff = e->d.kv_rowoff, .hstride = (long)MAX_SEQ * DEC_DK};
-        ctk_gemm(&g, s);
+        g.M = B; g.N = 3 * DEC_D; g.K = DEC_D; g.ksplit = 1; g.out = CT_GV_QKV;
+        g.Y = e->q; g.ldy = DEC_D;
+        g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)MAX_SEQ * DEC_DK;
+        g.kv_bf16 = e->esz == 2;
+        ctk_gemv(&g, s);
         step_attention(e, l, 0);
-        gemm(e, e->att, B, DEC_D, L->sa_ow, L->sa_ob, e->h, DEC_D, CT_EPI_FMADD, 1.0f, NULL);
+        gv(e, e->attf, DW(L->sa_ow), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
 
-        ctk_layernorm(e->ln, e->h, DW(L->ca_lnw), DW(L->ca_lnb), B, DEC_D, s);
-        gemm(e, e->ln, B, DEC_D, L->ca_qw, L->ca_qb, e->q, DEC_D, CT_EPI_STORE, 0, NULL);
+        ctk_ln_frag(e->h, e->lnf, e->parts, ks_o, DW(L->sa_ob), DW(L->ca_lnw), DW(L->ca_lnb), B, s);
+        gv(e, e->lnf, DW(L->ca_qw), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
         step_attention(e, l, 1);
-        gemm(e, e->att, B, DEC_D, L->ca_ow, L->ca_ob, e->h, DEC_D, CT_EPI_FMADD, 1.0f, NULL);
+        gv(e, e->attf, DW(L->ca_ow), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
 
-        ctk_layernorm(e->ln, e->h, DW(L->ffn_lnw), DW(L->ffn_lnb), B, DEC_D, s);
-        gemm(e, e->ln, B, DEC_D, L->ffn_w1, L->ffn_b1, e->mid, DEC_FF, CT_EPI_RELU, 0, NULL);
-        gemm(e, e->mid, B, DEC_FF, L->ffn_w2, L->ffn_b2, e->h, DEC_D, CT_EPI_FMADD, 1.0f, NULL);
+        ctk_ln_frag(e->h, e->lnf, e->parts, ks_o, DW(L->ca_ob), DW(L->ffn_lnw), DW(L->ffn_lnb), B, s);
+        gv(e, e->lnf, DW(L->ffn_w1), DW(L->ffn_b1), DEC_FF, DEC_D, CT_GV_FRAG, 1, NULL, 0, e->midf);
+        gv(e, e->midf, DW(L->ffn_w2), NULL, DEC_D, DEC_FF, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        np = ks_ff;
+        pb = DW(L->ffn_b2);
     }
-    ctk_layernorm(e->ln, e->h, DW(W->dlnw), DW(W->dlnb), B, DEC_D, s);
-    gemm(e, e->ln, B, DEC_D, W->etw, W->hdb, e->logits, VOCAB, CT_EPI_STORE, 0, NULL);
+    ctk_ln_frag(e->h, e->lnf, e->parts, np, pb, DW(W->dlnw), DW(W->dlnb), B, s);
+    gv(e, e->lnf, DW(W->etw), DW(W->hdb), VOCAB, DEC_D, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);
     ctk_eng_end(&e->d, e->logits, s);
 }
 

@@ -36,21 +36,48 @@ __device__ __forceinline__ void load8(const void *base, long off, float (&v)[8])
     }
 }
 
+// Output element col of row bq (= b*T_q + qi): plain fp32 at out[off], or
+// split hi/lo into the frag layout the next decode GEMM reads.
+__device__ __forceinline__ void store_out(const CtAttn &a, int bq, int col, long off, float v) {
+    if (a.out_frag) {
+        uint16_t hh, ll;
+        split_bf16(v, hh, ll);
+        const long o = ct_frag_off(bq, col, a.H * DEC_DK);
+        a.out_frag[o] = hh;
+        a.out_frag[o + 512] = ll;
+    } else {
+        a.out[off] = v;
+    }
+}
+
 template <bool BF16, bool VEC>
 __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
     const int bq = blockIdx.x, h = blockIdx.y;
     const int b = bq / a.T_q, qi = bq % a.T_q;
     const int T = a.lens ? a.lens[(long)b * a.lens_step] : a.len_const;
     const int tid = threadIdx.x, g = tid >> 4, l16 = tid & 15;
-    float *out = a.out + (long)b * a.q_sb + (long)qi * a.q_st + h * DEC_DK;
+    const long qoff = (long)b * a.q_sb + (long)qi * a.q_st + h * DEC_DK;
     if (T <= 0) {
-        if (tid < DEC_DK) out[tid] = 0.0f;
+        if (tid < DEC_DK) store_out(a, bq, h * DEC_DK + tid, qoff + tid, 0.0f);
         return;
     }
-    const float *qp = a.Q + (long)b * a.q_sb + (long)qi * a.q_st + h * DEC_DK + l16 * 8;
     float q[8];
+    if (a.q_parts) {
+        // query = ((part 0 + part 1) + ...) + bias, the decode GEMM's K-slices
+        const float *qp = a.q_parts + qoff + l16 * 8;
 #pragma unroll
-    for (int i = 0; i < 8; i++) q[i] = qp[i];
+        for (int i = 0; i < 8; i++) q[i] = qp[i];
+        for (int p = 1; p < a.q_nparts; p++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) q[i] += qp[p * a.q_pstride + i];
+        if (a.q_bias)
+#pragma unroll
+            for (int i = 0; i < 8; i++) q[i] += bf2f(a.q_bias[h * DEC_DK + l16 * 8 + i]);
+    } else {
+        const float *qp = a.Q + qoff + l16 * 8;
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = qp[i];
+    }
     const float *mrow = a.mask ? a.mask + (long)qi * T : nullptr;
     const long item = a.kv_index ? (long)a.kv_index[b] : (long)b;
     const long base = item * a.kv_sb + (long)h * a.kv_sh + l16 * 8;
@@ -114,7 +141,7 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
             num += w * so[j][tid];
             den += w * sl[j];
         }
-        out[tid] = num / den;
+        store_out(a, bq, h * DEC_DK + tid, qoff + tid, num / den);
     }
 }
 

@@ -1,0 +1,165 @@
+// k_gemv.hip — the decode step's GEMMs: one row per KV slot (M <= a few
+// hundred), weights streamed once per step.
+//
+// Activations arrive pre-split (hi + lo bf16) in frag layout, so every load
+// a lane issues is one contiguous 16-byte piece of a 1-KB run: no strided row
+// reads, no split arithmetic in the GEMM.  A workgroup of 8 wavefronts owns
+// 16*CB output columns, one 64-row block and one K-slice of 256*SPW columns;
+// wavefront w takes K-steps w, w+8, ... of the slice and issues all of its
+// loads before the first MFMA.  The 8 wave tiles are summed in LDS in wave
+// order.  With ksplit > 1 the slice sums are written as partial rows and the
+// consumer (the next LayerNorm, or the attention's query load) adds them in
+// slice order.  The split is a function of (N, K) only, so a row's bits never
+// depend on how many rows the step has.
+//
+// Semantics per output: backends/cpu/backend.c:124-182 (y = x W^T + b, ReLU,
+// fmadd), with x = hi + lo exactly representable to 2^-17 relative.
+#include "ct_dev.h"
+#include "ct_launch.h"
+#include "../../include/model_types.h"
+#include <stdio.h>
+#include <stdlib.h>
+
+namespace {
+
+constexpr int GV_WAVES = 8;
+
+template <int CB, int SPW>
+__global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int r = lane & 15, kg = lane >> 4;
+    const int c0 = blockIdx.x * 16 * CB, ks = blockIdx.y, z = blockIdx.z, m0 = z * 64;
+    const int nsteps = g.K >> 5;
+    const int s0 = ks * (GV_WAVES * SPW);
+    const int nrb = min(4, (g.M - m0 + 15) >> 4);
+    const uint16_t *ablk = g.A + ((long)z * nsteps << 12);
+    u16x8 ah[SPW][4], al[SPW][4], wv[SPW][CB];
+#pragma unroll
+    for (int j = 0; j < SPW; j++) {
+        const int st = s0 + w + GV_WAVES * j;
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            if (rb < nrb) {
+                const uint16_t *p = ablk + ((long)(st * 4 + rb) << 10) + lane * 8;
+                ah[j][rb] = *reinterpret_cast<const u16x8 *>(p);
+                al[j][rb] = *reinterpret_cast<const u16x8 *>(p + 512);
+            } else {
+                ah[j][rb] = al[j][rb] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+            wv[j][cb] = *reinterpret_cast<const u16x8 *>(g.W + (long)(c0 + cb * 16 + r) * g.K + st * 32 + kg * 8);
+    }
+    f32x4 acc[4][CB];
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) acc[rb][cb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < SPW; j++)
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            if (rb >= nrb) break;
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++) {
+                const bf16x8 b = as_bf16x8(wv[j][cb]);
+                acc[rb][cb] = mfma16(as_bf16x8(ah[j][rb]), b, acc[rb][cb]);
+                acc[rb][cb] = mfma16(as_bf16x8(al[j][rb]), b, acc[rb][cb]);
+            }
+        }
+    __shared__ float part[GV_WAVES][64][16 * CB + 1];
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) part[w][rb * 16 + kg * 4 + j][cb * 16 + r] = acc[rb][cb][j];
+    __syncthreads();
+
+    if (g.out == CT_GV_FRAG) {
+        // one thread per (row, 8 consecutive columns): a 16-byte piece per plane
+        for (int e = tid; e < 64 * 2 * CB; e += 64 * GV_WAVES) {
+            const int row = e / (2 * CB), grp = e % (2 * CB), m = m0 + row;
+            if (m >= g.M) continue;
+            u16x8 hv, lv;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int cc = grp * 8 + i;
+                float s = part[0][row][cc];
+#pragma unroll
+                for (int ww = 1; ww < GV_WAVES; ww++) s += part[ww][row][cc];
+                if (g.bias) s += bf2f(g.bias[c0 + cc]);
+                if (g.relu) s = s > 0.0f ? s : 0.0f;
+                uint16_t hh, ll;
+                split_bf16(s, hh, ll);
+                hv[i] = hh; lv[i] = ll;
+            }
+            const long o = ct_frag_off(m, c0 + grp * 8, g.N);
+            *reinterpret_cast<u16x8 *>(g.F + o) = hv;
+            *reinterpret_cast<u16x8 *>(g.F + o + 512) = lv;
+        }
+        return;
+    }
+    for (int e = tid; e < 64 * 16 * CB; e += 64 * GV_WAVES) {
+        const int row = e / (16 * CB), cc = e % (16 * CB), m = m0 + row, col = c0 + cc;
+        if (m >= g.M) continue;
+        float s = part[0][row][cc];
+#pragma unroll
+        for (int ww = 1; ww < GV_WAVES; ww++) s += part[ww][row][cc];
+        if (g.out == CT_GV_PARTIAL) {
+            g.Y[((long)ks * g.M + m) * g.N + col] = s;
+            continue;
+        }
+        if (g.bias) s += bf2f(g.bias[col]);
+        if (g.relu) s = s > 0.0f ? s : 0.0f;
+        if (g.out == CT_GV_DENSE || col < DEC_D) {
+            g.Y[(long)m * g.ldy + col] = s;
+            continue;
+        }
+        const long ro = g.rowoff[m];
+        if (ro < 0) continue;
+        const int seg = col / DEC_D, c = col - seg * DEC_D;
+        const long off = ro + (long)(c >> 7) * g.hstride + (c & 127);
+        void *base = seg == 1 ? g.kc : g.vc;
+        if (g.kv_bf16) reinterpret_cast<uint16_t *>(base)[off] = f2bf(s);
+        else reinterpret_cast<float *>(base)[off] = s;
+    }
+}
+
+[[noreturn]] void gv_fatal(const char *msg, const CtGemv *g) {
+    fprintf(stderr, "ctk_gemv: %s (M=%d N=%d K=%d ksplit=%d out=%d)\n", msg, g->M, g->N, g->K,
+            g->ksplit, g->out);
+    exit(1);
+}
+
+}  // namespace
+
+extern "C" int ctk_gemv_ksplit(int N, int K) {
+    if (N <= DEC_D && K == DEC_D) return 4;       // 256-column slices, one K-step per wave
+    if (N <= DEC_D && K == DEC_FF) return 8;      // 512-column slices
+    return 1;
+}
+
+extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
+    if (g->M <= 0) return;
+    const int ksplit = g->ksplit < 1 ? 1 : g->ksplit;
+    if (g->K % (256 * ksplit) != 0 || g->N % 16 != 0) gv_fatal("unsupported shape", g);
+    if (ksplit > 1 && g->out != CT_GV_PARTIAL) gv_fatal("a K split needs partial output", g);
+    if (g->out == CT_GV_QKV && g->N != 3 * DEC_D) gv_fatal("QKV output needs N = 3*DEC_D", g);
+    if (((uintptr_t)g->A & 15) || ((uintptr_t)g->W & 15) ||
+        (g->out == CT_GV_FRAG && ((uintptr_t)g->F & 15)))
+        gv_fatal("operands must be 16-byte aligned", g);
+    const int spw = g->K / ksplit / 256;
+    const int cb = (g->N >= 8192 && g->N % 64 == 0) ? 4 : 1;
+    const dim3 grid(g->N / (16 * cb), ksplit, (g->M + 63) / 64);
+    const dim3 block(64 * GV_WAVES);
+#define GV_CASE(CB, SPW)                                                          \
+    if (cb == CB && spw == SPW) {                                                 \
+        hipLaunchKernelGGL((gemv_kernel<CB, SPW>), grid, block, 0, s, *g);        \
+        return;                                                                   \
+    }
+    GV_CASE(1, 1) GV_CASE(1, 2) GV_CASE(1, 4) GV_CASE(4, 1) GV_CASE(4, 2) GV_CASE(4, 4)
+#undef GV_CASE
+    gv_fatal("no kernel for this K slice", g);
+}

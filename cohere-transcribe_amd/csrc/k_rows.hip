@@ -231,6 +231,76 @@ __global__ void inc_kernel(int *p) {
     if (threadIdx.x == 0) *p += 1;
 }
 
+// Decoder residual update + LayerNorm into frag layout (D = DEC_D), one wave
+// per row: h += ((parts[0] + parts[1]) + ...) + pbias (the K-slice sums of
+// the previous projection, added in slice order, then its bias), then the
+// two-pass LayerNorm of layernorm_vec_kernel, each output split hi/lo and
+// stored where the decode GEMM's lanes read it.
+__global__ __launch_bounds__(256) void ln_frag_kernel(float *h, uint16_t *frag, const float *parts,
+                                                      int nparts, long pstride, const uint16_t *pbias,
+                                                      const uint16_t *w, const uint16_t *b, int M) {
+    constexpr int V = 4, D = 256 * V;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    float4 *x = reinterpret_cast<float4 *>(h + (long)row * D);
+    float4 v[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) v[i] = x[lane + 64 * i];
+    if (nparts > 0) {
+        float4 a[V];
+        const float4 *p0 = reinterpret_cast<const float4 *>(parts + (long)row * D);
+#pragma unroll
+        for (int i = 0; i < V; i++) a[i] = p0[lane + 64 * i];
+        for (int p = 1; p < nparts; p++) {
+            const float4 *pp = reinterpret_cast<const float4 *>(parts + p * pstride + (long)row * D);
+#pragma unroll
+            for (int i = 0; i < V; i++) {
+                const float4 t = pp[lane + 64 * i];
+                a[i].x += t.x; a[i].y += t.y; a[i].z += t.z; a[i].w += t.w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < V; i++) {
+            const int d0 = 4 * (lane + 64 * i);
+            if (pbias) {
+                a[i].x += bf2f(pbias[d0]); a[i].y += bf2f(pbias[d0 + 1]);
+                a[i].z += bf2f(pbias[d0 + 2]); a[i].w += bf2f(pbias[d0 + 3]);
+            }
+            v[i].x += a[i].x; v[i].y += a[i].y; v[i].z += a[i].z; v[i].w += a[i].w;
+            x[lane + 64 * i] = v[i];
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    const float mu = wave_sum(s) / (float)D;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const float a = v[i].x - mu, bb = v[i].y - mu, c = v[i].z - mu, d = v[i].w - mu;
+        q += (a * a + bb * bb) + (c * c + d * d);
+    }
+    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int d0 = 4 * (lane + 64 * i);
+        const float o[4] = {(v[i].x - mu) * rs * bf2f(w[d0]) + bf2f(b[d0]),
+                            (v[i].y - mu) * rs * bf2f(w[d0 + 1]) + bf2f(b[d0 + 1]),
+                            (v[i].z - mu) * rs * bf2f(w[d0 + 2]) + bf2f(b[d0 + 2]),
+                            (v[i].w - mu) * rs * bf2f(w[d0 + 3]) + bf2f(b[d0 + 3])};
+        ushort4 h4, l4;
+        uint16_t hh[4], ll[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) split_bf16(o[j], hh[j], ll[j]);
+        h4.x = hh[0]; h4.y = hh[1]; h4.z = hh[2]; h4.w = hh[3];
+        l4.x = ll[0]; l4.y = ll[1]; l4.z = ll[2]; l4.w = ll[3];
+        const long off = ct_frag_off(row, d0, D);
+        *reinterpret_cast<ushort4 *>(frag + off) = h4;
+        *reinterpret_cast<ushort4 *>(frag + off + 512) = l4;
+    }
+}
+
 }  // namespace
 
 extern "C" void ctk_layernorm(float *dst, const float *src, const uint16_t *w, const uint16_t *b,
@@ -258,6 +328,18 @@ extern "C" void ctk_layernorm_split(uint16_t *hi, uint16_t *lo, const float *src
         hipLaunchKernelGGL(layernorm_split_kernel<4>, dim3((T + 3) / 4), dim3(256), 0, s, hi, lo, src, w, b, T);
     else
         hipLaunchKernelGGL(layernorm_split_kernel<5>, dim3((T + 3) / 4), dim3(256), 0, s, hi, lo, src, w, b, T);
+}
+
+extern "C" void ctk_ln_frag(float *h, uint16_t *frag, const float *parts, int nparts,
+                            const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,
+                            hipStream_t s) {
+    if (M <= 0) return;
+    if ((uintptr_t)h % 16 || (uintptr_t)frag % 16 || (nparts > 0 && (uintptr_t)parts % 16)) {
+        fprintf(stderr, "ctk_ln_frag: needs 16-byte aligned buffers\n");
+        exit(1);
+    }
+    hipLaunchKernelGGL(ln_frag_kernel, dim3((M + 3) / 4), dim3(256), 0, s, h, frag, parts, nparts,
+                       (long)M * DEC_D, pbias, w, b, M);
 }
 
 extern "C" void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, const int *pos_len,
