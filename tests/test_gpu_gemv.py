@@ -1,0 +1,277 @@
+"""GPU checks of the decode step's GEMM (ctk_gemv) and residual LayerNorm
+(ctk_ln_frag), called through libct_hip.so's C entry points.
+
+The activations are given directly as (hi, lo) bf16 pairs in the frag layout,
+so the exact operand is x = hi + lo and the float64 product x W^T is the
+reference; fp32 accumulation over K <= 4096 terms stays within 1e-5 of it
+(relative to the largest output).  Each row's result must not depend on how
+many rows the launch has, or where the row sits: bit-exact.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import ctbind as cb
+import kernel_suite as ks
+
+pytestmark = pytest.mark.gpu
+
+PARTIAL, DENSE, FRAG, QKV = 0, 1, 2, 3
+TOL = 1e-5
+
+
+class CtGemv(C.Structure):
+    _fields_ = [("A", C.c_void_p), ("W", C.c_void_p), ("bias", C.c_void_p),
+                ("M", C.c_int), ("N", C.c_int), ("K", C.c_int), ("ksplit", C.c_int),
+                ("out", C.c_int), ("relu", C.c_int),
+                ("Y", C.c_void_p), ("ldy", C.c_long), ("F", C.c_void_p),
+                ("kc", C.c_void_p), ("vc", C.c_void_p), ("rowoff", C.c_void_p),
+                ("hstride", C.c_long), ("kv_bf16", C.c_int)]
+
+
+def frag_index(M, K):
+    """uint16 offset of the hi plane of element (m, k) of an [M][K] frag
+    buffer: rows in 64-row blocks, K-steps of 32, 16-row groups of 1024
+    entries (hi plane then lo plane), lane 16*(k%32//8) + m%16, 8 entries per
+    lane."""
+    m = np.arange(M)[:, None]
+    k = np.arange(K)[None, :]
+    grp = ((m >> 6) * (K >> 5) + (k >> 5)) * 4 + ((m >> 4) & 3)
+    lane = (((k >> 3) & 3) << 4) + (m & 15)
+    return (grp << 10) + (lane << 3) + (k & 7)
+
+
+def frag_elems(M, K):
+    return (M + 63) // 64 * 64 * K * 2
+
+
+def to_frag(hi, lo):
+    M, K = hi.shape
+    buf = np.zeros(frag_elems(M, K), np.uint16)
+    idx = frag_index(M, K)
+    buf[idx] = hi
+    buf[idx + 512] = lo
+    return buf
+
+
+def from_frag(buf, M, K):
+    idx = frag_index(M, K)
+    return buf[idx], buf[idx + 512]
+
+
+def bf16_to_f32(u):
+    return (np.asarray(u, np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x):
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = u + 0x7FFF + ((u >> 16) & 1)
+    return (u >> 16).astype(np.uint16)
+
+
+def split(x):
+    hi = f32_to_bf16(x)
+    lo = f32_to_bf16(np.asarray(x, np.float32) - bf16_to_f32(hi))
+    return hi, lo
+
+
+@pytest.fixture(scope="module")
+def lib(hip):
+    L = C.CDLL(cb.HIP_LIB)
+    L.ctk_gemv.argtypes = [C.POINTER(CtGemv), C.c_void_p]
+    L.ctk_gemv_ksplit.argtypes = [C.c_int, C.c_int]
+    L.ctk_gemv_ksplit.restype = C.c_int
+    L.ctk_ln_frag.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                              C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
+    return L
+
+
+class Dev:
+    """Arena-backed device buffers of raw bytes."""
+
+    def __init__(self, hip):
+        self.hip = hip
+        self.ar = ks.ArenaDev(hip, floats=1 << 25)
+        self.ev = cb.HipEvents()
+
+    def put(self, a):
+        a = np.ascontiguousarray(a)
+        f = a.view(np.uint8)
+        pad = (-f.size) % 4
+        f = np.concatenate([f, np.zeros(pad, np.uint8)]) if pad else f
+        return self.ar.put(f.view(np.float32))[0]
+
+    def zeros(self, nbytes):
+        return self.put(np.zeros(nbytes, np.uint8))
+
+    def get(self, p, dtype, n):
+        self.ev.sync()
+        nb = np.dtype(dtype).itemsize * n
+        out = np.empty((nb + 3) // 4, np.float32)
+        self.hip.backend_dtoh(out.ctypes.data, p, out.nbytes)   # bytes (backend.h:46)
+        return out.view(np.uint8)[:nb].view(dtype).copy()
+
+
+def run_gemv(lib, dev, A_f32, pw, N, pb, out, relu=0, ksplit=1):
+    """pw / pb: device pointers of the bf16 weight [N][K] and bias (or None)."""
+    M, K = A_f32.shape
+    hi, lo = split(A_f32)
+    pa = dev.put(to_frag(hi, lo))
+    g = CtGemv(A=pa, W=pw, bias=pb, M=M, N=N, K=K, ksplit=ksplit, out=out, relu=relu)
+    if out == PARTIAL:
+        g.Y = dev.zeros(ksplit * M * N * 4)
+    elif out == DENSE:
+        g.Y = dev.zeros(M * N * 4)
+        g.ldy = N
+    elif out == FRAG:
+        g.F = dev.zeros(frag_elems(M, N) * 2)
+    dev.ev.sync()
+    lib.ctk_gemv(C.byref(g), None)
+    if out == PARTIAL:
+        return dev.get(g.Y, np.float32, ksplit * M * N).reshape(ksplit, M, N)
+    if out == DENSE:
+        return dev.get(g.Y, np.float32, M * N).reshape(M, N)
+    buf = dev.get(g.F, np.uint16, frag_elems(M, N))
+    h, l = from_frag(buf, M, N)
+    return h, l
+
+
+def exact_ref(A_f32, W_bf, bias_bf):
+    hi, lo = split(A_f32)
+    x = bf16_to_f32(hi).astype(np.float64) + bf16_to_f32(lo)
+    y = x @ bf16_to_f32(W_bf).astype(np.float64).T
+    if bias_bf is not None:
+        y = y + bf16_to_f32(bias_bf)
+    return y
+
+
+def rel(a, b):
+    return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+SHAPES = [(1024, 1024), (1024, 4096), (4096, 1024), (16384, 1024)]
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+def test_gemv_matches_float64(lib, hip, N, K):
+    dev = Dev(hip)
+    rng = np.random.default_rng(N + K)
+    W = f32_to_bf16(rng.standard_normal((N, K)).astype(np.float32) * 0.03)
+    b = f32_to_bf16(rng.standard_normal(N).astype(np.float32) * 0.1)
+    pw, pb = dev.put(W), dev.put(b)
+    ksplit = lib.ctk_gemv_ksplit(N, K)
+    for M in (1, 5, 64, 70, 130):
+        print(f"case: gemv N={N} K={K} M={M} ksplit={ksplit}", flush=True)
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        ref = exact_ref(A, W, b)
+        tol = TOL
+        if ksplit > 1:
+            parts = run_gemv(lib, dev, A, pw, N, None, PARTIAL, ksplit=ksplit)
+            got = parts.astype(np.float64).sum(0) + bf16_to_f32(b)
+        elif N >= 8192:
+            got = run_gemv(lib, dev, A, pw, N, pb, DENSE)
+        else:
+            h, l = run_gemv(lib, dev, A, pw, N, pb, FRAG, relu=1)
+            ref = np.maximum(ref, 0.0)
+            got = bf16_to_f32(h).astype(np.float64) + bf16_to_f32(l)
+            tol = 2e-5          # plus the hi/lo split of the output (2^-17)
+        e = rel(got, ref)
+        print(f"  relerr {e:.2e}")
+        assert e <= tol, (M, e)
+
+
+@pytest.mark.parametrize("N,K", [(1024, 1024), (4096, 1024), (16384, 1024)])
+def test_gemv_rows_independent_of_batch(lib, hip, N, K):
+    """Row r of a 130-row launch equals the same row launched alone, bit for bit."""
+    dev = Dev(hip)
+    rng = np.random.default_rng(7)
+    W = f32_to_bf16(rng.standard_normal((N, K)).astype(np.float32) * 0.03)
+    b = f32_to_bf16(rng.standard_normal(N).astype(np.float32) * 0.1)
+    A = rng.standard_normal((130, K)).astype(np.float32)
+    ksplit = lib.ctk_gemv_ksplit(N, K)
+    out = PARTIAL if ksplit > 1 else DENSE
+    pw = dev.put(W)
+    pb = dev.put(b) if out == DENSE else None
+    full = run_gemv(lib, dev, A, pw, N, pb, out, ksplit=ksplit)
+    for r in (0, 17, 63, 64, 129):
+        print(f"case: gemv row {r} alone N={N} K={K}", flush=True)
+        one = run_gemv(lib, dev, A[r:r + 1], pw, N, pb, out, ksplit=ksplit)
+        if out == PARTIAL:
+            assert np.array_equal(full[:, r].view(np.uint32), one[:, 0].view(np.uint32))
+        else:
+            assert np.array_equal(full[r].view(np.uint32), one[0].view(np.uint32))
+
+
+def test_gemv_qkv_scatter(lib, hip):
+    """QKV output: query rows dense, key/value rows into head-major caches at
+    rowoff[m] (bf16); rows with rowoff < 0 leave the caches untouched."""
+    dev = Dev(hip)
+    rng = np.random.default_rng(3)
+    M, K, N = 6, 1024, 3072
+    smax = 16
+    W = f32_to_bf16(rng.standard_normal((N, K)).astype(np.float32) * 0.03)
+    b = f32_to_bf16(rng.standard_normal(N).astype(np.float32) * 0.1)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    hi, lo = split(A)
+    cache_el = M * 8 * smax * 128
+    sentinel = np.full(cache_el, 0x3F80, np.uint16)      # 1.0 in bf16
+    kc, vc = dev.put(sentinel), dev.put(sentinel)
+    pos = np.array([3, -1, 0, 15, -1, 7])
+    rowoff = np.where(pos >= 0, (np.arange(M) * 8 * smax + pos) * 128, -1).astype(np.int64)
+    g = CtGemv(A=dev.put(to_frag(hi, lo)), W=dev.put(W), bias=dev.put(b), M=M, N=N, K=K, ksplit=1,
+               out=QKV, relu=0, Y=dev.zeros(M * 1024 * 4), ldy=1024, kc=kc, vc=vc,
+               rowoff=dev.put(rowoff), hstride=smax * 128, kv_bf16=1)
+    dev.ev.sync()
+    lib.ctk_gemv(C.byref(g), None)
+    q = dev.get(g.Y, np.float32, M * 1024).reshape(M, 1024)
+    kk = dev.get(kc, np.uint16, cache_el).reshape(M, 8, smax, 128)
+    vv = dev.get(vc, np.uint16, cache_el).reshape(M, 8, smax, 128)
+    ref = exact_ref(A, W, b)
+    assert rel(q, ref[:, :1024]) <= TOL
+    for m in range(M):
+        for name, cache, lo_c in (("k", kk, 1024), ("v", vv, 2048)):
+            if pos[m] < 0:
+                assert np.all(cache[m] == 0x3F80), (name, m)
+                continue
+            got = bf16_to_f32(cache[m, :, pos[m], :]).reshape(1024)
+            want = ref[m, lo_c:lo_c + 1024]
+            assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6, (name, m)
+            others = np.delete(cache[m], pos[m], axis=1)
+            assert np.all(others == 0x3F80), (name, m)
+
+
+def test_ln_frag(lib, hip):
+    """h += ((p0 + p1) + ...) + bias in that order, then LayerNorm (two-pass
+    mean / variance, eps 1e-5, backends/cpu/backend.c:109-122) split into frag."""
+    dev = Dev(hip)
+    rng = np.random.default_rng(5)
+    D = 1024
+    for M, nparts in ((1, 0), (64, 4), (70, 8)):
+        print(f"case: ln_frag M={M} nparts={nparts}", flush=True)
+        h = rng.standard_normal((M, D)).astype(np.float32)
+        parts = rng.standard_normal((max(nparts, 1), M, D)).astype(np.float32)
+        pb = f32_to_bf16(rng.standard_normal(D).astype(np.float32) * 0.1)
+        w = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32))
+        bb = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
+        ph = dev.put(h)
+        pf = dev.zeros(frag_elems(M, D) * 2)
+        pp = dev.put(parts)
+        dev.ev.sync()
+        lib.ctk_ln_frag(ph, pf, pp, nparts, dev.put(pb), dev.put(w), dev.put(bb), M, None)
+        h_new = dev.get(ph, np.float32, M * D).reshape(M, D)
+        if nparts:
+            acc = parts[0].copy()
+            for p in range(1, nparts):
+                acc = acc + parts[p]
+            want_h = h + (acc + bf16_to_f32(pb))
+            assert np.array_equal(h_new.view(np.uint32), want_h.astype(np.float32).view(np.uint32))
+        else:
+            assert np.array_equal(h_new, h)
+        x = h_new.astype(np.float64)
+        mu = x.mean(1, keepdims=True)
+        var = ((x - mu) ** 2).mean(1, keepdims=True)
+        ref = (x - mu) / np.sqrt(var + 1e-5) * bf16_to_f32(w) + bf16_to_f32(bb)
+        hi, lo = from_frag(dev.get(pf, np.uint16, frag_elems(M, D)), M, D)
+        got = bf16_to_f32(hi).astype(np.float64) + bf16_to_f32(lo)
+        assert rel(got, ref) <= 1e-5
