@@ -12,19 +12,29 @@ finished.  value = audio seconds transcribed per wall second (RTFx).
 Random-init weights at the model's dimensions (seeded, the converter's
 safetensors layout), seeded synthetic audio; nothing is downloaded.
 
-Also reported, measured live with HIP events on the engine's stream:
-  roofline           the decode-attention kernel (self + cross, bf16 KV) at
-                     the 128-slot ragged microbench shape (S ~ U(1,448),
-                     T_enc ~ U(25,375)): algorithmic K+V bytes per launch /
-                     average launch time, against 8 TB/s;
-  roofline_gemm      the encoder FFN GEMM (M = 16384 packed frames,
-                     1280 -> 5120): 2*M*N*K per launch / time, against the
-                     bf16 dense MFMA peak;
-  cpu_baseline       the oracle (fp32 C restatement of the reference CPU
-                     backend) on the host's cores on a bounded sample,
-                     extrapolated to this workload's audio/token mix.
+Also reported, measured live with HIP events on the engine's stream, each
+for one kernel family at a fixed shape (launched on its own, so a profiler's
+per-kernel averages of `bench.py --roofline-only` can be set beside them):
+  rooflines.attention     decode attention (self + cross, bf16 KV) at the
+                          128-slot ragged microbench shape (S ~ U(1,448),
+                          T_enc ~ U(25,375)): algorithmic K+V bytes per
+                          launch / average launch time, against 8 TB/s;
+  rooflines.decode_gemm   the 49 decode GEMMs of one step at the stream's 64
+                          slots: weight + activation-in + output bytes per
+                          launch / average launch time, against 8 TB/s;
+  rooflines.encoder_gemm  the packed encoder's FFN up-projection (M = 16384
+                          frames, 1280 -> 5120): 2*M*N*K per launch / time,
+                          against the bf16 dense MFMA peak;
+  roofline                the one of them whose kernels take the largest
+                          share of the stream's GPU time;
+  cpu_baseline            the oracle (fp32 C restatement of the reference CPU
+                          backend) on the host's cores on a bounded sample,
+                          extrapolated to this workload's audio/token mix.
+HBM traffic per launch (`traffic`) comes from rocprofv3 FETCH_SIZE and
+WRITE_SIZE counter runs recorded in profiles/traffic.json, when present.
 """
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -37,6 +47,10 @@ sys.path.insert(0, os.path.join(REPO, "cohere-transcribe_amd"))
 import ctbind as cb  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
+# The kernel family with the largest share of the stream's GPU time (from the
+# eager rocprofv3 profile of the stream).
+DOMINANT = "encoder_gemm"
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "audio-sec/sec (RTFx) + decode tokens/s at ragged batch 64; % HBM/MFMA peak"
 
@@ -69,13 +83,15 @@ def run_stream(hip, eng, ev, dev_pcm, offs, samples, limits):
     return t2 - t0, t2 - t1, steps
 
 
-def attention_roofline(hip, model, ev, reps=20):
-    """Decode-attention kernel at the 128-slot microbench shape."""
+def attention_roofline(hip, model, ev, reps=20, step_reps=0):
+    """Decode-attention kernel at the 128-slot microbench shape; with
+    step_reps > 0 also the whole decode step at that shape (eager steps)."""
     rng = np.random.default_rng(4)
     B = 128
     S = rng.integers(1, 449, B)
     T = rng.integers(25, 376, B)
     eng = cb.Engine(model, slots=B, max_requests=B, max_frames=376, kv_bf16=True)
+    step_ms = None
     try:
         eng.bench_fill(S, T, seed=9)
         eng.step()                     # sets per-slot lengths (S after append)
@@ -91,54 +107,121 @@ def attention_roofline(hip, model, ev, reps=20):
         S_now = S + 1
         bytes_step = 8 * float(np.sum(2 * (S_now + T) * cb.DEC_D * 2))
         bytes_launch = bytes_step / 16
-        # whole decode step at this shape (graph-free eager steps)
-        a2, b2 = ev.event(), ev.event()
-        ev.record(a2, s)
-        nstep = 5
-        for _ in range(nstep):
-            eng.step()
-        ev.record(b2, s)
-        step_ms = ev.ms(a2, b2) / nstep
+        if step_reps:
+            a2, b2 = ev.event(), ev.event()
+            ev.record(a2, s)
+            for _ in range(step_reps):
+                eng.step()
+            ev.record(b2, s)
+            step_ms = ev.ms(a2, b2) / step_reps
     finally:
         eng.close()
     achieved = bytes_launch / (per_launch_us * 1e-6) / 1e9
+    micro = {"slots": B, "attention_ms_per_step": round(per_launch_us * 16 / 1e3, 3),
+             "attention_GBs": round(bytes_step / (per_launch_us * 16e-6) / 1e9, 1)}
+    if step_ms is not None:
+        micro["step_ms"] = round(step_ms, 3)
     return {
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-        "kernel": "attn_kernel<bf16> (decode self+cross attention)",
+        "kernel": "attn_kernel<true, true> (decode self + cross attention, bf16 KV)",
         "avg_launch_us": round(per_launch_us, 3), "bytes_per_launch": int(bytes_launch),
         "workload": "128 slots, S~U(1,448)+1, T_enc~U(25,375), bf16 KV, 8 layers x (self, cross)",
-    }, {"slots": B, "step_ms": round(step_ms, 3),
-        "attention_ms_per_step": round(per_launch_us * 16 / 1e3, 3),
-        "attention_GBs": round(bytes_step / (per_launch_us * 16e-6) / 1e9, 1)}
+    }, micro
 
 
-def gemm_roofline(hip, model, ev, reps=10):
-    M, K, N = 16384, cb.ENC_D, cb.ENC_FF
-    base = hip.backend_arena_alloc(M * K + M * N)
-    x = np.random.default_rng(5).standard_normal((M, K)).astype(np.float32)
-    hip.backend_htod(base, x.ctypes.data, x.size)
-    y = base + M * K * 4
-    w, b = model.ptr("enc0.ff1_w1"), model.ptr("enc0.ff1_b1")
-    eng_stream = None
-    # the ABI launches on this thread's stream; an engine exposes that stream
-    tmp = cb.Engine(model, slots=1, max_requests=1, max_frames=8, kv_bf16=True)
+DEC_GEMMS = ([(3 * cb.DEC_D, cb.DEC_D), (cb.DEC_D, cb.DEC_D), (cb.DEC_D, cb.DEC_D), (cb.DEC_D, cb.DEC_D),
+              (cb.DEC_FF, cb.DEC_D), (cb.DEC_D, cb.DEC_FF)] * cb.DEC_N + [(cb.VOCAB, cb.DEC_D)])
+
+
+def decode_gemm_roofline(model, ev, slots=64, reps=20):
+    """The decode step's GEMMs alone (8 x QKV, out, cross Q, cross out, FFN up,
+    FFN down; LM head) at the stream's slot count."""
+    rng = np.random.default_rng(6)
+    S = rng.integers(1, 267, slots)
+    T = rng.integers(26, 377, slots)
+    eng = cb.Engine(model, slots=slots, max_requests=slots, max_frames=376, kv_bf16=True)
     try:
-        eng_stream = tmp.stream()
-        hip.backend_linear_silu(y, base, w, b, M, K, N)
-        a, bb = ev.event(), ev.event()
-        ev.record(a, eng_stream)
+        eng.bench_fill(S, T, seed=5)
+        eng.step()
+        s = eng.stream()
+        eng.decode_gemms_only()
+        a, b = ev.event(), ev.event()
+        ev.record(a, s)
         for _ in range(reps):
-            hip.backend_linear_silu(y, base, w, b, M, K, N)
-        ev.record(bb, eng_stream)
-        ms = ev.ms(a, bb) / reps
+            eng.decode_gemms_only()
+        ev.record(b, s)
+        step_us = ev.ms(a, b) * 1e3 / reps
     finally:
-        tmp.close()
+        eng.close()
+    n = len(DEC_GEMMS)
+    # weights once, activations in (fp32-equivalent hi+lo), outputs (fp32)
+    bytes_step = float(sum(N * K * 2 + slots * K * 4 + slots * N * 4 for N, K in DEC_GEMMS))
+    per_launch_us = step_us / n
+    achieved = bytes_step / (step_us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "gemv_kernel (decode GEMMs, all instances)", "avg_launch_us": round(per_launch_us, 3),
+            "bytes_per_launch": int(bytes_step / n), "launches_per_step": n,
+            "workload": f"{slots} slots, one step's 49 GEMMs (268.4 MB of bf16 weights)"}
+
+
+def encoder_gemm_roofline(model, ev, M=16384, reps=10):
+    K, N = cb.ENC_D, cb.ENC_FF
+    eng = cb.Engine(model, slots=1, max_requests=1, max_frames=8, kv_bf16=True)
+    try:
+        s = eng.stream()
+        eng.encoder_gemm(M)
+        a, b = ev.event(), ev.event()
+        ev.record(a, s)
+        for _ in range(reps):
+            eng.encoder_gemm(M)
+        ev.record(b, s)
+        ms = ev.ms(a, b) / reps
+    finally:
+        eng.close()
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     return {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
-            "kernel": "gemm_kernel (encoder FFN up, SiLU epilogue)", "avg_launch_us": round(ms * 1e3, 1),
-            "shape": f"M={M} N={N} K={K}", "note": "fp32 activations as hi+lo bf16: 2 MFMA passes"}
+            "kernel": "gemm_split_kernel<false> (encoder FFN up, SiLU, pre-split in/out)",
+            "avg_launch_us": round(ms * 1e3, 1), "flops_per_launch": 2 * M * N * K,
+            "workload": f"M={M} N={N} K={K}",
+            "note": "activations as hi+lo bf16 against exact bf16 weights: the MFMA pipe runs "
+                    "2x the algorithmic flops counted here"}
+
+
+def copy_calibration(ev, stream, mib=256):
+    """A plain device-to-device copy of known size on the engine stream, the
+    scale for FETCH_SIZE / WRITE_SIZE counter runs."""
+    rt = ev.rt
+    rt.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    rt.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    rt.hipFree.argtypes = [C.c_void_p]
+    n = mib << 20
+    src, dst = C.c_void_p(), C.c_void_p()
+    if rt.hipMalloc(C.byref(src), n) or rt.hipMalloc(C.byref(dst), n):
+        raise RuntimeError("hipMalloc failed")
+    try:
+        for _ in range(3):
+            if rt.hipMemcpyAsync(dst, src, n, 3, stream):
+                raise RuntimeError("hipMemcpyAsync failed")
+        ev.sync()
+    finally:
+        rt.hipFree(src)
+        rt.hipFree(dst)
+    return {"bytes": n}
+
+
+def with_traffic(rooflines):
+    """Fills `traffic` (HBM bytes per launch) from the counter runs."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return rooflines
+    with open(TRAFFIC_FILE) as f:
+        tr = json.load(f)
+    for k, r in rooflines.items():
+        if k in tr.get("per_launch_bytes", {}):
+            r["traffic"] = tr["per_launch_bytes"][k]
+    return rooflines
 
 
 def cpu_baseline(samples, limits):
@@ -174,6 +257,18 @@ def cpu_baseline(samples, limits):
                       "extrapolated to the stream's audio/token mix"}
 
 
+def measure_rooflines(hip, model, ev, step_reps=5):
+    att, micro = attention_roofline(hip, model, ev, step_reps=step_reps)
+    roofs = {"attention": att, "decode_gemm": decode_gemm_roofline(model, ev),
+             "encoder_gemm": encoder_gemm_roofline(model, ev)}
+    tmp = cb.Engine(model, slots=1, max_requests=1, max_frames=8, kv_bf16=True)
+    try:
+        copy_calibration(ev, tmp.stream())
+    finally:
+        tmp.close()
+    return with_traffic(roofs), micro
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -182,6 +277,10 @@ def main():
     ap.add_argument("--requests", type=int, default=256)
     ap.add_argument("--slots", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="run only the per-kernel roofline microbenchmarks (for profiling)")
+    ap.add_argument("--no-rooflines", action="store_true",
+                    help="run only the stream (for profiling its kernel mix)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (requests shard "
@@ -193,6 +292,11 @@ def main():
     hip.backend_weights_upload_blob(model.data_ptr, model.data_bytes)
     hip.backend_init(0)
     ev = cb.HipEvents()
+
+    if args.roofline_only:
+        roofs, micro = measure_rooflines(hip, model, ev, step_reps=0)
+        print(json.dumps({"rooflines": roofs, "decode_microbench": micro}))
+        return
 
     samples, limits = make_stream(args.requests, seed=3)
     offs = np.concatenate([[0], np.cumsum(samples)[:-1]])
@@ -222,8 +326,7 @@ def main():
     gen_tokens = int(np.sum(limits))
     dec_tps = gen_tokens / (float(np.sum(dec_times)) / args.steps)
 
-    roof, micro = attention_roofline(hip, model, ev)
-    roof_gemm = gemm_roofline(hip, model, ev)
+    roofs, micro = ({}, {}) if args.no_rooflines else measure_rooflines(hip, model, ev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(samples, limits)
 
     out = {
@@ -237,7 +340,8 @@ def main():
                    "generated_tokens": gen_tokens, "kv": "bf16", "parallelism": "single GPU"},
         "decode_tokens_per_s": round(dec_tps, 1),
         "decode_steps": int(np.mean(steps)),
-        "roofline": roof, "roofline_gemm": roof_gemm, "decode_microbench": micro,
+        "roofline": dict(roofs[DOMINANT], name=DOMINANT) if roofs else None, "rooflines": roofs,
+        "decode_microbench": micro,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -65,6 +65,7 @@ struct HipbEngine {
     int have_graph;
     int eager;           /* HIPB_EAGER=1: launch steps without a graph */
     int bench_mode;
+    int bench_gemm_M;    /* rows seeded by hipb_bench_encoder_gemm */
     /* log-mel front-end */
     CtMelTables mel_tab;
     float *d_hann, *d_twr, *d_twi, *d_fb;
@@ -681,13 +682,14 @@ static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint1
     ctk_gemv(&g, e->s);
 }
 
-static void step_launch(HipbEngine *e) {
+/* One decode step.  full == 0 launches only its GEMMs (timing support). */
+static void step_kernels(HipbEngine *e, int full) {
     const Weights *W = &e->W;
     const int B = e->d.slots;
     hipStream_t s = e->s;
     const int ks_o = ctk_gemv_ksplit(DEC_D, DEC_D), ks_ff = ctk_gemv_ksplit(DEC_D, DEC_FF);
-    ctk_eng_begin(&e->d, s);
-    ctk_embed_ln(e->h, e->d.tok, B, 0, e->d.pos_len, e->d.act, DW(W->etw), DW(W->epw),
+    if (full) ctk_eng_begin(&e->d, s);
+    if (full) ctk_embed_ln(e->h, e->d.tok, B, 0, e->d.pos_len, e->d.act, DW(W->etw), DW(W->epw),
                  DW(W->elnw), DW(W->elnb), s);
     /* each LayerNorm first adds the previous projection's K-slices + bias to h */
     int np = 0;
@@ -696,7 +698,7 @@ static void step_launch(HipbEngine *e) {
         const DLayer *L = &W->dec[l];
         void *ks, *vs;
         self_kv(e, l, &ks, &vs);
-        ctk_ln_frag(e->h, e->lnf, e->parts, np, pb, DW(L->sa_lnw), DW(L->sa_lnb), B, s);
+        if (full) ctk_ln_frag(e->h, e->lnf, e->parts, np, pb, DW(L->sa_lnw), DW(L->sa_lnb), B, s);
         CtGemv g;
         memset(&g, 0, sizeof g);
         g.A = e->lnf;
@@ -706,24 +708,26 @@ static void step_launch(HipbEngine *e) {
         g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)MAX_SEQ * DEC_DK;
         g.kv_bf16 = e->esz == 2;
         ctk_gemv(&g, s);
-        step_attention(e, l, 0);
+        if (full) step_attention(e, l, 0);
         gv(e, e->attf, DW(L->sa_ow), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
 
-        ctk_ln_frag(e->h, e->lnf, e->parts, ks_o, DW(L->sa_ob), DW(L->ca_lnw), DW(L->ca_lnb), B, s);
+        if (full) ctk_ln_frag(e->h, e->lnf, e->parts, ks_o, DW(L->sa_ob), DW(L->ca_lnw), DW(L->ca_lnb), B, s);
         gv(e, e->lnf, DW(L->ca_qw), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
-        step_attention(e, l, 1);
+        if (full) step_attention(e, l, 1);
         gv(e, e->attf, DW(L->ca_ow), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
 
-        ctk_ln_frag(e->h, e->lnf, e->parts, ks_o, DW(L->ca_ob), DW(L->ffn_lnw), DW(L->ffn_lnb), B, s);
+        if (full) ctk_ln_frag(e->h, e->lnf, e->parts, ks_o, DW(L->ca_ob), DW(L->ffn_lnw), DW(L->ffn_lnb), B, s);
         gv(e, e->lnf, DW(L->ffn_w1), DW(L->ffn_b1), DEC_FF, DEC_D, CT_GV_FRAG, 1, NULL, 0, e->midf);
         gv(e, e->midf, DW(L->ffn_w2), NULL, DEC_D, DEC_FF, CT_GV_PARTIAL, 0, NULL, 0, NULL);
         np = ks_ff;
         pb = DW(L->ffn_b2);
     }
-    ctk_ln_frag(e->h, e->lnf, e->parts, np, pb, DW(W->dlnw), DW(W->dlnb), B, s);
+    if (full) ctk_ln_frag(e->h, e->lnf, e->parts, np, pb, DW(W->dlnw), DW(W->dlnb), B, s);
     gv(e, e->lnf, DW(W->etw), DW(W->hdb), VOCAB, DEC_D, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);
-    ctk_eng_end(&e->d, e->logits, s);
+    if (full) ctk_eng_end(&e->d, e->logits, s);
 }
+
+static void step_launch(HipbEngine *e) { step_kernels(e, 1); }
 
 void hipb_step(HipbEngine *e) { step_launch(e); }
 
@@ -841,6 +845,22 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
     ECHK(hipStreamSynchronize(e->s));
     e->n_enc = B;
     e->bench_mode = 1;
+}
+
+void hipb_bench_decode_gemms(HipbEngine *e) { step_kernels(e, 0); }
+
+void hipb_bench_encoder_gemm(HipbEngine *e, int M) {
+    if (M < 1) CT_FATAL("hipb_bench_encoder_gemm: M < 1");
+    if (M > e->enc_cap || e->bench_gemm_M != M) {
+        enc_reserve(e, M, 8);
+        /* seeded operand, split as the producers write it: hi ~ N(0,1),
+         * lo ~ N(0,1) * 2^-9 */
+        ctk_fill_random(e->eln_h, (long)M * ENC_D, 1, 1.0f, 71, e->s);
+        ctk_fill_random(e->eln_l, (long)M * ENC_D, 1, 1.0f / 512.0f, 72, e->s);
+        e->bench_gemm_M = M;
+    }
+    const ELayer *L = &e->W.enc[0];
+    gemm_sp_silu_split(e, e->eln_h, e->eln_l, M, L->ff1_w1, L->ff1_b1, e->emid_h, e->emid_l);
 }
 
 void hipb_mel(HipbEngine *e, const float *pcm, int n_samples, float *mel_out) {

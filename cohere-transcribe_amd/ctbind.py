@@ -233,6 +233,8 @@ _ENGINE_SIGS = {
     "hipb_req_frames": ([C.c_void_p, C.c_int], C.c_int),
     "hipb_bench_fill": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64], None),
     "hipb_attention_only": ([C.c_void_p], None),
+    "hipb_bench_decode_gemms": ([C.c_void_p], None),
+    "hipb_bench_encoder_gemm": ([C.c_void_p, C.c_int], None),
     "hipb_stream": ([C.c_void_p], C.c_void_p),
 }
 
@@ -303,6 +305,12 @@ class Engine:
 
     def attention_only(self):
         self.L.hipb_attention_only(self.e)
+
+    def decode_gemms_only(self):
+        self.L.hipb_bench_decode_gemms(self.e)
+
+    def encoder_gemm(self, M):
+        self.L.hipb_bench_encoder_gemm(self.e, M)
 
     def stream(self):
         return self.L.hipb_stream(self.e)

@@ -96,6 +96,15 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
 /* Launches only the 16 decode-attention kernels of one step (8 layers x self
  * and cross) on the engine stream, for per-kernel timing. */
 void hipb_attention_only(HipbEngine *e);
+/* Launches only the decode GEMMs of one step (8 layers x QKV, out, cross Q,
+ * cross out, FFN up, FFN down, then the LM head) over the current step
+ * buffers on the engine stream, for per-kernel timing. */
+void hipb_bench_decode_gemms(HipbEngine *e);
+/* Launches the packed encoder's FFN up-projection (layer 0 weights: M frames
+ * x 1280 -> 5120, SiLU, pre-split input and output; the encoder runs this
+ * GEMM twice per layer) once on the engine stream.  The input is seeded when
+ * M changes. */
+void hipb_bench_encoder_gemm(HipbEngine *e, int M);
 /* The engine's HIP stream (hipStream_t), for events and profiling. */
 void *hipb_stream(HipbEngine *e);
 

@@ -116,6 +116,36 @@ def test_engine_batch_vs_single_bitexact(hip, hot, mels):
             assert np.array_equal(ha[0][k].view(np.uint32), hp[i][k].view(np.uint32)), (i, k)
 
 
+@pytest.mark.parametrize("kv_bf16", [False, True])
+def test_engine_logits_match_oracle(hip, hot, mels, kv_bf16):
+    """Logits behind every generated token, engine (4 slots, ragged) vs the
+    oracle's fp32 path: max relative error per row within 1e-2 (measured
+    ~1e-5: split-bf16 activations, fp32 accumulation)."""
+    eng = cb.Engine(hot, slots=4, max_requests=8, max_frames=64, kv_bf16=kv_bf16)
+    try:
+        for i, mel in enumerate(mels):
+            eng.submit(mel, LIMITS[i], FLAGS)
+        eng.encode()
+        hist = run_stepwise(eng, len(mels))
+    finally:
+        eng.close()
+    npr = len(cb.PROMPT)
+    worst = 0.0
+    for i, mel in enumerate(mels):
+        print(f"case: logits of request {i}, kv_bf16={kv_bf16}", flush=True)
+        toks, lg, _ = ob.transcribe(hot, mel, LIMITS[i], suppress=True, force=True, kv_bf16=kv_bf16,
+                                    want_logits=True)
+        # step npr-1+j produced generated token j; the last one is read after
+        # the slot was freed, so it is not in the history
+        n = min(len(hist[i]) - (npr - 1), len(toks))
+        assert n >= len(toks) - 1 >= 1
+        for j in range(n):
+            e = relerr(hist[i][npr - 1 + j], lg[j])
+            worst = max(worst, e)
+            assert e <= 1e-2, (i, j, e)
+    print(f"  worst logits relerr {worst:.2e}")
+
+
 def test_engine_continuous_batching(hip, hot, mels, oracle_runs):
     """Six requests through two slots: freed slots are refilled on device."""
     eng = cb.Engine(hot, slots=2, max_requests=8, max_frames=64, kv_bf16=True)
