@@ -200,6 +200,8 @@ void ctk_sub_dwconv(float *out, const float *in, int H, int Wd,
                     const uint16_t *w, const uint16_t *b, hipStream_t s);
 /* [T][16][256] -> [T][256*16] (channel-major flatten per frame). */
 void ctk_sub_flatten(float *out, const float *in, int T, hipStream_t s);
+/* The same, written as hi/lo bf16 planes (row stride 4096). */
+void ctk_sub_flatten_split(uint16_t *hi, uint16_t *lo, const float *in, int T, hipStream_t s);
 
 /* ---------------- log-mel front-end ---------------- */
 typedef struct {

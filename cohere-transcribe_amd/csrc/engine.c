@@ -530,10 +530,12 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         gemm(e, rb, T2 * 32, SUB_CH, W->s3w, W->s3b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
         ctk_sub_dwconv(rb, ra, T2, 32, DW(W->s5w), DW(W->s5b), s);
         gemm(e, rb, q->T_enc * 16, SUB_CH, W->s6w, W->s6b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
-        ctk_sub_flatten(rb, ra, q->T_enc, s);
-        gemm(e, rb, q->T_enc, SUB_CH * 16, W->sow, W->sob, e->ex + (size_t)seq_off[i] * ENC_D, ENC_D,
-             CT_EPI_STORE, 0, NULL);
+        /* flattened frames of every request go pre-split into packed rows
+         * (the FFN planes are free until layer 0) for one projection GEMM */
+        ctk_sub_flatten_split(e->emid_h + (size_t)seq_off[i] * SUB_CH * 16,
+                              e->emid_l + (size_t)seq_off[i] * SUB_CH * 16, ra, q->T_enc, s);
     }
+    gemm_sp(e, e->emid_h, e->emid_l, M, SUB_CH * 16, W->sow, W->sob, e->ex, ENC_D, CT_EPI_STORE, 0);
     /* relative positions for T_max; each clip reads its shifted window */
     ctk_rel_pos_emb(e->epe, T_max, ct_inv_freq(), s);
     for (int l = 0; l < ENC_N; l++) {
@@ -579,10 +581,11 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
                             e->eh + (size_t)seq_off[i] * DEC_D, (size_t)seq_T[i] * DEC_D * 4,
                             hipMemcpyDeviceToDevice, s));
     const size_t cross_l = (size_t)e->d.max_req * DEC_H * e->d.tmax * DEC_DK;
+    ctk_split(e->eln_h, e->eln_l, e->eh, (long)M * DEC_D, s);   /* LN planes are free now */
     for (int l = 0; l < DEC_N; l++) {
         CtGemm g;
         memset(&g, 0, sizeof g);
-        g.A = e->eh; g.lda = DEC_D;
+        g.Ahi = e->eln_h; g.Alo = e->eln_l; g.lda = DEC_D;
         g.W = e->wckv + (size_t)2 * l * DEC_D * DEC_D; g.bias = e->bckv + (size_t)2 * l * DEC_D;
         g.M = M; g.N = 2 * DEC_D; g.K = DEC_D; g.epi = CT_EPI_STORE;
         g.nseg = 2; g.seg_w = DEC_D;

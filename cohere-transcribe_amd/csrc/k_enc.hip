@@ -213,6 +213,19 @@ __global__ void sub_flatten_kernel(float *out, const float *in, int T) {
     out[i] = in[(t * 16 + f) * SUB_CH + c];
 }
 
+// The same flatten, written as hi/lo bf16 planes for the pre-split GEMM.
+__global__ void sub_flatten_split_kernel(uint16_t *hi, uint16_t *lo, const float *in, int T) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)T * 16 * SUB_CH) return;
+    const int f = (int)(i % 16);
+    const int c = (int)((i / 16) % SUB_CH);
+    const long t = i / (16 * SUB_CH);
+    uint16_t h, l;
+    split_bf16(in[(t * 16 + f) * SUB_CH + c], h, l);
+    hi[i] = h;
+    lo[i] = l;
+}
+
 inline unsigned nblk(long n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -302,6 +315,12 @@ extern "C" void ctk_sub_dwconv(float *out, const float *in, int H, int Wd,
     const long n = (long)((H + 1) / 2) * ((Wd + 1) / 2) * SUB_CH;
     if (n <= 0) return;
     hipLaunchKernelGGL(sub_dwconv_kernel, dim3(nblk(n)), dim3(256), 0, s, out, in, H, Wd, w, b);
+}
+
+extern "C" void ctk_sub_flatten_split(uint16_t *hi, uint16_t *lo, const float *in, int T, hipStream_t s) {
+    const long n = (long)T * 16 * SUB_CH;
+    if (n <= 0) return;
+    hipLaunchKernelGGL(sub_flatten_split_kernel, dim3(nblk(n)), dim3(256), 0, s, hi, lo, in, T);
 }
 
 extern "C" void ctk_sub_flatten(float *out, const float *in, int T, hipStream_t s) {

@@ -94,6 +94,77 @@ __device__ __forceinline__ void store_out(const CtGemm &g, int m, int col, float
     else *y = s;
 }
 
+// Eight consecutive columns col..col+7 of row m (same segment, same head),
+// with the bias already added: the 16-byte-store form of store_out.
+__device__ __forceinline__ void act8(const CtGemm &g, float (&v)[8]) {
+    if (g.epi == CT_EPI_SILU) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = v[i] / (1.0f + expf(-v[i]));
+    } else if (g.epi == CT_EPI_RELU) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = v[i] > 0.0f ? v[i] : 0.0f;
+    }
+}
+
+// As store_out: the activation applies to plain rows and to SPLIT segments;
+// DENSE and HEADS segments store the sum as it is.
+__device__ __forceinline__ void store_out8(const CtGemm &g, int m, int col, float (&v)[8]) {
+    float *yf = nullptr;
+    uint16_t *yb = nullptr;
+    if (g.nseg > 0) {
+        const int si = col / g.seg_w, c = col - si * g.seg_w;
+        const CtSeg &sg = g.seg[si];
+        if (sg.mode == CT_OUT_SPLIT) {
+            act8(g, v);
+            u16x8 h8, l8;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                uint16_t h, l;
+                split_bf16(v[i], h, l);
+                h8[i] = h; l8[i] = l;
+            }
+            *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(sg.base) + (long)m * sg.ld + c) = h8;
+            *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(sg.base_lo) + (long)m * sg.ld + c) = l8;
+            return;
+        }
+        if (sg.mode == CT_OUT_DENSE) {
+            yf = reinterpret_cast<float *>(sg.base) + (long)m * sg.ld + c;
+        } else {
+            const long ro = sg.rowoff[m];
+            if (ro < 0) return;
+            const long off = ro + (long)(c >> 7) * sg.hstride + (c & 127);
+            if (sg.mode == CT_OUT_HEADS_BF16) yb = reinterpret_cast<uint16_t *>(sg.base) + off;
+            else yf = reinterpret_cast<float *>(sg.base) + off;
+        }
+    } else {
+        long yrow = m;
+        if (g.row_len) {
+            const int len = g.row_len[(long)m * g.row_len_step];
+            if (len <= 0) return;
+            yrow = (long)m * g.row_stride + len - 1;
+        }
+        yf = g.Y + yrow * g.ldy + col;
+        act8(g, v);
+    }
+    if (yb) {
+        u16x8 b8;
+#pragma unroll
+        for (int i = 0; i < 8; i++) b8[i] = f2bf(v[i]);
+        *reinterpret_cast<u16x8 *>(yb) = b8;
+        return;
+    }
+    float4 *y4 = reinterpret_cast<float4 *>(yf);
+    if (g.nseg == 0 && g.epi == CT_EPI_FMADD) {
+        float4 a = y4[0], b = y4[1];
+        a.x += g.scale * v[0]; a.y += g.scale * v[1]; a.z += g.scale * v[2]; a.w += g.scale * v[3];
+        b.x += g.scale * v[4]; b.y += g.scale * v[5]; b.z += g.scale * v[6]; b.w += g.scale * v[7];
+        y4[0] = a; y4[1] = b;
+        return;
+    }
+    y4[0] = make_float4(v[0], v[1], v[2], v[3]);
+    y4[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
 // ---------------------------------------------------------------------------
 // Decoder-class GEMM (weights with K = 1024, or K = 4096 -> 1024): few rows
 // (one per decode slot), weight-stream bound.  A workgroup owns 16*CB output
@@ -395,7 +466,7 @@ __device__ __forceinline__ void lds_dma16(const void *g, uint16_t *lds_wave_base
 __device__ __forceinline__ int swz(int R, int c) { return c ^ ((R >> 2) & 3); }
 
 template <bool GLU>
-__global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int n_nt) {
+__global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int n_nt, int vepi) {
     __shared__ __attribute__((aligned(16))) uint16_t smem[SST * STAGE_ELEMS];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r = lane & 15, kg = lane >> 4;
@@ -519,20 +590,55 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
         }
         return;
     }
+    if (!vepi) {
 #pragma unroll
-    for (int cb = 0; cb < 4; cb++) {
-        const int col = c0 + wn + cb * 16 + r;
-        if (col >= g.N) continue;
-        const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
+        for (int cb = 0; cb < 4; cb++) {
+            const int col = c0 + wn + cb * 16 + r;
+            if (col >= g.N) continue;
+            const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
 #pragma unroll
-        for (int rb = 0; rb < 4; rb++)
+            for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int m = m0 + wm + rb * 16 + kg * 4 + j;
+                    if (m >= g.M) continue;
+                    if (g.row_mask && !g.row_mask[m]) continue;
+                    store_out(g, m, col, acc[rb][cb][j] + ba);
+                }
+        }
+        return;
+    }
+    // Vector epilogue: the 128 x 256 fp32 tile goes through the (now idle)
+    // LDS ring, then each thread finishes 8 consecutive columns of a row and
+    // writes them as 16-byte pieces, 32 threads per 1-KB row run.  Column
+    // groups of 16 are XOR-swizzled by row so the fragment writes spread over
+    // all banks.
+    float *sc = reinterpret_cast<float *>(smem);
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+        for (int cb = 0; cb < 4; cb++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int m = m0 + wm + rb * 16 + kg * 4 + j;
-                if (m >= g.M) continue;
-                if (g.row_mask && !g.row_mask[m]) continue;
-                store_out(g, m, col, acc[rb][cb][j] + ba);
+                const int row = wm + rb * 16 + kg * 4 + j;
+                const int col = (wn + cb * 16 + r) ^ (((row >> 2) & 3) << 4);
+                sc[row * SBN + col] = acc[rb][cb][j];
             }
+    __syncthreads();
+    for (int it = tid; it < SBM * (SBN / 8); it += 512) {
+        const int row = it / (SBN / 8), g8 = it % (SBN / 8);
+        const int m = m0 + row, col = c0 + g8 * 8;
+        if (m >= g.M || col >= g.N) continue;
+        if (g.row_mask && !g.row_mask[m]) continue;
+        const float4 *pv = reinterpret_cast<const float4 *>(sc + row * SBN + ((g8 * 8) ^ (((row >> 2) & 3) << 4)));
+        const float4 v0 = pv[0], v1 = pv[1];
+        float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        if (g.bias) {
+            const u16x8 b8 = *reinterpret_cast<const u16x8 *>(g.bias + col);
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] += bf2f(b8[i]);
+        }
+        store_out8(g, m, col, v);
     }
 }
 
@@ -678,6 +784,26 @@ static bool decoder_class(const CtGemm *g) {
     return g->epi != CT_EPI_GLU && (g->K == 1024 || (g->K == 4096 && g->N == 1024));
 }
 
+// The 16-byte epilogue needs 8-column groups that stay inside one segment
+// (and one 128-column head) and 16-byte aligned destinations.
+static int vector_epilogue_ok(const CtGemm *g) {
+    if (g->N % 8 || ((uintptr_t)g->bias & 15)) return 0;
+    if (g->nseg == 0) return ((uintptr_t)g->Y % 16 == 0) && g->ldy % 4 == 0;
+    if (g->seg_w % 8) return 0;
+    for (int i = 0; i < g->nseg; i++) {
+        const CtSeg *sg = &g->seg[i];
+        if (sg->mode == CT_OUT_SPLIT) {
+            if (((uintptr_t)sg->base & 15) || ((uintptr_t)sg->base_lo & 15) || sg->ld % 8) return 0;
+        } else if (sg->mode == CT_OUT_DENSE) {
+            if (((uintptr_t)sg->base & 15) || sg->ld % 4) return 0;
+        } else {
+            const int el = sg->mode == CT_OUT_HEADS_BF16 ? 8 : 4;   /* elements per 16 B */
+            if (((uintptr_t)sg->base & 15) || sg->hstride % el) return 0;
+        }
+    }
+    return 1;
+}
+
 extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
     if (g->M <= 0 || g->N <= 0) return;
     if (g->epi == CT_EPI_GLU && g->N != 2 * g->glu_half) {
@@ -695,8 +821,9 @@ extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
         const int n_mt = (g->M + SBM - 1) / SBM;
         const int n_nt = glu ? (g->glu_half + SBN / 2 - 1) / (SBN / 2) : (g->N + SBN - 1) / SBN;
         const int nt = n_mt * n_nt, per = (nt + 7) / 8;
-        if (glu) hipLaunchKernelGGL(gemm_split_kernel<true>, dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt);
-        else hipLaunchKernelGGL(gemm_split_kernel<false>, dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt);
+        const int vepi = vector_epilogue_ok(g);
+        if (glu) hipLaunchKernelGGL(gemm_split_kernel<true>, dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, 0);
+        else hipLaunchKernelGGL(gemm_split_kernel<false>, dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, vepi);
         return;
     }
     const bool vec = (g->K % 8 == 0) && (g->lda % 4 == 0) &&
