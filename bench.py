@@ -90,7 +90,7 @@ def attention_roofline(hip, model, ev, reps=20, step_reps=0):
     B = 128
     S = rng.integers(1, 449, B)
     T = rng.integers(25, 376, B)
-    eng = cb.Engine(model, slots=B, max_requests=B, max_frames=376, kv_bf16=True)
+    eng = cb.Engine(model, slots=B, max_requests=B, max_frames=376, kv_bf16=True, max_tokens=512)
     step_ms = None
     try:
         eng.bench_fill(S, T, seed=9)
@@ -138,9 +138,10 @@ def decode_gemm_roofline(model, ev, slots=64, reps=20):
     """The decode step's GEMMs alone (8 x QKV, out, cross Q, cross out, FFN up,
     FFN down; LM head) at the stream's slot count."""
     rng = np.random.default_rng(6)
-    S = rng.integers(1, 267, slots)
+    S = rng.integers(1, 201, slots)
     T = rng.integers(26, 377, slots)
-    eng = cb.Engine(model, slots=slots, max_requests=slots, max_frames=376, kv_bf16=True)
+    eng = cb.Engine(model, slots=slots, max_requests=slots, max_frames=376, kv_bf16=True,
+                    max_tokens=len(cb.PROMPT) + 256)
     try:
         eng.bench_fill(S, T, seed=5)
         eng.step()
@@ -302,7 +303,9 @@ def main():
     offs = np.concatenate([[0], np.cumsum(samples)[:-1]])
     total = int(np.sum(samples))
     pcm = np.concatenate([cb.synth_audio(int(n), 1000 + i) for i, n in enumerate(samples)])
-    eng = cb.Engine(model, slots=args.slots, max_requests=args.requests, max_frames=376, kv_bf16=True)
+    # self caches sized for the longest request (prompt + 256 tokens)
+    eng = cb.Engine(model, slots=args.slots, max_requests=args.requests, max_frames=376, kv_bf16=True,
+                    max_tokens=len(cb.PROMPT) + 256)
     # device-resident input: the PCM buffer lives in a second engine-independent
     # allocation (the backend arena)
     dev_pcm = hip.backend_arena_alloc(total)

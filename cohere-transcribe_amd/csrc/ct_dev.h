@@ -43,10 +43,22 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, CT_WAVE));
     return v;
 }
-// Sum over aligned groups of 16 lanes.
+// Lane exchange within a row of 16 lanes (DPP): CTRL 0xB1 = quad_perm
+// [1,0,3,2], 0x4E = quad_perm [2,3,0,1], 0x141 = row_half_mirror (lane i of
+// each 8 reads 7-i), 0x140 = row_mirror (lane i reads 15-i).
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of 16 lanes.  Each stage adds the same pair of
+// partial sums as an xor-1/2/4/8 butterfly, so every lane holds the same
+// value, computed in the same order.
 __device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, CT_WAVE);
+    v += dpp_row<0xB1>(v);
+    v += dpp_row<0x4E>(v);
+    v += dpp_row<0x141>(v);
+    v += dpp_row<0x140>(v);
     return v;
 }
 

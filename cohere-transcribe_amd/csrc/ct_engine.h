@@ -11,11 +11,23 @@ extern "C" {
 
 #define CT_PROMPT_MAX 16
 #define CT_MAX_KSPLIT 8    /* largest ctk_gemv_ksplit() of a decoder weight */
+/* Spare rows per (slot, head) of the self caches: without them every
+ * (slot, head) block starts on the same 256-KB boundary and the workgroups
+ * of a step stream from the same memory channels at the same time. */
+#ifndef CT_KV_PAD
+#define CT_KV_PAD 0
+#endif
+/* Keys per workgroup of the decode attention; longer caches are split over
+ * several workgroups and merged. */
+#ifndef CT_ATTN_CHUNK
+#define CT_ATTN_CHUNK 0
+#endif
 
 /* All pointers are device memory.  Slot-major arrays have `slots` entries,
  * request-major arrays `max_req`. */
 typedef struct {
     int slots, max_req, smax, tmax;
+    int kv_rows;       /* rows per (slot, head) of the self caches (>= smax)    */
     /* slot table */
     int  *slot_req;    /* request in the slot, -1 when free                    */
     int  *slot_S;      /* tokens already in the slot's self cache              */

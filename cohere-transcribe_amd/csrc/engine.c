@@ -40,13 +40,16 @@ struct HipbEngine {
     /* repacked weights: [Wq;Wk;Wv] per layer, [Wk;Wv] cross per layer */
     uint16_t *wqkv, *bqkv, *wckv, *bckv;
     /* caches */
-    void *kself, *vself;       /* [L][slots][H][smax][128] */
+    void *kself, *vself;       /* [L][slots][H][kv_rows][128] */
     void *kcross, *vcross;     /* [L][max_req][H][tmax][128] */
     float *enc_pool;           /* [max_req][tmax][DEC_D] */
     /* step activations: h residual rows (fp32); lnf/attf/midf the decode
      * GEMMs' inputs in frag layout; parts K-slice partial sums */
     float *h, *q, *parts, *logits;
     uint16_t *lnf, *attf, *midf;
+    /* attention key split: partial softmax states per (slot, head, chunk) */
+    int attn_chunks;
+    float *att_ml, *att_po;
     /* encoder workspace (lazy) */
     int enc_cap;               /* frames */
     int sub_cap;               /* subsampling scratch floats */
@@ -177,6 +180,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     if (cfg->slots < 1 || cfg->slots > CT_MAX_BATCH) CT_FATAL("hipb_create: slots outside [1, 256]");
     if (cfg->max_frames < 1 || cfg->max_frames > 2048) CT_FATAL("hipb_create: max_frames outside [1, 2048]");
     if (cfg->max_requests < 1) CT_FATAL("hipb_create: max_requests < 1");
+    if (cfg->max_tokens < 0 || cfg->max_tokens > MAX_SEQ) CT_FATAL("hipb_create: max_tokens outside [0, MAX_SEQ]");
     HipbEngine *e = calloc(1, sizeof *e);
     if (!e) CT_FATAL("out of host memory");
     e->cfg = *cfg;
@@ -187,7 +191,9 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     const int S = cfg->slots, R = cfg->max_requests;
     const int tmax = (cfg->max_frames + 7) / 8 * 8;
     CtEngDev *d = &e->d;
-    d->slots = S; d->max_req = R; d->smax = MAX_SEQ; d->tmax = tmax;
+    d->slots = S; d->max_req = R; d->tmax = tmax;
+    d->smax = cfg->max_tokens > 0 ? cfg->max_tokens : MAX_SEQ;
+    d->kv_rows = d->smax + CT_KV_PAD;
     d->slot_req = dmalloc(S * sizeof(int));
     d->slot_S = dmalloc(S * sizeof(int));
     d->act = dmalloc(S * sizeof(int));
@@ -202,7 +208,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     d->req_np = dmalloc(R * sizeof(int));
     d->req_ngen = dmalloc(R * sizeof(int));
     d->req_prompt = dmalloc((size_t)R * CT_PROMPT_MAX * sizeof(int));
-    d->req_out = dmalloc((size_t)R * MAX_SEQ * sizeof(int));
+    d->req_out = dmalloc((size_t)R * d->smax * sizeof(int));
     d->q = dmalloc(4 * sizeof(int));
     ECHK(hipMemsetAsync(d->slot_req, 0xff, S * sizeof(int), e->s));   /* -1: free */
     ECHK(hipMemsetAsync(d->slot_S, 0, S * sizeof(int), e->s));
@@ -227,7 +233,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
         ECHK(hipMemcpyAsync((char *)e->bckv + (2 * l) * bsz, DW(L->ca_kb), bsz, hipMemcpyDeviceToDevice, e->s));
         ECHK(hipMemcpyAsync((char *)e->bckv + (2 * l + 1) * bsz, DW(L->ca_vb), bsz, hipMemcpyDeviceToDevice, e->s));
     }
-    const size_t self_el = (size_t)DEC_N * S * DEC_H * MAX_SEQ * DEC_DK;
+    const size_t self_el = (size_t)DEC_N * S * DEC_H * d->kv_rows * DEC_DK;
     const size_t cross_el = (size_t)DEC_N * R * DEC_H * tmax * DEC_DK;
     e->kself = dmalloc(self_el * e->esz);
     e->vself = dmalloc(self_el * e->esz);
@@ -241,6 +247,13 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->attf = dmalloc(ct_frag_elems(S, DEC_D) * 2);
     e->midf = dmalloc(ct_frag_elems(S, DEC_FF) * 2);
     e->logits = dmalloc((size_t)S * VOCAB * 4);
+    if (CT_ATTN_CHUNK > 0) {
+        const int longest = d->smax > tmax ? d->smax : tmax;
+        e->attn_chunks = (longest + CT_ATTN_CHUNK - 1) / (CT_ATTN_CHUNK > 0 ? CT_ATTN_CHUNK : 1);
+        const size_t items = (size_t)S * DEC_H * e->attn_chunks;
+        e->att_ml = dmalloc(items * 2 * 4);
+        e->att_po = dmalloc(items * DEC_DK * 4);
+    }
     ECHK(hipMemsetAsync(e->h, 0, (size_t)S * DEC_D * 4, e->s));
     e->req = calloc(R, sizeof(HostReq));
     const char *eg = getenv("HIPB_EAGER");
@@ -260,6 +273,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->kself, e->vself, e->kcross, e->vcross,
                     e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
+                    e->att_ml, e->att_po,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
                     e->eh, e->esub, e->emel, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
                     e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
@@ -338,6 +352,7 @@ static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prom
     if (e->n_req >= e->cfg.max_requests) CT_FATAL("hipb_submit: request pool full");
     if (n_prompt < 1 || n_prompt > CT_PROMPT_MAX) CT_FATAL("hipb_submit: prompt length outside [1, 16]");
     if (limit < 1) CT_FATAL("hipb_submit: limit < 1");
+    if (n_prompt + limit > e->d.smax) CT_FATAL("hipb_submit: prompt + limit exceeds the engine's max_tokens");
     const int Te = t_enc_of(T_mel);
     if (T_mel < 1 || Te > e->d.tmax || Te > e->cfg.max_frames) CT_FATAL("hipb_submit: clip longer than max_frames");
     const int r = e->n_req++;
@@ -644,11 +659,15 @@ static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, 
         a.q_bias = q_bias;
     }
     a.out_frag = e->attf;
+    a.chunk = CT_ATTN_CHUNK;
+    a.max_chunks = e->attn_chunks;
+    a.part_ml = e->att_ml;
+    a.part_o = e->att_po;
     ctk_attn(&a, e->s);
 }
 
 static void self_kv(HipbEngine *e, int l, void **k, void **v) {
-    const size_t per = (size_t)e->d.slots * DEC_H * MAX_SEQ * DEC_DK * e->esz;
+    const size_t per = (size_t)e->d.slots * DEC_H * e->d.kv_rows * DEC_DK * e->esz;
     *k = (char *)e->kself + l * per;
     *v = (char *)e->vself + l * per;
 }
@@ -663,7 +682,7 @@ static void step_attention(HipbEngine *e, int l, int cross) {
     void *k, *v;
     if (!cross) {
         self_kv(e, l, &k, &v);
-        attn(e, k, v, (long)DEC_H * MAX_SEQ * DEC_DK, (long)MAX_SEQ * DEC_DK, e->d.pos_len, NULL, NULL);
+        attn(e, k, v, (long)DEC_H * e->d.kv_rows * DEC_DK, (long)e->d.kv_rows * DEC_DK, e->d.pos_len, NULL, NULL);
     } else {
         cross_kv(e, l, &k, &v);
         attn(e, k, v, (long)DEC_H * e->d.tmax * DEC_DK, (long)e->d.tmax * DEC_DK,
@@ -708,7 +727,7 @@ static void step_kernels(HipbEngine *e, int full) {
         g.W = e->wqkv + (size_t)3 * l * DEC_D * DEC_D; g.bias = e->bqkv + (size_t)3 * l * DEC_D;
         g.M = B; g.N = 3 * DEC_D; g.K = DEC_D; g.ksplit = 1; g.out = CT_GV_QKV;
         g.Y = e->q; g.ldy = DEC_D;
-        g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)MAX_SEQ * DEC_DK;
+        g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)e->d.kv_rows * DEC_DK;
         g.kv_bf16 = e->esz == 2;
         ctk_gemv(&g, s);
         if (full) step_attention(e, l, 0);
@@ -784,7 +803,7 @@ int hipb_tokens(HipbEngine *e, int req, int *out, int cap) {
     ECHK(hipStreamSynchronize(e->s));
     ECHK(hipMemcpy(&n, e->d.req_ngen + req, sizeof(int), hipMemcpyDeviceToHost));
     if (n > cap) n = cap;
-    if (n > 0) ECHK(hipMemcpy(out, e->d.req_out + (size_t)req * MAX_SEQ, n * sizeof(int), hipMemcpyDeviceToHost));
+    if (n > 0) ECHK(hipMemcpy(out, e->d.req_out + (size_t)req * e->d.smax, n * sizeof(int), hipMemcpyDeviceToHost));
     return n;
 }
 
@@ -817,17 +836,17 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
     if (B > e->d.max_req) CT_FATAL("hipb_bench_fill: needs max_requests >= slots");
     int *buf = e->h_tmp;
     for (int s = 0; s < B; s++) {
-        if (S[s] < 1 || S[s] > MAX_SEQ - 64) CT_FATAL("hipb_bench_fill: S outside [1, MAX_SEQ-64]");
+        if (S[s] < 1 || S[s] > e->d.smax - 64) CT_FATAL("hipb_bench_fill: S outside [1, max_tokens-64]");
         if (T_enc[s] < 1 || T_enc[s] > e->d.tmax) CT_FATAL("hipb_bench_fill: T_enc outside [1, max_frames]");
     }
     /* one synthetic request per slot: no prompt, one generated token, never
-     * finishes within the benchmark (limit MAX_SEQ, EOS suppressed) */
+     * finishes within the benchmark (limit max_tokens, EOS suppressed) */
     for (int s = 0; s < B; s++) buf[s] = s;
     ECHK(hipMemcpy(e->d.slot_req, buf, B * sizeof(int), hipMemcpyHostToDevice));
     for (int s = 0; s < B; s++) buf[s] = S[s] - 1;
     ECHK(hipMemcpy(e->d.slot_S, buf, B * sizeof(int), hipMemcpyHostToDevice));
     ECHK(hipMemcpy(e->d.req_T, T_enc, B * sizeof(int), hipMemcpyHostToDevice));
-    for (int s = 0; s < B; s++) buf[s] = MAX_SEQ;
+    for (int s = 0; s < B; s++) buf[s] = e->d.smax;
     ECHK(hipMemcpy(e->d.req_limit, buf, B * sizeof(int), hipMemcpyHostToDevice));
     for (int s = 0; s < B; s++) buf[s] = HIPB_SUPPRESS_EOS;
     ECHK(hipMemcpy(e->d.req_flags, buf, B * sizeof(int), hipMemcpyHostToDevice));
@@ -836,10 +855,10 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
     for (int s = 0; s < B; s++) buf[s] = 1;
     ECHK(hipMemcpy(e->d.req_ngen, buf, B * sizeof(int), hipMemcpyHostToDevice));
     for (int s = 0; s < B; s++)
-        ECHK(hipMemcpy(e->d.req_out + (size_t)s * MAX_SEQ, &(int){100 + s}, sizeof(int), hipMemcpyHostToDevice));
+        ECHK(hipMemcpy(e->d.req_out + (size_t)s * e->d.smax, &(int){100 + s}, sizeof(int), hipMemcpyHostToDevice));
     int q[4] = {B, B, 0, 0};
     ECHK(hipMemcpy(e->d.q, q, sizeof q, hipMemcpyHostToDevice));
-    const long self_el = (long)DEC_N * B * DEC_H * MAX_SEQ * DEC_DK;
+    const long self_el = (long)DEC_N * B * DEC_H * e->d.kv_rows * DEC_DK;
     const long cross_el = (long)DEC_N * e->d.max_req * DEC_H * e->d.tmax * DEC_DK;
     ctk_fill_random(e->kself, self_el, e->esz == 2, 0.1f, seed, e->s);
     ctk_fill_random(e->vself, self_el, e->esz == 2, 0.1f, seed + 1, e->s);

@@ -1,7 +1,8 @@
 // k_attn.hip — ragged scaled-dot-product attention for the decoder.
 //
 // One workgroup per (item, query row, head).  Sixteen 16-lane groups stream
-// the item's keys (group g takes keys g, g+16, ...); each lane owns 8 of the
+// the item's keys (group g takes keys g, g+16, ..., 8 of them per loop trip:
+// loads first, then one softmax update per trip); each lane owns 8 of the
 // 128 head dimensions, so a key row is read as one contiguous 256 B (bf16) or
 // 512 B (fp32) segment.  Each group keeps an online softmax (running max,
 // running sum, weighted V); the 16 partial states are merged in LDS in a fixed
@@ -11,11 +12,16 @@
 // Semantics: backends/cpu/backend.c:339-360 (scores * 1/sqrt(128) + mask,
 // softmax, weighted sum of V), 410-413 (T_k from the device counter),
 // 478-500 (ragged batch: T_k per item from the latched S or T_enc).
+#include <type_traits>
 #include "ct_dev.h"
+#include <stdio.h>
+#include <stdlib.h>
 #include "ct_launch.h"
 #include "../../include/model_types.h"
 
 namespace {
+
+constexpr int CT_ATTN_QPARTS = 8;   // most query partial slices a launch may pass
 
 template <bool BF16, bool VEC>
 __device__ __forceinline__ void load8(const void *base, long off, float (&v)[8]) {
@@ -52,76 +58,130 @@ __device__ __forceinline__ void store_out(const CtAttn &a, int bq, int col, long
 
 template <bool BF16, bool VEC>
 __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
-    const int bq = blockIdx.x, h = blockIdx.y;
+    const int bq = blockIdx.x, h = blockIdx.y, ch = blockIdx.z;
     const int b = bq / a.T_q, qi = bq % a.T_q;
-    const int T = a.lens ? a.lens[(long)b * a.lens_step] : a.len_const;
     const int tid = threadIdx.x, g = tid >> 4, l16 = tid & 15;
     const long qoff = (long)b * a.q_sb + (long)qi * a.q_st + h * DEC_DK;
-    if (T <= 0) {
-        if (tid < DEC_DK) store_out(a, bq, h * DEC_DK + tid, qoff + tid, 0.0f);
-        return;
-    }
+    // Every load the prologue needs is issued before any of them is used:
+    // the length, the cache index and the query (or its K-slice partials).
+    const int T = a.lens ? a.lens[(long)b * a.lens_step] : a.len_const;
+    const long item = a.kv_index ? (long)a.kv_index[b] : (long)b;
     float q[8];
     if (a.q_parts) {
         // query = ((part 0 + part 1) + ...) + bias, the decode GEMM's K-slices
         const float *qp = a.q_parts + qoff + l16 * 8;
+        float4 pr[CT_ATTN_QPARTS][2];
 #pragma unroll
-        for (int i = 0; i < 8; i++) q[i] = qp[i];
-        for (int p = 1; p < a.q_nparts; p++)
+        for (int p = 0; p < CT_ATTN_QPARTS; p++)
+            if (p < a.q_nparts) {
+                pr[p][0] = *reinterpret_cast<const float4 *>(qp + p * a.q_pstride);
+                pr[p][1] = *reinterpret_cast<const float4 *>(qp + p * a.q_pstride + 4);
+            }
+        const u16x8 bb = a.q_bias ? *reinterpret_cast<const u16x8 *>(a.q_bias + h * DEC_DK + l16 * 8)
+                                  : (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+        q[0] = pr[0][0].x; q[1] = pr[0][0].y; q[2] = pr[0][0].z; q[3] = pr[0][0].w;
+        q[4] = pr[0][1].x; q[5] = pr[0][1].y; q[6] = pr[0][1].z; q[7] = pr[0][1].w;
 #pragma unroll
-            for (int i = 0; i < 8; i++) q[i] += qp[p * a.q_pstride + i];
+        for (int p = 1; p < CT_ATTN_QPARTS; p++)
+            if (p < a.q_nparts) {
+                q[0] += pr[p][0].x; q[1] += pr[p][0].y; q[2] += pr[p][0].z; q[3] += pr[p][0].w;
+                q[4] += pr[p][1].x; q[5] += pr[p][1].y; q[6] += pr[p][1].z; q[7] += pr[p][1].w;
+            }
         if (a.q_bias)
 #pragma unroll
-            for (int i = 0; i < 8; i++) q[i] += bf2f(a.q_bias[h * DEC_DK + l16 * 8 + i]);
+            for (int i = 0; i < 8; i++) q[i] += bf2f(bb[i]);
     } else {
         const float *qp = a.Q + qoff + l16 * 8;
 #pragma unroll
         for (int i = 0; i < 8; i++) q[i] = qp[i];
     }
+    if (T <= 0) {
+        if (ch == 0 && tid < DEC_DK) store_out(a, bq, h * DEC_DK + tid, qoff + tid, 0.0f);
+        return;
+    }
+    // keys [kb, ke) of this workgroup: one chunk of a.chunk keys (the last
+    // of at most max_chunks takes the rest), or all of them
+    const int nch = a.chunk > 0 ? min((T + a.chunk - 1) / a.chunk, a.max_chunks) : 1;
+    if (ch >= nch) return;
+    const int kb = a.chunk > 0 ? ch * a.chunk : 0;
+    const int ke = ch == nch - 1 ? T : kb + a.chunk;
     const float *mrow = a.mask ? a.mask + (long)qi * T : nullptr;
-    const long item = a.kv_index ? (long)a.kv_index[b] : (long)b;
     const long base = item * a.kv_sb + (long)h * a.kv_sh + l16 * 8;
 
     float m = -INFINITY, l = 0.0f, o[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) o[i] = 0.0f;
 
-    for (int k = g; k < T; k += 32) {
-        // two keys in flight per group: k and k + 16
-        const int k2 = k + 16;
-        const bool has2 = k2 < T;
-        float kv0[8], kv1[8], vv0[8], vv1[8];
-        load8<BF16, VEC>(a.K, base + (long)k * a.kv_st, kv0);
-        load8<BF16, VEC>(a.V, base + (long)k * a.kv_st, vv0);
-        if (has2) {
-            load8<BF16, VEC>(a.K, base + (long)k2 * a.kv_st, kv1);
-            load8<BF16, VEC>(a.V, base + (long)k2 * a.kv_st, vv1);
-        }
-        float d0 = 0.0f, d1 = 0.0f;
+    // KPI keys per group per trip, all loads issued first: group g takes keys
+    // g, g + 16, g + 32, ... in that order (the order the softmax sees them)
+#ifndef CT_ATTN_KPI
+#define CT_ATTN_KPI 2
+#endif
+    constexpr int KPI = BF16 ? CT_ATTN_KPI : 4;
+    // keeps the raw 16-byte rows in registers until use (bf16: 8 VGPRs a key)
+    using Raw = typename std::conditional<BF16 && VEC, u16x8, float[8]>::type;
+    for (int k0 = kb + g; k0 < ke; k0 += 16 * KPI) {
+        Raw kr[KPI], vr[KPI];
 #pragma unroll
-        for (int i = 0; i < 8; i++) d0 += q[i] * kv0[i];
-        if (has2) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) d1 += q[i] * kv1[i];
+        for (int j = 0; j < KPI; j++) {
+            const int k = k0 + 16 * j;
+            if (k < ke) {
+                if constexpr (BF16 && VEC) {
+                    const uint16_t *kp = reinterpret_cast<const uint16_t *>(a.K) + base + (long)k * a.kv_st;
+                    const uint16_t *vp = reinterpret_cast<const uint16_t *>(a.V) + base + (long)k * a.kv_st;
+                    kr[j] = *reinterpret_cast<const u16x8 *>(kp);
+                    vr[j] = *reinterpret_cast<const u16x8 *>(vp);
+                } else {
+                    load8<BF16, VEC>(a.K, base + (long)k * a.kv_st, kr[j]);
+                    load8<BF16, VEC>(a.V, base + (long)k * a.kv_st, vr[j]);
+                }
+            }
         }
-        float s0 = group16_sum(d0) * a.scale + (mrow ? mrow[k] : 0.0f);
-        float s1 = group16_sum(d1) * a.scale + ((mrow && has2) ? mrow[k2] : 0.0f);
-        {
-            const float mn = fmaxf(m, s0);
-            const float c = expf(m - mn), p = expf(s0 - mn);
-            l = l * c + p;
+        // chunked online softmax: the trip's scores together, one rescale
+        float sc[KPI];
 #pragma unroll
-            for (int i = 0; i < 8; i++) o[i] = o[i] * c + p * vv0[i];
-            m = mn;
-        }
-        if (has2) {
-            const float mn = fmaxf(m, s1);
-            const float c = expf(m - mn), p = expf(s1 - mn);
-            l = l * c + p;
+        for (int j = 0; j < KPI; j++) {
+            float d = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) o[i] = o[i] * c + p * vv1[i];
-            m = mn;
+            for (int i = 0; i < 8; i++) {
+                float kf;
+                if constexpr (BF16 && VEC) kf = bf2f(kr[j][i]);
+                else kf = kr[j][i];
+                d += q[i] * kf;
+            }
+            sc[j] = d;
         }
+#pragma unroll
+        for (int j = 0; j < KPI; j++) {
+            const int k = k0 + 16 * j;
+            sc[j] = k < ke ? group16_sum(sc[j]) * a.scale + (mrow ? mrow[k] : 0.0f) : -INFINITY;
+        }
+        float mx = sc[0];
+#pragma unroll
+        for (int j = 1; j < KPI; j++) mx = fmaxf(mx, sc[j]);
+        const float mn = fmaxf(m, mx);
+        const float c = expf(m - mn);
+        float p[KPI], ps = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KPI; j++) {
+            p[j] = k0 + 16 * j < ke ? expf(sc[j] - mn) : 0.0f;
+            ps += p[j];
+        }
+        l = l * c + ps;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float acc = o[i] * c;
+#pragma unroll
+            for (int j = 0; j < KPI; j++) {
+                if (k0 + 16 * j >= ke) break;
+                float vf;
+                if constexpr (BF16 && VEC) vf = bf2f(vr[j][i]);
+                else vf = vr[j][i];
+                acc += p[j] * vf;
+            }
+            o[i] = acc;
+        }
+        m = mn;
     }
 
     __shared__ float sm[16], sl[16], so[16][DEC_DK];
@@ -141,15 +201,54 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
             num += w * so[j][tid];
             den += w * sl[j];
         }
-        store_out(a, bq, h * DEC_DK + tid, qoff + tid, num / den);
+        if (nch == 1) {
+            store_out(a, bq, h * DEC_DK + tid, qoff + tid, num / den);
+        } else {
+            // partial state of this chunk, merged by attn_merge_kernel
+            const long pi = ((long)bq * a.H + h) * a.max_chunks + ch;
+            a.part_o[pi * DEC_DK + tid] = num;
+            if (tid == 0) { a.part_ml[2 * pi] = M; a.part_ml[2 * pi + 1] = den; }
+        }
     }
+}
+
+// Items split into chunks: out = sum_c e^(M_c - M) num_c / sum_c e^(M_c - M)
+// den_c over the chunks in order, M = max_c M_c.  Items with one chunk were
+// written by attn_kernel.
+__global__ __launch_bounds__(DEC_DK) void attn_merge_kernel(CtAttn a) {
+    const int bq = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int b = bq / a.T_q, qi = bq % a.T_q;
+    const int T = a.lens ? a.lens[(long)b * a.lens_step] : a.len_const;
+    const int nch = min((T + a.chunk - 1) / a.chunk, a.max_chunks);
+    if (T <= 0 || nch <= 1) return;
+    const long p0 = ((long)bq * a.H + h) * a.max_chunks;
+    float M = -INFINITY;
+    for (int c = 0; c < nch; c++) M = fmaxf(M, a.part_ml[2 * (p0 + c)]);
+    float num = 0.0f, den = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        const float w = expf(a.part_ml[2 * (p0 + c)] - M);
+        num += w * a.part_o[(p0 + c) * DEC_DK + tid];
+        den += w * a.part_ml[2 * (p0 + c) + 1];
+    }
+    const long qoff = (long)b * a.q_sb + (long)qi * a.q_st + h * DEC_DK;
+    store_out(a, bq, h * DEC_DK + tid, qoff + tid, num / den);
 }
 
 }  // namespace
 
 extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
     if (a->B <= 0 || a->T_q <= 0) return;
-    const dim3 grid(a->B * a->T_q, a->H);
+    if (a->q_parts && (a->q_nparts < 1 || a->q_nparts > 8 || a->q_pstride % 4 ||
+                       ((uintptr_t)a->q_parts & 15) || (a->q_bias && ((uintptr_t)a->q_bias & 15)) ||
+                       a->q_sb % 4 || a->q_st % 4)) {
+        fprintf(stderr, "ctk_attn: query partials need 1..8 slices and 16-byte aligned rows\n");
+        exit(1);
+    }
+    if (a->chunk > 0 && (!a->part_o || !a->part_ml || a->max_chunks < 1 || a->mask)) {
+        fprintf(stderr, "ctk_attn: a key split needs partial buffers, max_chunks >= 1 and no mask\n");
+        exit(1);
+    }
+    const dim3 grid(a->B * a->T_q, a->H, a->chunk > 0 ? a->max_chunks : 1);
     // 16-byte vector loads need every 8-element K/V segment aligned.
     const long esz = a->kv_bf16 ? 2 : 4, need = 16 / esz;
     const bool vec = ((uintptr_t)a->K % 16 == 0) && ((uintptr_t)a->V % 16 == 0) &&
@@ -161,4 +260,6 @@ extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
         if (vec) hipLaunchKernelGGL((attn_kernel<false, true>), grid, dim3(256), 0, s, *a);
         else hipLaunchKernelGGL((attn_kernel<false, false>), grid, dim3(256), 0, s, *a);
     }
+    if (a->chunk > 0)
+        hipLaunchKernelGGL(attn_merge_kernel, dim3(a->B * a->T_q, a->H), dim3(DEC_DK), 0, s, *a);
 }

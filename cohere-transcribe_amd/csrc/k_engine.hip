@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d) {
             d.pos_len[s] = S;
             d.cross_len[s] = d.req_T[r];
             d.cross_idx[s] = r;
-            d.kv_rowoff[s] = ((long)s * DEC_H * d.smax + (S - 1)) * DEC_DK;
+            d.kv_rowoff[s] = ((long)s * DEC_H * d.kv_rows + (S - 1)) * DEC_DK;
         } else {
             d.act[s] = 0;
             d.tok[s] = 0;

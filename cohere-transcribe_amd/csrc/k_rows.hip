@@ -231,74 +231,63 @@ __global__ void inc_kernel(int *p) {
     if (threadIdx.x == 0) *p += 1;
 }
 
-// Decoder residual update + LayerNorm into frag layout (D = DEC_D), one wave
-// per row: h += ((parts[0] + parts[1]) + ...) + pbias (the K-slice sums of
-// the previous projection, added in slice order, then its bias), then the
-// two-pass LayerNorm of layernorm_vec_kernel, each output split hi/lo and
-// stored where the decode GEMM's lanes read it.
+// Decoder residual update + LayerNorm into frag layout (D = DEC_D), one
+// 256-thread workgroup per row, a float4 per thread: h += ((parts[0] +
+// parts[1]) + ...) + pbias (the K-slice sums of the previous projection, in
+// slice order, then its bias), then the two-pass LayerNorm (mean, then the
+// variance of the centred values, eps 1e-5), each output split hi/lo and
+// stored where the decode GEMM's lanes read it.  NP (the number of slices)
+// is a template parameter so every load is issued before the first add.
+template <int NP>
 __global__ __launch_bounds__(256) void ln_frag_kernel(float *h, uint16_t *frag, const float *parts,
-                                                      int nparts, long pstride, const uint16_t *pbias,
-                                                      const uint16_t *w, const uint16_t *b, int M) {
-    constexpr int V = 4, D = 256 * V;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= M) return;
+                                                      long pstride, const uint16_t *pbias,
+                                                      const uint16_t *w, const uint16_t *b) {
+    constexpr int D = DEC_D;
+    const int row = blockIdx.x, t = threadIdx.x, wv = t >> 6, lane = t & 63;
     float4 *x = reinterpret_cast<float4 *>(h + (long)row * D);
-    float4 v[V];
+    float4 v = x[t];
+    const int d0 = 4 * t;
+    if (NP > 0) {
+        float4 pr[NP > 0 ? NP : 1];
 #pragma unroll
-    for (int i = 0; i < V; i++) v[i] = x[lane + 64 * i];
-    if (nparts > 0) {
-        float4 a[V];
-        const float4 *p0 = reinterpret_cast<const float4 *>(parts + (long)row * D);
+        for (int p = 0; p < NP; p++)
+            pr[p] = reinterpret_cast<const float4 *>(parts + p * pstride + (long)row * D)[t];
+        float4 a = pr[0];
 #pragma unroll
-        for (int i = 0; i < V; i++) a[i] = p0[lane + 64 * i];
-        for (int p = 1; p < nparts; p++) {
-            const float4 *pp = reinterpret_cast<const float4 *>(parts + p * pstride + (long)row * D);
-#pragma unroll
-            for (int i = 0; i < V; i++) {
-                const float4 t = pp[lane + 64 * i];
-                a[i].x += t.x; a[i].y += t.y; a[i].z += t.z; a[i].w += t.w;
-            }
+        for (int p = 1; p < NP; p++) {
+            a.x += pr[p].x; a.y += pr[p].y; a.z += pr[p].z; a.w += pr[p].w;
         }
-#pragma unroll
-        for (int i = 0; i < V; i++) {
-            const int d0 = 4 * (lane + 64 * i);
-            if (pbias) {
-                a[i].x += bf2f(pbias[d0]); a[i].y += bf2f(pbias[d0 + 1]);
-                a[i].z += bf2f(pbias[d0 + 2]); a[i].w += bf2f(pbias[d0 + 3]);
-            }
-            v[i].x += a[i].x; v[i].y += a[i].y; v[i].z += a[i].z; v[i].w += a[i].w;
-            x[lane + 64 * i] = v[i];
+        if (pbias) {
+            a.x += bf2f(pbias[d0]); a.y += bf2f(pbias[d0 + 1]);
+            a.z += bf2f(pbias[d0 + 2]); a.w += bf2f(pbias[d0 + 3]);
         }
+        v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+        x[t] = v;
     }
-    float s = 0.0f;
+    __shared__ float red[2][4];
+    const float s = wave_sum((v.x + v.y) + (v.z + v.w));
+    if (lane == 0) red[0][wv] = s;
+    __syncthreads();
+    const float mu = ((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])) / (float)D;
+    const float c0 = v.x - mu, c1 = v.y - mu, c2 = v.z - mu, c3 = v.w - mu;
+    const float q = wave_sum((c0 * c0 + c1 * c1) + (c2 * c2 + c3 * c3));
+    if (lane == 0) red[1][wv] = q;
+    __syncthreads();
+    const float var = ((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) / (float)D;
+    const float rs = 1.0f / sqrtf(var + 1e-5f);
+    const float o[4] = {c0 * rs * bf2f(w[d0]) + bf2f(b[d0]),
+                        c1 * rs * bf2f(w[d0 + 1]) + bf2f(b[d0 + 1]),
+                        c2 * rs * bf2f(w[d0 + 2]) + bf2f(b[d0 + 2]),
+                        c3 * rs * bf2f(w[d0 + 3]) + bf2f(b[d0 + 3])};
+    ushort4 h4, l4;
+    uint16_t hh[4], ll[4];
 #pragma unroll
-    for (int i = 0; i < V; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    const float mu = wave_sum(s) / (float)D;
-    float q = 0.0f;
-#pragma unroll
-    for (int i = 0; i < V; i++) {
-        const float a = v[i].x - mu, bb = v[i].y - mu, c = v[i].z - mu, d = v[i].w - mu;
-        q += (a * a + bb * bb) + (c * c + d * d);
-    }
-    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
-#pragma unroll
-    for (int i = 0; i < V; i++) {
-        const int d0 = 4 * (lane + 64 * i);
-        const float o[4] = {(v[i].x - mu) * rs * bf2f(w[d0]) + bf2f(b[d0]),
-                            (v[i].y - mu) * rs * bf2f(w[d0 + 1]) + bf2f(b[d0 + 1]),
-                            (v[i].z - mu) * rs * bf2f(w[d0 + 2]) + bf2f(b[d0 + 2]),
-                            (v[i].w - mu) * rs * bf2f(w[d0 + 3]) + bf2f(b[d0 + 3])};
-        ushort4 h4, l4;
-        uint16_t hh[4], ll[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) split_bf16(o[j], hh[j], ll[j]);
-        h4.x = hh[0]; h4.y = hh[1]; h4.z = hh[2]; h4.w = hh[3];
-        l4.x = ll[0]; l4.y = ll[1]; l4.z = ll[2]; l4.w = ll[3];
-        const long off = ct_frag_off(row, d0, D);
-        *reinterpret_cast<ushort4 *>(frag + off) = h4;
-        *reinterpret_cast<ushort4 *>(frag + off + 512) = l4;
-    }
+    for (int j = 0; j < 4; j++) split_bf16(o[j], hh[j], ll[j]);
+    h4.x = hh[0]; h4.y = hh[1]; h4.z = hh[2]; h4.w = hh[3];
+    l4.x = ll[0]; l4.y = ll[1]; l4.z = ll[2]; l4.w = ll[3];
+    const long off = ct_frag_off(row, d0, D);
+    *reinterpret_cast<ushort4 *>(frag + off) = h4;
+    *reinterpret_cast<ushort4 *>(frag + off + 512) = l4;
 }
 
 }  // namespace
@@ -338,8 +327,17 @@ extern "C" void ctk_ln_frag(float *h, uint16_t *frag, const float *parts, int np
         fprintf(stderr, "ctk_ln_frag: needs 16-byte aligned buffers\n");
         exit(1);
     }
-    hipLaunchKernelGGL(ln_frag_kernel, dim3((M + 3) / 4), dim3(256), 0, s, h, frag, parts, nparts,
-                       (long)M * DEC_D, pbias, w, b, M);
+    const long ps = (long)M * DEC_D;
+    switch (nparts) {
+    case 0: hipLaunchKernelGGL(ln_frag_kernel<0>, dim3(M), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b); break;
+    case 1: hipLaunchKernelGGL(ln_frag_kernel<1>, dim3(M), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b); break;
+    case 2: hipLaunchKernelGGL(ln_frag_kernel<2>, dim3(M), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b); break;
+    case 4: hipLaunchKernelGGL(ln_frag_kernel<4>, dim3(M), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b); break;
+    case 8: hipLaunchKernelGGL(ln_frag_kernel<8>, dim3(M), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b); break;
+    default:
+        fprintf(stderr, "ctk_ln_frag: %d partial slices not supported (0, 1, 2, 4, 8)\n", nparts);
+        exit(1);
+    }
 }
 
 extern "C" void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, const int *pos_len,

@@ -38,6 +38,8 @@ typedef struct {
     int max_requests;   /* request pool capacity                                */
     int max_frames;     /* largest encoder length a request may have (<= 2048) */
     int kv_bf16;        /* 1: bf16 KV caches, 0: fp32                           */
+    int max_tokens;     /* longest prompt + limit of any request (sizes the self
+                           caches), <= MAX_SEQ; 0 means MAX_SEQ                 */
 } HipbConfig;
 
 /* Request policy flags. */

@@ -148,7 +148,9 @@ def test_engine_logits_match_oracle(hip, hot, mels, kv_bf16):
 
 def test_engine_continuous_batching(hip, hot, mels, oracle_runs):
     """Six requests through two slots: freed slots are refilled on device."""
-    eng = cb.Engine(hot, slots=2, max_requests=8, max_frames=64, kv_bf16=True)
+    # self caches sized to the longest request (max_tokens)
+    eng = cb.Engine(hot, slots=2, max_requests=8, max_frames=64, kv_bf16=True,
+                    max_tokens=len(cb.PROMPT) + max(LIMITS))
     order = [0, 1, 2, 2, 0, 1]
     try:
         for i in order:
