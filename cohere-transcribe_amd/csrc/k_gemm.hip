@@ -286,7 +286,7 @@ __global__ __launch_bounds__(64 * DSPLIT) void gemm_dec_kernel(CtGemm g) {
 constexpr int BT = 128, BK = 32, LDP = BK + 8;   // LDS row pitch 80 B (conflict-free b128 reads)
 
 template <bool GLU>
-__global__ __launch_bounds__(256) void gemm_big_kernel(CtGemm g, int n_mt, int n_nt) {
+__global__ __launch_bounds__(256) void gemm_big_kernel(CtGemm g, int n_mt, int n_nt, int vepi) {
     // one LDS block: [A hi x2][A lo x2][W x2] stage buffers; the GLU epilogue
     // reuses its first 32 KB
     __shared__ __attribute__((aligned(16))) uint16_t smem[6 * BT * LDP];
@@ -419,20 +419,46 @@ __global__ __launch_bounds__(256) void gemm_big_kernel(CtGemm g, int n_mt, int n
         }
         return;
     }
+    // epilogue in two 64-row halves through LDS (32 KB each): each thread
+    // finishes 8 consecutive columns of a row (16-byte stores when vepi)
+    __syncthreads();
+    float *sc = reinterpret_cast<float *>(smem);
 #pragma unroll
-    for (int cb = 0; cb < 4; cb++) {
-        const int col = c0 + wnn + cb * 16 + r;
-        if (col >= g.N) continue;
-        const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
+    for (int half = 0; half < 2; half++) {
+        if ((wm >> 6) == half) {
 #pragma unroll
-        for (int rb = 0; rb < 4; rb++)
+            for (int rb = 0; rb < 4; rb++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int m = m0 + wm + rb * 16 + kg * 4 + j;
-                if (m >= g.M) continue;
-                if (g.row_mask && !g.row_mask[m]) continue;
-                store_out(g, m, col, acc[rb][cb][j] + ba);
+                for (int cb = 0; cb < 4; cb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int row = rb * 16 + kg * 4 + j;
+                        sc[row * BT + ((wnn + cb * 16 + r) ^ (((row >> 2) & 3) << 4))] = acc[rb][cb][j];
+                    }
+        }
+        __syncthreads();
+        for (int it = tid; it < 64 * (BT / 8); it += 256) {
+            const int row = it / (BT / 8), g8 = it % (BT / 8);
+            const int m = m0 + 64 * half + row, col = c0 + g8 * 8;
+            if (m >= g.M || col >= g.N) continue;
+            if (g.row_mask && !g.row_mask[m]) continue;
+            const float4 *pv = reinterpret_cast<const float4 *>(sc + row * BT + ((g8 * 8) ^ (((row >> 2) & 3) << 4)));
+            const float4 v0 = pv[0], v1 = pv[1];
+            float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            if (vepi) {
+                if (g.bias) {
+                    const u16x8 b8 = *reinterpret_cast<const u16x8 *>(g.bias + col);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] += bf2f(b8[i]);
+                }
+                store_out8(g, m, col, v);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (col + i < g.N) store_out(g, m, col + i, v[i] + (g.bias ? bf2f(g.bias[col + i]) : 0.0f));
             }
+        }
+        __syncthreads();
     }
 }
 
@@ -451,6 +477,10 @@ __global__ __launch_bounds__(256) void gemm_big_kernel(CtGemm g, int n_mt, int n
 // Per element: K-steps in order, hi then lo (as every other GEMM kernel).
 // ---------------------------------------------------------------------------
 constexpr int SBM = 128, SBN = 256, SBK = 32, SST = 4, SGM = 4;
+// rows from which the 256-row tile kernel takes pre-split GEMMs
+#ifndef CT_SPLIT256_MIN_M
+#define CT_SPLIT256_MIN_M 1024
+#endif
 constexpr int S_A = SBM * SBK, S_W = SBN * SBK;       // elements per operand tile
 constexpr int STAGE_ELEMS = 2 * S_A + S_W;            // Ahi, Alo, W
 constexpr int S_INSTR = STAGE_ELEMS / 512;            // 1-KB DMA instructions per stage (32)
@@ -590,27 +620,9 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
         }
         return;
     }
-    if (!vepi) {
-#pragma unroll
-        for (int cb = 0; cb < 4; cb++) {
-            const int col = c0 + wn + cb * 16 + r;
-            if (col >= g.N) continue;
-            const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
-#pragma unroll
-            for (int rb = 0; rb < 4; rb++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int m = m0 + wm + rb * 16 + kg * 4 + j;
-                    if (m >= g.M) continue;
-                    if (g.row_mask && !g.row_mask[m]) continue;
-                    store_out(g, m, col, acc[rb][cb][j] + ba);
-                }
-        }
-        return;
-    }
-    // Vector epilogue: the 128 x 256 fp32 tile goes through the (now idle)
-    // LDS ring, then each thread finishes 8 consecutive columns of a row and
-    // writes them as 16-byte pieces, 32 threads per 1-KB row run.  Column
+    // Epilogue: the 128 x 256 fp32 tile goes through the (now idle) LDS ring,
+    // then each thread finishes 8 consecutive columns of a row and writes them
+    // as 16-byte pieces (when vepi allows), 32 threads per 1-KB row run.  Column
     // groups of 16 are XOR-swizzled by row so the fragment writes spread over
     // all banks.
     float *sc = reinterpret_cast<float *>(smem);
@@ -634,11 +646,164 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
         const float4 v0 = pv[0], v1 = pv[1];
         float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         if (g.bias) {
-            const u16x8 b8 = *reinterpret_cast<const u16x8 *>(g.bias + col);
+            if (vepi) {
+                const u16x8 b8 = *reinterpret_cast<const u16x8 *>(g.bias + col);
 #pragma unroll
-            for (int i = 0; i < 8; i++) v[i] += bf2f(b8[i]);
+                for (int i = 0; i < 8; i++) v[i] += bf2f(b8[i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] += col + i < g.N ? bf2f(g.bias[col + i]) : 0.0f;
+            }
         }
-        store_out8(g, m, col, v);
+        if (vepi) {
+            store_out8(g, m, col, v);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (col + i < g.N) store_out(g, m, col + i, v[i]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The same pre-split GEMM with 256 x 256 tiles for many-row problems: 8 waves
+// as 4 (rows) x 2 (columns), each a 64 x 128 sub-tile (4 x 8 MFMA 16x16x32,
+// hi then lo), so a K-step reads 16 fragments from LDS for 64 MFMAs (the
+// 128-row tile reads 12 for 32) and one barrier covers twice the work.
+// 3-stage ring of 48 KB (A hi, A lo: 256 x 32 each; W: 256 x 32), 6 DMA
+// instructions per wave per stage.  Per element the sequence is unchanged.
+// ---------------------------------------------------------------------------
+constexpr int TBM = 256, TST = 3;
+constexpr int T_A = TBM * SBK;
+constexpr int T_STAGE = 2 * T_A + S_W;
+constexpr int T_PER_WAVE = T_STAGE / 512 / 8;     // 6
+
+__global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, int n_nt, int vepi) {
+    __shared__ __attribute__((aligned(16))) uint16_t smem[TST * T_STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int r = lane & 15, kg = lane >> 4;
+    const int nt = n_mt * n_nt;
+    const int per = (nt + 7) / 8;
+    const int t = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (t >= nt) return;
+    const int gsize = SGM * n_nt;
+    const int grp = t / gsize, rem = t % gsize;
+    const int gm = min(SGM, n_mt - grp * SGM);
+    const int tn = rem / gm, tm = grp * SGM + rem % gm;
+    const int m0 = tm * TBM, c0 = tn * SBN;
+
+    // instruction i = wv + 8*j: i < 16 A-hi rows 16i.., i < 32 A-lo, else W
+    const uint16_t *src[T_PER_WAVE];
+    int dst[T_PER_WAVE];
+#pragma unroll
+    for (int j = 0; j < T_PER_WAVE; j++) {
+        const int i = wv + 8 * j;
+        const int Rl = lane >> 2, ch = lane & 3;
+        if (i < 32) {
+            const int R = (i & 15) * 16 + Rl;
+            const int m = min(m0 + R, g.M - 1);
+            src[j] = (i < 16 ? g.Ahi : g.Alo) + (long)m * g.lda + swz(R, ch) * 8;
+            dst[j] = (i < 16 ? 0 : T_A) + (i & 15) * 16 * SBK;
+        } else {
+            const int R = (i - 32) * 16 + Rl;
+            const int n = min(c0 + R, g.N - 1);
+            src[j] = g.W + (long)n * g.K + swz(R, ch) * 8;
+            dst[j] = 2 * T_A + (i - 32) * 16 * SBK;
+        }
+    }
+    auto issue = [&](int kt) {
+        uint16_t *stage = smem + (kt % TST) * T_STAGE;
+#pragma unroll
+        for (int j = 0; j < T_PER_WAVE; j++) lds_dma16(src[j] + kt * SBK, stage + dst[j]);
+    };
+
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const int wm = (wv >> 1) * 64, wn = (wv & 1) * 128;
+    const int nk = g.K / SBK;
+#pragma unroll
+    for (int p = 0; p < TST - 1; p++)
+        if (p < nk) issue(p);
+    for (int kt = 0; kt < nk; kt++) {
+        // this wave's part of stage kt landed; at most one younger stage in flight
+        if (kt + 1 < nk) __builtin_amdgcn_s_waitcnt((T_PER_WAVE & 0xF) | (0x7 << 4) | (0xF << 8));
+        else __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + TST - 1 < nk) issue(kt + TST - 1);
+        const uint16_t *st = smem + (kt % TST) * T_STAGE;
+        const uint16_t *sAh = st, *sAl = st + T_A, *sW = st + 2 * T_A;
+        bf16x8 bfr[8];
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++) {
+            const int R = wn + cb * 16 + r;
+            bfr[cb] = as_bf16x8(*reinterpret_cast<const u16x8 *>(sW + R * SBK + swz(R, kg) * 8));
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            const int R = wm + rb * 16 + r;
+            const int off = R * SBK + swz(R, kg) * 8;
+            const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAh + off));
+            const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
+#pragma unroll
+            for (int cb = 0; cb < 8; cb++) {
+                acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
+                acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    // epilogue in two 128-row halves through the LDS ring (128 KB each); rows
+    // finish 8 columns per thread (16-byte stores when vepi allows)
+    float *sc = reinterpret_cast<float *>(smem);
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+        if ((wm >> 7) == half) {
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                for (int cb = 0; cb < 8; cb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int row = wm - 128 * half + rb * 16 + kg * 4 + j;
+                        const int col = (wn + cb * 16 + r) ^ (((row >> 2) & 3) << 4);
+                        sc[row * SBN + col] = acc[rb][cb][j];
+                    }
+        }
+        __syncthreads();
+        for (int it = tid; it < 128 * (SBN / 8); it += 512) {
+            const int row = it / (SBN / 8), g8 = it % (SBN / 8);
+            const int m = m0 + 128 * half + row, col = c0 + g8 * 8;
+            if (m >= g.M || col >= g.N) continue;
+            if (g.row_mask && !g.row_mask[m]) continue;
+            const float4 *pv = reinterpret_cast<const float4 *>(sc + row * SBN + ((g8 * 8) ^ (((row >> 2) & 3) << 4)));
+            const float4 v0 = pv[0], v1 = pv[1];
+            float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            if (g.bias) {
+                if (vepi) {
+                    const u16x8 b8 = *reinterpret_cast<const u16x8 *>(g.bias + col);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] += bf2f(b8[i]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] += col + i < g.N ? bf2f(g.bias[col + i]) : 0.0f;
+                }
+            }
+            if (vepi) {
+                store_out8(g, m, col, v);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (col + i < g.N) store_out(g, m, col + i, v[i]);
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -804,6 +969,21 @@ static int vector_epilogue_ok(const CtGemm *g) {
     return 1;
 }
 
+// Tile-count model for the two pre-split kernels: a 256-row tile costs about
+// 1.74 128-row tiles (measured), and tiles run in rounds over the CUs.
+static int prefer_256(int M, int n_nt) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+    }
+    const long t128 = (long)((M + SBM - 1) / SBM) * n_nt, t256 = (long)((M + TBM - 1) / TBM) * n_nt;
+    const double r128 = (double)((t128 + cus - 1) / cus), r256 = (double)((t256 + cus - 1) / cus);
+    return r256 * 1.74 < r128;
+}
+
 extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
     if (g->M <= 0 || g->N <= 0) return;
     if (g->epi == CT_EPI_GLU && g->N != 2 * g->glu_half) {
@@ -822,6 +1002,11 @@ extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
         const int n_nt = glu ? (g->glu_half + SBN / 2 - 1) / (SBN / 2) : (g->N + SBN - 1) / SBN;
         const int nt = n_mt * n_nt, per = (nt + 7) / 8;
         const int vepi = vector_epilogue_ok(g);
+        if (!glu && g->M >= CT_SPLIT256_MIN_M && prefer_256(g->M, n_nt)) {
+            const int n_mt2 = (g->M + TBM - 1) / TBM, nt2 = n_mt2 * n_nt, per2 = (nt2 + 7) / 8;
+            hipLaunchKernelGGL(gemm_split256_kernel, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
+            return;
+        }
         if (glu) hipLaunchKernelGGL(gemm_split_kernel<true>, dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, 0);
         else hipLaunchKernelGGL(gemm_split_kernel<false>, dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, vepi);
         return;
@@ -842,8 +1027,9 @@ extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
         const int n_nt = glu ? (g->glu_half + BT / 2 - 1) / (BT / 2) : (g->N + BT - 1) / BT;
         const int nt = n_mt * n_nt, per = (nt + 7) / 8;
         const int blocks = per * 8;
-        if (glu) hipLaunchKernelGGL(gemm_big_kernel<true>, dim3(blocks), dim3(256), 0, s, *g, n_mt, n_nt);
-        else hipLaunchKernelGGL(gemm_big_kernel<false>, dim3(blocks), dim3(256), 0, s, *g, n_mt, n_nt);
+        if (glu) hipLaunchKernelGGL(gemm_big_kernel<true>, dim3(blocks), dim3(256), 0, s, *g, n_mt, n_nt, 0);
+        else hipLaunchKernelGGL(gemm_big_kernel<false>, dim3(blocks), dim3(256), 0, s, *g, n_mt, n_nt,
+                                vector_epilogue_ok(g));
         return;
     }
     if (vec) { if (glu) dispatch<true, true>(*g, s); else dispatch<true, false>(*g, s); }
