@@ -13,20 +13,34 @@
 namespace {
 
 // ---------------------------------------------------------------------------
-// Relative-position attention core (backends/cpu/backend.c:262-296).
-// Workgroup = QB query rows x one head.  S[q][k] = ((Q_q+u).K_k)*s +
+// Relative-position attention core (backends/cpu/backend.c:262-296) on fp32
+// MFMA (v_mfma_f32_16x16x4f32: exact fp32 products, fp32 sums).
+// Workgroup = 16 query rows x one head, 4 waves.  S[q][k] = ((Q_q+u).K_k)*s +
 // ((Q_q+v).P_{k+T-1-q})*s with s = 1/sqrt(160), softmax over k, then S V.
-// Phase A walks keys, phase B walks the P window (T+QB-1 rows); each score
-// receives exactly one term from each phase.
+//   A: 16 x 16 score tiles over the keys (waves take tiles w, w+4, ...);
+//   B: 16 x 16 tiles over the window of T+15 P rows the block needs; window
+//      row j of query i is key j + i - 15, so each product lands on exactly
+//      one score and is added there;
+//   softmax per row in LDS; C: O = S V as 10 tiles of 16 head dimensions.
+// MFMA lanes: A[i][k] from lane 16k + i, B[k][j] from lane 16k + j, result
+// D[4(l/16) + r][l%16] in lane l.  Scores live in LDS, row stride ldS.
+// Rows of Q, K, P, V must be 16-byte aligned (the launchers check).
 // ---------------------------------------------------------------------------
-template <int QB, bool PACKED>
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+constexpr int RQ = 16;                // query rows per workgroup
+constexpr int RKS = ENC_DK / 4;       // 40 MFMA K-steps over the head dimension
+
+template <bool PACKED>
 __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float *Q, const float *K,
                                                           const float *V, const float *P,
                                                           const uint16_t *pbu, const uint16_t *pbv,
                                                           int T_arg, int T_max, const int *seq_off,
                                                           const int *seq_T, const int *blk_seq,
-                                                          const int *blk_q0) {
-    extern __shared__ float smem[];
+                                                          const int *blk_q0, int ldS) {
+    extern __shared__ float S[];      // [RQ][ldS]
     int T, q0;
     long off = 0;
     if (PACKED) {
@@ -37,63 +51,83 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
         P += (long)(T_max - T) * ENC_D;     // this clip's window of the T_max table
     } else {
         T = T_arg;
-        q0 = blockIdx.x * QB;
+        q0 = blockIdx.x * RQ;
     }
     Q += off * ENC_D; K += off * ENC_D; V += off * ENC_D; O += off * ENC_D;
-    float *qu = smem;                         // [QB][160]
-    float *qv = qu + QB * ENC_DK;             // [QB][160]
-    float *S = qv + QB * ENC_DK;              // [QB][T]
-    const int h = blockIdx.y, tid = threadIdx.x;
-    const int nq = min(QB, T - q0);
+    const int h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int li = lane & 15, lk = lane >> 4;
+    const int nq = min(RQ, T - q0);
+    const long hc = (long)h * ENC_DK;
     const float sc = 1.0f / sqrtf((float)ENC_DK);
-    for (int i = tid; i < QB * ENC_DK; i += 256) {
-        const int qi = i / ENC_DK, d = i % ENC_DK;
-        const float x = qi < nq ? Q[(long)(q0 + qi) * ENC_D + h * ENC_DK + d] : 0.0f;
-        qu[i] = x + bf2f(pbu[h * ENC_DK + d]);
-        qv[i] = x + bf2f(pbv[h * ENC_DK + d]);
+
+    // The MFMA K index of step st in lane group lk is head dim 40*lk + st:
+    // every lane reads one contiguous 160-byte run of a row (10 float4).
+    // A fragments of Q+u and Q+v: row li.
+    float au[RKS], av[RKS];
+    {
+        const bool ok = li < nq;
+        const float4 *qp = reinterpret_cast<const float4 *>(Q + (long)(q0 + li) * ENC_D + hc + RKS * lk);
+#pragma unroll
+        for (int c = 0; c < RKS / 4; c++) {
+            const float4 x = ok ? qp[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int st = 4 * c + e, d = RKS * lk + st;
+                au[st] = xs[e] + bf2f(pbu[hc + d]);
+                av[st] = xs[e] + bf2f(pbv[hc + d]);
+            }
+        }
+    }
+    // A: content scores
+    const int nkt = (T + 15) / 16;
+    for (int kt = w; kt < nkt; kt += 4) {
+        const int key = kt * 16 + li;
+        const bool ok = key < T;
+        const float4 *kp = reinterpret_cast<const float4 *>(K + (long)key * ENC_D + hc + RKS * lk);
+        float b[RKS];
+#pragma unroll
+        for (int c = 0; c < RKS / 4; c++) {
+            const float4 x = ok ? kp[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            b[4 * c] = x.x; b[4 * c + 1] = x.y; b[4 * c + 2] = x.z; b[4 * c + 3] = x.w;
+        }
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < RKS; st++) acc = mfma4(au[st], b[st], acc);
+        if (ok) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) S[(4 * lk + j) * ldS + key] = acc[j] * sc;
+        }
     }
     __syncthreads();
-    // phase A: content term
-    for (int k = tid; k < T; k += 256) {
-        const float *kr = K + (long)k * ENC_D + h * ENC_DK;
-        float acc[QB];
+    // B: position scores over window rows p = plo + win, win in [0, T+15)
+    const int plo = T - 1 - (q0 + RQ - 1);
+    const int nwt = (T + RQ - 1 + 15) / 16;
+    for (int wt = w; wt < nwt; wt += 4) {
+        const int win = wt * 16 + li, p = plo + win;
+        const bool ok = win < T + RQ - 1 && p >= 0 && p <= 2 * T - 2;
+        const float4 *pp = reinterpret_cast<const float4 *>(P + (long)p * ENC_D + hc + RKS * lk);
+        float b[RKS];
 #pragma unroll
-        for (int qi = 0; qi < QB; qi++) acc[qi] = 0.0f;
-        for (int d = 0; d < ENC_DK; d++) {
-            const float kd = kr[d];
-#pragma unroll
-            for (int qi = 0; qi < QB; qi++) acc[qi] += qu[qi * ENC_DK + d] * kd;
+        for (int c = 0; c < RKS / 4; c++) {
+            const float4 x = ok ? pp[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            b[4 * c] = x.x; b[4 * c + 1] = x.y; b[4 * c + 2] = x.z; b[4 * c + 3] = x.w;
         }
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int qi = 0; qi < QB; qi++) S[qi * T + k] = acc[qi] * sc;
-    }
-    __syncthreads();
-    // phase B: position term over the window of P rows this query block uses
-    const int plo = T - 1 - (q0 + QB - 1);
-    const int nwin = T + QB - 1;
-    for (int w = tid; w < nwin; w += 256) {
-        const int p = plo + w;
-        if (p < 0 || p > 2 * T - 2) continue;
-        const float *pr = P + (long)p * ENC_D + h * ENC_DK;
-        float acc[QB];
+        for (int st = 0; st < RKS; st++) acc = mfma4(av[st], b[st], acc);
+        // column li of the tile is window row win; query i = 4*lk + j reads
+        // it as key win + i - 15
 #pragma unroll
-        for (int qi = 0; qi < QB; qi++) acc[qi] = 0.0f;
-        for (int d = 0; d < ENC_DK; d++) {
-            const float pd = pr[d];
-#pragma unroll
-            for (int qi = 0; qi < QB; qi++) acc[qi] += qv[qi * ENC_DK + d] * pd;
-        }
-#pragma unroll
-        for (int qi = 0; qi < QB; qi++) {
-            const int k = p - (T - 1) + q0 + qi;
-            if (qi < nq && k >= 0 && k < T) S[qi * T + k] += acc[qi] * sc;
+        for (int j = 0; j < 4; j++) {
+            const int qi = 4 * lk + j, k = win + qi - (RQ - 1);
+            if (ok && qi < nq && k >= 0 && k < T) S[qi * ldS + k] += acc[j] * sc;
         }
     }
     __syncthreads();
     // softmax per row (backends/cpu/backend.c:67-73)
-    const int wv = tid >> 6, lane = tid & 63;
-    for (int qi = wv; qi < nq; qi += 4) {
-        float *row = S + qi * T;
+    for (int qi = w; qi < nq; qi += 4) {
+        float *row = S + qi * ldS;
         float mx = -INFINITY;
         for (int k = lane; k < T; k += 64) mx = fmaxf(mx, row[k]);
         mx = wave_max(mx);
@@ -103,17 +137,35 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
         for (int k = lane; k < T; k += 64) row[k] /= sum;
     }
     __syncthreads();
-    if (tid < ENC_DK) {
-        const int d = tid;
-        float acc[QB];
+    // C: O = S V, 10 tiles of 16 dimensions, keys in steps of 4
+    for (int dt = w; dt < ENC_DK / 16; dt += 4) {
+        const int d = dt * 16 + li;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const float *vp = V + hc + d;
+        const float *sr = S + (li < nq ? li : 0) * ldS;
+        int k0 = 0;
+        for (; k0 + 32 <= T; k0 += 32) {
+            float a[8], bv[8];
 #pragma unroll
-        for (int qi = 0; qi < QB; qi++) acc[qi] = 0.0f;
-        for (int k = 0; k < T; k++) {
-            const float v = V[(long)k * ENC_D + h * ENC_DK + d];
+            for (int u = 0; u < 8; u++) {
+                const int k = k0 + 4 * u + lk;
+                a[u] = sr[k];
+                bv[u] = vp[(long)k * ENC_D];
+            }
 #pragma unroll
-            for (int qi = 0; qi < QB; qi++) acc[qi] += S[qi * T + k] * v;
+            for (int u = 0; u < 8; u++) acc = mfma4(a[u], bv[u], acc);
         }
-        for (int qi = 0; qi < nq; qi++) O[(long)(q0 + qi) * ENC_D + h * ENC_DK + d] = acc[qi];
+        for (; k0 < T; k0 += 4) {
+            const int k = k0 + lk;
+            const float a = k < T ? sr[k] : 0.0f;
+            const float bv = k < T ? vp[(long)k * ENC_D] : 0.0f;
+            acc = mfma4(a, bv, acc);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int qi = 4 * lk + j;
+            if (qi < nq) O[(long)(q0 + qi) * ENC_D + hc + d] = acc[j];
+        }
     }
 }
 
@@ -230,7 +282,27 @@ inline unsigned nblk(long n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
 
-static int relpos_qb(int max_T) { return max_T <= 512 ? 16 : 4; }
+static int relpos_qb(int) { return RQ; }
+
+// Score rows of ldS floats: T rounded up to 16, plus 4 so that 16 rows x 4
+// columns of a fragment read fall in distinct banks.
+static int relpos_lds(int max_T, size_t *bytes) {
+    const int ldS = (max_T + 15) / 16 * 16 + 4;
+    *bytes = (size_t)RQ * ldS * sizeof(float);
+    return ldS;
+}
+
+template <bool PACKED>
+static void relpos_allow_lds(size_t bytes) {
+    static size_t allowed = 64 * 1024;
+    if (bytes <= allowed) return;
+    if (hipFuncSetAttribute((const void *)relpos_attn_kernel<PACKED>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess) {
+        fprintf(stderr, "relpos_attn: cannot reserve %zu bytes of LDS\n", bytes);
+        exit(1);
+    }
+    allowed = bytes;
+}
 
 extern "C" void ctk_relpos_attn(float *O, const float *Q, const float *K, const float *V,
                                 const float *P, const uint16_t *pbu, const uint16_t *pbv,
@@ -240,15 +312,16 @@ extern "C" void ctk_relpos_attn(float *O, const float *Q, const float *K, const 
         fprintf(stderr, "ctk_relpos_attn: T=%d exceeds the supported 2048 frames\n", T);
         exit(1);
     }
-    const int qb = relpos_qb(T);
-    const size_t lds = (2 * qb * ENC_DK + qb * (size_t)T) * sizeof(float);
-    const dim3 grid((T + qb - 1) / qb, ENC_H);
-    if (qb == 16)
-        hipLaunchKernelGGL((relpos_attn_kernel<16, false>), grid, dim3(256), lds, s,
-                           O, Q, K, V, P, pbu, pbv, T, T, nullptr, nullptr, nullptr, nullptr);
-    else
-        hipLaunchKernelGGL((relpos_attn_kernel<4, false>), grid, dim3(256), lds, s,
-                           O, Q, K, V, P, pbu, pbv, T, T, nullptr, nullptr, nullptr, nullptr);
+    if (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)P) & 15) {
+        fprintf(stderr, "ctk_relpos_attn: Q, K, V and P must be 16-byte aligned\n");
+        exit(1);
+    }
+    size_t lds;
+    const int ldS = relpos_lds(T, &lds);
+    relpos_allow_lds<false>(lds);
+    const dim3 grid((T + RQ - 1) / RQ, ENC_H);
+    hipLaunchKernelGGL((relpos_attn_kernel<false>), grid, dim3(256), lds, s,
+                       O, Q, K, V, P, pbu, pbv, T, T, nullptr, nullptr, nullptr, nullptr, ldS);
 }
 
 extern "C" int ctk_relpos_plan(int *blk_seq, int *blk_q0, const int *seq_T, int n_seq) {
@@ -274,15 +347,16 @@ extern "C" void ctk_relpos_attn_packed(float *O, const float *Q, const float *K,
         fprintf(stderr, "ctk_relpos_attn_packed: T=%d exceeds the supported 2048 frames\n", max_T);
         exit(1);
     }
-    const int qb = relpos_qb(max_T);
-    const size_t lds = (2 * qb * ENC_DK + qb * (size_t)max_T) * sizeof(float);
+    if (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)P) & 15) {
+        fprintf(stderr, "ctk_relpos_attn: Q, K, V and P must be 16-byte aligned\n");
+        exit(1);
+    }
+    size_t lds;
+    const int ldS = relpos_lds(max_T, &lds);
+    relpos_allow_lds<true>(lds);
     const dim3 grid(n_blk, ENC_H);
-    if (qb == 16)
-        hipLaunchKernelGGL((relpos_attn_kernel<16, true>), grid, dim3(256), lds, s,
-                           O, Q, K, V, P, pbu, pbv, 0, T_max, seq_off, seq_T, blk_seq, blk_q0);
-    else
-        hipLaunchKernelGGL((relpos_attn_kernel<4, true>), grid, dim3(256), lds, s,
-                           O, Q, K, V, P, pbu, pbv, 0, T_max, seq_off, seq_T, blk_seq, blk_q0);
+    hipLaunchKernelGGL((relpos_attn_kernel<true>), grid, dim3(256), lds, s,
+                       O, Q, K, V, P, pbu, pbv, 0, T_max, seq_off, seq_T, blk_seq, blk_q0, ldS);
 }
 
 extern "C" void ctk_dwconv_bn_silu(float *out, const float *in, int T, const uint16_t *dww,
