@@ -184,7 +184,7 @@ def encoder_gemm_roofline(model, ev, M=16384, reps=10):
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     return {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
-            "kernel": "gemm_split_kernel<false> (encoder FFN up, SiLU, pre-split in/out)",
+            "kernel": "gemm_split256_kernel (encoder FFN up, SiLU, pre-split in/out)",
             "avg_launch_us": round(ms * 1e3, 1), "flops_per_launch": 2 * M * N * K,
             "workload": f"M={M} N={N} K={K}",
             "note": "activations as hi+lo bf16 against exact bf16 weights: the MFMA pipe runs "

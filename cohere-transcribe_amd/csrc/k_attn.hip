@@ -21,7 +21,11 @@
 
 namespace {
 
-constexpr int CT_ATTN_QPARTS = 8;   // most query partial slices a launch may pass
+constexpr int CT_ATTN_QPARTS = 4;   // most query partial slices a launch may pass
+// lanes per key (16: 8 head dims a lane, 8: 16 a lane)
+#ifndef CT_ATTN_LPK
+#define CT_ATTN_LPK 16
+#endif
 
 template <bool BF16, bool VEC>
 __device__ __forceinline__ void load8(const void *base, long off, float (&v)[8]) {
@@ -56,44 +60,62 @@ __device__ __forceinline__ void store_out(const CtAttn &a, int bq, int col, long
     }
 }
 
-template <bool BF16, bool VEC>
+// Sum over aligned groups of LPK lanes (16 or 8), every lane gets the result.
+template <int LPK>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_row<0xB1>(v);
+    v += dpp_row<0x4E>(v);
+    v += dpp_row<0x141>(v);
+    if (LPK == 16) v += dpp_row<0x140>(v);
+    return v;
+}
+
+// LPK lanes per key: lane s of a group owns head dims [s*DPL, s*DPL + DPL),
+// DPL = 128 / LPK, read as NV 16-byte (bf16) pieces; NG = 256 / LPK groups
+// stream keys g, g + NG, ... (KPI of them per trip, loads first).
+template <bool BF16, bool VEC, int LPK>
 __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
+    constexpr int DPL = DEC_DK / LPK, NV = DPL / 8, NG = 256 / LPK;
     const int bq = blockIdx.x, h = blockIdx.y, ch = blockIdx.z;
     const int b = bq / a.T_q, qi = bq % a.T_q;
-    const int tid = threadIdx.x, g = tid >> 4, l16 = tid & 15;
+    const int tid = threadIdx.x, g = tid / LPK, ls = tid % LPK;
     const long qoff = (long)b * a.q_sb + (long)qi * a.q_st + h * DEC_DK;
     // Every load the prologue needs is issued before any of them is used:
     // the length, the cache index and the query (or its K-slice partials).
     const int T = a.lens ? a.lens[(long)b * a.lens_step] : a.len_const;
     const long item = a.kv_index ? (long)a.kv_index[b] : (long)b;
-    float q[8];
+    float q[DPL];
     if (a.q_parts) {
         // query = ((part 0 + part 1) + ...) + bias, the decode GEMM's K-slices
-        const float *qp = a.q_parts + qoff + l16 * 8;
-        float4 pr[CT_ATTN_QPARTS][2];
+        const float *qp = a.q_parts + qoff + ls * DPL;
+        float4 pr[CT_ATTN_QPARTS][DPL / 4];
 #pragma unroll
         for (int p = 0; p < CT_ATTN_QPARTS; p++)
             if (p < a.q_nparts) {
-                pr[p][0] = *reinterpret_cast<const float4 *>(qp + p * a.q_pstride);
-                pr[p][1] = *reinterpret_cast<const float4 *>(qp + p * a.q_pstride + 4);
+#pragma unroll
+                for (int c = 0; c < DPL / 4; c++)
+                    pr[p][c] = *reinterpret_cast<const float4 *>(qp + p * a.q_pstride + 4 * c);
             }
-        const u16x8 bb = a.q_bias ? *reinterpret_cast<const u16x8 *>(a.q_bias + h * DEC_DK + l16 * 8)
-                                  : (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
-        q[0] = pr[0][0].x; q[1] = pr[0][0].y; q[2] = pr[0][0].z; q[3] = pr[0][0].w;
-        q[4] = pr[0][1].x; q[5] = pr[0][1].y; q[6] = pr[0][1].z; q[7] = pr[0][1].w;
+#pragma unroll
+        for (int c = 0; c < DPL / 4; c++) {
+            q[4 * c] = pr[0][c].x; q[4 * c + 1] = pr[0][c].y; q[4 * c + 2] = pr[0][c].z; q[4 * c + 3] = pr[0][c].w;
+        }
 #pragma unroll
         for (int p = 1; p < CT_ATTN_QPARTS; p++)
             if (p < a.q_nparts) {
-                q[0] += pr[p][0].x; q[1] += pr[p][0].y; q[2] += pr[p][0].z; q[3] += pr[p][0].w;
-                q[4] += pr[p][1].x; q[5] += pr[p][1].y; q[6] += pr[p][1].z; q[7] += pr[p][1].w;
+#pragma unroll
+                for (int c = 0; c < DPL / 4; c++) {
+                    q[4 * c] += pr[p][c].x; q[4 * c + 1] += pr[p][c].y;
+                    q[4 * c + 2] += pr[p][c].z; q[4 * c + 3] += pr[p][c].w;
+                }
             }
         if (a.q_bias)
 #pragma unroll
-            for (int i = 0; i < 8; i++) q[i] += bf2f(bb[i]);
+            for (int i = 0; i < DPL; i++) q[i] += bf2f(a.q_bias[h * DEC_DK + ls * DPL + i]);
     } else {
-        const float *qp = a.Q + qoff + l16 * 8;
+        const float *qp = a.Q + qoff + ls * DPL;
 #pragma unroll
-        for (int i = 0; i < 8; i++) q[i] = qp[i];
+        for (int i = 0; i < DPL; i++) q[i] = qp[i];
     }
     if (T <= 0) {
         if (ch == 0 && tid < DEC_DK) store_out(a, bq, h * DEC_DK + tid, qoff + tid, 0.0f);
@@ -106,34 +128,34 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
     const int kb = a.chunk > 0 ? ch * a.chunk : 0;
     const int ke = ch == nch - 1 ? T : kb + a.chunk;
     const float *mrow = a.mask ? a.mask + (long)qi * T : nullptr;
-    const long base = item * a.kv_sb + (long)h * a.kv_sh + l16 * 8;
+    const long base = item * a.kv_sb + (long)h * a.kv_sh + ls * DPL;
 
-    float m = -INFINITY, l = 0.0f, o[8];
+    float m = -INFINITY, l = 0.0f, o[DPL];
 #pragma unroll
-    for (int i = 0; i < 8; i++) o[i] = 0.0f;
+    for (int i = 0; i < DPL; i++) o[i] = 0.0f;
 
-    // KPI keys per group per trip, all loads issued first: group g takes keys
-    // g, g + 16, g + 32, ... in that order (the order the softmax sees them)
 #ifndef CT_ATTN_KPI
 #define CT_ATTN_KPI 2
 #endif
     constexpr int KPI = BF16 ? CT_ATTN_KPI : 4;
-    // keeps the raw 16-byte rows in registers until use (bf16: 8 VGPRs a key)
+    // raw 16-byte pieces stay in registers until use (bf16: 4 VGPRs a piece)
     using Raw = typename std::conditional<BF16 && VEC, u16x8, float[8]>::type;
-    for (int k0 = kb + g; k0 < ke; k0 += 16 * KPI) {
-        Raw kr[KPI], vr[KPI];
+    for (int k0 = kb + g; k0 < ke; k0 += NG * KPI) {
+        Raw kr[KPI][NV], vr[KPI][NV];
 #pragma unroll
         for (int j = 0; j < KPI; j++) {
-            const int k = k0 + 16 * j;
+            const int k = k0 + NG * j;
             if (k < ke) {
-                if constexpr (BF16 && VEC) {
-                    const uint16_t *kp = reinterpret_cast<const uint16_t *>(a.K) + base + (long)k * a.kv_st;
-                    const uint16_t *vp = reinterpret_cast<const uint16_t *>(a.V) + base + (long)k * a.kv_st;
-                    kr[j] = *reinterpret_cast<const u16x8 *>(kp);
-                    vr[j] = *reinterpret_cast<const u16x8 *>(vp);
-                } else {
-                    load8<BF16, VEC>(a.K, base + (long)k * a.kv_st, kr[j]);
-                    load8<BF16, VEC>(a.V, base + (long)k * a.kv_st, vr[j]);
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const long off = base + (long)k * a.kv_st + 8 * v;
+                    if constexpr (BF16 && VEC) {
+                        kr[j][v] = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.K) + off);
+                        vr[j][v] = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.V) + off);
+                    } else {
+                        load8<BF16, VEC>(a.K, off, kr[j][v]);
+                        load8<BF16, VEC>(a.V, off, vr[j][v]);
+                    }
                 }
             }
         }
@@ -143,18 +165,20 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
         for (int j = 0; j < KPI; j++) {
             float d = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float kf;
-                if constexpr (BF16 && VEC) kf = bf2f(kr[j][i]);
-                else kf = kr[j][i];
-                d += q[i] * kf;
-            }
+            for (int v = 0; v < NV; v++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    float kf;
+                    if constexpr (BF16 && VEC) kf = bf2f(kr[j][v][i]);
+                    else kf = kr[j][v][i];
+                    d += q[8 * v + i] * kf;
+                }
             sc[j] = d;
         }
 #pragma unroll
         for (int j = 0; j < KPI; j++) {
-            const int k = k0 + 16 * j;
-            sc[j] = k < ke ? group16_sum(sc[j]) * a.scale + (mrow ? mrow[k] : 0.0f) : -INFINITY;
+            const int k = k0 + NG * j;
+            sc[j] = k < ke ? group_sum<LPK>(sc[j]) * a.scale + (mrow ? mrow[k] : 0.0f) : -INFINITY;
         }
         float mx = sc[0];
 #pragma unroll
@@ -164,38 +188,40 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
         float p[KPI], ps = 0.0f;
 #pragma unroll
         for (int j = 0; j < KPI; j++) {
-            p[j] = k0 + 16 * j < ke ? expf(sc[j] - mn) : 0.0f;
+            p[j] = k0 + NG * j < ke ? expf(sc[j] - mn) : 0.0f;
             ps += p[j];
         }
         l = l * c + ps;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float acc = o[i] * c;
+        for (int v = 0; v < NV; v++)
 #pragma unroll
-            for (int j = 0; j < KPI; j++) {
-                if (k0 + 16 * j >= ke) break;
-                float vf;
-                if constexpr (BF16 && VEC) vf = bf2f(vr[j][i]);
-                else vf = vr[j][i];
-                acc += p[j] * vf;
+            for (int i = 0; i < 8; i++) {
+                float acc = o[8 * v + i] * c;
+#pragma unroll
+                for (int j = 0; j < KPI; j++) {
+                    if (k0 + NG * j >= ke) break;
+                    float vf;
+                    if constexpr (BF16 && VEC) vf = bf2f(vr[j][v][i]);
+                    else vf = vr[j][v][i];
+                    acc += p[j] * vf;
+                }
+                o[8 * v + i] = acc;
             }
-            o[i] = acc;
-        }
         m = mn;
     }
 
-    __shared__ float sm[16], sl[16], so[16][DEC_DK];
-    if (l16 == 0) { sm[g] = m; sl[g] = l; }
+    __shared__ float sm[NG], sl[NG], so[NG][DEC_DK];
+    if (ls == 0) { sm[g] = m; sl[g] = l; }
 #pragma unroll
-    for (int i = 0; i < 8; i++) so[g][l16 * 8 + i] = o[i];
+    for (int i = 0; i < DPL; i++) so[g][ls * DPL + i] = o[i];
     __syncthreads();
     if (tid < DEC_DK) {
         float M = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 16; j++) M = fmaxf(M, sm[j]);
+        for (int j = 0; j < NG; j++) M = fmaxf(M, sm[j]);
         float num = 0.0f, den = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
+        for (int j = 0; j < NG; j++) {
             if (sm[j] == -INFINITY) continue;
             const float w = expf(sm[j] - M);
             num += w * so[j][tid];
@@ -238,10 +264,10 @@ __global__ __launch_bounds__(DEC_DK) void attn_merge_kernel(CtAttn a) {
 
 extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
     if (a->B <= 0 || a->T_q <= 0) return;
-    if (a->q_parts && (a->q_nparts < 1 || a->q_nparts > 8 || a->q_pstride % 4 ||
+    if (a->q_parts && (a->q_nparts < 1 || a->q_nparts > CT_ATTN_QPARTS || a->q_pstride % 4 ||
                        ((uintptr_t)a->q_parts & 15) || (a->q_bias && ((uintptr_t)a->q_bias & 15)) ||
                        a->q_sb % 4 || a->q_st % 4)) {
-        fprintf(stderr, "ctk_attn: query partials need 1..8 slices and 16-byte aligned rows\n");
+        fprintf(stderr, "ctk_attn: query partials need 1..4 slices and 16-byte aligned rows\n");
         exit(1);
     }
     if (a->chunk > 0 && (!a->part_o || !a->part_ml || a->max_chunks < 1 || a->mask)) {
@@ -253,12 +279,13 @@ extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
     const long esz = a->kv_bf16 ? 2 : 4, need = 16 / esz;
     const bool vec = ((uintptr_t)a->K % 16 == 0) && ((uintptr_t)a->V % 16 == 0) &&
                      a->kv_sb % need == 0 && a->kv_st % need == 0 && a->kv_sh % need == 0;
+    constexpr int LPK = CT_ATTN_LPK;
     if (a->kv_bf16) {
-        if (vec) hipLaunchKernelGGL((attn_kernel<true, true>), grid, dim3(256), 0, s, *a);
-        else hipLaunchKernelGGL((attn_kernel<true, false>), grid, dim3(256), 0, s, *a);
+        if (vec) hipLaunchKernelGGL((attn_kernel<true, true, LPK>), grid, dim3(256), 0, s, *a);
+        else hipLaunchKernelGGL((attn_kernel<true, false, LPK>), grid, dim3(256), 0, s, *a);
     } else {
-        if (vec) hipLaunchKernelGGL((attn_kernel<false, true>), grid, dim3(256), 0, s, *a);
-        else hipLaunchKernelGGL((attn_kernel<false, false>), grid, dim3(256), 0, s, *a);
+        if (vec) hipLaunchKernelGGL((attn_kernel<false, true, LPK>), grid, dim3(256), 0, s, *a);
+        else hipLaunchKernelGGL((attn_kernel<false, false, LPK>), grid, dim3(256), 0, s, *a);
     }
     if (a->chunk > 0)
         hipLaunchKernelGGL(attn_merge_kernel, dim3(a->B * a->T_q, a->H), dim3(DEC_DK), 0, s, *a);
