@@ -30,7 +30,8 @@
 /* ------------------------------------------------------------------ */
 /* Process-wide state: one read-only weight blob per device.           */
 /* ------------------------------------------------------------------ */
-static void *g_blob[CT_MAX_DEVICES];
+static void *g_blob[CT_MAX_DEVICES];        /* blob start on each device          */
+static void *g_blob_alloc[CT_MAX_DEVICES];  /* the allocation it sits in          */
 static float *g_inv_freq[CT_MAX_DEVICES];
 static const uint8_t *g_host_base;
 static size_t g_blob_bytes;
@@ -83,10 +84,21 @@ void backend_weights_upload_blob(const void *host_base, size_t bytes) {
     pthread_mutex_lock(&g_lock);
     g_host_base = (const uint8_t *)host_base;
     g_blob_bytes = bytes;
+    /* A safetensors blob (8-byte header length, then a JSON header padded to
+     * 8 bytes, convert.py:217-220) is placed so that its data section starts
+     * 16-byte aligned on the device: every tensor of the model is a multiple
+     * of 16 bytes, so all of them can then be read in 16-byte pieces. */
+    size_t shift = 0;
+    if (bytes > 9) {
+        uint64_t hlen = 0;
+        memcpy(&hlen, host_base, 8);
+        if (hlen < bytes - 8 && ((const char *)host_base)[8] == '{') shift = (16 - (8 + hlen) % 16) % 16;
+    }
     for (int d = 0; d < n; d++) {
         CHK(hipSetDevice(d));
-        if (g_blob[d]) CHK(hipFree(g_blob[d]));
-        CHK(hipMalloc(&g_blob[d], bytes ? bytes : 1));
+        if (g_blob_alloc[d]) CHK(hipFree(g_blob_alloc[d]));
+        CHK(hipMalloc(&g_blob_alloc[d], bytes + 16));
+        g_blob[d] = (char *)g_blob_alloc[d] + shift;
         CHK(hipMemcpy(g_blob[d], host_base, bytes, hipMemcpyHostToDevice));
     }
     g_ndev = n;
@@ -154,7 +166,7 @@ void backend_destroy(void) {
     pthread_mutex_lock(&g_lock);
     for (int d = 0; d < CT_MAX_DEVICES; d++) {
         if (g_blob[d] || g_inv_freq[d]) CHK(hipSetDevice(d));
-        if (g_blob[d]) { CHK(hipFree(g_blob[d])); g_blob[d] = NULL; }
+        if (g_blob_alloc[d]) { CHK(hipFree(g_blob_alloc[d])); g_blob_alloc[d] = NULL; g_blob[d] = NULL; }
         if (g_inv_freq[d]) { CHK(hipFree(g_inv_freq[d])); g_inv_freq[d] = NULL; }
     }
     g_ndev = 0;

@@ -173,33 +173,66 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
 // Depthwise conv (k = 9, zero padding 4 inside the sequence) + inference
 // BatchNorm + SiLU (backends/cpu/backend.c:312-334).
 // ---------------------------------------------------------------------------
+// One thread per 8 consecutive channels of a row (16-byte loads of the
+// activations and of every per-channel parameter); the arithmetic per
+// element is the scalar form's.
 __global__ void dwconv_bn_silu_kernel(float *out, uint16_t *out_hi, uint16_t *out_lo,
                                       const float *in, int M, const int *row_start,
                                       const int *row_len, const uint16_t *dww,
                                       const uint16_t *dwb, const uint16_t *bnw, const uint16_t *bnb,
                                       const uint16_t *bnm, const uint16_t *bnv) {
+    constexpr int G = ENC_D / 8;
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)M * ENC_D) return;
-    const int r = (int)(i / ENC_D), c = (int)(i % ENC_D);
+    if (i >= (long)M * G) return;
+    const int r = (int)(i / G), c0 = (int)(i % G) * 8;
     const int st = row_start ? row_start[r] : 0;       // this row's sequence: [st, st + T)
     const int T = row_len ? row_len[r] : M;
     const int t = r - st;
-    float s = bf2f(dwb[c]);
+    // taps of the 8 channels: dww[c][k] for c0 <= c < c0 + 8, 72 contiguous values
+    uint16_t wk[8 * ENC_CK];
+#pragma unroll
+    for (int v = 0; v < ENC_CK; v++) {
+        const u16x8 w8 = *reinterpret_cast<const u16x8 *>(dww + c0 * ENC_CK + 8 * v);
+#pragma unroll
+        for (int e = 0; e < 8; e++) wk[8 * v + e] = w8[e];
+    }
+    const u16x8 b8 = *reinterpret_cast<const u16x8 *>(dwb + c0);
+    float s[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) s[e] = bf2f(b8[e]);
 #pragma unroll
     for (int k = 0; k < ENC_CK; k++) {
         const int ti = t - (ENC_CK - 1) / 2 + k;
         if (ti < 0 || ti >= T) continue;
-        s += bf2f(dww[c * ENC_CK + k]) * in[(long)(st + ti) * ENC_D + c];
+        const float4 *x = reinterpret_cast<const float4 *>(in + (long)(st + ti) * ENC_D + c0);
+        const float4 x0 = x[0], x1 = x[1];
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) s[e] += bf2f(wk[e * ENC_CK + k]) * xv[e];
     }
-    const float v = (s - bf2f(bnm[c])) / sqrtf(bf2f(bnv[c]) + 1e-5f) * bf2f(bnw[c]) + bf2f(bnb[c]);
-    const float o = v / (1.0f + expf(-v));
+    const u16x8 m8 = *reinterpret_cast<const u16x8 *>(bnm + c0), v8 = *reinterpret_cast<const u16x8 *>(bnv + c0);
+    const u16x8 w8 = *reinterpret_cast<const u16x8 *>(bnw + c0), bb8 = *reinterpret_cast<const u16x8 *>(bnb + c0);
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float v = (s[e] - bf2f(m8[e])) / sqrtf(bf2f(v8[e]) + 1e-5f) * bf2f(w8[e]) + bf2f(bb8[e]);
+        o[e] = v / (1.0f + expf(-v));
+    }
+    const long oi = (long)r * ENC_D + c0;
     if (out_hi) {
-        uint16_t h, l;
-        split_bf16(o, h, l);
-        out_hi[i] = h;
-        out_lo[i] = l;
+        u16x8 h8, l8;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            uint16_t hh, ll;
+            split_bf16(o[e], hh, ll);
+            h8[e] = hh; l8[e] = ll;
+        }
+        *reinterpret_cast<u16x8 *>(out_hi + oi) = h8;
+        *reinterpret_cast<u16x8 *>(out_lo + oi) = l8;
     } else {
-        out[i] = o;
+        float4 *y = reinterpret_cast<float4 *>(out + oi);
+        y[0] = make_float4(o[0], o[1], o[2], o[3]);
+        y[1] = make_float4(o[4], o[5], o[6], o[7]);
     }
 }
 
@@ -282,6 +315,18 @@ inline unsigned nblk(long n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
 
+// The 8-channel form reads every operand in 16-byte pieces.
+static void dw_check(const float *out, const uint16_t *out_hi, const float *in, const uint16_t *dww,
+                     const uint16_t *dwb, const uint16_t *bnw, const uint16_t *bnb,
+                     const uint16_t *bnm, const uint16_t *bnv) {
+    const uintptr_t a = (uintptr_t)out | (uintptr_t)out_hi | (uintptr_t)in | (uintptr_t)dww |
+                        (uintptr_t)dwb | (uintptr_t)bnw | (uintptr_t)bnb | (uintptr_t)bnm | (uintptr_t)bnv;
+    if (a & 15) {
+        fprintf(stderr, "dwconv: activations and parameters must be 16-byte aligned\n");
+        exit(1);
+    }
+}
+
 static int relpos_qb(int) { return RQ; }
 
 // Score rows of ldS floats: T rounded up to 16, plus 4 so that 16 rows x 4
@@ -363,7 +408,8 @@ extern "C" void ctk_dwconv_bn_silu(float *out, const float *in, int T, const uin
                                    const uint16_t *dwb, const uint16_t *bnw, const uint16_t *bnb,
                                    const uint16_t *bnm, const uint16_t *bnv, hipStream_t s) {
     if (T <= 0) return;
-    hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)T * ENC_D)), dim3(256), 0, s,
+    dw_check(out, nullptr, in, dww, dwb, bnw, bnb, bnm, bnv);
+    hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)T * (ENC_D / 8))), dim3(256), 0, s,
                        out, nullptr, nullptr, in, T, nullptr, nullptr, dww, dwb, bnw, bnb, bnm, bnv);
 }
 
@@ -373,7 +419,9 @@ extern "C" void ctk_dwconv_bn_silu_packed(uint16_t *out_hi, uint16_t *out_lo, co
                                           const uint16_t *bnw, const uint16_t *bnb,
                                           const uint16_t *bnm, const uint16_t *bnv, hipStream_t s) {
     if (M <= 0) return;
-    hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)M * ENC_D)), dim3(256), 0, s,
+    dw_check(nullptr, out_hi, in, dww, dwb, bnw, bnb, bnm, bnv);
+    if ((uintptr_t)out_lo & 15) { fprintf(stderr, "dwconv: outputs must be 16-byte aligned\n"); exit(1); }
+    hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)M * (ENC_D / 8))), dim3(256), 0, s,
                        nullptr, out_hi, out_lo, in, M, row_start, row_len, dww, dwb, bnw, bnb, bnm, bnv);
 }
 
