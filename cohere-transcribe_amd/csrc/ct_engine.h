@@ -9,7 +9,13 @@
 extern "C" {
 #endif
 
-#define CT_PROMPT_MAX 16
+/* Prompt ids a request may hold: a submitted prompt (at most
+ * CT_PROMPT_SUBMIT_MAX) plus the tokens a chained chunk carries over from
+ * its predecessor (at most CT_CARRY_MAX, transcribe.c:476). */
+#define CT_PROMPT_SUBMIT_MAX 16
+#define CT_CARRY_MAX 64
+#define CT_PROMPT_MAX (CT_PROMPT_SUBMIT_MAX + CT_CARRY_MAX)
+#define CT_ENG_MAX_SLOTS 256  /* slots an engine may have (the ABI's MAX_BATCH) */
 #define CT_MAX_KSPLIT 8    /* largest ctk_gemv_ksplit() of a decoder weight */
 /* Spare rows per (slot, head) of the self caches: without them every
  * (slot, head) block starts on the same 256-KB boundary and the workgroups
@@ -41,8 +47,15 @@ typedef struct {
     int  *req_T, *req_limit, *req_flags, *req_np, *req_ngen;
     int  *req_prompt;  /* [max_req][CT_PROMPT_MAX]                             */
     int  *req_out;     /* [max_req][smax] generated tokens                     */
-    /* queue: q[0] next request to admit, q[1] requests ready (encoded),
-     * q[2] requests finished */
+    /* chained chunks of one long recording: the request admitted after
+     * this one finishes (its prompt then gets the carried tokens), or -1 */
+    int  *req_next;
+    /* ready ring: request ids in admission order; rq[q[0]..q[1]) wait for a
+     * slot.  pend[slot] is a chained successor that eng_end released in that
+     * slot this step (-1 if none); eng_begin appends them in slot order. */
+    int  *rq, *pend;
+    /* q[0] next ring entry to admit, q[1] ring entries written, q[2]
+     * requests finished */
     int  *q;
 } CtEngDev;
 

@@ -28,6 +28,7 @@ typedef struct {
     const float *dpcm;   /* ... or samples already in device memory          */
     int n;               /* samples of a PCM request                          */
     int T_mel, T_enc;
+    int chained;         /* admitted only after its predecessor chunk ends    */
 } HostReq;
 
 struct HipbEngine {
@@ -210,10 +211,15 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     d->req_prompt = dmalloc((size_t)R * CT_PROMPT_MAX * sizeof(int));
     d->req_out = dmalloc((size_t)R * d->smax * sizeof(int));
     d->q = dmalloc(4 * sizeof(int));
+    d->req_next = dmalloc(R * sizeof(int));
+    d->rq = dmalloc(R * sizeof(int));
+    d->pend = dmalloc(S * sizeof(int));
     ECHK(hipMemsetAsync(d->slot_req, 0xff, S * sizeof(int), e->s));   /* -1: free */
     ECHK(hipMemsetAsync(d->slot_S, 0, S * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->req_ngen, 0, R * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->q, 0, 4 * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->req_next, 0xff, R * sizeof(int), e->s));   /* -1: no successor */
+    ECHK(hipMemsetAsync(d->pend, 0xff, S * sizeof(int), e->s));
 
     /* repack [Wq;Wk;Wv] and cross [Wk;Wv] contiguously (device to device) */
     const size_t wsz = (size_t)DEC_D * DEC_D * 2, bsz = (size_t)DEC_D * 2;
@@ -271,6 +277,7 @@ void hipb_destroy(HipbEngine *e) {
     void *ptrs[] = {e->d.slot_req, e->d.slot_S, e->d.act, e->d.tok, e->d.pos_len, e->d.cross_len,
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
+                    e->d.req_next, e->d.rq, e->d.pend,
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->kself, e->vself, e->kcross, e->vcross,
                     e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
                     e->att_ml, e->att_po,
@@ -301,6 +308,8 @@ void hipb_reset(HipbEngine *e) {
     ECHK(hipMemsetAsync(e->d.slot_S, 0, e->d.slots * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.req_ngen, 0, e->d.max_req * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.q, 0, 4 * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(e->d.req_next, 0xff, e->d.max_req * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(e->d.pend, 0xff, e->d.slots * sizeof(int), e->s));
     ECHK(hipStreamSynchronize(e->s));
 }
 
@@ -337,6 +346,32 @@ int hipb_submit_pcm(HipbEngine *e, const float *pcm, int n_samples, const int *p
     return r;
 }
 
+int hipb_submit_pcm_chunked(HipbEngine *e, const float *pcm, int n_samples, const int *prompt,
+                            int n_prompt, int limit, int flags, float silence_db, float silence_dur,
+                            float target_sec, int *first_req) {
+    if (n_prompt < 2) CT_FATAL("hipb_submit_pcm_chunked: the prompt needs at least 2 ids (pre + post)");
+    if (n_prompt + CT_CARRY_MAX + limit > e->d.smax)
+        CT_FATAL("hipb_submit_pcm_chunked: prompt + 64 carried ids + limit exceeds the engine's max_tokens");
+    const int cap = n_samples / HOP_LEN + 1;
+    int *b = malloc((size_t)2 * cap * sizeof(int));
+    if (!b) CT_FATAL("out of host memory");
+    const int nc = hipb_chunk_bounds(pcm, n_samples, silence_db, silence_dur, target_sec, b, cap);
+    if (e->n_req + nc > e->cfg.max_requests) CT_FATAL("hipb_submit_pcm_chunked: request pool full");
+    const int r0 = e->n_req;
+    for (int c = 0; c < nc; c++) {
+        const int r = hipb_submit_pcm(e, pcm + b[2 * c], b[2 * c + 1] - b[2 * c], prompt, n_prompt,
+                                      limit, flags);
+        e->req[r].chained = c > 0;
+    }
+    free(b);
+    /* link chunk c to chunk c + 1 */
+    int *nx = e->h_tmp;
+    for (int c = 0; c + 1 < nc; c++) nx[c] = r0 + c + 1;
+    if (nc > 1) ECHK(hipMemcpy(e->d.req_next + r0, nx, (size_t)(nc - 1) * sizeof(int), hipMemcpyHostToDevice));
+    if (first_req) *first_req = r0;
+    return nc;
+}
+
 int hipb_submit_pcm_device(HipbEngine *e, const float *dev_pcm, int n_samples, const int *prompt,
                            int n_prompt, int limit, int flags) {
     if (n_samples < HOP_LEN) CT_FATAL("hipb_submit_pcm_device: clip shorter than one hop (160 samples)");
@@ -350,7 +385,7 @@ static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prom
                          int flags) {
     if (e->bench_mode) CT_FATAL("hipb_submit: engine is in microbenchmark mode");
     if (e->n_req >= e->cfg.max_requests) CT_FATAL("hipb_submit: request pool full");
-    if (n_prompt < 1 || n_prompt > CT_PROMPT_MAX) CT_FATAL("hipb_submit: prompt length outside [1, 16]");
+    if (n_prompt < 1 || n_prompt > CT_PROMPT_SUBMIT_MAX) CT_FATAL("hipb_submit: prompt length outside [1, 16]");
     if (limit < 1) CT_FATAL("hipb_submit: limit < 1");
     if (n_prompt + limit > e->d.smax) CT_FATAL("hipb_submit: prompt + limit exceeds the engine's max_tokens");
     const int Te = t_enc_of(T_mel);
@@ -631,9 +666,21 @@ void hipb_encode(HipbEngine *e, int max_batch_frames) {
         }
         r = r1;
     }
+    /* publish: append the newly encoded requests that wait for no
+     * predecessor to the ready ring, in submission order, after whatever the
+     * device appended itself (chained successors) */
+    const int r0 = e->n_enc;
     e->n_enc = r;
-    /* publish: requests [0, n_enc) may now be admitted */
-    ECHK(hipMemcpy(e->d.q + 1, &e->n_enc, sizeof(int), hipMemcpyHostToDevice));
+    int q1 = 0, k = 0;
+    ECHK(hipMemcpy(&q1, e->d.q + 1, sizeof(int), hipMemcpyDeviceToHost));
+    int *ids = e->h_tmp;
+    for (int i = r0; i < r; i++)
+        if (!e->req[i].chained) ids[k++] = i;
+    if (k) {
+        ECHK(hipMemcpy(e->d.rq + q1, ids, (size_t)k * sizeof(int), hipMemcpyHostToDevice));
+        q1 += k;
+        ECHK(hipMemcpy(e->d.q + 1, &q1, sizeof(int), hipMemcpyHostToDevice));
+    }
 }
 
 /* ------------------------------------------------------------------ */
@@ -768,27 +815,37 @@ int hipb_finished(HipbEngine *e) {
     return v;
 }
 
+static void ensure_graph(HipbEngine *e) {
+    if (e->have_graph || e->eager) return;
+    ECHK(hipStreamBeginCapture(e->s, hipStreamCaptureModeThreadLocal));
+    step_launch(e);
+    ECHK(hipStreamEndCapture(e->s, &e->graph));
+    ECHK(hipGraphInstantiate(&e->exec, e->graph, NULL, NULL, 0));
+    e->have_graph = 1;
+}
+
+static void launch_step(HipbEngine *e) {
+    if (e->eager) step_launch(e);
+    else ECHK(hipGraphLaunch(e->exec, e->s));
+}
+
+void hipb_bench_steps(HipbEngine *e, int n) {
+    ensure_graph(e);
+    for (int i = 0; i < n; i++) launch_step(e);
+}
+
 long hipb_run(HipbEngine *e, int chunk) {
     if (chunk < 1) chunk = 1;
-    if (!e->have_graph && !e->eager) {
-        ECHK(hipStreamBeginCapture(e->s, hipStreamCaptureModeThreadLocal));
-        step_launch(e);
-        ECHK(hipStreamEndCapture(e->s, &e->graph));
-        ECHK(hipGraphInstantiate(&e->exec, e->graph, NULL, NULL, 0));
-        e->have_graph = 1;
-    }
+    ensure_graph(e);
     long steps = 0;
     /* every admitted request finishes within prompt + limit <= prompt +
      * MAX_SEQ steps of its admission, and some request is admitted whenever
      * a slot frees up */
-    const long bound = (long)(e->n_enc / e->d.slots + 2) * (MAX_SEQ + CT_PROMPT_MAX + 1);
+    const long bound = (long)(e->n_enc + 2) * (MAX_SEQ + CT_PROMPT_MAX + 1);
     for (;;) {
         if (hipb_finished(e) >= e->n_enc) break;
         if (steps > bound) CT_FATAL("hipb_run: requests did not finish within the step bound");
-        for (int i = 0; i < chunk; i++) {
-            if (e->eager) step_launch(e);
-            else ECHK(hipGraphLaunch(e->exec, e->s));
-        }
+        for (int i = 0; i < chunk; i++) launch_step(e);
         steps += chunk;
     }
     return steps;

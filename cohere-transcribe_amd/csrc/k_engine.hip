@@ -18,22 +18,35 @@ namespace {
 
 __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d) {
     const int tid = threadIdx.x;
+    // Slot table and released successors read in parallel into LDS; the
+    // admission itself is one sequential pass over slots in slot order.
+    __shared__ int s_req[CT_ENG_MAX_SLOTS], s_pend[CT_ENG_MAX_SLOTS], s_new[CT_ENG_MAX_SLOTS];
+    for (int s = tid; s < d.slots; s += 256) {
+        s_req[s] = d.slot_req[s];
+        s_pend[s] = d.pend[s];
+        s_new[s] = 0;
+    }
+    __syncthreads();
     if (tid == 0) {
-        int nxt = d.q[0];
-        const int ready = d.q[1];
+        int nxt = d.q[0], ready = d.q[1];
+        for (int s = 0; s < d.slots; s++)
+            if (s_pend[s] >= 0) d.rq[ready++] = s_pend[s];
         for (int s = 0; s < d.slots; s++) {
-            if (d.slot_req[s] < 0 && nxt < ready) {
-                d.slot_req[s] = nxt++;
-                d.slot_S[s] = 0;
+            if (s_req[s] < 0 && nxt < ready) {
+                s_req[s] = d.rq[nxt++];
+                s_new[s] = 1;
             }
         }
         d.q[0] = nxt;
+        d.q[1] = ready;
     }
     __syncthreads();
     for (int s = tid; s < d.slots; s += 256) {
-        const int r = d.slot_req[s];
+        if (s_pend[s] >= 0) d.pend[s] = -1;
+        const int r = s_req[s];
+        d.slot_req[s] = r;
         if (r >= 0) {
-            int S = d.slot_S[s];
+            int S = s_new[s] ? 0 : d.slot_S[s];
             const int np = d.req_np[r];
             const int t = S < np ? d.req_prompt[r * CT_PROMPT_MAX + S]
                                  : d.req_out[(long)r * d.smax + d.req_ngen[r] - 1];
@@ -107,6 +120,22 @@ __global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *l
     const bool fin = (best == EOS_ID && !(flags & 1)) || ng + 1 >= lim || S >= d.smax;
     if (fin) {
         d.slot_req[s] = -1;
+        const int nx = d.req_next[r];
+        if (nx >= 0) {
+            // The successor's prompt becomes pre + carry + post: its first two
+            // ids, then the last <= CT_CARRY_MAX generated ids of this
+            // request without its final one, then the rest of its own prompt
+            // (transcribe.c:382-387, 510-529).
+            const int gen = ng + 1;
+            const int nc = min(gen > 0 ? gen - 1 : 0, CT_CARRY_MAX);
+            int *pp = d.req_prompt + (long)nx * CT_PROMPT_MAX;
+            const int np = d.req_np[nx];
+            for (int i = np - 1; i >= 2; i--) pp[i + nc] = pp[i];
+            const int *og = d.req_out + (long)r * d.smax;
+            for (int i = 0; i < nc; i++) pp[2 + i] = og[gen - 1 - nc + i];
+            d.req_np[nx] = np + nc;
+            d.pend[s] = nx;
+        }
         atomicAdd(&d.q[2], 1);
     }
 }

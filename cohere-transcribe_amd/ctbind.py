@@ -235,6 +235,7 @@ _ENGINE_SIGS = {
     "hipb_attention_only": ([C.c_void_p], None),
     "hipb_bench_decode_gemms": ([C.c_void_p], None),
     "hipb_bench_encoder_gemm": ([C.c_void_p, C.c_int], None),
+    "hipb_bench_steps": ([C.c_void_p, C.c_int], None),
     "hipb_stream": ([C.c_void_p], C.c_void_p),
 }
 
@@ -312,6 +313,9 @@ class Engine:
     def encoder_gemm(self, M):
         self.L.hipb_bench_encoder_gemm(self.e, M)
 
+    def bench_steps(self, n):
+        self.L.hipb_bench_steps(self.e, n)
+
     def stream(self):
         return self.L.hipb_stream(self.e)
 
@@ -326,7 +330,39 @@ _ENGINE_SIGS.update({
     "hipb_mel": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p], None),
     "hipb_reset": ([C.c_void_p], None),
     "hipb_submit_pcm_device": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int], C.c_int),
+    "hipb_submit_pcm_chunked": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                 C.c_float, C.c_float, C.c_float, C.POINTER(C.c_int)], C.c_int),
+    "hipb_chunk_bounds": ([C.c_void_p, C.c_int, C.c_float, C.c_float, C.c_float, C.c_void_p, C.c_int],
+                          C.c_int),
 })
+
+
+def chunk_bounds(samples, silence_db=float("nan"), silence_dur=0.2, target_sec=20.0):
+    """Chunk boundaries of a long recording, [(start, end), ...] in samples
+    (hipb_chunk_bounds, host code of libct_hip.so)."""
+    lib = engine_lib()
+    samples = np.ascontiguousarray(samples, np.float32)
+    cap = len(samples) // HOP_LEN + 1
+    b = np.zeros(2 * cap, np.int32)
+    n = lib.hipb_chunk_bounds(samples.ctypes.data, len(samples), silence_db, silence_dur, target_sec,
+                              b.ctypes.data, cap)
+    if n < 0:
+        raise MemoryError("hipb_chunk_bounds: out of host memory")
+    return [(int(b[2 * i]), int(b[2 * i + 1])) for i in range(n)]
+
+
+def _engine_chunked(self, pcm, limit, flags=HIPB_SUPPRESS_EOS, prompt=None, silence_db=float("nan"),
+                    silence_dur=0.2, target_sec=20.0):
+    """Queues a long recording as chained chunk requests; returns their ids."""
+    pcm = np.ascontiguousarray(pcm, np.float32)
+    p = np.ascontiguousarray(prompt if prompt is not None else PROMPT, dtype=np.int32)
+    first = C.c_int(-1)
+    n = self.L.hipb_submit_pcm_chunked(self.e, pcm.ctypes.data, len(pcm), p.ctypes.data, len(p), limit,
+                                       flags, silence_db, silence_dur, target_sec, C.byref(first))
+    return list(range(first.value, first.value + n))
+
+
+Engine.submit_pcm_chunked = _engine_chunked
 
 
 def _engine_extra(self, pcm, limit, flags=HIPB_SUPPRESS_EOS, prompt=None):

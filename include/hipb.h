@@ -60,6 +60,22 @@ int  hipb_submit(HipbEngine *e, const float *mel, int T_mel, const int *prompt, 
  * spectrogram is computed on the GPU at encode time (transcribe.c:177-214). */
 int  hipb_submit_pcm(HipbEngine *e, const float *pcm, int n_samples, const int *prompt,
                      int n_prompt, int limit, int flags);
+/* Long recordings (transcribe.c:397-535): splits 16 kHz PCM (host memory)
+ * at silences and queues one request per chunk, ids consecutive from
+ * *first_req.  Chunk c + 1 is admitted only after chunk c has finished; its
+ * prompt is then this prompt with chunk c's last <= 64 generated ids (the
+ * final one excluded) inserted after the first two ids.  silence_db NAN picks
+ * the threshold from the recording's noise floor; the reference's defaults
+ * are silence_dur 0.2 s and target_sec 20 s.  Requires n_prompt >= 2 and
+ * n_prompt + 64 + limit <= max_tokens; every chunk must fit max_frames.
+ * Returns the number of chunks. */
+int  hipb_submit_pcm_chunked(HipbEngine *e, const float *pcm, int n_samples, const int *prompt,
+                             int n_prompt, int limit, int flags, float silence_db,
+                             float silence_dur, float target_sec, int *first_req);
+/* The chunk boundaries alone: chunk i is samples [bounds[2i], bounds[2i+1]).
+ * Returns the number of chunks (at most cap), -1 if out of memory. */
+int  hipb_chunk_bounds(const float *pcm, int n_samples, float silence_db, float silence_dur,
+                       float target_sec, int *bounds, int cap);
 /* The same with the samples already in device memory (not copied; they must
  * stay valid until hipb_encode returns). */
 int  hipb_submit_pcm_device(HipbEngine *e, const float *dev_pcm, int n_samples, const int *prompt,
@@ -107,6 +123,11 @@ void hipb_bench_decode_gemms(HipbEngine *e);
  * GEMM twice per layer) once on the engine stream.  The input is seeded when
  * M changes. */
 void hipb_bench_encoder_gemm(HipbEngine *e, int M);
+
+/* Launches n decode steps (graph replays, or eager steps under HIPB_EAGER=1)
+ * on the engine's stream without waiting and without checking for finished
+ * requests: the step-time benchmark over slots filled by hipb_bench_fill. */
+void hipb_bench_steps(HipbEngine *e, int n);
 /* The engine's HIP stream (hipStream_t), for events and profiling. */
 void *hipb_stream(HipbEngine *e);
 

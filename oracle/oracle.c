@@ -629,3 +629,88 @@ void orc_compute_mel(const float *samples, int n, float *mel) {
     }
     free(s); free(fb);
 }
+
+/* ------------------------------------------------------------------ */
+/* Long-audio chunking                                                 */
+/* ------------------------------------------------------------------ */
+
+/* transcribe.c:397-404: RMS of each 10 ms frame, one sequential fp32 sum of
+ * squares (the reference's -O3 -march=native build contracts it to FMA). */
+static void orc_frame_rms(const float *x, int n_frames, float *rms) {
+    for (int f = 0; f < n_frames; f++) {
+        float sum = 0.0f;
+        for (int i = 0; i < HOP_LEN; i++) sum = fmaf(x[f * HOP_LEN + i], x[f * HOP_LEN + i], sum);
+        rms[f] = sqrtf(sum / HOP_LEN);
+    }
+}
+
+/* transcribe.c:406-421: histogram of RMS in 1024 buckets of width 1/1024;
+ * the first bucket b at which the cumulative count reaches n_frames/20 gives
+ * the threshold (b/1024)*10 (+20 dB). */
+static float orc_auto_threshold(const float *rms, int n_frames) {
+    int *hist = calloc(1024, sizeof(int));
+    for (int f = 0; f < n_frames; f++) {
+        int b = (int)(rms[f] * 1024);
+        if (b > 1023) b = 1023;
+        hist[b]++;
+    }
+    const int target = n_frames / 20;
+    float t = 1.0f;
+    int cum = 0;
+    for (int b = 0; b < 1024; b++) {
+        cum += hist[b];
+        if (cum >= target) { t = ((float)b / 1024) * 10.0f; break; }
+    }
+    free(hist);
+    return t;
+}
+
+/* transcribe.c:429-446: a quiet run [s, f) of at least
+ * (int)(dur*SR/HOP_LEN) frames that is followed by a loud frame f yields the
+ * cut ((s + f)/2)*HOP_LEN; a run reaching the end yields nothing. */
+static int orc_find_cuts(const float *rms, int n_frames, float thresh, float dur, int *cuts, int cap) {
+    const int min_frames = (int)(dur * SR / HOP_LEN);
+    int n = 0, quiet = 0, s = 0;
+    for (int f = 0; f < n_frames; f++) {
+        if (rms[f] < thresh) {
+            if (!quiet) { quiet = 1; s = f; }
+        } else if (quiet) {
+            if (f - s >= min_frames && n < cap) cuts[n++] = ((s + f) / 2) * HOP_LEN;
+            quiet = 0;
+        }
+    }
+    return n;
+}
+
+/* transcribe.c:456-465: keep cut i when it lies at least target_samp samples
+ * after the previously kept cut (the start counts as kept at 0). */
+static int orc_keep_cuts(int *cuts, int n, int target_samp) {
+    int kept = 0, prev = 0;
+    for (int i = 0; i < n; i++)
+        if (cuts[i] - prev >= target_samp) { prev = cuts[i]; cuts[kept++] = prev; }
+    return kept;
+}
+
+/* transcribe.c:486-533: threshold (auto, or 10^(dB/20)), cuts, targets,
+ * then the chunks between consecutive cuts, skipping empty ones. */
+int orc_chunk_bounds(const float *samples, int n_samples, float silence_db, float silence_dur,
+                     float target_sec, int *bounds, int cap) {
+    const int n_frames = n_samples / HOP_LEN;
+    float *rms = xmalloc((size_t)n_frames * sizeof(float));
+    orc_frame_rms(samples, n_frames, rms);
+    const float thresh = isnan(silence_db) ? orc_auto_threshold(rms, n_frames)
+                                           : powf(10.0f, silence_db / 20.0f);
+    int *cuts = xmalloc(4096 * sizeof(int));
+    int n = orc_find_cuts(rms, n_frames, thresh, silence_dur, cuts, 4096);
+    free(rms);
+    n = orc_keep_cuts(cuts, n, (int)(target_sec * SR));
+    int nb = 0, start = 0;
+    for (int c = 0; c <= n; c++) {
+        const int end = c < n ? cuts[c] : n_samples;
+        if (end <= start) { start = end; continue; }
+        if (nb < cap) { bounds[2 * nb] = start; bounds[2 * nb + 1] = end; nb++; }
+        start = end;
+    }
+    free(cuts);
+    return nb;
+}

@@ -89,6 +89,12 @@ int  orc_T_mel(int n_samples);
 void orc_compute_mel(const float *samples, int n, float *mel /* N_MELS x T_mel */);
 void orc_mel_filterbank(float *fb /* N_MELS x N_BINS */);
 
+/* ---- long-audio chunking (transcribe.c:397-535) ---- */
+/* Chunk i is samples [bounds[2i], bounds[2i+1]); returns the chunk count
+ * (at most cap).  silence_db NAN: automatic threshold. */
+int  orc_chunk_bounds(const float *samples, int n_samples, float silence_db, float silence_dur,
+                      float target_sec, int *bounds, int cap);
+
 #ifdef __cplusplus
 }
 #endif

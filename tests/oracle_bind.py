@@ -44,8 +44,10 @@ _SIGS = {
     "orc_transcribe": [_P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P],
     "orc_compute_mel": [_P, _I, _P],
     "orc_mel_filterbank": [_P],
+    "orc_chunk_bounds": [_P, _I, _F, _F, _F, _P, _I],
 }
-_RET = {"orc_argmax": _I, "orc_T_enc": _I, "orc_T_mel": _I, "orc_transcribe": _I}
+_RET = {"orc_argmax": _I, "orc_T_enc": _I, "orc_T_mel": _I, "orc_transcribe": _I,
+        "orc_chunk_bounds": _I}
 
 
 def _bind(lib, sigs, rets):
@@ -88,6 +90,38 @@ def transcribe(model, mel, limit, suppress=True, force=False, kv_bf16=False,
                                 ptr(prompt), len(prompt), limit, int(suppress), int(force),
                                 int(kv_bf16), ptr(toks), ptr(lg), ptr(eh))
     return toks[:n], (lg[:n] if lg is not None else None), eh
+
+
+def chunk_bounds(samples, silence_db=float("nan"), silence_dur=0.2, target_sec=20.0):
+    """Oracle chunking of a long recording: [(start, end), ...] in samples."""
+    samples = np.ascontiguousarray(samples, np.float32)
+    cap = len(samples) // 160 + 1
+    b = np.zeros(2 * cap, np.int32)
+    n = oracle().orc_chunk_bounds(ptr(samples), len(samples), silence_db, silence_dur, target_sec,
+                                  ptr(b), cap)
+    return [(int(b[2 * i]), int(b[2 * i + 1])) for i in range(n)]
+
+
+CARRY_MAX = 64
+
+
+def transcribe_chunked(model, samples, limit, prompt=None, suppress=True, force=False,
+                       kv_bf16=False, want_logits=False, **split):
+    """Oracle long-audio transcription (transcribe.c:480-533): chunks in
+    order, each prompt = prompt[:2] + carry + prompt[2:], carry = the last
+    <= 64 generated ids of the previous chunk without its final one
+    (transcribe.c:382-387).  Returns [(bounds, prompt, tokens), ...], with
+    each chunk's per-token logits appended when want_logits."""
+    prompt = list(prompt if prompt is not None else cb.PROMPT)
+    out, carry = [], []
+    for (a, b) in chunk_bounds(samples, **split):
+        p = prompt[:2] + carry + prompt[2:]
+        toks, lg, _ = transcribe(model, compute_mel(samples[a:b]), limit, suppress=suppress,
+                                 force=force, kv_bf16=kv_bf16, prompt=p, want_logits=want_logits)
+        out.append(((a, b), p, toks) + ((lg,) if want_logits else ()))
+        n = min(max(len(toks) - 1, 0), CARRY_MAX)
+        carry = [int(t) for t in toks[len(toks) - 1 - n:len(toks) - 1]]
+    return out
 
 
 def compute_mel(samples):

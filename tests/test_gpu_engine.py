@@ -224,3 +224,82 @@ def test_packed_encoder_bitexact_vs_abi_encoder(hip, hot):
             assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), i
     finally:
         eng.close()
+
+
+def long_recording(seed, n_seg=4, seg=5600, gap=1600):
+    """Speech-like segments (cb.synth_audio) separated by 0.1 s of low noise."""
+    rng = np.random.default_rng(seed)
+    parts = []
+    for i in range(n_seg):
+        parts.append(cb.synth_audio(seg + 160 * i, seed * 10 + i))
+        parts.append((rng.standard_normal(gap) * 0.002).astype(np.float32))
+    return np.concatenate(parts[:-1])
+
+
+SPLIT = dict(silence_db=-40.0, silence_dur=0.05, target_sec=0.2)
+CHUNK_LIMIT = 5
+# Recordings whose chunk decodes have no near-tie: the oracle's best and
+# second-best logit differ by > 1e-3 relative at every chosen token (ties
+# closer than the engine-vs-oracle logit error, ~1e-4, may go either way).
+REC_SEEDS = (2, 14)
+
+
+@pytest.fixture(scope="module")
+def chunked_oracle(hot):
+    out = {}
+    for s in REC_SEEDS:
+        runs = ob.transcribe_chunked(hot, long_recording(s), CHUNK_LIMIT, suppress=True, force=True,
+                                     kv_bf16=True, want_logits=True, **SPLIT)
+        for _, _, toks, lg in runs:
+            for i in range(len(toks) - 1):          # the last token is the forced EOS
+                l = lg[i].astype(np.float64)
+                l[3] = -np.inf                      # EOS suppressed
+                top = np.sort(l)[::-1]
+                assert (top[0] - top[1]) / abs(top[0]) > 1e-3, (s, i)
+        out[s] = [r[:3] for r in runs]
+    return out
+
+
+def test_engine_chunked_carry_matches_oracle(hip, hot, mels, oracle_runs, chunked_oracle):
+    """Two long recordings queued as chained chunks plus one plain request on
+    two slots: every chunk waits for its predecessor, gets the carried ids in
+    its prompt on the device, and decodes to the oracle's tokens."""
+    eng = cb.Engine(hot, slots=2, max_requests=16, max_frames=64, kv_bf16=True,
+                    max_tokens=len(cb.PROMPT) + 64 + CHUNK_LIMIT)
+    try:
+        a, b = REC_SEEDS
+        ids = {}
+        ids[a] = eng.submit_pcm_chunked(long_recording(a), CHUNK_LIMIT, FLAGS, **SPLIT)
+        plain = eng.submit(mels[0], LIMITS[0], FLAGS)
+        ids[b] = eng.submit_pcm_chunked(long_recording(b), CHUNK_LIMIT, FLAGS, **SPLIT)
+        eng.encode(max_batch_frames=64)
+        eng.run(chunk=4)
+        assert eng.finished() == len(ids[a]) + len(ids[b]) + 1
+        assert np.array_equal(eng.tokens(plain), oracle_runs[(True, 0)][0])
+        for s in REC_SEEDS:
+            ref = chunked_oracle[s]
+            print(f"case: recording {s}: {len(ref)} chunks, prompts "
+                  f"{[len(p) for _, p, _ in ref]}", flush=True)
+            assert len(ids[s]) == len(ref) >= 3
+            for r, (_, _, toks) in zip(ids[s], ref):
+                assert np.array_equal(eng.tokens(r), toks), (s, r)
+    finally:
+        eng.close()
+
+
+def test_engine_chunk_equals_request_with_carried_prompt(hip, hot, chunked_oracle):
+    """A chained chunk gives the same tokens as the same audio submitted on
+    its own with the carried prompt written out on the host."""
+    rec = long_recording(REC_SEEDS[0])
+    ref = chunked_oracle[REC_SEEDS[0]]
+    eng = cb.Engine(hot, slots=3, max_requests=8, max_frames=64, kv_bf16=True,
+                    max_tokens=len(cb.PROMPT) + 64 + CHUNK_LIMIT)
+    try:
+        rids = [eng.submit_pcm(rec[a:b], CHUNK_LIMIT, FLAGS, prompt=np.asarray(p, np.int32))
+                for (a, b), p, _ in ref[1:]]
+        eng.encode()
+        eng.run(chunk=2)
+        for r, (_, _, toks) in zip(rids, ref[1:]):
+            assert np.array_equal(eng.tokens(r), toks), r
+    finally:
+        eng.close()
