@@ -277,6 +277,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--requests", type=int, default=256)
     ap.add_argument("--slots", type=int, default=64)
+    ap.add_argument("--prefill-rows", type=int, default=16,
+                    help="spare step rows that feed prompts several tokens a step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the per-kernel roofline microbenchmarks (for profiling)")
@@ -305,7 +307,7 @@ def main():
     pcm = np.concatenate([cb.synth_audio(int(n), 1000 + i) for i, n in enumerate(samples)])
     # self caches sized for the longest request (prompt + 256 tokens)
     eng = cb.Engine(model, slots=args.slots, max_requests=args.requests, max_frames=376, kv_bf16=True,
-                    max_tokens=len(cb.PROMPT) + 256)
+                    max_tokens=len(cb.PROMPT) + 256, prefill_rows=args.prefill_rows)
     # device-resident input: the PCM buffer lives in a second engine-independent
     # allocation (the backend arena)
     dev_pcm = hip.backend_arena_alloc(total)
@@ -339,7 +341,8 @@ def main():
         "data": "synthetic (seeded audio, random-init weights at model dims)",
         "config": {"workload": "continuous-batching stream: 256 requests, clips lognormal(median 6 s) "
                                "in [1,30] s, forced decode lengths U[8,256], <= 64 in flight",
-                   "requests": args.requests, "slots": args.slots, "audio_sec": round(audio, 1),
+                   "requests": args.requests, "slots": args.slots,
+                   "prefill_rows": args.prefill_rows, "audio_sec": round(audio, 1),
                    "generated_tokens": gen_tokens, "kv": "bf16", "parallelism": "single GPU"},
         "decode_tokens_per_s": round(dec_tps, 1),
         "decode_steps": int(np.mean(steps)),

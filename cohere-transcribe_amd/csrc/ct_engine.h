@@ -33,16 +33,20 @@ extern "C" {
  * request-major arrays `max_req`. */
 typedef struct {
     int slots, max_req, smax, tmax;
+    int rows;          /* step rows: slots + spare prompt rows                  */
     int kv_rows;       /* rows per (slot, head) of the self caches (>= smax)    */
     /* slot table */
     int  *slot_req;    /* request in the slot, -1 when free                    */
     int  *slot_S;      /* tokens already in the slot's self cache              */
-    int  *act;         /* 1 if the slot decodes this step                      */
-    int  *tok;         /* token embedded this step                             */
-    int  *pos_len;     /* self length after this step's append (0 when idle)   */
-    int  *cross_len;   /* encoder frames of the slot's request (0 when idle)   */
-    int  *cross_idx;   /* request whose cross K/V the slot reads               */
-    long *kv_rowoff;   /* element offset of this step's self K/V row, -1 idle  */
+    /* step rows [rows]: row s < slots is slot s's row, rows past `slots`
+     * carry extra prompt tokens of a slot (row_slot) */
+    int  *act;         /* 1 if the row decodes this step                       */
+    int  *tok;         /* token embedded in the row                            */
+    int  *pos_len;     /* self length the row attends to (position + 1)        */
+    int  *cross_len;   /* encoder frames of the row's request (0 when idle)    */
+    int  *cross_idx;   /* request whose cross K/V the row reads                */
+    int  *row_slot;    /* slot whose self cache the row writes and reads       */
+    long *kv_rowoff;   /* element offset of the row's self K/V entry, -1 idle  */
     /* requests */
     int  *req_T, *req_limit, *req_flags, *req_np, *req_ngen;
     int  *req_prompt;  /* [max_req][CT_PROMPT_MAX]                             */
@@ -55,13 +59,14 @@ typedef struct {
      * slot this step (-1 if none); eng_begin appends them in slot order. */
     int  *rq, *pend;
     /* q[0] next ring entry to admit, q[1] ring entries written, q[2]
-     * requests finished */
+     * requests finished, q[3] prompt tokens not yet fed after the last step */
     int  *q;
 } CtEngDev;
 
-/* Admission + per-slot step inputs (one workgroup; admission is sequential
- * over slots in slot order, so scheduling is deterministic). */
-void ctk_eng_begin(const CtEngDev *d, hipStream_t s);
+/* Admission + the step's rows (one workgroup; admission and spare-row
+ * dealing go in slot order, so scheduling is deterministic).  extra: spare
+ * prompt rows this step may use (0 .. rows - slots). */
+void ctk_eng_begin(const CtEngDev *d, int extra, hipStream_t s);
 /* Argmax with the request's policy, token append, retirement. */
 void ctk_eng_end(const CtEngDev *d, const float *logits, hipStream_t s);
 /* Seeded fill of n elements (N(0,1)*scale approx.), bf16 or fp32. */

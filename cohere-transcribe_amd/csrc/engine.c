@@ -47,6 +47,9 @@ struct HipbEngine {
     /* step activations: h residual rows (fp32); lnf/attf/midf the decode
      * GEMMs' inputs in frag layout; parts K-slice partial sums */
     float *h, *q, *parts, *logits;
+    int M;                     /* rows of the step being launched */
+    long stepped;              /* steps launched since creation or reset */
+    int prefill_min;           /* unfed prompt tokens that select the wide step */
     uint16_t *lnf, *attf, *midf;
     /* attention key split: partial softmax states per (slot, head, chunk) */
     int attn_chunks;
@@ -64,9 +67,9 @@ struct HipbEngine {
     int n_req, n_enc;
     int *h_tmp;                /* pinned staging */
     /* graph */
-    hipGraph_t graph;
-    hipGraphExec_t exec;
-    int have_graph;
+    hipGraph_t graph[2];       /* [0] slots rows, [1] with the spare prompt rows */
+    hipGraphExec_t exec[2];
+    int have_graph[2];
     int eager;           /* HIPB_EAGER=1: launch steps without a graph */
     int bench_mode;
     int bench_gemm_M;    /* rows seeded by hipb_bench_encoder_gemm */
@@ -192,17 +195,21 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     const int S = cfg->slots, R = cfg->max_requests;
     const int tmax = (cfg->max_frames + 7) / 8 * 8;
     CtEngDev *d = &e->d;
-    d->slots = S; d->max_req = R; d->tmax = tmax;
+    if (cfg->prefill_rows < 0 || cfg->prefill_rows > CT_MAX_BATCH)
+        CT_FATAL("hipb_create: prefill_rows outside [0, 256]");
+    const int NR = S + cfg->prefill_rows;   /* step rows */
+    d->slots = S; d->max_req = R; d->tmax = tmax; d->rows = NR;
     d->smax = cfg->max_tokens > 0 ? cfg->max_tokens : MAX_SEQ;
     d->kv_rows = d->smax + CT_KV_PAD;
     d->slot_req = dmalloc(S * sizeof(int));
     d->slot_S = dmalloc(S * sizeof(int));
-    d->act = dmalloc(S * sizeof(int));
-    d->tok = dmalloc(S * sizeof(int));
-    d->pos_len = dmalloc(S * sizeof(int));
-    d->cross_len = dmalloc(S * sizeof(int));
-    d->cross_idx = dmalloc(S * sizeof(int));
-    d->kv_rowoff = dmalloc(S * sizeof(long));
+    d->act = dmalloc(NR * sizeof(int));
+    d->tok = dmalloc(NR * sizeof(int));
+    d->pos_len = dmalloc(NR * sizeof(int));
+    d->cross_len = dmalloc(NR * sizeof(int));
+    d->cross_idx = dmalloc(NR * sizeof(int));
+    d->row_slot = dmalloc(NR * sizeof(int));
+    d->kv_rowoff = dmalloc(NR * sizeof(long));
     d->req_T = dmalloc(R * sizeof(int));
     d->req_limit = dmalloc(R * sizeof(int));
     d->req_flags = dmalloc(R * sizeof(int));
@@ -246,12 +253,12 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->kcross = dmalloc(cross_el * e->esz);
     e->vcross = dmalloc(cross_el * e->esz);
     e->enc_pool = dmalloc((size_t)R * tmax * DEC_D * sizeof(float));
-    e->h = dmalloc((size_t)S * DEC_D * 4);
-    e->q = dmalloc((size_t)S * DEC_D * 4);
-    e->parts = dmalloc((size_t)CT_MAX_KSPLIT * S * DEC_D * 4);
-    e->lnf = dmalloc(ct_frag_elems(S, DEC_D) * 2);
-    e->attf = dmalloc(ct_frag_elems(S, DEC_D) * 2);
-    e->midf = dmalloc(ct_frag_elems(S, DEC_FF) * 2);
+    e->h = dmalloc((size_t)NR * DEC_D * 4);
+    e->q = dmalloc((size_t)NR * DEC_D * 4);
+    e->parts = dmalloc((size_t)CT_MAX_KSPLIT * NR * DEC_D * 4);
+    e->lnf = dmalloc(ct_frag_elems(NR, DEC_D) * 2);
+    e->attf = dmalloc(ct_frag_elems(NR, DEC_D) * 2);
+    e->midf = dmalloc(ct_frag_elems(NR, DEC_FF) * 2);
     e->logits = dmalloc((size_t)S * VOCAB * 4);
     if (CT_ATTN_CHUNK > 0) {
         const int longest = d->smax > tmax ? d->smax : tmax;
@@ -260,10 +267,21 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
         e->att_ml = dmalloc(items * 2 * 4);
         e->att_po = dmalloc(items * DEC_DK * 4);
     }
-    ECHK(hipMemsetAsync(e->h, 0, (size_t)S * DEC_D * 4, e->s));
+    ECHK(hipMemsetAsync(e->h, 0, (size_t)NR * DEC_D * 4, e->s));
+    ECHK(hipMemsetAsync(d->act, 0, NR * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->tok, 0, NR * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->pos_len, 0, NR * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->cross_len, 0, NR * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->cross_idx, 0, NR * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->row_slot, 0, NR * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->kv_rowoff, 0xff, NR * sizeof(long), e->s));
+    e->M = S;
     e->req = calloc(R, sizeof(HostReq));
     const char *eg = getenv("HIPB_EAGER");
     e->eager = eg && eg[0] == '1';
+    const char *pm = getenv("HIPB_PREFILL_MIN");
+    e->prefill_min = pm ? atoi(pm) : 1;
+    if (e->prefill_min < 1) e->prefill_min = 1;
     mel_tables_init(e);
     ECHK(hipHostMalloc((void **)&e->h_tmp, (size_t)(R + 8) * (MAX_SEQ + 8) * sizeof(int), 0));
     ECHK(hipStreamSynchronize(e->s));
@@ -273,8 +291,10 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
 void hipb_destroy(HipbEngine *e) {
     if (!e) return;
     ECHK(hipStreamSynchronize(e->s));
-    if (e->have_graph) { hipGraphExecDestroy(e->exec); hipGraphDestroy(e->graph); }
+    for (int w = 0; w < 2; w++)
+        if (e->have_graph[w]) { hipGraphExecDestroy(e->exec[w]); hipGraphDestroy(e->graph[w]); }
     void *ptrs[] = {e->d.slot_req, e->d.slot_S, e->d.act, e->d.tok, e->d.pos_len, e->d.cross_len,
+                    e->d.row_slot,
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
                     e->d.req_next, e->d.rq, e->d.pend,
@@ -304,6 +324,7 @@ void hipb_reset(HipbEngine *e) {
     }
     e->n_req = e->n_enc = 0;
     e->bench_mode = 0;
+    e->stepped = 0;
     ECHK(hipMemsetAsync(e->d.slot_req, 0xff, e->d.slots * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.slot_S, 0, e->d.slots * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.req_ngen, 0, e->d.max_req * sizeof(int), e->s));
@@ -697,12 +718,12 @@ static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, 
     a.K = K; a.V = V; a.kv_bf16 = e->esz == 2;
     a.kv_sb = item_stride; a.kv_st = DEC_DK; a.kv_sh = head_stride;
     a.lens = lens; a.lens_step = 1; a.kv_index = kv_index;
-    a.T_q = 1; a.B = e->d.slots; a.H = DEC_H;
+    a.T_q = 1; a.B = e->M; a.H = DEC_H;
     a.scale = 0.08838834764831845f;   /* 1/sqrt(128) */
     if (q_bias) {
         a.q_parts = e->parts;
         a.q_nparts = ctk_gemv_ksplit(DEC_D, DEC_D);
-        a.q_pstride = (long)e->d.slots * DEC_D;
+        a.q_pstride = (long)e->M * DEC_D;
         a.q_bias = q_bias;
     }
     a.out_frag = e->attf;
@@ -729,7 +750,8 @@ static void step_attention(HipbEngine *e, int l, int cross) {
     void *k, *v;
     if (!cross) {
         self_kv(e, l, &k, &v);
-        attn(e, k, v, (long)DEC_H * e->d.kv_rows * DEC_DK, (long)e->d.kv_rows * DEC_DK, e->d.pos_len, NULL, NULL);
+        attn(e, k, v, (long)DEC_H * e->d.kv_rows * DEC_DK, (long)e->d.kv_rows * DEC_DK, e->d.pos_len,
+             e->d.row_slot, NULL);
     } else {
         cross_kv(e, l, &k, &v);
         attn(e, k, v, (long)DEC_H * e->d.tmax * DEC_DK, (long)e->d.tmax * DEC_DK,
@@ -743,7 +765,7 @@ static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint1
     CtGemv g;
     memset(&g, 0, sizeof g);
     g.A = A; g.W = Wd; g.bias = bd;
-    g.M = e->d.slots; g.N = N; g.K = K;
+    g.M = e->M; g.N = N; g.K = K;
     g.out = out; g.relu = relu;
     g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, K) : 1;
     g.Y = out == CT_GV_PARTIAL ? e->parts : Y;
@@ -751,13 +773,16 @@ static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint1
     ctk_gemv(&g, e->s);
 }
 
-/* One decode step.  full == 0 launches only its GEMMs (timing support). */
-static void step_kernels(HipbEngine *e, int full) {
+/* One decode step over slots rows, or (wide) over slots + prefill_rows rows
+ * whose spare rows feed prompts several tokens a step.  full == 0 launches
+ * only its GEMMs (timing support). */
+static void step_kernels(HipbEngine *e, int full, int wide) {
     const Weights *W = &e->W;
-    const int B = e->d.slots;
+    const int B = wide ? e->d.rows : e->d.slots;
     hipStream_t s = e->s;
     const int ks_o = ctk_gemv_ksplit(DEC_D, DEC_D), ks_ff = ctk_gemv_ksplit(DEC_D, DEC_FF);
-    if (full) ctk_eng_begin(&e->d, s);
+    e->M = B;
+    if (full) ctk_eng_begin(&e->d, B - e->d.slots, s);
     if (full) ctk_embed_ln(e->h, e->d.tok, B, 0, e->d.pos_len, e->d.act, DW(W->etw), DW(W->epw),
                  DW(W->elnw), DW(W->elnb), s);
     /* each LayerNorm first adds the previous projection's K-slices + bias to h */
@@ -792,13 +817,29 @@ static void step_kernels(HipbEngine *e, int full) {
         pb = DW(L->ffn_b2);
     }
     if (full) ctk_ln_frag(e->h, e->lnf, e->parts, np, pb, DW(W->dlnw), DW(W->dlnb), B, s);
+    /* logits only for the slots' own rows */
+    e->M = e->d.slots;
     gv(e, e->lnf, DW(W->etw), DW(W->hdb), VOCAB, DEC_D, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);
     if (full) ctk_eng_end(&e->d, e->logits, s);
+    e->M = e->d.slots;
 }
 
-static void step_launch(HipbEngine *e) { step_kernels(e, 1); }
+static void step_launch(HipbEngine *e, int wide) { step_kernels(e, 1, wide); }
 
-void hipb_step(HipbEngine *e) { step_launch(e); }
+/* The wide step while prompt tokens wait to be fed, or before the first
+ * step while requests wait for admission. */
+static int want_wide(const HipbEngine *e, const int *q) {
+    return e->d.rows > e->d.slots && (q[3] >= e->prefill_min || (e->stepped == 0 && q[1] > q[0]));
+}
+
+static void read_queue(HipbEngine *e, int *q);
+
+void hipb_step(HipbEngine *e) {
+    int q[4];
+    read_queue(e, q);
+    step_launch(e, want_wide(e, q));
+    e->stepped++;
+}
 
 void hipb_attention_only(HipbEngine *e) {
     for (int l = 0; l < DEC_N; l++) {
@@ -807,46 +848,57 @@ void hipb_attention_only(HipbEngine *e) {
     }
 }
 
-int hipb_finished(HipbEngine *e) {
-    int v = 0;
-    ECHK(hipMemcpyAsync(e->h_tmp, e->d.q + 2, sizeof(int), hipMemcpyDeviceToHost, e->s));
+/* Reads the queue words (synchronises): q[0..3]. */
+static void read_queue(HipbEngine *e, int *q) {
+    ECHK(hipMemcpyAsync(e->h_tmp, e->d.q, 4 * sizeof(int), hipMemcpyDeviceToHost, e->s));
     ECHK(hipStreamSynchronize(e->s));
-    v = e->h_tmp[0];
-    return v;
+    memcpy(q, e->h_tmp, 4 * sizeof(int));
 }
 
-static void ensure_graph(HipbEngine *e) {
-    if (e->have_graph || e->eager) return;
+int hipb_finished(HipbEngine *e) {
+    int q[4];
+    read_queue(e, q);
+    return q[2];
+}
+
+static void ensure_graph(HipbEngine *e, int wide) {
+    if (e->have_graph[wide] || e->eager) return;
     ECHK(hipStreamBeginCapture(e->s, hipStreamCaptureModeThreadLocal));
-    step_launch(e);
-    ECHK(hipStreamEndCapture(e->s, &e->graph));
-    ECHK(hipGraphInstantiate(&e->exec, e->graph, NULL, NULL, 0));
-    e->have_graph = 1;
+    step_launch(e, wide);
+    ECHK(hipStreamEndCapture(e->s, &e->graph[wide]));
+    ECHK(hipGraphInstantiate(&e->exec[wide], e->graph[wide], NULL, NULL, 0));
+    e->have_graph[wide] = 1;
 }
 
-static void launch_step(HipbEngine *e) {
-    if (e->eager) step_launch(e);
-    else ECHK(hipGraphLaunch(e->exec, e->s));
+static void launch_step(HipbEngine *e, int wide) {
+    if (e->eager) step_launch(e, wide);
+    else ECHK(hipGraphLaunch(e->exec[wide], e->s));
 }
 
 void hipb_bench_steps(HipbEngine *e, int n) {
-    ensure_graph(e);
-    for (int i = 0; i < n; i++) launch_step(e);
+    ensure_graph(e, 0);
+    for (int i = 0; i < n; i++) launch_step(e, 0);
 }
 
 long hipb_run(HipbEngine *e, int chunk) {
     if (chunk < 1) chunk = 1;
-    ensure_graph(e);
+    const int spare = e->d.rows - e->d.slots;
+    ensure_graph(e, 0);
+    if (spare) ensure_graph(e, 1);
     long steps = 0;
     /* every admitted request finishes within prompt + limit <= prompt +
      * MAX_SEQ steps of its admission, and some request is admitted whenever
      * a slot frees up */
     const long bound = (long)(e->n_enc + 2) * (MAX_SEQ + CT_PROMPT_MAX + 1);
     for (;;) {
-        if (hipb_finished(e) >= e->n_enc) break;
+        int q[4];
+        read_queue(e, q);
+        if (q[2] >= e->n_enc) break;
         if (steps > bound) CT_FATAL("hipb_run: requests did not finish within the step bound");
-        for (int i = 0; i < chunk; i++) launch_step(e);
+        const int wide = want_wide(e, q);
+        for (int i = 0; i < chunk; i++) launch_step(e, wide);
         steps += chunk;
+        e->stepped += chunk;
     }
     return steps;
 }
@@ -926,7 +978,7 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
     e->bench_mode = 1;
 }
 
-void hipb_bench_decode_gemms(HipbEngine *e) { step_kernels(e, 0); }
+void hipb_bench_decode_gemms(HipbEngine *e) { step_kernels(e, 0, 0); }
 
 void hipb_bench_encoder_gemm(HipbEngine *e, int M) {
     if (M < 1) CT_FATAL("hipb_bench_encoder_gemm: M < 1");

@@ -11,16 +11,48 @@
 #include "ct_engine.h"
 #include "../../include/model_types.h"
 #include <limits.h>
+#include <stdio.h>
+#include <stdlib.h>
 
 #define EOS_ID 3   // model.h:24
 
 namespace {
 
-__global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d) {
+// Writes row `row` of the step: token `tok` of slot s's request r at
+// position pos (0-based) of the slot's self cache.
+__device__ __forceinline__ void set_row(const CtEngDev &d, int row, int s, int r, int tok, int pos) {
+    d.act[row] = 1;
+    d.tok[row] = tok;
+    d.pos_len[row] = pos + 1;
+    d.cross_len[row] = d.req_T[r];
+    d.cross_idx[row] = r;
+    d.row_slot[row] = s;
+    d.kv_rowoff[row] = ((long)s * DEC_H * d.kv_rows + pos) * DEC_DK;
+}
+
+__device__ __forceinline__ void clear_row(const CtEngDev &d, int row) {
+    d.act[row] = 0;
+    d.tok[row] = 0;
+    d.pos_len[row] = 0;
+    d.cross_len[row] = 0;
+    d.cross_idx[row] = 0;
+    d.row_slot[row] = 0;
+    d.kv_rowoff[row] = -1;
+}
+
+// Admission, then the rows of this step.  Slot s always owns row s, which
+// carries the slot's last token of the step (so the LM head and eng_end stay
+// per slot).  With `extra` spare rows (rows slots .. slots+extra-1), a slot
+// still feeding its prompt takes up to `extra` more prompt tokens this step,
+// spare rows dealt in slot order; each row is an ordinary decode row at its
+// own position, so a prompt fed k tokens per step gives the same bits as one
+// per step.  q[3] receives the prompt tokens still unfed after this step.
+__global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     const int tid = threadIdx.x;
     // Slot table and released successors read in parallel into LDS; the
     // admission itself is one sequential pass over slots in slot order.
     __shared__ int s_req[CT_ENG_MAX_SLOTS], s_pend[CT_ENG_MAX_SLOTS], s_new[CT_ENG_MAX_SLOTS];
+    __shared__ int s_wsum[4], s_left[4];
     for (int s = tid; s < d.slots; s += 256) {
         s_req[s] = d.slot_req[s];
         s_pend[s] = d.pend[s];
@@ -41,32 +73,53 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d) {
         d.q[1] = ready;
     }
     __syncthreads();
-    for (int s = tid; s < d.slots; s += 256) {
+    // slot tid (slots <= 256): spare rows wanted, then their exclusive prefix
+    const int s = tid;
+    int r = -1, S = 0, np = 0, want = 0;
+    if (s < d.slots) {
         if (s_pend[s] >= 0) d.pend[s] = -1;
-        const int r = s_req[s];
+        r = s_req[s];
         d.slot_req[s] = r;
         if (r >= 0) {
-            int S = s_new[s] ? 0 : d.slot_S[s];
-            const int np = d.req_np[r];
-            const int t = S < np ? d.req_prompt[r * CT_PROMPT_MAX + S]
-                                 : d.req_out[(long)r * d.smax + d.req_ngen[r] - 1];
-            S += 1;
-            d.slot_S[s] = S;
-            d.act[s] = 1;
-            d.tok[s] = t;
-            d.pos_len[s] = S;
-            d.cross_len[s] = d.req_T[r];
-            d.cross_idx[s] = r;
-            d.kv_rowoff[s] = ((long)s * DEC_H * d.kv_rows + (S - 1)) * DEC_DK;
-        } else {
-            d.act[s] = 0;
-            d.tok[s] = 0;
-            d.pos_len[s] = 0;
-            d.cross_len[s] = 0;
-            d.cross_idx[s] = 0;
-            d.kv_rowoff[s] = -1;
+            S = s_new[s] ? 0 : d.slot_S[s];
+            np = d.req_np[r];
+            if (S < np) want = min(np - S, 1 + extra) - 1;
         }
     }
+    int x = want;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if ((tid & 63) >= o) x += y;
+    }
+    if ((tid & 63) == 63) s_wsum[tid >> 6] = x;
+    __syncthreads();
+    int base = x - want;
+    for (int w = 0; w < (tid >> 6); w++) base += s_wsum[w];
+    const int wanted = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+    const int granted = max(0, min(want, extra - base));
+    int left = 0;
+    if (r >= 0) {
+        const int k = 1 + granted;
+        for (int j = 0; j < granted; j++)
+            set_row(d, d.slots + base + j, s, r, d.req_prompt[r * CT_PROMPT_MAX + S + j], S + j);
+        const int p = S + k - 1;
+        const int t = p < np ? d.req_prompt[r * CT_PROMPT_MAX + p]
+                             : d.req_out[(long)r * d.smax + d.req_ngen[r] - 1];
+        set_row(d, s, s, r, t, p);
+        d.slot_S[s] = S + k;
+        left = max(0, np - (S + k));
+    } else if (s < d.slots) {
+        clear_row(d, s);
+    }
+    // spare rows nobody took this step
+    for (int i = min(wanted, extra) + tid; i < extra; i += 256) clear_row(d, d.slots + i);
+    // prompt tokens still to feed, summed over slots
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) left += __shfl_xor(left, o, 64);
+    if ((tid & 63) == 0) s_left[tid >> 6] = left;
+    __syncthreads();
+    if (tid == 0) d.q[3] = s_left[0] + s_left[1] + s_left[2] + s_left[3];
 }
 
 __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
@@ -162,8 +215,13 @@ __global__ void fill_random_kernel(void *p, long n, int bf16, float scale, uint6
 
 }  // namespace
 
-extern "C" void ctk_eng_begin(const CtEngDev *d, hipStream_t s) {
-    hipLaunchKernelGGL(eng_begin_kernel, dim3(1), dim3(256), 0, s, *d);
+extern "C" void ctk_eng_begin(const CtEngDev *d, int extra, hipStream_t s) {
+    if (d->slots > CT_ENG_MAX_SLOTS || extra < 0 || d->slots + extra > d->rows) {
+        fprintf(stderr, "ctk_eng_begin: %d slots + %d spare rows exceed the engine's %d rows\n",
+                d->slots, extra, d->rows);
+        exit(1);
+    }
+    hipLaunchKernelGGL(eng_begin_kernel, dim3(1), dim3(256), 0, s, *d, extra);
 }
 
 extern "C" void ctk_eng_end(const CtEngDev *d, const float *logits, hipStream_t s) {

@@ -40,6 +40,10 @@ typedef struct {
     int kv_bf16;        /* 1: bf16 KV caches, 0: fp32                           */
     int max_tokens;     /* longest prompt + limit of any request (sizes the self
                            caches), <= MAX_SEQ; 0 means MAX_SEQ                 */
+    int prefill_rows;   /* spare step rows for prompts (0..256): while prompt
+                           tokens wait, hipb_run launches a step of slots +
+                           prefill_rows rows that feeds several prompt tokens
+                           of a slot at once (same bits as one per step)       */
 } HipbConfig;
 
 /* Request policy flags. */

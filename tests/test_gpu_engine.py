@@ -260,12 +260,14 @@ def chunked_oracle(hot):
     return out
 
 
-def test_engine_chunked_carry_matches_oracle(hip, hot, mels, oracle_runs, chunked_oracle):
+@pytest.mark.parametrize("prefill_rows", [0, 8])
+def test_engine_chunked_carry_matches_oracle(hip, hot, mels, oracle_runs, chunked_oracle, prefill_rows):
     """Two long recordings queued as chained chunks plus one plain request on
     two slots: every chunk waits for its predecessor, gets the carried ids in
-    its prompt on the device, and decodes to the oracle's tokens."""
+    its prompt on the device, and decodes to the oracle's tokens (with and
+    without spare prompt rows)."""
     eng = cb.Engine(hot, slots=2, max_requests=16, max_frames=64, kv_bf16=True,
-                    max_tokens=len(cb.PROMPT) + 64 + CHUNK_LIMIT)
+                    max_tokens=len(cb.PROMPT) + 64 + CHUNK_LIMIT, prefill_rows=prefill_rows)
     try:
         a, b = REC_SEEDS
         ids = {}
@@ -301,5 +303,52 @@ def test_engine_chunk_equals_request_with_carried_prompt(hip, hot, chunked_oracl
         eng.run(chunk=2)
         for r, (_, _, toks) in zip(rids, ref[1:]):
             assert np.array_equal(eng.tokens(r), toks), r
+    finally:
+        eng.close()
+
+
+def test_engine_prefill_rows_bitexact(hip, hot, mels):
+    """Spare prompt rows feed a 16-id prompt in 1 step (16 rows) or 4 steps
+    (3 rows: 4 ids a step) instead of 16: the generated ids and the logits
+    of the last step are the same bits as with one prompt id per step."""
+    prompt = np.asarray(list(cb.PROMPT) + [20, 21, 22, 23, 24, 25], np.int32)
+    limit = 6
+    res = {}
+    for P in (0, 3, 16):
+        eng = cb.Engine(hot, slots=1, max_requests=1, max_frames=64, kv_bf16=True,
+                        max_tokens=len(prompt) + limit, prefill_rows=P)
+        try:
+            eng.submit(mels[1], limit, FLAGS, prompt=prompt)
+            eng.encode()
+            steps = 0
+            while eng.finished() < 1:
+                eng.step()
+                steps += 1
+                assert steps < 64
+            res[P] = (eng.tokens(0), eng.logits(0), steps)
+        finally:
+            eng.close()
+        print(f"case: prefill_rows={P}: {res[P][2]} steps", flush=True)
+    assert [res[P][2] for P in (0, 3, 16)] == [16 + limit - 1, 4 + limit - 1, 1 + limit - 1]
+    for P in (3, 16):
+        assert np.array_equal(res[P][0], res[0][0]), P
+        assert np.array_equal(res[P][1].view(np.uint32), res[0][1].view(np.uint32)), P
+
+
+def test_engine_prefill_rows_continuous_batching(hip, hot, mels, oracle_runs):
+    """Six requests through two slots with 5 spare prompt rows (two slots
+    compete for them when both admit at once): the oracle's tokens."""
+    eng = cb.Engine(hot, slots=2, max_requests=8, max_frames=64, kv_bf16=True,
+                    max_tokens=len(cb.PROMPT) + max(LIMITS), prefill_rows=5)
+    order = [0, 1, 2, 2, 0, 1]
+    try:
+        for i in order:
+            eng.submit(mels[i], LIMITS[i], FLAGS)
+        eng.encode()
+        steps = eng.run(chunk=1)
+        assert eng.finished() == len(order)
+        for r, i in enumerate(order):
+            assert np.array_equal(eng.tokens(r), oracle_runs[(True, i)][0]), (r, i)
+        print(f"case: 6 requests, 2 slots, 5 spare rows: {steps} steps", flush=True)
     finally:
         eng.close()
