@@ -88,7 +88,7 @@ enum {
 };
 typedef struct {
     const uint16_t *A;        /* frag-ordered activations [M][K]                      */
-    const uint16_t *W;        /* [N][K] bf16                                           */
+    const uint16_t *W;        /* [N][K] bf16, or tiled (wtile)                         */
     const uint16_t *bias;     /* [N] bf16 or NULL (ignored for CT_GV_PARTIAL)          */
     int M, N, K;
     int ksplit;               /* K-slices (workgroups along K); 1 unless PARTIAL       */
@@ -99,9 +99,18 @@ typedef struct {
     const long *rowoff;
     long hstride;
     int kv_bf16;
+    int wtile;                /* 1: W in the tile layout of ctk_tile_w                 */
 } CtGemv;
 /* Requires N % 16 == 0 (N % 64 == 0 when N >= 8192), K % (256 * steps) == 0. */
 void ctk_gemv(const CtGemv *g, hipStream_t s);
+/* Tile layout of a decode-GEMM weight W[N][K] (N % 16 == 0, K % 32 == 0):
+ * one 1024-entry tile per (16 output rows, K-step of 32), tiles ordered
+ * row block major; lane l of a tile holds W[16*rb + (l & 15)][32*st +
+ * 8*(l >> 4) .. +7], so a wavefront's weight load is one contiguous 1 KB. */
+static inline CT_HD long ct_wtile_off(int n, int k, int K) {
+    return ((((long)(n >> 4) * (K >> 5) + (k >> 5)) * 64 + (((k >> 3) & 3) << 4) + (n & 15)) << 3) + (k & 7);
+}
+void ctk_tile_w(const uint16_t *W, uint16_t *Wt, int N, int K, hipStream_t s);
 /* K-slices the decode GEMM uses for an N x K weight (a function of the shape
  * only, so every row's result is independent of M). */
 int  ctk_gemv_ksplit(int N, int K);

@@ -40,6 +40,12 @@ struct HipbEngine {
     CtEngDev d;
     /* repacked weights: [Wq;Wk;Wv] per layer, [Wk;Wv] cross per layer */
     uint16_t *wqkv, *bqkv, *wckv, *bckv;
+    /* decode-GEMM weights in the tile layout (ctk_tile_w), one allocation:
+     * per layer [Wq;Wk;Wv], Wo, Wq_cross, Wo_cross, W_ffn1, W_ffn2; then the
+     * tied LM head */
+    uint16_t *wtile;
+    const uint16_t *wt_qkv[DEC_N], *wt_o[DEC_N], *wt_cq[DEC_N], *wt_co[DEC_N], *wt_f1[DEC_N],
+        *wt_f2[DEC_N], *wt_lm;
     /* caches */
     void *kself, *vself;       /* [L][slots][H][kv_rows][128] */
     void *kcross, *vcross;     /* [L][max_req][H][tmax][128] */
@@ -246,6 +252,22 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
         ECHK(hipMemcpyAsync((char *)e->bckv + (2 * l) * bsz, DW(L->ca_kb), bsz, hipMemcpyDeviceToDevice, e->s));
         ECHK(hipMemcpyAsync((char *)e->bckv + (2 * l + 1) * bsz, DW(L->ca_vb), bsz, hipMemcpyDeviceToDevice, e->s));
     }
+    {
+        const size_t DD = (size_t)DEC_D * DEC_D, per = 3 * DD + 3 * DD + 2 * (size_t)DEC_FF * DEC_D;
+        e->wtile = dmalloc((DEC_N * per + (size_t)VOCAB * DEC_D) * 2);
+        uint16_t *p = e->wtile;
+        for (int l = 0; l < DEC_N; l++) {
+            const DLayer *L = &W->dec[l];
+            ctk_tile_w(e->wqkv + 3 * l * DD, p, 3 * DEC_D, DEC_D, e->s); e->wt_qkv[l] = p; p += 3 * DD;
+            ctk_tile_w(DW(L->sa_ow), p, DEC_D, DEC_D, e->s); e->wt_o[l] = p; p += DD;
+            ctk_tile_w(DW(L->ca_qw), p, DEC_D, DEC_D, e->s); e->wt_cq[l] = p; p += DD;
+            ctk_tile_w(DW(L->ca_ow), p, DEC_D, DEC_D, e->s); e->wt_co[l] = p; p += DD;
+            ctk_tile_w(DW(L->ffn_w1), p, DEC_FF, DEC_D, e->s); e->wt_f1[l] = p; p += (size_t)DEC_FF * DEC_D;
+            ctk_tile_w(DW(L->ffn_w2), p, DEC_D, DEC_FF, e->s); e->wt_f2[l] = p; p += (size_t)DEC_FF * DEC_D;
+        }
+        ctk_tile_w(DW(W->etw), p, VOCAB, DEC_D, e->s);
+        e->wt_lm = p;
+    }
     const size_t self_el = (size_t)DEC_N * S * DEC_H * d->kv_rows * DEC_DK;
     const size_t cross_el = (size_t)DEC_N * R * DEC_H * tmax * DEC_DK;
     e->kself = dmalloc(self_el * e->esz);
@@ -298,7 +320,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
                     e->d.req_next, e->d.rq, e->d.pend,
-                    e->wqkv, e->bqkv, e->wckv, e->bckv, e->kself, e->vself, e->kcross, e->vcross,
+                    e->wqkv, e->bqkv, e->wckv, e->bckv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
                     e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
                     e->att_ml, e->att_po,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
@@ -760,11 +782,18 @@ static void step_attention(HipbEngine *e, int l, int cross) {
 }
 
 /* Decode GEMM over all slots; CT_GV_PARTIAL outputs go to parts. */
+/* Decode GEMMs read the tiled weight copies (one contiguous 1 KB per
+ * wavefront load); CT_ENG_WTILE=0 builds the row-major reads instead. */
+#ifndef CT_ENG_WTILE
+#define CT_ENG_WTILE 1
+#endif
+#define WT(tiled, rowmajor) (CT_ENG_WTILE ? (tiled) : (rowmajor))
+
 static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint16_t *bd, int N, int K,
                int out, int relu, float *Y, long ldy, uint16_t *F) {
     CtGemv g;
     memset(&g, 0, sizeof g);
-    g.A = A; g.W = Wd; g.bias = bd;
+    g.A = A; g.W = Wd; g.bias = bd; g.wtile = CT_ENG_WTILE;
     g.M = e->M; g.N = N; g.K = K;
     g.out = out; g.relu = relu;
     g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, K) : 1;
@@ -796,30 +825,31 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         CtGemv g;
         memset(&g, 0, sizeof g);
         g.A = e->lnf;
-        g.W = e->wqkv + (size_t)3 * l * DEC_D * DEC_D; g.bias = e->bqkv + (size_t)3 * l * DEC_D;
+        g.W = WT(e->wt_qkv[l], e->wqkv + (size_t)3 * l * DEC_D * DEC_D); g.wtile = CT_ENG_WTILE;
+        g.bias = e->bqkv + (size_t)3 * l * DEC_D;
         g.M = B; g.N = 3 * DEC_D; g.K = DEC_D; g.ksplit = 1; g.out = CT_GV_QKV;
         g.Y = e->q; g.ldy = DEC_D;
         g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)e->d.kv_rows * DEC_DK;
         g.kv_bf16 = e->esz == 2;
         ctk_gemv(&g, s);
         if (full) step_attention(e, l, 0);
-        gv(e, e->attf, DW(L->sa_ow), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        gv(e, e->attf, WT(e->wt_o[l], DW(L->sa_ow)), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
 
         if (full) ctk_ln_frag(e->h, e->lnf, e->parts, ks_o, DW(L->sa_ob), DW(L->ca_lnw), DW(L->ca_lnb), B, s);
-        gv(e, e->lnf, DW(L->ca_qw), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        gv(e, e->lnf, WT(e->wt_cq[l], DW(L->ca_qw)), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
         if (full) step_attention(e, l, 1);
-        gv(e, e->attf, DW(L->ca_ow), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        gv(e, e->attf, WT(e->wt_co[l], DW(L->ca_ow)), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
 
         if (full) ctk_ln_frag(e->h, e->lnf, e->parts, ks_o, DW(L->ca_ob), DW(L->ffn_lnw), DW(L->ffn_lnb), B, s);
-        gv(e, e->lnf, DW(L->ffn_w1), DW(L->ffn_b1), DEC_FF, DEC_D, CT_GV_FRAG, 1, NULL, 0, e->midf);
-        gv(e, e->midf, DW(L->ffn_w2), NULL, DEC_D, DEC_FF, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        gv(e, e->lnf, WT(e->wt_f1[l], DW(L->ffn_w1)), DW(L->ffn_b1), DEC_FF, DEC_D, CT_GV_FRAG, 1, NULL, 0, e->midf);
+        gv(e, e->midf, WT(e->wt_f2[l], DW(L->ffn_w2)), NULL, DEC_D, DEC_FF, CT_GV_PARTIAL, 0, NULL, 0, NULL);
         np = ks_ff;
         pb = DW(L->ffn_b2);
     }
     if (full) ctk_ln_frag(e->h, e->lnf, e->parts, np, pb, DW(W->dlnw), DW(W->dlnb), B, s);
     /* logits only for the slots' own rows */
     e->M = e->d.slots;
-    gv(e, e->lnf, DW(W->etw), DW(W->hdb), VOCAB, DEC_D, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);
+    gv(e, e->lnf, WT(e->wt_lm, DW(W->etw)), DW(W->hdb), VOCAB, DEC_D, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);
     if (full) ctk_eng_end(&e->d, e->logits, s);
     e->M = e->d.slots;
 }

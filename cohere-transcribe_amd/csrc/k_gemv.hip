@@ -49,7 +49,9 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
         }
 #pragma unroll
         for (int cb = 0; cb < CB; cb++)
-            wv[j][cb] = *reinterpret_cast<const u16x8 *>(g.W + (long)(c0 + cb * 16 + r) * g.K + st * 32 + kg * 8);
+            wv[j][cb] = *reinterpret_cast<const u16x8 *>(
+                g.wtile ? g.W + ((((long)(c0 >> 4) + cb) * nsteps + st) << 9) + lane * 8
+                        : g.W + (long)(c0 + cb * 16 + r) * g.K + st * 32 + kg * 8);
     }
     f32x4 acc[4][CB];
 #pragma unroll
@@ -127,6 +129,17 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
     }
 }
 
+// One thread per 16-byte piece of the tiled weight.
+__global__ __launch_bounds__(256) void tile_w_kernel(const uint16_t *W, uint16_t *Wt, int N, int K) {
+    const long piece = blockIdx.x * 256L + threadIdx.x, pieces = (long)N * K / 8;
+    if (piece >= pieces) return;
+    const int lane = (int)(piece & 63);
+    const long tile = piece >> 6;
+    const int nsteps = K >> 5, st = (int)(tile % nsteps), rb = (int)(tile / nsteps);
+    const int n = rb * 16 + (lane & 15), k = st * 32 + (lane >> 4) * 8;
+    *reinterpret_cast<u16x8 *>(Wt + piece * 8) = *reinterpret_cast<const u16x8 *>(W + (long)n * K + k);
+}
+
 [[noreturn]] void gv_fatal(const char *msg, const CtGemv *g) {
     fprintf(stderr, "ctk_gemv: %s (M=%d N=%d K=%d ksplit=%d out=%d)\n", msg, g->M, g->N, g->K,
             g->ksplit, g->out);
@@ -134,6 +147,15 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
 }
 
 }  // namespace
+
+extern "C" void ctk_tile_w(const uint16_t *W, uint16_t *Wt, int N, int K, hipStream_t s) {
+    if (N % 16 || K % 32 || ((uintptr_t)W & 15) || ((uintptr_t)Wt & 15)) {
+        fprintf(stderr, "ctk_tile_w: needs N %% 16 == 0, K %% 32 == 0 and 16-byte aligned buffers\n");
+        exit(1);
+    }
+    const long pieces = (long)N * K / 8;
+    hipLaunchKernelGGL(tile_w_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, W, Wt, N, K);
+}
 
 extern "C" int ctk_gemv_ksplit(int N, int K) {
     if (N <= DEC_D && K == DEC_D) return 4;       // 256-column slices, one K-step per wave

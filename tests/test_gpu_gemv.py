@@ -27,7 +27,7 @@ class CtGemv(C.Structure):
                 ("out", C.c_int), ("relu", C.c_int),
                 ("Y", C.c_void_p), ("ldy", C.c_long), ("F", C.c_void_p),
                 ("kc", C.c_void_p), ("vc", C.c_void_p), ("rowoff", C.c_void_p),
-                ("hstride", C.c_long), ("kv_bf16", C.c_int)]
+                ("hstride", C.c_long), ("kv_bf16", C.c_int), ("wtile", C.c_int)]
 
 
 def frag_index(M, K):
@@ -82,6 +82,7 @@ def lib(hip):
     L.ctk_gemv.argtypes = [C.POINTER(CtGemv), C.c_void_p]
     L.ctk_gemv_ksplit.argtypes = [C.c_int, C.c_int]
     L.ctk_gemv_ksplit.restype = C.c_int
+    L.ctk_tile_w.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
     L.ctk_ln_frag.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                               C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
     return L
@@ -113,12 +114,13 @@ class Dev:
         return out.view(np.uint8)[:nb].view(dtype).copy()
 
 
-def run_gemv(lib, dev, A_f32, pw, N, pb, out, relu=0, ksplit=1):
-    """pw / pb: device pointers of the bf16 weight [N][K] and bias (or None)."""
+def run_gemv(lib, dev, A_f32, pw, N, pb, out, relu=0, ksplit=1, wtile=0):
+    """pw / pb: device pointers of the bf16 weight [N][K] (tiled if wtile)
+    and bias (or None)."""
     M, K = A_f32.shape
     hi, lo = split(A_f32)
     pa = dev.put(to_frag(hi, lo))
-    g = CtGemv(A=pa, W=pw, bias=pb, M=M, N=N, K=K, ksplit=ksplit, out=out, relu=relu)
+    g = CtGemv(A=pa, W=pw, bias=pb, M=M, N=N, K=K, ksplit=ksplit, out=out, relu=relu, wtile=wtile)
     if out == PARTIAL:
         g.Y = dev.zeros(ksplit * M * N * 4)
     elif out == DENSE:
@@ -275,3 +277,45 @@ def test_ln_frag(lib, hip):
         hi, lo = from_frag(dev.get(pf, np.uint16, frag_elems(M, D)), M, D)
         got = bf16_to_f32(hi).astype(np.float64) + bf16_to_f32(lo)
         assert rel(got, ref) <= 1e-5
+
+
+def wtile_index(N, K):
+    """uint16 offset of W[n][k] in the tile layout: one 1024-entry tile per
+    (16 rows, K-step of 32), row-block major; lane 16*(k%32//8) + n%16 holds
+    8 consecutive k."""
+    n = np.arange(N)[:, None]
+    k = np.arange(K)[None, :]
+    tile = (n >> 4) * (K >> 5) + (k >> 5)
+    lane = (((k >> 3) & 3) << 4) + (n & 15)
+    return (tile << 9) + (lane << 3) + (k & 7)
+
+
+@pytest.mark.parametrize("N,K,out", [(1024, 1024, PARTIAL), (3072, 1024, DENSE), (4096, 1024, FRAG),
+                                     (1024, 4096, PARTIAL), (16384, 1024, DENSE)])
+def test_gemv_tiled_weights(lib, hip, N, K, out):
+    """ctk_tile_w writes the tile layout (checked element by element against
+    the index formula), and the GEMM on tiled weights gives the same bits as
+    on row-major ones."""
+    dev = Dev(hip)
+    rng = np.random.default_rng(N * 3 + K)
+    W = f32_to_bf16(rng.standard_normal((N, K)).astype(np.float32) * 0.03)
+    b = f32_to_bf16(rng.standard_normal(N).astype(np.float32) * 0.1)
+    pw, pb = dev.put(W), dev.put(b)
+    pt = dev.zeros(N * K * 2)
+    dev.ev.sync()
+    lib.ctk_tile_w(pw, pt, N, K, None)
+    tiled = dev.get(pt, np.uint16, N * K)
+    want = np.zeros(N * K, np.uint16)
+    want[wtile_index(N, K)] = W
+    assert np.array_equal(tiled, want)
+    ksplit = lib.ctk_gemv_ksplit(N, K) if out == PARTIAL else 1
+    for M in (1, 37, 64, 130):
+        print(f"case: tiled gemv N={N} K={K} out={out} M={M}", flush=True)
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        bias = None if out == PARTIAL else pb
+        a = run_gemv(lib, dev, A, pw, N, bias, out, relu=int(out == FRAG), ksplit=ksplit)
+        t = run_gemv(lib, dev, A, pt, N, bias, out, relu=int(out == FRAG), ksplit=ksplit, wtile=1)
+        if out == FRAG:
+            assert np.array_equal(a[0], t[0]) and np.array_equal(a[1], t[1]), M
+        else:
+            assert np.array_equal(a.view(np.uint32), t.view(np.uint32)), M
