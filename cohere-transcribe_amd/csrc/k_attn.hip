@@ -1,12 +1,13 @@
 // k_attn.hip — ragged scaled-dot-product attention for the decoder.
 //
 // One workgroup per (item, query row, head).  Sixteen 16-lane groups stream
-// the item's keys (group g takes keys g, g+16, ..., 8 of them per loop trip:
-// loads first, then one softmax update per trip); each lane owns 8 of the
-// 128 head dimensions, so a key row is read as one contiguous 256 B (bf16) or
-// 512 B (fp32) segment.  Each group keeps an online softmax (running max,
-// running sum, weighted V); the 16 partial states are merged in LDS in a fixed
-// order.  The key split depends only on the item's own length, so an item's
+// the item's keys (group g takes keys g, g+16, ..., KPI of them per loop
+// trip, one softmax update per trip, the next trip's loads in flight while
+// the current one is used); each lane owns 8 of the 128 head dimensions, so
+// a key row is read as one contiguous 256 B (bf16) or 512 B (fp32) segment.
+// Each group keeps an online softmax (running max, running sum, weighted V)
+// in base 2 on the hardware exp2; the 16 partial states are merged in LDS in
+// a fixed order.  The key split depends only on the item's own length, so an item's
 // result is the same whatever else is in the batch.
 //
 // Semantics: backends/cpu/backend.c:339-360 (scores * 1/sqrt(128) + mask,
@@ -22,6 +23,10 @@
 namespace {
 
 constexpr int CT_ATTN_QPARTS = 4;   // most query partial slices a launch may pass
+// 1: two key trips in flight per lane group (software pipelined)
+#ifndef CT_ATTN_PIPE
+#define CT_ATTN_PIPE 1
+#endif
 // lanes per key (16: 8 head dims a lane, 8: 16 a lane)
 #ifndef CT_ATTN_LPK
 #define CT_ATTN_LPK 16
@@ -60,6 +65,11 @@ __device__ __forceinline__ void store_out(const CtAttn &a, int bq, int col, long
     }
 }
 
+// Softmax weights as 2^x on the hardware exp2 (e^y = 2^(y log2 e), the
+// log2 e folded into the score scale); 2^-inf = 0.
+constexpr float LOG2E = 1.4426950408889634f;
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // Sum over aligned groups of LPK lanes (16 or 8), every lane gets the result.
 template <int LPK>
 __device__ __forceinline__ float group_sum(float v) {
@@ -73,7 +83,7 @@ __device__ __forceinline__ float group_sum(float v) {
 // LPK lanes per key: lane s of a group owns head dims [s*DPL, s*DPL + DPL),
 // DPL = 128 / LPK, read as NV 16-byte (bf16) pieces; NG = 256 / LPK groups
 // stream keys g, g + NG, ... (KPI of them per trip, loads first).
-template <bool BF16, bool VEC, int LPK>
+template <bool BF16, bool VEC, int LPK, bool MASK>
 __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
     constexpr int DPL = DEC_DK / LPK, NV = DPL / 8, NG = 256 / LPK;
     const int bq = blockIdx.x, h = blockIdx.y, ch = blockIdx.z;
@@ -127,7 +137,9 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
     if (ch >= nch) return;
     const int kb = a.chunk > 0 ? ch * a.chunk : 0;
     const int ke = ch == nch - 1 ? T : kb + a.chunk;
-    const float *mrow = a.mask ? a.mask + (long)qi * T : nullptr;
+    const float *mrow = MASK ? a.mask + (long)qi * T : nullptr;
+    // scores and running maxima are kept in base 2: s * scale * log2(e)
+    const float scale2 = a.scale * LOG2E;
     const long base = item * a.kv_sb + (long)h * a.kv_sh + ls * DPL;
 
     float m = -INFINITY, l = 0.0f, o[DPL];
@@ -140,26 +152,29 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
     constexpr int KPI = BF16 ? CT_ATTN_KPI : 4;
     // raw 16-byte pieces stay in registers until use (bf16: 4 VGPRs a piece)
     using Raw = typename std::conditional<BF16 && VEC, u16x8, float[8]>::type;
-    for (int k0 = kb + g; k0 < ke; k0 += NG * KPI) {
-        Raw kr[KPI][NV], vr[KPI][NV];
+    // trip at k0: keys k0 + NG*j (j < KPI) of this lane group.  Keys past
+    // the end re-read the last key (in bounds, never used): the loads carry
+    // no branch, so the wait before each use counts exactly the loads
+    // issued after it and the next trip's loads stay in flight.
+    auto load_trip = [&](int k0, Raw (&kr)[KPI][NV], Raw (&vr)[KPI][NV]) {
 #pragma unroll
         for (int j = 0; j < KPI; j++) {
-            const int k = k0 + NG * j;
-            if (k < ke) {
+            const int k = min(k0 + NG * j, ke - 1);
 #pragma unroll
-                for (int v = 0; v < NV; v++) {
-                    const long off = base + (long)k * a.kv_st + 8 * v;
-                    if constexpr (BF16 && VEC) {
-                        kr[j][v] = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.K) + off);
-                        vr[j][v] = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.V) + off);
-                    } else {
-                        load8<BF16, VEC>(a.K, off, kr[j][v]);
-                        load8<BF16, VEC>(a.V, off, vr[j][v]);
-                    }
+            for (int v = 0; v < NV; v++) {
+                const long off = base + (long)k * a.kv_st + 8 * v;
+                if constexpr (BF16 && VEC) {
+                    kr[j][v] = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.K) + off);
+                    vr[j][v] = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.V) + off);
+                } else {
+                    load8<BF16, VEC>(a.K, off, kr[j][v]);
+                    load8<BF16, VEC>(a.V, off, vr[j][v]);
                 }
             }
         }
-        // chunked online softmax: the trip's scores together, one rescale
+    };
+    // chunked online softmax: the trip's scores together, one rescale
+    auto use_trip = [&](int k0, const Raw (&kr)[KPI][NV], const Raw (&vr)[KPI][NV]) {
         float sc[KPI];
 #pragma unroll
         for (int j = 0; j < KPI; j++) {
@@ -178,17 +193,17 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
 #pragma unroll
         for (int j = 0; j < KPI; j++) {
             const int k = k0 + NG * j;
-            sc[j] = k < ke ? group_sum<LPK>(sc[j]) * a.scale + (mrow ? mrow[k] : 0.0f) : -INFINITY;
+            sc[j] = k < ke ? group_sum<LPK>(sc[j]) * scale2 + (MASK ? mrow[k] * LOG2E : 0.0f) : -INFINITY;
         }
         float mx = sc[0];
 #pragma unroll
         for (int j = 1; j < KPI; j++) mx = fmaxf(mx, sc[j]);
         const float mn = fmaxf(m, mx);
-        const float c = expf(m - mn);
+        const float c = exp2_hw(m - mn);
         float p[KPI], ps = 0.0f;
 #pragma unroll
         for (int j = 0; j < KPI; j++) {
-            p[j] = k0 + NG * j < ke ? expf(sc[j] - mn) : 0.0f;
+            p[j] = k0 + NG * j < ke ? exp2_hw(sc[j] - mn) : 0.0f;
             ps += p[j];
         }
         l = l * c + ps;
@@ -208,7 +223,29 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
                 o[8 * v + i] = acc;
             }
         m = mn;
+    };
+    constexpr int STEP = NG * KPI;
+#if CT_ATTN_PIPE
+    // two trips in flight: the next trip's loads are issued before the
+    // current trip is used (register sets A and B alternate)
+    Raw kA[KPI][NV], vA[KPI][NV], kB[KPI][NV], vB[KPI][NV];
+    int k0 = kb + g;
+    if (k0 < ke) load_trip(k0, kA, vA);
+    for (; k0 < ke; k0 += 2 * STEP) {
+        const int k1 = k0 + STEP;
+        load_trip(k1, kB, vB);
+        use_trip(k0, kA, vA);
+        if (k1 >= ke) break;
+        load_trip(k1 + STEP, kA, vA);
+        use_trip(k1, kB, vB);
     }
+#else
+    for (int k0 = kb + g; k0 < ke; k0 += STEP) {
+        Raw kr[KPI][NV], vr[KPI][NV];
+        load_trip(k0, kr, vr);
+        use_trip(k0, kr, vr);
+    }
+#endif
 
     __shared__ float sm[NG], sl[NG], so[NG][DEC_DK];
     if (ls == 0) { sm[g] = m; sl[g] = l; }
@@ -223,7 +260,7 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
 #pragma unroll
         for (int j = 0; j < NG; j++) {
             if (sm[j] == -INFINITY) continue;
-            const float w = expf(sm[j] - M);
+            const float w = exp2_hw(sm[j] - M);
             num += w * so[j][tid];
             den += w * sl[j];
         }
@@ -252,7 +289,7 @@ __global__ __launch_bounds__(DEC_DK) void attn_merge_kernel(CtAttn a) {
     for (int c = 0; c < nch; c++) M = fmaxf(M, a.part_ml[2 * (p0 + c)]);
     float num = 0.0f, den = 0.0f;
     for (int c = 0; c < nch; c++) {
-        const float w = expf(a.part_ml[2 * (p0 + c)] - M);
+        const float w = exp2_hw(a.part_ml[2 * (p0 + c)] - M);
         num += w * a.part_o[(p0 + c) * DEC_DK + tid];
         den += w * a.part_ml[2 * (p0 + c) + 1];
     }
@@ -280,13 +317,15 @@ extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
     const bool vec = ((uintptr_t)a->K % 16 == 0) && ((uintptr_t)a->V % 16 == 0) &&
                      a->kv_sb % need == 0 && a->kv_st % need == 0 && a->kv_sh % need == 0;
     constexpr int LPK = CT_ATTN_LPK;
-    if (a->kv_bf16) {
-        if (vec) hipLaunchKernelGGL((attn_kernel<true, true, LPK>), grid, dim3(256), 0, s, *a);
-        else hipLaunchKernelGGL((attn_kernel<true, false, LPK>), grid, dim3(256), 0, s, *a);
+#define AK(B, V, M) hipLaunchKernelGGL((attn_kernel<B, V, LPK, M>), grid, dim3(256), 0, s, *a)
+    if (a->mask) {
+        if (a->kv_bf16) { if (vec) AK(true, true, true); else AK(true, false, true); }
+        else { if (vec) AK(false, true, true); else AK(false, false, true); }
     } else {
-        if (vec) hipLaunchKernelGGL((attn_kernel<false, true, LPK>), grid, dim3(256), 0, s, *a);
-        else hipLaunchKernelGGL((attn_kernel<false, false, LPK>), grid, dim3(256), 0, s, *a);
+        if (a->kv_bf16) { if (vec) AK(true, true, false); else AK(true, false, false); }
+        else { if (vec) AK(false, true, false); else AK(false, false, false); }
     }
+#undef AK
     if (a->chunk > 0)
         hipLaunchKernelGGL(attn_merge_kernel, dim3(a->B * a->T_q, a->H), dim3(DEC_DK), 0, s, *a);
 }
