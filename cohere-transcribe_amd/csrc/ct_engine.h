@@ -23,11 +23,6 @@ extern "C" {
 #ifndef CT_KV_PAD
 #define CT_KV_PAD 0
 #endif
-/* Keys per workgroup of the decode attention; longer caches are split over
- * several workgroups and merged. */
-#ifndef CT_ATTN_CHUNK
-#define CT_ATTN_CHUNK 0
-#endif
 
 /* All pointers are device memory.  Slot-major arrays have `slots` entries,
  * request-major arrays `max_req`. */

@@ -170,12 +170,6 @@ typedef struct {
     /* optional: write the output split hi/lo in frag layout (K = H*128),
      * row b*T_q + qi, instead of out */
     uint16_t       *out_frag;
-    /* optional key split: items longer than chunk keys are processed by
-     * ceil(T/chunk) <= max_chunks workgroups whose partial softmax states
-     * (part_ml [B*T_q][H][max_chunks][2], part_o [..][128]) a second kernel
-     * merges in chunk order.  No mask. */
-    int    chunk, max_chunks;
-    float *part_ml, *part_o;
 } CtAttn;
 /* Head dim fixed at DEC_DK (128). */
 void ctk_attn(const CtAttn *a, hipStream_t s);

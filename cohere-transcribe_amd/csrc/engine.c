@@ -57,9 +57,6 @@ struct HipbEngine {
     long stepped;              /* steps launched since creation or reset */
     int prefill_min;           /* unfed prompt tokens that select the wide step */
     uint16_t *lnf, *attf, *midf;
-    /* attention key split: partial softmax states per (slot, head, chunk) */
-    int attn_chunks;
-    float *att_ml, *att_po;
     /* encoder workspace (lazy) */
     int enc_cap;               /* frames */
     int sub_cap;               /* subsampling scratch floats */
@@ -282,13 +279,6 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->attf = dmalloc(ct_frag_elems(NR, DEC_D) * 2);
     e->midf = dmalloc(ct_frag_elems(NR, DEC_FF) * 2);
     e->logits = dmalloc((size_t)S * VOCAB * 4);
-    if (CT_ATTN_CHUNK > 0) {
-        const int longest = d->smax > tmax ? d->smax : tmax;
-        e->attn_chunks = (longest + CT_ATTN_CHUNK - 1) / (CT_ATTN_CHUNK > 0 ? CT_ATTN_CHUNK : 1);
-        const size_t items = (size_t)S * DEC_H * e->attn_chunks;
-        e->att_ml = dmalloc(items * 2 * 4);
-        e->att_po = dmalloc(items * DEC_DK * 4);
-    }
     ECHK(hipMemsetAsync(e->h, 0, (size_t)NR * DEC_D * 4, e->s));
     ECHK(hipMemsetAsync(d->act, 0, NR * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->tok, 0, NR * sizeof(int), e->s));
@@ -322,7 +312,6 @@ void hipb_destroy(HipbEngine *e) {
                     e->d.req_next, e->d.rq, e->d.pend,
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
                     e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
-                    e->att_ml, e->att_po,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
                     e->eh, e->esub, e->emel, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
                     e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
@@ -749,10 +738,6 @@ static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, 
         a.q_bias = q_bias;
     }
     a.out_frag = e->attf;
-    a.chunk = CT_ATTN_CHUNK;
-    a.max_chunks = e->attn_chunks;
-    a.part_ml = e->att_ml;
-    a.part_o = e->att_po;
     ctk_attn(&a, e->s);
 }
 

@@ -86,7 +86,7 @@ __device__ __forceinline__ float group_sum(float v) {
 template <bool BF16, bool VEC, int LPK, bool MASK>
 __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
     constexpr int DPL = DEC_DK / LPK, NV = DPL / 8, NG = 256 / LPK;
-    const int bq = blockIdx.x, h = blockIdx.y, ch = blockIdx.z;
+    const int bq = blockIdx.x, h = blockIdx.y;
     const int b = bq / a.T_q, qi = bq % a.T_q;
     const int tid = threadIdx.x, g = tid / LPK, ls = tid % LPK;
     const long qoff = (long)b * a.q_sb + (long)qi * a.q_st + h * DEC_DK;
@@ -128,15 +128,10 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
         for (int i = 0; i < DPL; i++) q[i] = qp[i];
     }
     if (T <= 0) {
-        if (ch == 0 && tid < DEC_DK) store_out(a, bq, h * DEC_DK + tid, qoff + tid, 0.0f);
+        if (tid < DEC_DK) store_out(a, bq, h * DEC_DK + tid, qoff + tid, 0.0f);
         return;
     }
-    // keys [kb, ke) of this workgroup: one chunk of a.chunk keys (the last
-    // of at most max_chunks takes the rest), or all of them
-    const int nch = a.chunk > 0 ? min((T + a.chunk - 1) / a.chunk, a.max_chunks) : 1;
-    if (ch >= nch) return;
-    const int kb = a.chunk > 0 ? ch * a.chunk : 0;
-    const int ke = ch == nch - 1 ? T : kb + a.chunk;
+    const int kb = 0, ke = T;
     const float *mrow = MASK ? a.mask + (long)qi * T : nullptr;
     // scores and running maxima are kept in base 2: s * scale * log2(e)
     const float scale2 = a.scale * LOG2E;
@@ -264,37 +259,8 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
             num += w * so[j][tid];
             den += w * sl[j];
         }
-        if (nch == 1) {
-            store_out(a, bq, h * DEC_DK + tid, qoff + tid, num / den);
-        } else {
-            // partial state of this chunk, merged by attn_merge_kernel
-            const long pi = ((long)bq * a.H + h) * a.max_chunks + ch;
-            a.part_o[pi * DEC_DK + tid] = num;
-            if (tid == 0) { a.part_ml[2 * pi] = M; a.part_ml[2 * pi + 1] = den; }
-        }
+        store_out(a, bq, h * DEC_DK + tid, qoff + tid, num / den);
     }
-}
-
-// Items split into chunks: out = sum_c e^(M_c - M) num_c / sum_c e^(M_c - M)
-// den_c over the chunks in order, M = max_c M_c.  Items with one chunk were
-// written by attn_kernel.
-__global__ __launch_bounds__(DEC_DK) void attn_merge_kernel(CtAttn a) {
-    const int bq = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const int b = bq / a.T_q, qi = bq % a.T_q;
-    const int T = a.lens ? a.lens[(long)b * a.lens_step] : a.len_const;
-    const int nch = min((T + a.chunk - 1) / a.chunk, a.max_chunks);
-    if (T <= 0 || nch <= 1) return;
-    const long p0 = ((long)bq * a.H + h) * a.max_chunks;
-    float M = -INFINITY;
-    for (int c = 0; c < nch; c++) M = fmaxf(M, a.part_ml[2 * (p0 + c)]);
-    float num = 0.0f, den = 0.0f;
-    for (int c = 0; c < nch; c++) {
-        const float w = exp2_hw(a.part_ml[2 * (p0 + c)] - M);
-        num += w * a.part_o[(p0 + c) * DEC_DK + tid];
-        den += w * a.part_ml[2 * (p0 + c) + 1];
-    }
-    const long qoff = (long)b * a.q_sb + (long)qi * a.q_st + h * DEC_DK;
-    store_out(a, bq, h * DEC_DK + tid, qoff + tid, num / den);
 }
 
 }  // namespace
@@ -307,11 +273,7 @@ extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
         fprintf(stderr, "ctk_attn: query partials need 1..4 slices and 16-byte aligned rows\n");
         exit(1);
     }
-    if (a->chunk > 0 && (!a->part_o || !a->part_ml || a->max_chunks < 1 || a->mask)) {
-        fprintf(stderr, "ctk_attn: a key split needs partial buffers, max_chunks >= 1 and no mask\n");
-        exit(1);
-    }
-    const dim3 grid(a->B * a->T_q, a->H, a->chunk > 0 ? a->max_chunks : 1);
+    const dim3 grid(a->B * a->T_q, a->H);
     // 16-byte vector loads need every 8-element K/V segment aligned.
     const long esz = a->kv_bf16 ? 2 : 4, need = 16 / esz;
     const bool vec = ((uintptr_t)a->K % 16 == 0) && ((uintptr_t)a->V % 16 == 0) &&
@@ -326,6 +288,4 @@ extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
         else { if (vec) AK(false, true, false); else AK(false, false, false); }
     }
 #undef AK
-    if (a->chunk > 0)
-        hipLaunchKernelGGL(attn_merge_kernel, dim3(a->B * a->T_q, a->H), dim3(DEC_DK), 0, s, *a);
 }
