@@ -17,6 +17,14 @@ constexpr int LN_MAXV = 32;   // register-cached elements per lane (D <= 2048)
 // (backends/cpu/backend.c:109-122).
 __device__ __forceinline__ void ln_row(float (&v)[LN_MAXV], int D, int lane,
                                        const uint16_t *w, const uint16_t *b, float *dst) {
+    // gain and bias loaded before the reductions, so their latency overlaps
+    float wv[LN_MAXV], bv[LN_MAXV];
+#pragma unroll
+    for (int i = 0; i < LN_MAXV; i++) {
+        const int d = lane + i * 64;
+        wv[i] = d < D ? bf2f(w[d]) : 0.0f;
+        bv[i] = d < D ? bf2f(b[d]) : 0.0f;
+    }
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < LN_MAXV; i++) {
@@ -34,7 +42,7 @@ __device__ __forceinline__ void ln_row(float (&v)[LN_MAXV], int D, int lane,
 #pragma unroll
     for (int i = 0; i < LN_MAXV; i++) {
         const int d = lane + i * 64;
-        if (d < D) dst[d] = (v[i] - mu) * rs * bf2f(w[d]) + bf2f(b[d]);
+        if (d < D) dst[d] = (v[i] - mu) * rs * wv[i] + bv[i];
     }
 }
 
@@ -65,8 +73,14 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(float *dst, const fl
     if (row >= T) return;
     const float4 *x = reinterpret_cast<const float4 *>(src + (long)row * D);
     float4 v[V];
+    ushort4 w4[V], b4[V];
 #pragma unroll
     for (int i = 0; i < V; i++) v[i] = x[lane + 64 * i];
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        w4[i] = reinterpret_cast<const ushort4 *>(w)[lane + 64 * i];
+        b4[i] = reinterpret_cast<const ushort4 *>(b)[lane + 64 * i];
+    }
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < V; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
@@ -81,12 +95,11 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(float *dst, const fl
     float4 *y = reinterpret_cast<float4 *>(dst + (long)row * D);
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int d0 = 4 * (lane + 64 * i);
         float4 o;
-        o.x = (v[i].x - mu) * rs * bf2f(w[d0]) + bf2f(b[d0]);
-        o.y = (v[i].y - mu) * rs * bf2f(w[d0 + 1]) + bf2f(b[d0 + 1]);
-        o.z = (v[i].z - mu) * rs * bf2f(w[d0 + 2]) + bf2f(b[d0 + 2]);
-        o.w = (v[i].w - mu) * rs * bf2f(w[d0 + 3]) + bf2f(b[d0 + 3]);
+        o.x = (v[i].x - mu) * rs * bf2f(w4[i].x) + bf2f(b4[i].x);
+        o.y = (v[i].y - mu) * rs * bf2f(w4[i].y) + bf2f(b4[i].y);
+        o.z = (v[i].z - mu) * rs * bf2f(w4[i].z) + bf2f(b4[i].z);
+        o.w = (v[i].w - mu) * rs * bf2f(w4[i].w) + bf2f(b4[i].w);
         y[lane + 64 * i] = o;
     }
 }
@@ -102,8 +115,14 @@ __global__ __launch_bounds__(256) void layernorm_split_kernel(uint16_t *hi, uint
     if (row >= T) return;
     const float4 *x = reinterpret_cast<const float4 *>(src + (long)row * D);
     float4 v[V];
+    ushort4 w4[V], b4[V];
 #pragma unroll
     for (int i = 0; i < V; i++) v[i] = x[lane + 64 * i];
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        w4[i] = reinterpret_cast<const ushort4 *>(w)[lane + 64 * i];
+        b4[i] = reinterpret_cast<const ushort4 *>(b)[lane + 64 * i];
+    }
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < V; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
@@ -117,11 +136,10 @@ __global__ __launch_bounds__(256) void layernorm_split_kernel(uint16_t *hi, uint
     const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int d0 = 4 * (lane + 64 * i);
-        const float o[4] = {(v[i].x - mu) * rs * bf2f(w[d0]) + bf2f(b[d0]),
-                            (v[i].y - mu) * rs * bf2f(w[d0 + 1]) + bf2f(b[d0 + 1]),
-                            (v[i].z - mu) * rs * bf2f(w[d0 + 2]) + bf2f(b[d0 + 2]),
-                            (v[i].w - mu) * rs * bf2f(w[d0 + 3]) + bf2f(b[d0 + 3])};
+        const float o[4] = {(v[i].x - mu) * rs * bf2f(w4[i].x) + bf2f(b4[i].x),
+                            (v[i].y - mu) * rs * bf2f(w4[i].y) + bf2f(b4[i].y),
+                            (v[i].z - mu) * rs * bf2f(w4[i].z) + bf2f(b4[i].z),
+                            (v[i].w - mu) * rs * bf2f(w4[i].w) + bf2f(b4[i].w)};
         ushort4 h4, l4;
         uint16_t hh[4], ll[4];
 #pragma unroll
@@ -245,21 +263,26 @@ __global__ __launch_bounds__(256) void ln_frag_kernel(float *h, uint16_t *frag, 
     constexpr int D = DEC_D;
     const int row = blockIdx.x, t = threadIdx.x, wv = t >> 6, lane = t & 63;
     float4 *x = reinterpret_cast<float4 *>(h + (long)row * D);
-    float4 v = x[t];
     const int d0 = 4 * t;
-    if (NP > 0) {
-        float4 pr[NP > 0 ? NP : 1];
+    // every load first: the row, its partial slices, then the three bf16
+    // vectors (4 entries = 8 bytes each)
+    float4 v = x[t];
+    float4 pr[NP > 0 ? NP : 1];
 #pragma unroll
-        for (int p = 0; p < NP; p++)
-            pr[p] = reinterpret_cast<const float4 *>(parts + p * pstride + (long)row * D)[t];
+    for (int p = 0; p < NP; p++)
+        pr[p] = reinterpret_cast<const float4 *>(parts + p * pstride + (long)row * D)[t];
+    const ushort4 pb4 = (NP > 0 && pbias) ? reinterpret_cast<const ushort4 *>(pbias)[t] : make_ushort4(0, 0, 0, 0);
+    const ushort4 w4 = reinterpret_cast<const ushort4 *>(w)[t];
+    const ushort4 b4 = reinterpret_cast<const ushort4 *>(b)[t];
+    if (NP > 0) {
         float4 a = pr[0];
 #pragma unroll
         for (int p = 1; p < NP; p++) {
             a.x += pr[p].x; a.y += pr[p].y; a.z += pr[p].z; a.w += pr[p].w;
         }
         if (pbias) {
-            a.x += bf2f(pbias[d0]); a.y += bf2f(pbias[d0 + 1]);
-            a.z += bf2f(pbias[d0 + 2]); a.w += bf2f(pbias[d0 + 3]);
+            a.x += bf2f(pb4.x); a.y += bf2f(pb4.y);
+            a.z += bf2f(pb4.z); a.w += bf2f(pb4.w);
         }
         v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
         x[t] = v;
@@ -275,10 +298,10 @@ __global__ __launch_bounds__(256) void ln_frag_kernel(float *h, uint16_t *frag, 
     __syncthreads();
     const float var = ((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) / (float)D;
     const float rs = 1.0f / sqrtf(var + 1e-5f);
-    const float o[4] = {c0 * rs * bf2f(w[d0]) + bf2f(b[d0]),
-                        c1 * rs * bf2f(w[d0 + 1]) + bf2f(b[d0 + 1]),
-                        c2 * rs * bf2f(w[d0 + 2]) + bf2f(b[d0 + 2]),
-                        c3 * rs * bf2f(w[d0 + 3]) + bf2f(b[d0 + 3])};
+    const float o[4] = {c0 * rs * bf2f(w4.x) + bf2f(b4.x),
+                        c1 * rs * bf2f(w4.y) + bf2f(b4.y),
+                        c2 * rs * bf2f(w4.z) + bf2f(b4.z),
+                        c3 * rs * bf2f(w4.w) + bf2f(b4.w)};
     ushort4 h4, l4;
     uint16_t hh[4], ll[4];
 #pragma unroll
@@ -295,7 +318,8 @@ __global__ __launch_bounds__(256) void ln_frag_kernel(float *h, uint16_t *frag, 
 extern "C" void ctk_layernorm(float *dst, const float *src, const uint16_t *w, const uint16_t *b,
                               int T, int D, hipStream_t s) {
     if (T <= 0) return;
-    const bool al = ((uintptr_t)dst % 16 == 0) && ((uintptr_t)src % 16 == 0);
+    const bool al = ((uintptr_t)dst % 16 == 0) && ((uintptr_t)src % 16 == 0) &&
+                    ((uintptr_t)w % 8 == 0) && ((uintptr_t)b % 8 == 0);
     if (al && D == 1024)
         hipLaunchKernelGGL(layernorm_vec_kernel<4>, dim3((T + 3) / 4), dim3(256), 0, s, dst, src, w, b, T);
     else if (al && D == 1280)
@@ -309,8 +333,9 @@ extern "C" void ctk_layernorm(float *dst, const float *src, const uint16_t *w, c
 extern "C" void ctk_layernorm_split(uint16_t *hi, uint16_t *lo, const float *src, const uint16_t *w,
                                     const uint16_t *b, int T, int D, hipStream_t s) {
     if (T <= 0) return;
-    if ((uintptr_t)src % 16 || (uintptr_t)hi % 8 || (uintptr_t)lo % 8 || (D != 1024 && D != 1280)) {
-        fprintf(stderr, "ctk_layernorm_split: needs D in {1024, 1280} and aligned rows\n");
+    if ((uintptr_t)src % 16 || (uintptr_t)hi % 8 || (uintptr_t)lo % 8 || (uintptr_t)w % 8 ||
+        (uintptr_t)b % 8 || (D != 1024 && D != 1280)) {
+        fprintf(stderr, "ctk_layernorm_split: needs D in {1024, 1280}, aligned rows and 8-byte aligned gain/bias\n");
         exit(1);
     }
     if (D == 1024)
@@ -325,6 +350,10 @@ extern "C" void ctk_ln_frag(float *h, uint16_t *frag, const float *parts, int np
     if (M <= 0) return;
     if ((uintptr_t)h % 16 || (uintptr_t)frag % 16 || (nparts > 0 && (uintptr_t)parts % 16)) {
         fprintf(stderr, "ctk_ln_frag: needs 16-byte aligned buffers\n");
+        exit(1);
+    }
+    if ((uintptr_t)w % 8 || (uintptr_t)b % 8 || (pbias && (uintptr_t)pbias % 8)) {
+        fprintf(stderr, "ctk_ln_frag: LayerNorm gain/bias and the partials' bias need 8-byte alignment\n");
         exit(1);
     }
     const long ps = (long)M * DEC_D;
