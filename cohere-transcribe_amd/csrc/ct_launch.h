@@ -209,6 +209,16 @@ void ctk_sub_dwconv(float *out, const float *in, int H, int Wd,
                     const uint16_t *w, const uint16_t *b, hipStream_t s);
 /* [T][16][256] -> [T][256*16] (channel-major flatten per frame). */
 void ctk_sub_flatten(float *out, const float *in, int T, hipStream_t s);
+/* The subsampling convolutions over n requests packed along time: request r
+ * owns rows off[r] .. off[r + 1] (off: n + 1 ascending device ints from 0) of
+ * each stage; rows1 / rows_out = off[n] of the output stage.  conv0 reads
+ * request r's mel (N_MELS x tmel[r], row stride tmel[r]) at mel + moff[r]. */
+void ctk_sub_conv0_packed(float *out, const float *mel, const int *o1, const int *tmel,
+                          const int *moff, int n, int rows1, const uint16_t *w,
+                          const uint16_t *b, hipStream_t s);
+void ctk_sub_dwconv_packed(float *out, const float *in, const int *oin, const int *oout, int n,
+                           int rows_out, int Wd, const uint16_t *w, const uint16_t *b,
+                           hipStream_t s);
 /* The same, written as hi/lo bf16 planes (row stride 4096). */
 void ctk_sub_flatten_split(uint16_t *hi, uint16_t *lo, const float *in, int T, hipStream_t s);
 

@@ -60,6 +60,7 @@ struct HipbEngine {
     /* encoder workspace (lazy) */
     int enc_cap;               /* frames */
     int sub_cap;               /* subsampling scratch floats */
+    int *e_subtab;             /* packed subsampling group tables */
     float *ex, *eln, *emid, *eq, *ek, *ev, *eo, *eg, *edw, *epe, *ep, *eh, *esub, *emel;
     uint16_t *eln_h, *eln_l, *emid_h, *emid_l, *eo_h, *eo_l, *edw_h, *edw_l;  /* pre-split GEMM inputs */
     size_t emel_cap;
@@ -313,7 +314,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
                     e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
-                    e->eh, e->esub, e->emel, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
+                    e->eh, e->esub, e->emel, e->e_subtab, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
                     e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
                     e->d_fb_lo, e->d_fb_hi, e->epcm, e->e_clips, e->e_frame_clip,
                     e->eln_h, e->eln_l, e->emid_h, e->emid_l, e->eo_h, e->eo_l, e->edw_h, e->edw_l};
@@ -444,9 +445,16 @@ int hipb_req_frames(HipbEngine *e, int req) {
     return (req >= 0 && req < e->n_req) ? e->req[req].T_enc : 0;
 }
 
+/* Subsampling scratch (floats) at least this large: 80 Mi floats (320 MB)
+ * hold the stage buffers of about 5 minutes of audio, packed. */
+#define CT_SUB_PACK_FLOATS (80 << 20)
+
 static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     const int T1 = (max_tmel + 1) / 2, T2 = (T1 + 1) / 2;
-    const int sub = SUB_CH * (T1 * 64 + T2 * 32);
+    /* one request's stage buffers, and at least CT_SUB_PACK_FLOATS so that
+     * several requests' subsampling runs packed */
+    int sub = SUB_CH * (T1 * 64 + T2 * 32);
+    if (sub < CT_SUB_PACK_FLOATS) sub = CT_SUB_PACK_FLOATS;
     if (frames <= e->enc_cap && sub <= e->sub_cap) return;
     ECHK(hipStreamSynchronize(e->s));
     float **bufs[] = {&e->ex, &e->eln, &e->emid, &e->eq, &e->ek, &e->ev, &e->eo, &e->eg, &e->edw, &e->eh};
@@ -459,6 +467,7 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     for (size_t i = 0; i < sizeof ib / sizeof ib[0]; i++)
         if (*ib[i]) { ECHK(hipFree(*ib[i])); *ib[i] = NULL; }
     if (e->e_rowoff) ECHK(hipFree(e->e_rowoff));
+    if (e->e_subtab) ECHK(hipFree(e->e_subtab));
     if (e->esub) ECHK(hipFree(e->esub));
     if (!e->epe) {
         e->epe = dmalloc((size_t)(2 * e->d.tmax - 1) * ENC_D * 4);
@@ -492,6 +501,8 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     e->e_seq_T = dmalloc(rows * sizeof(int));
     e->e_blk_seq = dmalloc(rows * sizeof(int));
     e->e_blk_q0 = dmalloc(rows * sizeof(int));
+    /* subsampling group tables: 5 (n + 1) ints per group, at most n groups */
+    e->e_subtab = dmalloc((size_t)10 * (rows + 1) * sizeof(int));
     const int sc = sub > e->sub_cap ? sub : e->sub_cap;
     e->esub = dmalloc((size_t)sc * 4);
     e->enc_cap = M;
@@ -599,24 +610,58 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     }
     size_t moff = 0;
     const Weights *W = &e->W;
+    int *mel_off = malloc(n * sizeof(int));
     for (int i = 0; i < n; i++) {
         HostReq *q = &e->req[r0 + i];
-        float *mel = e->emel + moff;
-        moff += (size_t)N_MELS * q->T_mel;
+        mel_off[i] = (int)moff;
         if (q->mel)
-            ECHK(hipMemcpyAsync(mel, q->mel, (size_t)N_MELS * q->T_mel * 4, hipMemcpyHostToDevice, s));
-        const int T1 = (q->T_mel + 1) / 2, T2 = (T1 + 1) / 2;
-        float *ra = e->esub, *rb = e->esub + (size_t)SUB_CH * T1 * 64;
-        ctk_sub_conv0(ra, mel, q->T_mel, q->T_mel, DW(W->s0w), DW(W->s0b), s);
-        ctk_sub_dwconv(rb, ra, T1, 64, DW(W->s2w), DW(W->s2b), s);
-        gemm(e, rb, T2 * 32, SUB_CH, W->s3w, W->s3b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
-        ctk_sub_dwconv(rb, ra, T2, 32, DW(W->s5w), DW(W->s5b), s);
-        gemm(e, rb, q->T_enc * 16, SUB_CH, W->s6w, W->s6b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
-        /* flattened frames of every request go pre-split into packed rows
-         * (the FFN planes are free until layer 0) for one projection GEMM */
-        ctk_sub_flatten_split(e->emid_h + (size_t)seq_off[i] * SUB_CH * 16,
-                              e->emid_l + (size_t)seq_off[i] * SUB_CH * 16, ra, q->T_enc, s);
+            ECHK(hipMemcpyAsync(e->emel + moff, q->mel, (size_t)N_MELS * q->T_mel * 4, hipMemcpyHostToDevice, s));
+        moff += (size_t)N_MELS * q->T_mel;
     }
+    /* subsampling over groups of requests packed along time, each group as
+     * large as the scratch allows: conv0 -> ra, depthwise -> rb, pointwise ->
+     * ra, depthwise -> rb, pointwise -> ra, then the flattened frames go
+     * pre-split into the packed rows (the FFN planes are free until layer 0)
+     * for one projection GEMM.  The group tables (row offsets of the three
+     * stages, mel lengths and offsets) are staged in distinct parts of the
+     * pinned buffer, so no group overwrites one still to be copied. */
+    int *tab_h = e->h_tmp, *tab_d = e->e_subtab;
+    for (int g0 = 0; g0 < n;) {
+        long s1 = 0, s2 = 0;
+        int g1 = g0;
+        while (g1 < n) {
+            const int tm = e->req[r0 + g1].T_mel, T1 = (tm + 1) / 2, T2 = (T1 + 1) / 2;
+            const long a = (long)T1 * 64 * SUB_CH, b = (long)T2 * 32 * SUB_CH;
+            if (g1 > g0 && s1 + a + s2 + b > e->sub_cap) break;
+            s1 += a; s2 += b; g1++;
+        }
+        const int ng = g1 - g0, L = ng + 1;
+        int *o1 = tab_h, *o2 = o1 + L, *o3 = o2 + L, *tm = o3 + L, *mo = tm + L;
+        o1[0] = o2[0] = o3[0] = 0;
+        for (int j = 0; j < ng; j++) {
+            const HostReq *q = &e->req[r0 + g0 + j];
+            const int T1 = (q->T_mel + 1) / 2, T2 = (T1 + 1) / 2;
+            o1[j + 1] = o1[j] + T1;
+            o2[j + 1] = o2[j] + T2;
+            o3[j + 1] = o3[j] + q->T_enc;
+            tm[j] = q->T_mel;
+            mo[j] = mel_off[g0 + j];
+        }
+        ECHK(hipMemcpyAsync(tab_d, tab_h, (size_t)5 * L * sizeof(int), hipMemcpyHostToDevice, s));
+        const int *d1 = tab_d, *d2 = d1 + L, *d3 = d2 + L, *dtm = d3 + L, *dmo = dtm + L;
+        float *ra = e->esub, *rb = e->esub + s1;
+        ctk_sub_conv0_packed(ra, e->emel, d1, dtm, dmo, ng, o1[ng], DW(W->s0w), DW(W->s0b), s);
+        ctk_sub_dwconv_packed(rb, ra, d1, d2, ng, o2[ng], 64, DW(W->s2w), DW(W->s2b), s);
+        gemm(e, rb, o2[ng] * 32, SUB_CH, W->s3w, W->s3b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
+        ctk_sub_dwconv_packed(rb, ra, d2, d3, ng, o3[ng], 32, DW(W->s5w), DW(W->s5b), s);
+        gemm(e, rb, o3[ng] * 16, SUB_CH, W->s6w, W->s6b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
+        ctk_sub_flatten_split(e->emid_h + (size_t)seq_off[g0] * SUB_CH * 16,
+                              e->emid_l + (size_t)seq_off[g0] * SUB_CH * 16, ra, o3[ng], s);
+        tab_h += 5 * L;
+        tab_d += 5 * L;
+        g0 = g1;
+    }
+    free(mel_off);
     gemm_sp(e, e->emid_h, e->emid_l, M, SUB_CH * 16, W->sow, W->sob, e->ex, ENC_D, CT_EPI_STORE, 0);
     /* relative positions for T_max; each clip reads its shifted window */
     ctk_rel_pos_emb(e->epe, T_max, ct_inv_freq(), s);

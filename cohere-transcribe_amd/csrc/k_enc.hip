@@ -288,6 +288,76 @@ __global__ void sub_dwconv_kernel(float *out, const float *in, int H, int Wd,
     out[i] = s;
 }
 
+// Request of packed row tau: the r with off[r] <= tau < off[r + 1] (off has
+// n + 1 ascending entries, off[0] = 0).
+__device__ __forceinline__ int packed_owner(const int *off, int n, int tau) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (off[mid] <= tau) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// sub_conv0_kernel over several requests at once: request r's mel
+// (N_MELS x tmel[r], row stride tmel[r]) sits at mel + moff[r], its output
+// rows at o1[r] .. o1[r + 1] of the packed [sum T1][64][256] output.  Same
+// per-element arithmetic as the one-request kernel.
+__global__ void sub_conv0_packed_kernel(float *out, const float *mel, const int *o1, const int *tmel,
+                                        const int *moff, int n, const uint16_t *w, const uint16_t *b) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)o1[n] * 64 * SUB_CH) return;
+    const int oc = (int)(i % SUB_CH);
+    const int ow = (int)((i / SUB_CH) % 64);
+    const int tau = (int)(i / (SUB_CH * 64));
+    const int r = packed_owner(o1, n, tau);
+    const int oh = tau - o1[r], T_mel = tmel[r];
+    const float *m = mel + moff[r];
+    float s = bf2f(b[oc]);
+#pragma unroll
+    for (int kh = 0; kh < 3; kh++) {
+        const int ih = oh * 2 - 1 + kh;
+        if (ih < 0 || ih >= T_mel) continue;
+#pragma unroll
+        for (int kw = 0; kw < 3; kw++) {
+            const int iw = ow * 2 - 1 + kw;
+            if (iw < 0 || iw >= N_MELS) continue;
+            s += m[(long)iw * T_mel + ih] * bf2f(w[oc * 9 + kh * 3 + kw]);
+        }
+    }
+    out[i] = s > 0.0f ? s : 0.0f;
+}
+
+// sub_dwconv_kernel over several requests: request r's input rows
+// oin[r] .. oin[r + 1] of [sum H][Wd][256], output rows oout[r] .. oout[r+1]
+// of [sum (H+1)/2][(Wd+1)/2][256].
+__global__ void sub_dwconv_packed_kernel(float *out, const float *in, const int *oin, const int *oout,
+                                         int n, int Wd, const uint16_t *w, const uint16_t *b) {
+    const int Wo = (Wd + 1) / 2;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)oout[n] * Wo * SUB_CH) return;
+    const int c = (int)(i % SUB_CH);
+    const int ow = (int)((i / SUB_CH) % Wo);
+    const int tau = (int)(i / ((long)SUB_CH * Wo));
+    const int r = packed_owner(oout, n, tau);
+    const int oh = tau - oout[r], H = oin[r + 1] - oin[r];
+    const float *x = in + (long)oin[r] * Wd * SUB_CH;
+    float s = bf2f(b[c]);
+#pragma unroll
+    for (int kh = 0; kh < 3; kh++) {
+        const int ih = oh * 2 - 1 + kh;
+        if (ih < 0 || ih >= H) continue;
+#pragma unroll
+        for (int kw = 0; kw < 3; kw++) {
+            const int iw = ow * 2 - 1 + kw;
+            if (iw < 0 || iw >= Wd) continue;
+            s += x[((long)ih * Wd + iw) * SUB_CH + c] * bf2f(w[c * 9 + kh * 3 + kw]);
+        }
+    }
+    out[i] = s;
+}
+
 // [T][16][256] -> [T][ch*16 + f] (backends/cpu/backend.c:222-226).
 __global__ void sub_flatten_kernel(float *out, const float *in, int T) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -437,6 +507,22 @@ extern "C" void ctk_sub_dwconv(float *out, const float *in, int H, int Wd,
     const long n = (long)((H + 1) / 2) * ((Wd + 1) / 2) * SUB_CH;
     if (n <= 0) return;
     hipLaunchKernelGGL(sub_dwconv_kernel, dim3(nblk(n)), dim3(256), 0, s, out, in, H, Wd, w, b);
+}
+
+extern "C" void ctk_sub_conv0_packed(float *out, const float *mel, const int *o1, const int *tmel,
+                                     const int *moff, int n, int rows1, const uint16_t *w,
+                                     const uint16_t *b, hipStream_t s) {
+    const long cnt = (long)rows1 * 64 * SUB_CH;
+    if (cnt <= 0 || n <= 0) return;
+    hipLaunchKernelGGL(sub_conv0_packed_kernel, dim3(nblk(cnt)), dim3(256), 0, s, out, mel, o1, tmel, moff, n, w, b);
+}
+
+extern "C" void ctk_sub_dwconv_packed(float *out, const float *in, const int *oin, const int *oout, int n,
+                                      int rows_out, int Wd, const uint16_t *w, const uint16_t *b,
+                                      hipStream_t s) {
+    const long cnt = (long)rows_out * ((Wd + 1) / 2) * SUB_CH;
+    if (cnt <= 0 || n <= 0) return;
+    hipLaunchKernelGGL(sub_dwconv_packed_kernel, dim3(nblk(cnt)), dim3(256), 0, s, out, in, oin, oout, n, Wd, w, b);
 }
 
 extern "C" void ctk_sub_flatten_split(uint16_t *hi, uint16_t *lo, const float *in, int T, hipStream_t s) {
