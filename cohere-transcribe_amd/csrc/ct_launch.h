@@ -183,12 +183,14 @@ void ctk_relpos_attn(float *O, const float *Q, const float *K, const float *V,
 /* Packed clips: sequence i has T = seq_T[i] rows starting at row seq_off[i]
  * of Q/K/V/O; its P rows are the window of a table built for T_max, shifted
  * by T_max - T (model.h:586-592).  Work items (clip, 16-query block) are
- * listed in blk_seq/blk_q0 (n_blk entries, built by ctk_relpos_plan). */
+ * listed in blk_seq/blk_q0 (n_blk entries, built by ctk_relpos_plan).  The
+ * output goes to O (fp32) or, with O NULL, split hi/lo into the planes Oh, Ol. */
 int  ctk_relpos_plan(int *blk_seq, int *blk_q0, const int *seq_T, int n_seq);
-void ctk_relpos_attn_packed(float *O, const float *Q, const float *K, const float *V,
-                            const float *P, int T_max, const uint16_t *pbu, const uint16_t *pbv,
-                            const int *seq_off, const int *seq_T, const int *blk_seq,
-                            const int *blk_q0, int n_blk, int max_T, hipStream_t s);
+void ctk_relpos_attn_packed(float *O, uint16_t *Oh, uint16_t *Ol, const float *Q,
+                            const float *K, const float *V, const float *P, int T_max,
+                            const uint16_t *pbu, const uint16_t *pbv, const int *seq_off,
+                            const int *seq_T, const int *blk_seq, const int *blk_q0, int n_blk,
+                            int max_T, hipStream_t s);
 /* Depthwise conv k=9 (zero pad 4 inside the sequence) + BN + SiLU.  With
  * row_start/row_len (per row: first row and length of its sequence) the rows
  * are packed sequences; otherwise one sequence of T rows. */

@@ -677,9 +677,9 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_kw, L->sa_kb, e->ek, ENC_D, CT_EPI_STORE, 0);
         gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_vw, L->sa_vb, e->ev, ENC_D, CT_EPI_STORE, 0);
         gemm(e, e->epe, 2 * T_max - 1, ENC_D, L->sa_pw, NULL, e->ep, ENC_D, CT_EPI_STORE, 0, NULL);
-        ctk_relpos_attn_packed(e->eo, e->eq, e->ek, e->ev, e->ep, T_max, DW(L->sa_pbu), DW(L->sa_pbv),
-                               e->e_seq_off, e->e_seq_T, e->e_blk_seq, e->e_blk_q0, nblk, T_max, s);
-        ctk_split(e->eo_h, e->eo_l, e->eo, (long)M * ENC_D, s);
+        ctk_relpos_attn_packed(NULL, e->eo_h, e->eo_l, e->eq, e->ek, e->ev, e->ep, T_max, DW(L->sa_pbu),
+                               DW(L->sa_pbv), e->e_seq_off, e->e_seq_T, e->e_blk_seq, e->e_blk_q0, nblk,
+                               T_max, s);
         gemm_sp(e, e->eo_h, e->eo_l, M, ENC_D, L->sa_ow, L->sa_ob, e->ex, ENC_D, CT_EPI_FMADD, 1.0f);
         /* x += Conv(LN x) */
         ctk_layernorm_split(e->eln_h, e->eln_l, e->ex, DW(L->cv_lnw), DW(L->cv_lnb), M, ENC_D, s);

@@ -39,7 +39,8 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
                                                           const uint16_t *pbu, const uint16_t *pbv,
                                                           int T_arg, int T_max, const int *seq_off,
                                                           const int *seq_T, const int *blk_seq,
-                                                          const int *blk_q0, int ldS) {
+                                                          const int *blk_q0, int ldS,
+                                                          uint16_t *Oh, uint16_t *Ol) {
     extern __shared__ float S[];      // [RQ][ldS]
     int T, q0;
     long off = 0;
@@ -53,7 +54,10 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
         T = T_arg;
         q0 = blockIdx.x * RQ;
     }
-    Q += off * ENC_D; K += off * ENC_D; V += off * ENC_D; O += off * ENC_D;
+    Q += off * ENC_D; K += off * ENC_D; V += off * ENC_D;
+    // the output goes to O, or split hi/lo to the planes Oh/Ol
+    if (Oh) { Oh += off * ENC_D; Ol += off * ENC_D; }
+    else O += off * ENC_D;
     const int h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lk = lane >> 4;
     const int nq = min(RQ, T - q0);
@@ -164,7 +168,16 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int qi = 4 * lk + j;
-            if (qi < nq) O[(long)(q0 + qi) * ENC_D + hc + d] = acc[j];
+            if (qi >= nq) continue;
+            const long o = (long)(q0 + qi) * ENC_D + hc + d;
+            if (Oh) {
+                uint16_t hh, ll;
+                split_bf16(acc[j], hh, ll);
+                Oh[o] = hh;
+                Ol[o] = ll;
+            } else {
+                O[o] = acc[j];
+            }
         }
     }
 }
@@ -436,7 +449,8 @@ extern "C" void ctk_relpos_attn(float *O, const float *Q, const float *K, const 
     relpos_allow_lds<false>(lds);
     const dim3 grid((T + RQ - 1) / RQ, ENC_H);
     hipLaunchKernelGGL((relpos_attn_kernel<false>), grid, dim3(256), lds, s,
-                       O, Q, K, V, P, pbu, pbv, T, T, nullptr, nullptr, nullptr, nullptr, ldS);
+                       O, Q, K, V, P, pbu, pbv, T, T, nullptr, nullptr, nullptr, nullptr, ldS,
+                       nullptr, nullptr);
 }
 
 extern "C" int ctk_relpos_plan(int *blk_seq, int *blk_q0, const int *seq_T, int n_seq) {
@@ -452,11 +466,11 @@ extern "C" int ctk_relpos_plan(int *blk_seq, int *blk_q0, const int *seq_T, int 
     return n;
 }
 
-extern "C" void ctk_relpos_attn_packed(float *O, const float *Q, const float *K, const float *V,
-                                       const float *P, int T_max, const uint16_t *pbu,
-                                       const uint16_t *pbv, const int *seq_off, const int *seq_T,
-                                       const int *blk_seq, const int *blk_q0, int n_blk, int max_T,
-                                       hipStream_t s) {
+extern "C" void ctk_relpos_attn_packed(float *O, uint16_t *Oh, uint16_t *Ol, const float *Q,
+                                       const float *K, const float *V, const float *P, int T_max,
+                                       const uint16_t *pbu, const uint16_t *pbv, const int *seq_off,
+                                       const int *seq_T, const int *blk_seq, const int *blk_q0,
+                                       int n_blk, int max_T, hipStream_t s) {
     if (n_blk <= 0) return;
     if (max_T > 2048) {
         fprintf(stderr, "ctk_relpos_attn_packed: T=%d exceeds the supported 2048 frames\n", max_T);
@@ -466,12 +480,16 @@ extern "C" void ctk_relpos_attn_packed(float *O, const float *Q, const float *K,
         fprintf(stderr, "ctk_relpos_attn: Q, K, V and P must be 16-byte aligned\n");
         exit(1);
     }
+    if (!O == !Oh || !Oh != !Ol) {
+        fprintf(stderr, "ctk_relpos_attn_packed: give either O or both planes Oh, Ol\n");
+        exit(1);
+    }
     size_t lds;
     const int ldS = relpos_lds(max_T, &lds);
     relpos_allow_lds<true>(lds);
     const dim3 grid(n_blk, ENC_H);
     hipLaunchKernelGGL((relpos_attn_kernel<true>), grid, dim3(256), lds, s,
-                       O, Q, K, V, P, pbu, pbv, 0, T_max, seq_off, seq_T, blk_seq, blk_q0, ldS);
+                       O, Q, K, V, P, pbu, pbv, 0, T_max, seq_off, seq_T, blk_seq, blk_q0, ldS, Oh, Ol);
 }
 
 extern "C" void ctk_dwconv_bn_silu(float *out, const float *in, int T, const uint16_t *dww,

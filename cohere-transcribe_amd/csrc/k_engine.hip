@@ -18,13 +18,13 @@
 
 namespace {
 
-// Writes row `row` of the step: token `tok` of slot s's request r at
-// position pos (0-based) of the slot's self cache.
-__device__ __forceinline__ void set_row(const CtEngDev &d, int row, int s, int r, int tok, int pos) {
+// Writes row `row` of the step: token `tok` of slot s's request r (T_enc
+// frames) at position pos (0-based) of the slot's self cache.
+__device__ __forceinline__ void set_row(const CtEngDev &d, int row, int s, int r, int T, int tok, int pos) {
     d.act[row] = 1;
     d.tok[row] = tok;
     d.pos_len[row] = pos + 1;
-    d.cross_len[row] = d.req_T[r];
+    d.cross_len[row] = T;
     d.cross_idx[row] = r;
     d.row_slot[row] = s;
     d.kv_rowoff[row] = ((long)s * DEC_H * d.kv_rows + pos) * DEC_DK;
@@ -47,45 +47,55 @@ __device__ __forceinline__ void clear_row(const CtEngDev &d, int row) {
 // spare rows dealt in slot order; each row is an ordinary decode row at its
 // own position, so a prompt fed k tokens per step gives the same bits as one
 // per step.  q[3] receives the prompt tokens still unfed after this step.
+// Thread s serves slot s (slots <= 256).  Everything a slot that keeps its
+// request needs is loaded in the first phase, beside the slot table and the
+// queue words, so only newly admitted slots wait for a second round.
 __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
-    const int tid = threadIdx.x;
-    // Slot table and released successors read in parallel into LDS; the
-    // admission itself is one sequential pass over slots in slot order.
+    const int tid = threadIdx.x, s = tid;
     __shared__ int s_req[CT_ENG_MAX_SLOTS], s_pend[CT_ENG_MAX_SLOTS], s_new[CT_ENG_MAX_SLOTS];
     __shared__ int s_wsum[4], s_left[4];
-    for (int s = tid; s < d.slots; s += 256) {
-        s_req[s] = d.slot_req[s];
-        s_pend[s] = d.pend[s];
+    int r = -1, S = 0, np = 0, ng = 0, T = 0, pend = -1, q0 = 0, q1 = 0;
+    if (s < d.slots) {
+        r = d.slot_req[s];
+        pend = d.pend[s];
+        S = d.slot_S[s];
+    }
+    if (tid == 0) { q0 = d.q[0]; q1 = d.q[1]; }
+    if (r >= 0) { np = d.req_np[r]; ng = d.req_ngen[r]; T = d.req_T[r]; }
+    if (s < d.slots) {
+        s_req[s] = r;
+        s_pend[s] = pend;
         s_new[s] = 0;
     }
     __syncthreads();
+    // released successors join the ring in slot order, then free slots take
+    // ring entries in slot order
     if (tid == 0) {
-        int nxt = d.q[0], ready = d.q[1];
-        for (int s = 0; s < d.slots; s++)
-            if (s_pend[s] >= 0) d.rq[ready++] = s_pend[s];
-        for (int s = 0; s < d.slots; s++) {
-            if (s_req[s] < 0 && nxt < ready) {
-                s_req[s] = d.rq[nxt++];
-                s_new[s] = 1;
+        int nxt = q0, ready = q1;
+        for (int x = 0; x < d.slots; x++)
+            if (s_pend[x] >= 0) d.rq[ready++] = s_pend[x];
+        for (int x = 0; x < d.slots; x++) {
+            if (s_req[x] < 0 && nxt < ready) {
+                s_req[x] = d.rq[nxt++];
+                s_new[x] = 1;
             }
         }
         d.q[0] = nxt;
         d.q[1] = ready;
     }
     __syncthreads();
-    // slot tid (slots <= 256): spare rows wanted, then their exclusive prefix
-    const int s = tid;
-    int r = -1, S = 0, np = 0, want = 0;
+    int want = 0;
     if (s < d.slots) {
-        if (s_pend[s] >= 0) d.pend[s] = -1;
+        if (pend >= 0) d.pend[s] = -1;
         r = s_req[s];
         d.slot_req[s] = r;
-        if (r >= 0) {
-            S = s_new[s] ? 0 : d.slot_S[s];
-            np = d.req_np[r];
-            if (S < np) want = min(np - S, 1 + extra) - 1;
+        if (s_new[s]) {
+            S = 0;
+            np = d.req_np[r]; ng = d.req_ngen[r]; T = d.req_T[r];
         }
+        if (r >= 0 && S < np) want = min(np - S, 1 + extra) - 1;
     }
+    // exclusive prefix of the spare rows wanted, in slot order
     int x = want;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -99,14 +109,13 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     const int wanted = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
     const int granted = max(0, min(want, extra - base));
     int left = 0;
-    if (r >= 0) {
+    if (s < d.slots && r >= 0) {
         const int k = 1 + granted;
         for (int j = 0; j < granted; j++)
-            set_row(d, d.slots + base + j, s, r, d.req_prompt[r * CT_PROMPT_MAX + S + j], S + j);
+            set_row(d, d.slots + base + j, s, r, T, d.req_prompt[r * CT_PROMPT_MAX + S + j], S + j);
         const int p = S + k - 1;
-        const int t = p < np ? d.req_prompt[r * CT_PROMPT_MAX + p]
-                             : d.req_out[(long)r * d.smax + d.req_ngen[r] - 1];
-        set_row(d, s, s, r, t, p);
+        const int t = p < np ? d.req_prompt[r * CT_PROMPT_MAX + p] : d.req_out[(long)r * d.smax + ng - 1];
+        set_row(d, s, s, r, T, t, p);
         d.slot_S[s] = S + k;
         left = max(0, np - (S + k));
     } else if (s < d.slots) {
