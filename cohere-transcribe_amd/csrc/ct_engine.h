@@ -49,12 +49,19 @@ typedef struct {
     /* chained chunks of one long recording: the request admitted after
      * this one finishes (its prompt then gets the carried tokens), or -1 */
     int  *req_next;
-    /* ready ring: request ids in admission order; rq[q[0]..q[1]) wait for a
-     * slot.  pend[slot] is a chained successor that eng_end released in that
-     * slot this step (-1 if none); eng_begin appends them in slot order. */
+    /* successor ring: chained chunks released by their predecessors;
+     * rq[q[0]..q[1]) wait for a slot.  pend[slot] is a successor that eng_end
+     * released in that slot this step (-1 if none); eng_begin appends them in
+     * slot order.  Only the step kernels write rq and pend. */
     int  *rq, *pend;
-    /* q[0] next ring entry to admit, q[1] ring entries written, q[2]
-     * requests finished, q[3] prompt tokens not yet fed after the last step */
+    /* fresh queue: requests that wait for no predecessor, in submission
+     * order, published by the host once encoded (the ids, then the count
+     * q[5]); fq[q[4]..q[5]) wait for a slot.  Read with device-coherent
+     * loads: the host may publish while steps run on another stream. */
+    int  *fq;
+    /* q[0] next successor to admit, q[1] successors written, q[2] requests
+     * finished, q[3] prompt tokens not yet fed after the last step, q[4] next
+     * fresh request to admit, q[5] fresh requests published */
     int  *q;
 } CtEngDev;
 

@@ -18,9 +18,12 @@
 #include "ct_launch.h"
 
 #include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 typedef struct {
     float *mel;          /* host copy until encoded (mel requests) ...        */
@@ -54,6 +57,14 @@ struct HipbEngine {
      * GEMMs' inputs in frag layout; parts K-slice partial sums */
     float *h, *q, *parts, *logits;
     int M;                     /* rows of the step being launched */
+    /* encoder side: its stream (the engine stream, or a second stream while
+     * hipb_process overlaps encoding with decoding), pinned staging of its
+     * own, and the host count of requests published to the fresh queue */
+    hipStream_t s2, enc_s;
+    int *h_enc;
+    int fq_count;
+    int proc_batch;            /* encoder batch frames of hipb_process */
+    atomic_int enc_done;       /* the encoder thread has published every batch */
     long stepped;              /* steps launched since creation or reset */
     int prefill_min;           /* unfed prompt tokens that select the wide step */
     uint16_t *lnf, *attf, *midf;
@@ -105,7 +116,7 @@ static void gemm(HipbEngine *e, const float *A, int M, int K, const uint16_t *Wh
     g.A = A; g.lda = K; g.W = DW(Wh); g.bias = DW(bh);
     g.Y = Y; g.ldy = N; g.M = M; g.N = N; g.K = K; g.epi = epi; g.scale = scale;
     g.row_mask = row_mask;
-    ctk_gemm(&g, e->s);
+    ctk_gemm(&g, e->enc_s);
 }
 
 /* Slaney mel scale and the librosa-style filterbank the reference builds in
@@ -168,7 +179,7 @@ static void gemm_sp(HipbEngine *e, const uint16_t *Ah, const uint16_t *Al, int M
     memset(&g, 0, sizeof g);
     g.Ahi = Ah; g.Alo = Al; g.lda = K; g.W = DW(Wh); g.bias = DW(bh);
     g.Y = Y; g.ldy = N; g.M = M; g.N = N; g.K = K; g.epi = epi; g.scale = scale;
-    ctk_gemm(&g, e->s);
+    ctk_gemm(&g, e->enc_s);
 }
 
 /* FFN up projection with SiLU, written pre-split for the down projection. */
@@ -180,7 +191,7 @@ static void gemm_sp_silu_split(HipbEngine *e, const uint16_t *Ah, const uint16_t
     g.M = M; g.N = ENC_FF; g.K = ENC_D; g.epi = CT_EPI_SILU;
     g.nseg = 1; g.seg_w = ENC_FF;
     g.seg[0].mode = CT_OUT_SPLIT; g.seg[0].base = Oh; g.seg[0].base_lo = Ol; g.seg[0].ld = ENC_FF;
-    ctk_gemm(&g, e->s);
+    ctk_gemm(&g, e->enc_s);
 }
 
 HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
@@ -194,6 +205,8 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->cfg = *cfg;
     e->W = *W;
     e->s = ct_t.stream;
+    ECHK(hipStreamCreate(&e->s2));   /* the encoder's stream in hipb_process */
+    e->enc_s = e->s;
     e->dev = ct_t.dev;
     e->esz = cfg->kv_bf16 ? 2 : 4;
     const int S = cfg->slots, R = cfg->max_requests;
@@ -221,14 +234,15 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     d->req_ngen = dmalloc(R * sizeof(int));
     d->req_prompt = dmalloc((size_t)R * CT_PROMPT_MAX * sizeof(int));
     d->req_out = dmalloc((size_t)R * d->smax * sizeof(int));
-    d->q = dmalloc(4 * sizeof(int));
+    d->q = dmalloc(8 * sizeof(int));
+    d->fq = dmalloc(R * sizeof(int));
     d->req_next = dmalloc(R * sizeof(int));
     d->rq = dmalloc(R * sizeof(int));
     d->pend = dmalloc(S * sizeof(int));
     ECHK(hipMemsetAsync(d->slot_req, 0xff, S * sizeof(int), e->s));   /* -1: free */
     ECHK(hipMemsetAsync(d->slot_S, 0, S * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->req_ngen, 0, R * sizeof(int), e->s));
-    ECHK(hipMemsetAsync(d->q, 0, 4 * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->q, 0, 8 * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->req_next, 0xff, R * sizeof(int), e->s));   /* -1: no successor */
     ECHK(hipMemsetAsync(d->pend, 0xff, S * sizeof(int), e->s));
 
@@ -297,6 +311,8 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     if (e->prefill_min < 1) e->prefill_min = 1;
     mel_tables_init(e);
     ECHK(hipHostMalloc((void **)&e->h_tmp, (size_t)(R + 8) * (MAX_SEQ + 8) * sizeof(int), 0));
+    /* subsampling group tables (<= 10 (R + 1) ints per batch) + published ids */
+    ECHK(hipHostMalloc((void **)&e->h_enc, (size_t)(11 * R + 64) * sizeof(int), 0));
     ECHK(hipStreamSynchronize(e->s));
     return e;
 }
@@ -310,7 +326,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->d.row_slot,
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
-                    e->d.req_next, e->d.rq, e->d.pend,
+                    e->d.req_next, e->d.rq, e->d.pend, e->d.fq,
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
                     e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
@@ -323,6 +339,8 @@ void hipb_destroy(HipbEngine *e) {
     for (int r = 0; r < e->n_req; r++) { free(e->req[r].mel); free(e->req[r].pcm); }
     free(e->req);
     ECHK(hipHostFree(e->h_tmp));
+    ECHK(hipHostFree(e->h_enc));
+    ECHK(hipStreamDestroy(e->s2));
     free(e);
 }
 
@@ -335,12 +353,13 @@ void hipb_reset(HipbEngine *e) {
         memset(&e->req[r], 0, sizeof e->req[r]);
     }
     e->n_req = e->n_enc = 0;
+    e->fq_count = 0;
     e->bench_mode = 0;
     e->stepped = 0;
     ECHK(hipMemsetAsync(e->d.slot_req, 0xff, e->d.slots * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.slot_S, 0, e->d.slots * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.req_ngen, 0, e->d.max_req * sizeof(int), e->s));
-    ECHK(hipMemsetAsync(e->d.q, 0, 4 * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(e->d.q, 0, 8 * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.req_next, 0xff, e->d.max_req * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.pend, 0xff, e->d.slots * sizeof(int), e->s));
     ECHK(hipStreamSynchronize(e->s));
@@ -456,7 +475,7 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     int sub = SUB_CH * (T1 * 64 + T2 * 32);
     if (sub < CT_SUB_PACK_FLOATS) sub = CT_SUB_PACK_FLOATS;
     if (frames <= e->enc_cap && sub <= e->sub_cap) return;
-    ECHK(hipStreamSynchronize(e->s));
+    ECHK(hipStreamSynchronize(e->enc_s));
     float **bufs[] = {&e->ex, &e->eln, &e->emid, &e->eq, &e->ek, &e->ev, &e->eo, &e->eg, &e->edw, &e->eh};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
         if (*bufs[i]) { ECHK(hipFree(*bufs[i])); *bufs[i] = NULL; }
@@ -510,6 +529,40 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
 }
 
 /* Encodes requests [r0, r1) as one packed batch. */
+/* Grows the mel, PCM and clip-table buffers for the batch [r0, r1). */
+static void batch_buffers(HipbEngine *e, int r0, int r1) {
+    size_t mel_need = 0, pcm_need = 0;
+    int nclip = 0, nfr = 0;
+    for (int r = r0; r < r1; r++) {
+        mel_need += (size_t)N_MELS * e->req[r].T_mel;
+        if (e->req[r].pcm || e->req[r].dpcm) {
+            if (e->req[r].pcm) pcm_need += e->req[r].n;
+            nclip++;
+            nfr += e->req[r].T_mel;
+        }
+    }
+    if (mel_need > e->emel_cap) {
+        if (e->emel) ECHK(hipFree(e->emel));
+        e->emel = dmalloc(mel_need * 4);
+        e->emel_cap = mel_need;
+    }
+    if (pcm_need > e->epcm_cap) {
+        if (e->epcm) ECHK(hipFree(e->epcm));
+        e->epcm = dmalloc(pcm_need * 4);
+        e->epcm_cap = pcm_need;
+    }
+    if (nclip > e->clips_cap) {
+        if (e->e_clips) ECHK(hipFree(e->e_clips));
+        e->e_clips = dmalloc((size_t)nclip * sizeof(CtMelClip));
+        e->clips_cap = nclip;
+    }
+    if (nfr > e->frames_cap) {
+        if (e->e_frame_clip) ECHK(hipFree(e->e_frame_clip));
+        e->e_frame_clip = dmalloc((size_t)nfr * sizeof(int));
+        e->frames_cap = nfr;
+    }
+}
+
 static void encode_batch(HipbEngine *e, int r0, int r1) {
     const int n = r1 - r0;
     int M = 0, tmel_max = 0, T_max = 0;
@@ -519,7 +572,7 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         if (e->req[r].T_enc > T_max) T_max = e->req[r].T_enc;
     }
     enc_reserve(e, M, tmel_max);
-    hipStream_t s = e->s;
+    hipStream_t s = e->enc_s;
     /* host-side row tables */
     int *row_start = malloc(M * sizeof(int)), *row_len = malloc(M * sizeof(int));
     long *rowoff = malloc(M * sizeof(long));
@@ -548,40 +601,17 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     ECHK(hipMemcpyAsync(e->e_blk_seq, blk_seq, nblk * sizeof(int), hipMemcpyHostToDevice, s));
     ECHK(hipMemcpyAsync(e->e_blk_q0, blk_q0, nblk * sizeof(int), hipMemcpyHostToDevice, s));
 
-    /* subsampling per request into packed rows (scratch as the ABI path) */
-    size_t mel_need = 0;
-    for (int r = r0; r < r1; r++) mel_need += (size_t)N_MELS * e->req[r].T_mel;
-    if (mel_need > e->emel_cap) {
-        if (e->emel) ECHK(hipFree(e->emel));
-        e->emel = dmalloc(mel_need * 4);
-        e->emel_cap = mel_need;
-    }
+    /* mel for every request of the batch, then the subsampling */
+    batch_buffers(e, r0, r1);
     /* log-mel on the GPU for PCM requests, uploaded mel otherwise */
     {
-        size_t pcm_need = 0;
         int nclip = 0, nfr = 0;
         for (int r = r0; r < r1; r++)
             if (e->req[r].pcm || e->req[r].dpcm) {
-                if (e->req[r].pcm) pcm_need += e->req[r].n;
                 nclip++;
                 nfr += e->req[r].T_mel;
             }
         if (nclip) {
-            if (pcm_need > e->epcm_cap) {
-                if (e->epcm) ECHK(hipFree(e->epcm));
-                e->epcm = dmalloc(pcm_need * 4);
-                e->epcm_cap = pcm_need;
-            }
-            if (nclip > e->clips_cap) {
-                if (e->e_clips) ECHK(hipFree(e->e_clips));
-                e->e_clips = dmalloc((size_t)nclip * sizeof(CtMelClip));
-                e->clips_cap = nclip;
-            }
-            if (nfr > e->frames_cap) {
-                if (e->e_frame_clip) ECHK(hipFree(e->e_frame_clip));
-                e->e_frame_clip = dmalloc((size_t)nfr * sizeof(int));
-                e->frames_cap = nfr;
-            }
             CtMelClip *cl = malloc(nclip * sizeof *cl);
             int *fc = malloc(nfr * sizeof(int));
             size_t po = 0, mo = 0;
@@ -625,7 +655,7 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
      * for one projection GEMM.  The group tables (row offsets of the three
      * stages, mel lengths and offsets) are staged in distinct parts of the
      * pinned buffer, so no group overwrites one still to be copied. */
-    int *tab_h = e->h_tmp, *tab_d = e->e_subtab;
+    int *tab_h = e->h_enc, *tab_d = e->e_subtab;
     for (int g0 = 0; g0 < n;) {
         long s1 = 0, s2 = 0;
         int g1 = g0;
@@ -727,37 +757,53 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     free(row_start); free(row_len); free(rowoff); free(seq_off); free(seq_T); free(blk_seq); free(blk_q0);
 }
 
+/* Appends the requests of [r0, r1) that wait for no predecessor to the fresh
+ * queue, in submission order: the ids first, then the new count, both copied
+ * on the encoder stream, which is then drained (the step kernel reads them
+ * with device-coherent loads, possibly while running on the other stream). */
+static void publish(HipbEngine *e, int r0, int r1) {
+    int *ids = e->h_enc + 10 * e->d.max_req + 16, k = 0;
+    for (int i = r0; i < r1; i++)
+        if (!e->req[i].chained) ids[k++] = i;
+    if (!k) return;
+    ECHK(hipMemcpyAsync(e->d.fq + e->fq_count, ids, (size_t)k * sizeof(int), hipMemcpyHostToDevice, e->enc_s));
+    e->fq_count += k;
+    int *cnt = e->h_enc + 10 * e->d.max_req + 8;
+    *cnt = e->fq_count;
+    ECHK(hipMemcpyAsync(e->d.q + 5, cnt, sizeof(int), hipMemcpyHostToDevice, e->enc_s));
+    ECHK(hipStreamSynchronize(e->enc_s));
+}
+
+static void release_inputs(HipbEngine *e, int r0, int r1) {
+    for (int i = r0; i < r1; i++) {
+        free(e->req[i].mel); e->req[i].mel = NULL;
+        free(e->req[i].pcm); e->req[i].pcm = NULL;
+    }
+}
+
+/* The next batch of not yet encoded requests: [r, *r1) with at most
+ * max_batch_frames encoder frames (at least one request). */
+static int next_batch(const HipbEngine *e, int r, int max_batch_frames) {
+    int frames = 0, r1 = r;
+    while (r1 < e->n_req && (r1 == r || frames + e->req[r1].T_enc <= max_batch_frames)) {
+        frames += e->req[r1].T_enc;
+        r1++;
+    }
+    return r1;
+}
+
 void hipb_encode(HipbEngine *e, int max_batch_frames) {
     if (max_batch_frames < e->d.tmax) max_batch_frames = e->d.tmax;
     int r = e->n_enc;
     while (r < e->n_req) {
-        int frames = 0, r1 = r;
-        while (r1 < e->n_req && (r1 == r || frames + e->req[r1].T_enc <= max_batch_frames)) {
-            frames += e->req[r1].T_enc;
-            r1++;
-        }
+        const int r1 = next_batch(e, r, max_batch_frames);
         encode_batch(e, r, r1);
-        for (int i = r; i < r1; i++) {
-            free(e->req[i].mel); e->req[i].mel = NULL;
-            free(e->req[i].pcm); e->req[i].pcm = NULL;
-        }
+        release_inputs(e, r, r1);
         r = r1;
     }
-    /* publish: append the newly encoded requests that wait for no
-     * predecessor to the ready ring, in submission order, after whatever the
-     * device appended itself (chained successors) */
     const int r0 = e->n_enc;
     e->n_enc = r;
-    int q1 = 0, k = 0;
-    ECHK(hipMemcpy(&q1, e->d.q + 1, sizeof(int), hipMemcpyDeviceToHost));
-    int *ids = e->h_tmp;
-    for (int i = r0; i < r; i++)
-        if (!e->req[i].chained) ids[k++] = i;
-    if (k) {
-        ECHK(hipMemcpy(e->d.rq + q1, ids, (size_t)k * sizeof(int), hipMemcpyHostToDevice));
-        q1 += k;
-        ECHK(hipMemcpy(e->d.q + 1, &q1, sizeof(int), hipMemcpyHostToDevice));
-    }
+    publish(e, r0, r);
 }
 
 /* ------------------------------------------------------------------ */
@@ -889,13 +935,14 @@ static void step_launch(HipbEngine *e, int wide) { step_kernels(e, 1, wide); }
 /* The wide step while prompt tokens wait to be fed, or before the first
  * step while requests wait for admission. */
 static int want_wide(const HipbEngine *e, const int *q) {
-    return e->d.rows > e->d.slots && (q[3] >= e->prefill_min || (e->stepped == 0 && q[1] > q[0]));
+    return e->d.rows > e->d.slots &&
+           (q[3] >= e->prefill_min || (e->stepped == 0 && (q[1] > q[0] || q[5] > q[4])));
 }
 
 static void read_queue(HipbEngine *e, int *q);
 
 void hipb_step(HipbEngine *e) {
-    int q[4];
+    int q[8];
     read_queue(e, q);
     step_launch(e, want_wide(e, q));
     e->stepped++;
@@ -910,13 +957,13 @@ void hipb_attention_only(HipbEngine *e) {
 
 /* Reads the queue words (synchronises): q[0..3]. */
 static void read_queue(HipbEngine *e, int *q) {
-    ECHK(hipMemcpyAsync(e->h_tmp, e->d.q, 4 * sizeof(int), hipMemcpyDeviceToHost, e->s));
+    ECHK(hipMemcpyAsync(e->h_tmp, e->d.q, 8 * sizeof(int), hipMemcpyDeviceToHost, e->s));
     ECHK(hipStreamSynchronize(e->s));
-    memcpy(q, e->h_tmp, 4 * sizeof(int));
+    memcpy(q, e->h_tmp, 8 * sizeof(int));
 }
 
 int hipb_finished(HipbEngine *e) {
-    int q[4];
+    int q[8];
     read_queue(e, q);
     return q[2];
 }
@@ -951,7 +998,7 @@ long hipb_run(HipbEngine *e, int chunk) {
      * a slot frees up */
     const long bound = (long)(e->n_enc + 2) * (MAX_SEQ + CT_PROMPT_MAX + 1);
     for (;;) {
-        int q[4];
+        int q[8];
         read_queue(e, q);
         if (q[2] >= e->n_enc) break;
         if (steps > bound) CT_FATAL("hipb_run: requests did not finish within the step bound");
@@ -960,6 +1007,79 @@ long hipb_run(HipbEngine *e, int chunk) {
         steps += chunk;
         e->stepped += chunk;
     }
+    return steps;
+}
+
+/* hipb_process: the encoder runs on a worker thread and the second stream,
+ * publishing each batch to the fresh queue as soon as its cross K/V are
+ * written, while the calling thread keeps launching decode steps. */
+static void *enc_worker(void *arg) {
+    HipbEngine *e = arg;
+    ECHK(hipSetDevice(e->dev));
+    ct_t.dev = e->dev;                 /* weight pointers translate per device */
+    for (int r = e->n_enc; r < e->n_req;) {
+        const int r1 = next_batch(e, r, e->proc_batch);
+        encode_batch(e, r, r1);
+        release_inputs(e, r, r1);
+        publish(e, r, r1);
+        r = r1;
+    }
+    atomic_store(&e->enc_done, 1);
+    return NULL;
+}
+
+long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
+    if (chunk < 1) chunk = 1;
+    if (max_batch_frames < e->d.tmax) max_batch_frames = e->d.tmax;
+    const int spare = e->d.rows - e->d.slots;
+    /* graphs captured and every encoder buffer sized before the worker
+     * starts: no capture, allocation or free runs beside the other stream */
+    ensure_graph(e, 0);
+    if (spare) ensure_graph(e, 1);
+    {
+        int frames_max = 0, tmel_max = 0;
+        for (int r = e->n_enc; r < e->n_req;) {
+            const int r1 = next_batch(e, r, max_batch_frames);
+            int f = 0;
+            for (int i = r; i < r1; i++) {
+                f += e->req[i].T_enc;
+                if (e->req[i].T_mel > tmel_max) tmel_max = e->req[i].T_mel;
+            }
+            if (f > frames_max) frames_max = f;
+            batch_buffers(e, r, r1);
+            r = r1;
+        }
+        if (frames_max) enc_reserve(e, frames_max, tmel_max);
+    }
+    ECHK(hipStreamSynchronize(e->s));
+    e->enc_s = e->s2;
+    e->proc_batch = max_batch_frames;
+    atomic_store(&e->enc_done, 0);
+    pthread_t th;
+    if (pthread_create(&th, NULL, enc_worker, e)) CT_FATAL("hipb_process: cannot start the encoder thread");
+    long steps = 0;
+    const long bound = (long)(e->n_req + 2) * (MAX_SEQ + CT_PROMPT_MAX + 1);
+    for (;;) {
+        int q[8];
+        read_queue(e, q);
+        const int done = atomic_load(&e->enc_done);
+        if (done && q[2] >= e->n_req) break;
+        /* every admitted request finished and none waits: wait for the
+         * encoder instead of stepping empty slots (a released successor
+         * joins at the next step once the encoder has published or ended) */
+        if (!done && q[2] >= q[0] + q[4] && q[0] >= q[1] && q[4] >= q[5]) {
+            usleep(50);
+            continue;
+        }
+        if (steps > bound) CT_FATAL("hipb_process: requests did not finish within the step bound");
+        const int wide = want_wide(e, q);
+        for (int i = 0; i < chunk; i++) launch_step(e, wide);
+        steps += chunk;
+        e->stepped += chunk;
+    }
+    pthread_join(th, NULL);
+    e->enc_s = e->s;
+    e->n_enc = e->n_req;
     return steps;
 }
 
@@ -1025,7 +1145,7 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
     ECHK(hipMemcpy(e->d.req_ngen, buf, B * sizeof(int), hipMemcpyHostToDevice));
     for (int s = 0; s < B; s++)
         ECHK(hipMemcpy(e->d.req_out + (size_t)s * e->d.smax, &(int){100 + s}, sizeof(int), hipMemcpyHostToDevice));
-    int q[4] = {B, B, 0, 0};
+    int q[8] = {B, B, 0, 0, 0, 0, 0, 0};
     ECHK(hipMemcpy(e->d.q, q, sizeof q, hipMemcpyHostToDevice));
     const long self_el = (long)DEC_N * B * DEC_H * e->d.kv_rows * DEC_DK;
     const long cross_el = (long)DEC_N * e->d.max_req * DEC_H * e->d.tmax * DEC_DK;

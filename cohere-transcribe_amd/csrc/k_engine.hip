@@ -54,13 +54,16 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     const int tid = threadIdx.x, s = tid;
     __shared__ int s_req[CT_ENG_MAX_SLOTS], s_pend[CT_ENG_MAX_SLOTS], s_new[CT_ENG_MAX_SLOTS];
     __shared__ int s_wsum[4], s_left[4];
-    int r = -1, S = 0, np = 0, ng = 0, T = 0, pend = -1, q0 = 0, q1 = 0;
+    int r = -1, S = 0, np = 0, ng = 0, T = 0, pend = -1, q0 = 0, q1 = 0, f0 = 0, f1 = 0;
     if (s < d.slots) {
         r = d.slot_req[s];
         pend = d.pend[s];
         S = d.slot_S[s];
     }
-    if (tid == 0) { q0 = d.q[0]; q1 = d.q[1]; }
+    if (tid == 0) {
+        q0 = d.q[0]; q1 = d.q[1]; f0 = d.q[4];
+        f1 = __hip_atomic_load(&d.q[5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (r >= 0) { np = d.req_np[r]; ng = d.req_ngen[r]; T = d.req_T[r]; }
     if (s < d.slots) {
         s_req[s] = r;
@@ -69,19 +72,21 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     }
     __syncthreads();
     // released successors join the ring in slot order, then free slots take
-    // ring entries in slot order
+    // waiting successors, then fresh requests, in slot order
     if (tid == 0) {
-        int nxt = q0, ready = q1;
+        int nxt = q0, ready = q1, fn = f0;
         for (int x = 0; x < d.slots; x++)
             if (s_pend[x] >= 0) d.rq[ready++] = s_pend[x];
         for (int x = 0; x < d.slots; x++) {
-            if (s_req[x] < 0 && nxt < ready) {
-                s_req[x] = d.rq[nxt++];
-                s_new[x] = 1;
-            }
+            if (s_req[x] >= 0) continue;
+            if (nxt < ready) s_req[x] = d.rq[nxt++];
+            else if (fn < f1) s_req[x] = __hip_atomic_load(&d.fq[fn++], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else continue;
+            s_new[x] = 1;
         }
         d.q[0] = nxt;
         d.q[1] = ready;
+        d.q[4] = fn;
     }
     __syncthreads();
     int want = 0;

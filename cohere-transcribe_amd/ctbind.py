@@ -226,6 +226,7 @@ _ENGINE_SIGS = {
     "hipb_encode": ([C.c_void_p, C.c_int], None),
     "hipb_step": ([C.c_void_p], None),
     "hipb_run": ([C.c_void_p, C.c_int], C.c_long),
+    "hipb_process": ([C.c_void_p, C.c_int, C.c_int], C.c_long),
     "hipb_finished": ([C.c_void_p], C.c_int),
     "hipb_tokens": ([C.c_void_p, C.c_int, C.c_void_p, C.c_int], C.c_int),
     "hipb_slot_of": ([C.c_void_p, C.c_int], C.c_int),
@@ -279,6 +280,10 @@ class Engine:
 
     def run(self, chunk=8):
         return self.L.hipb_run(self.e, chunk)
+
+    def process(self, max_batch_frames=8192, chunk=8):
+        """Encode and decode overlapped (hipb_process)."""
+        return self.L.hipb_process(self.e, max_batch_frames, chunk)
 
     def finished(self):
         return self.L.hipb_finished(self.e)

@@ -100,6 +100,14 @@ void hipb_step(HipbEngine *e);
  * per host check.
  * Returns the number of steps run. */
 long hipb_run(HipbEngine *e, int chunk);
+/* hipb_encode and hipb_run overlapped: a worker thread encodes the requests
+ * not yet encoded on a second stream, in packed batches of at most
+ * max_batch_frames encoder frames, each published to the slot table as soon
+ * as its cross-attention K/V are written, while the calling thread runs
+ * decode steps (chunk per host check) until every submitted request has
+ * finished.  Same tokens as hipb_encode then hipb_run.  Returns the number
+ * of steps. */
+long hipb_process(HipbEngine *e, int max_batch_frames, int chunk);
 /* Number of requests finished so far (device counter, synchronises). */
 int  hipb_finished(HipbEngine *e);
 

@@ -352,3 +352,27 @@ def test_engine_prefill_rows_continuous_batching(hip, hot, mels, oracle_runs):
         print(f"case: 6 requests, 2 slots, 5 spare rows: {steps} steps", flush=True)
     finally:
         eng.close()
+
+
+def test_engine_process_overlapped(hip, hot, mels, oracle_runs, chunked_oracle):
+    """hipb_process: encoding (several batches, on its own stream and
+    thread) overlapped with decoding; plain and chained requests give the
+    oracle's tokens, and a second round on the same engine too."""
+    eng = cb.Engine(hot, slots=2, max_requests=24, max_frames=64, kv_bf16=True,
+                    max_tokens=len(cb.PROMPT) + 64 + CHUNK_LIMIT, prefill_rows=4)
+    try:
+        for rnd in range(2):
+            eng.reset()
+            order = [0, 1, 2, 2, 0, 1]
+            plain = [eng.submit(mels[i], LIMITS[i], FLAGS) for i in order]
+            chunks = eng.submit_pcm_chunked(long_recording(REC_SEEDS[1]), CHUNK_LIMIT, FLAGS, **SPLIT)
+            steps = eng.process(max_batch_frames=64, chunk=2)
+            print(f"case: process round {rnd}: {len(plain)} + {len(chunks)} requests, {steps} steps",
+                  flush=True)
+            assert eng.finished() == len(plain) + len(chunks)
+            for r, i in zip(plain, order):
+                assert np.array_equal(eng.tokens(r), oracle_runs[(True, i)][0]), (rnd, r, i)
+            for r, (_, _, toks) in zip(chunks, chunked_oracle[REC_SEEDS[1]]):
+                assert np.array_equal(eng.tokens(r), toks), (rnd, r)
+    finally:
+        eng.close()
