@@ -813,13 +813,13 @@ void hipb_encode(HipbEngine *e, int max_batch_frames) {
  * layout) for the out-projection.  The query is q (self) or the Q
  * projection's K-slice partials plus bias (cross). */
 static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, long head_stride,
-                 const int *lens, const int *kv_index, const uint16_t *q_bias) {
+                 int rows, const int *lens, const int *kv_index, const uint16_t *q_bias) {
     CtAttn a;
     memset(&a, 0, sizeof a);
     a.Q = e->q; a.q_sb = DEC_D; a.q_st = DEC_D;
     a.K = K; a.V = V; a.kv_bf16 = e->esz == 2;
     a.kv_sb = item_stride; a.kv_st = DEC_DK; a.kv_sh = head_stride;
-    a.lens = lens; a.lens_step = 1; a.kv_index = kv_index;
+    a.lens = lens; a.lens_step = 1; a.kv_index = kv_index; a.kv_rows = rows;
     a.T_q = 1; a.B = e->M; a.H = DEC_H;
     a.scale = 0.08838834764831845f;   /* 1/sqrt(128) */
     if (q_bias) {
@@ -848,11 +848,13 @@ static void step_attention(HipbEngine *e, int l, int cross) {
     void *k, *v;
     if (!cross) {
         self_kv(e, l, &k, &v);
-        attn(e, k, v, (long)DEC_H * e->d.kv_rows * DEC_DK, (long)e->d.kv_rows * DEC_DK, e->d.pos_len,
-             e->d.row_slot, NULL);
+        /* row s is slot s's own row: only the spare rows of a wide step
+         * need the row -> slot table */
+        attn(e, k, v, (long)DEC_H * e->d.kv_rows * DEC_DK, (long)e->d.kv_rows * DEC_DK, e->d.kv_rows,
+             e->d.pos_len, e->M > e->d.slots ? e->d.row_slot : NULL, NULL);
     } else {
         cross_kv(e, l, &k, &v);
-        attn(e, k, v, (long)DEC_H * e->d.tmax * DEC_DK, (long)e->d.tmax * DEC_DK,
+        attn(e, k, v, (long)DEC_H * e->d.tmax * DEC_DK, (long)e->d.tmax * DEC_DK, e->d.tmax,
              e->d.cross_len, e->d.cross_idx, DW(e->W.dec[l].ca_qb));
     }
 }

@@ -31,6 +31,13 @@ constexpr int CT_ATTN_QPARTS = 4;   // most query partial slices a launch may pa
 #ifndef CT_ATTN_LPK
 #define CT_ATTN_LPK 16
 #endif
+// threads per workgroup (NT / LPK lane groups)
+#ifndef CT_ATTN_NT
+#define CT_ATTN_NT 256
+#endif
+// rows per item (CtAttn.kv_rows) from which the first key trip is issued
+// ahead of the item's length
+constexpr int CT_ATTN_EARLY_ROWS = 32;
 
 template <bool BF16, bool VEC>
 __device__ __forceinline__ void load8(const void *base, long off, float (&v)[8]) {
@@ -81,19 +88,48 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 // LPK lanes per key: lane s of a group owns head dims [s*DPL, s*DPL + DPL),
-// DPL = 128 / LPK, read as NV 16-byte (bf16) pieces; NG = 256 / LPK groups
+// DPL = 128 / LPK, read as NV 16-byte (bf16) pieces; NG = NT / LPK groups
 // stream keys g, g + NG, ... (KPI of them per trip, loads first).
-template <bool BF16, bool VEC, int LPK, bool MASK>
-__global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
-    constexpr int DPL = DEC_DK / LPK, NV = DPL / 8, NG = 256 / LPK;
+template <bool BF16, bool VEC, int LPK, bool MASK, int NT, bool EARLY>
+__global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
+    constexpr int DPL = DEC_DK / LPK, NV = DPL / 8, NG = NT / LPK;
     const int bq = blockIdx.x, h = blockIdx.y;
     const int b = bq / a.T_q, qi = bq % a.T_q;
     const int tid = threadIdx.x, g = tid / LPK, ls = tid % LPK;
     const long qoff = (long)b * a.q_sb + (long)qi * a.q_st + h * DEC_DK;
     // Every load the prologue needs is issued before any of them is used:
-    // the length, the cache index and the query (or its K-slice partials).
+    // the length, the cache index, (EARLY) the first key trip and the query
+    // (or its K-slice partials).
     const int T = a.lens ? a.lens[(long)b * a.lens_step] : a.len_const;
     const long item = a.kv_index ? (long)a.kv_index[b] : (long)b;
+    const long base = item * a.kv_sb + (long)h * a.kv_sh + ls * DPL;
+#ifndef CT_ATTN_KPI
+#define CT_ATTN_KPI 2
+#endif
+    constexpr int KPI = BF16 ? CT_ATTN_KPI : 4;
+    constexpr int STEP = NG * KPI;
+    static_assert(!EARLY || STEP <= CT_ATTN_EARLY_ROWS, "the first trip must stay inside the allocation");
+    // raw 16-byte pieces stay in registers until use (bf16: 4 VGPRs a piece)
+    using Raw = typename std::conditional<BF16 && VEC, u16x8, float[8]>::type;
+    auto load_key = [&](int k, int v, Raw &kr, Raw &vr) {
+        const long off = base + (long)k * a.kv_st + 8 * v;
+        if constexpr (BF16 && VEC) {
+            kr = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.K) + off);
+            vr = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.V) + off);
+        } else {
+            load8<BF16, VEC>(a.K, off, kr);
+            load8<BF16, VEC>(a.V, off, vr);
+        }
+    };
+    Raw kA[KPI][NV], vA[KPI][NV];
+    if constexpr (EARLY) {
+        // keys g + NG*j < STEP <= rows allocated per item: in bounds whatever
+        // the length; keys past it are never used
+#pragma unroll
+        for (int j = 0; j < KPI; j++)
+#pragma unroll
+            for (int v = 0; v < NV; v++) load_key(g + NG * j, v, kA[j][v], vA[j][v]);
+    }
     float q[DPL];
     if (a.q_parts) {
         // query = ((part 0 + part 1) + ...) + bias, the decode GEMM's K-slices
@@ -135,18 +171,11 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
     const float *mrow = MASK ? a.mask + (long)qi * T : nullptr;
     // scores and running maxima are kept in base 2: s * scale * log2(e)
     const float scale2 = a.scale * LOG2E;
-    const long base = item * a.kv_sb + (long)h * a.kv_sh + ls * DPL;
 
     float m = -INFINITY, l = 0.0f, o[DPL];
 #pragma unroll
     for (int i = 0; i < DPL; i++) o[i] = 0.0f;
 
-#ifndef CT_ATTN_KPI
-#define CT_ATTN_KPI 2
-#endif
-    constexpr int KPI = BF16 ? CT_ATTN_KPI : 4;
-    // raw 16-byte pieces stay in registers until use (bf16: 4 VGPRs a piece)
-    using Raw = typename std::conditional<BF16 && VEC, u16x8, float[8]>::type;
     // trip at k0: keys k0 + NG*j (j < KPI) of this lane group.  Keys past
     // the end re-read the last key (in bounds, never used): the loads carry
     // no branch, so the wait before each use counts exactly the loads
@@ -156,16 +185,7 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
         for (int j = 0; j < KPI; j++) {
             const int k = min(k0 + NG * j, ke - 1);
 #pragma unroll
-            for (int v = 0; v < NV; v++) {
-                const long off = base + (long)k * a.kv_st + 8 * v;
-                if constexpr (BF16 && VEC) {
-                    kr[j][v] = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.K) + off);
-                    vr[j][v] = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.V) + off);
-                } else {
-                    load8<BF16, VEC>(a.K, off, kr[j][v]);
-                    load8<BF16, VEC>(a.V, off, vr[j][v]);
-                }
-            }
+            for (int v = 0; v < NV; v++) load_key(k, v, kr[j][v], vr[j][v]);
         }
     };
     // chunked online softmax: the trip's scores together, one rescale
@@ -219,13 +239,12 @@ __global__ __launch_bounds__(256) void attn_kernel(CtAttn a) {
             }
         m = mn;
     };
-    constexpr int STEP = NG * KPI;
 #if CT_ATTN_PIPE
     // two trips in flight: the next trip's loads are issued before the
     // current trip is used (register sets A and B alternate)
-    Raw kA[KPI][NV], vA[KPI][NV], kB[KPI][NV], vB[KPI][NV];
+    Raw kB[KPI][NV], vB[KPI][NV];
     int k0 = kb + g;
-    if (k0 < ke) load_trip(k0, kA, vA);
+    if (!EARLY && k0 < ke) load_trip(k0, kA, vA);
     for (; k0 < ke; k0 += 2 * STEP) {
         const int k1 = k0 + STEP;
         load_trip(k1, kB, vB);
@@ -279,13 +298,19 @@ extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
     const bool vec = ((uintptr_t)a->K % 16 == 0) && ((uintptr_t)a->V % 16 == 0) &&
                      a->kv_sb % need == 0 && a->kv_st % need == 0 && a->kv_sh % need == 0;
     constexpr int LPK = CT_ATTN_LPK;
-#define AK(B, V, M) hipLaunchKernelGGL((attn_kernel<B, V, LPK, M>), grid, dim3(256), 0, s, *a)
+    constexpr int NT = CT_ATTN_NT;
+    // the first key trip ahead of the length: decode caches (bf16, vector
+    // loads) with enough rows per item
+    const bool early = !a->mask && a->kv_bf16 && vec && a->kv_rows >= CT_ATTN_EARLY_ROWS;
+#define AK(B, V, M, E) hipLaunchKernelGGL((attn_kernel<B, V, LPK, M, NT, E>), grid, dim3(NT), 0, s, *a)
     if (a->mask) {
-        if (a->kv_bf16) { if (vec) AK(true, true, true); else AK(true, false, true); }
-        else { if (vec) AK(false, true, true); else AK(false, false, true); }
+        if (a->kv_bf16) { if (vec) AK(true, true, true, false); else AK(true, false, true, false); }
+        else { if (vec) AK(false, true, true, false); else AK(false, false, true, false); }
+    } else if (early) {
+        AK(true, true, false, true);
     } else {
-        if (a->kv_bf16) { if (vec) AK(true, true, false); else AK(true, false, false); }
-        else { if (vec) AK(false, true, false); else AK(false, false, false); }
+        if (a->kv_bf16) { if (vec) AK(true, true, false, false); else AK(true, false, false, false); }
+        else { if (vec) AK(false, true, false, false); else AK(false, false, false, false); }
     }
 #undef AK
 }

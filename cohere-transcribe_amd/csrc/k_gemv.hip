@@ -173,7 +173,9 @@ extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
         (g->out == CT_GV_FRAG && ((uintptr_t)g->F & 15)))
         gv_fatal("operands must be 16-byte aligned", g);
     const int spw = g->K / ksplit / 256;
-    const int cb = (g->N >= 8192 && g->N % 64 == 0) ? 4 : 1;
+    // columns per workgroup: 64 for the LM head; 32 for the long-K
+    // projection (its 512-column K-slices leave 256 workgroups); else 16
+    const int cb = (g->N >= 8192 && g->N % 64 == 0) ? 4 : (g->K >= 4096 && g->N % 32 == 0) ? 2 : 1;
     const dim3 grid(g->N / (16 * cb), ksplit, (g->M + 63) / 64);
     const dim3 block(64 * GV_WAVES);
 #define GV_CASE(CB, SPW)                                                          \
@@ -181,7 +183,8 @@ extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
         hipLaunchKernelGGL((gemv_kernel<CB, SPW>), grid, block, 0, s, *g);        \
         return;                                                                   \
     }
-    GV_CASE(1, 1) GV_CASE(1, 2) GV_CASE(1, 4) GV_CASE(4, 1) GV_CASE(4, 2) GV_CASE(4, 4)
+    GV_CASE(1, 1) GV_CASE(1, 2) GV_CASE(1, 4) GV_CASE(2, 1) GV_CASE(2, 2) GV_CASE(2, 4)
+    GV_CASE(4, 1) GV_CASE(4, 2) GV_CASE(4, 4)
 #undef GV_CASE
     gv_fatal("no kernel for this K slice", g);
 }

@@ -183,7 +183,7 @@ def test_gemv_matches_float64(lib, hip, N, K):
         assert e <= tol, (M, e)
 
 
-@pytest.mark.parametrize("N,K", [(1024, 1024), (4096, 1024), (16384, 1024)])
+@pytest.mark.parametrize("N,K", [(1024, 1024), (1024, 4096), (4096, 1024), (16384, 1024)])
 def test_gemv_rows_independent_of_batch(lib, hip, N, K):
     """Row r of a 130-row launch equals the same row launched alone, bit for bit."""
     dev = Dev(hip)
