@@ -158,8 +158,9 @@ typedef struct {
     int   lens_step;
     int   len_const;          /* ... or this when lens == NULL                          */
     const int   *kv_index;    /* optional: item b reads K/V block kv_index[b]          */
-    int   kv_rows;            /* key rows allocated per item (0: unknown); with >= 32
-                                 bf16 rows the first keys are read before the length */
+    int   kv_rows;            /* key rows allocated per item (0: unknown); with at least
+                                 one key trip's rows (32) of bf16 the first keys are
+                                 read before the length                                */
     const float *mask;        /* optional additive [T_q][T_k] mask (B == 1)            */
     int   T_q, B, H;
     float scale;

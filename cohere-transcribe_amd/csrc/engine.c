@@ -81,6 +81,11 @@ struct HipbEngine {
     HostReq *req;
     int n_req, n_enc;
     int *h_tmp;                /* pinned staging */
+    /* request fields as submitted (pinned): length, limit, flags, prompt
+     * length, successor, then the prompts; requests [meta_lo, n_req) are
+     * not on the device yet (flush_meta) */
+    int *h_meta;
+    int meta_lo;
     /* graph */
     hipGraph_t graph[2];       /* [0] slots rows, [1] with the spare prompt rows */
     hipGraphExec_t exec[2];
@@ -311,6 +316,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     if (e->prefill_min < 1) e->prefill_min = 1;
     mel_tables_init(e);
     ECHK(hipHostMalloc((void **)&e->h_tmp, (size_t)(R + 8) * (MAX_SEQ + 8) * sizeof(int), 0));
+    ECHK(hipHostMalloc((void **)&e->h_meta, (size_t)R * (5 + CT_PROMPT_MAX) * sizeof(int), 0));
     /* subsampling group tables (<= 10 (R + 1) ints per batch) + published ids */
     ECHK(hipHostMalloc((void **)&e->h_enc, (size_t)(11 * R + 64) * sizeof(int), 0));
     ECHK(hipStreamSynchronize(e->s));
@@ -339,6 +345,7 @@ void hipb_destroy(HipbEngine *e) {
     for (int r = 0; r < e->n_req; r++) { free(e->req[r].mel); free(e->req[r].pcm); }
     free(e->req);
     ECHK(hipHostFree(e->h_tmp));
+    ECHK(hipHostFree(e->h_meta));
     ECHK(hipHostFree(e->h_enc));
     ECHK(hipStreamDestroy(e->s2));
     free(e);
@@ -353,6 +360,7 @@ void hipb_reset(HipbEngine *e) {
         memset(&e->req[r], 0, sizeof e->req[r]);
     }
     e->n_req = e->n_enc = 0;
+    e->meta_lo = 0;
     e->fq_count = 0;
     e->bench_mode = 0;
     e->stepped = 0;
@@ -375,6 +383,29 @@ static int t_enc_of(int T_mel) {
 
 static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prompt, int limit,
                          int flags);
+
+/* Host mirror of the request fields: field f (0 length, 1 limit, 2 flags,
+ * 3 prompt length, 4 successor) of request r, and r's prompt. */
+static int *meta_field(HipbEngine *e, int f) { return e->h_meta + (size_t)f * e->d.max_req; }
+static int *meta_prompt(HipbEngine *e, int r) {
+    return e->h_meta + (size_t)5 * e->d.max_req + (size_t)r * CT_PROMPT_MAX;
+}
+
+/* Uploads the fields of the requests submitted since the last upload, in
+ * one copy per field, on the engine stream: ahead of every step that could
+ * admit them (the device edits a chained request's prompt only after its
+ * predecessor, uploaded with it, has decoded). */
+static void flush_meta(HipbEngine *e) {
+    const int lo = e->meta_lo, n = e->n_req - lo;
+    if (n <= 0) return;
+    int *const dst[5] = {e->d.req_T, e->d.req_limit, e->d.req_flags, e->d.req_np, e->d.req_next};
+    for (int f = 0; f < 5; f++)
+        ECHK(hipMemcpyAsync(dst[f] + lo, meta_field(e, f) + lo, (size_t)n * sizeof(int),
+                            hipMemcpyHostToDevice, e->s));
+    ECHK(hipMemcpyAsync(e->d.req_prompt + (size_t)lo * CT_PROMPT_MAX, meta_prompt(e, lo),
+                        (size_t)n * CT_PROMPT_MAX * sizeof(int), hipMemcpyHostToDevice, e->s));
+    e->meta_lo = e->n_req;
+}
 
 int hipb_submit(HipbEngine *e, const float *mel, int T_mel, const int *prompt, int n_prompt,
                 int limit, int flags) {
@@ -417,9 +448,7 @@ int hipb_submit_pcm_chunked(HipbEngine *e, const float *pcm, int n_samples, cons
     }
     free(b);
     /* link chunk c to chunk c + 1 */
-    int *nx = e->h_tmp;
-    for (int c = 0; c + 1 < nc; c++) nx[c] = r0 + c + 1;
-    if (nc > 1) ECHK(hipMemcpy(e->d.req_next + r0, nx, (size_t)(nc - 1) * sizeof(int), hipMemcpyHostToDevice));
+    for (int c = 0; c + 1 < nc; c++) meta_field(e, 4)[r0 + c] = r0 + c + 1;
     if (first_req) *first_req = r0;
     return nc;
 }
@@ -447,16 +476,16 @@ static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prom
     memset(q, 0, sizeof *q);
     q->T_mel = T_mel;
     q->T_enc = Te;
-    int meta[4 + CT_PROMPT_MAX];
-    meta[0] = Te; meta[1] = limit; meta[2] = flags; meta[3] = n_prompt;
-    memset(meta + 4, 0, sizeof(int) * CT_PROMPT_MAX);
-    memcpy(meta + 4, prompt, (size_t)n_prompt * sizeof(int));
-    ECHK(hipMemcpy(e->d.req_T + r, &meta[0], sizeof(int), hipMemcpyHostToDevice));
-    ECHK(hipMemcpy(e->d.req_limit + r, &meta[1], sizeof(int), hipMemcpyHostToDevice));
-    ECHK(hipMemcpy(e->d.req_flags + r, &meta[2], sizeof(int), hipMemcpyHostToDevice));
-    ECHK(hipMemcpy(e->d.req_np + r, &meta[3], sizeof(int), hipMemcpyHostToDevice));
-    ECHK(hipMemcpy(e->d.req_prompt + (size_t)r * CT_PROMPT_MAX, meta + 4, CT_PROMPT_MAX * sizeof(int),
-                   hipMemcpyHostToDevice));
+    /* request r's mirror entries are rewritten only after hipb_reset, which
+     * waits for the stream, so no upload is still reading them */
+    meta_field(e, 0)[r] = Te;
+    meta_field(e, 1)[r] = limit;
+    meta_field(e, 2)[r] = flags;
+    meta_field(e, 3)[r] = n_prompt;
+    meta_field(e, 4)[r] = -1;
+    int *pp = meta_prompt(e, r);
+    memset(pp, 0, sizeof(int) * CT_PROMPT_MAX);
+    memcpy(pp, prompt, (size_t)n_prompt * sizeof(int));
     return r;
 }
 
@@ -793,6 +822,7 @@ static int next_batch(const HipbEngine *e, int r, int max_batch_frames) {
 }
 
 void hipb_encode(HipbEngine *e, int max_batch_frames) {
+    flush_meta(e);
     if (max_batch_frames < e->d.tmax) max_batch_frames = e->d.tmax;
     int r = e->n_enc;
     while (r < e->n_req) {
@@ -944,6 +974,7 @@ static int want_wide(const HipbEngine *e, const int *q) {
 static void read_queue(HipbEngine *e, int *q);
 
 void hipb_step(HipbEngine *e) {
+    flush_meta(e);
     int q[8];
     read_queue(e, q);
     step_launch(e, want_wide(e, q));
@@ -990,6 +1021,7 @@ void hipb_bench_steps(HipbEngine *e, int n) {
 }
 
 long hipb_run(HipbEngine *e, int chunk) {
+    flush_meta(e);
     if (chunk < 1) chunk = 1;
     const int spare = e->d.rows - e->d.slots;
     ensure_graph(e, 0);
@@ -1031,6 +1063,7 @@ static void *enc_worker(void *arg) {
 }
 
 long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
+    flush_meta(e);
     if (chunk < 1) chunk = 1;
     if (max_batch_frames < e->d.tmax) max_batch_frames = e->d.tmax;
     const int spare = e->d.rows - e->d.slots;

@@ -35,9 +35,13 @@ constexpr int CT_ATTN_QPARTS = 4;   // most query partial slices a launch may pa
 #ifndef CT_ATTN_NT
 #define CT_ATTN_NT 256
 #endif
-// rows per item (CtAttn.kv_rows) from which the first key trip is issued
-// ahead of the item's length
-constexpr int CT_ATTN_EARLY_ROWS = 32;
+// keys per lane group per trip (bf16; fp32 caches use 4)
+#ifndef CT_ATTN_KPI
+#define CT_ATTN_KPI 2
+#endif
+// rows per item (CtAttn.kv_rows) from which the first key trip (of bf16
+// caches) is issued ahead of the item's length: one trip's keys
+constexpr int CT_ATTN_EARLY_ROWS = CT_ATTN_NT / CT_ATTN_LPK * CT_ATTN_KPI;
 
 template <bool BF16, bool VEC>
 __device__ __forceinline__ void load8(const void *base, long off, float (&v)[8]) {
@@ -103,9 +107,6 @@ __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
     const int T = a.lens ? a.lens[(long)b * a.lens_step] : a.len_const;
     const long item = a.kv_index ? (long)a.kv_index[b] : (long)b;
     const long base = item * a.kv_sb + (long)h * a.kv_sh + ls * DPL;
-#ifndef CT_ATTN_KPI
-#define CT_ATTN_KPI 2
-#endif
     constexpr int KPI = BF16 ? CT_ATTN_KPI : 4;
     constexpr int STEP = NG * KPI;
     static_assert(!EARLY || STEP <= CT_ATTN_EARLY_ROWS, "the first trip must stay inside the allocation");
