@@ -32,6 +32,7 @@ typedef struct {
     int n;               /* samples of a PCM request                          */
     int T_mel, T_enc;
     int chained;         /* admitted only after its predecessor chunk ends    */
+    long pool_off;       /* first frame of its encoder output in enc_pool     */
 } HostReq;
 
 struct HipbEngine {
@@ -52,7 +53,9 @@ struct HipbEngine {
     /* caches */
     void *kself, *vself;       /* [L][slots][H][kv_rows][128] */
     void *kcross, *vcross;     /* [L][max_req][H][tmax][128] */
-    float *enc_pool;           /* [max_req][tmax][DEC_D] */
+    float *enc_pool;           /* encoder outputs, packed batch after batch:
+                                  <= max_req * tmax frames of DEC_D floats */
+    long pool_frames;          /* frames of enc_pool in use */
     /* step activations: h residual rows (fp32); lnf/attf/midf the decode
      * GEMMs' inputs in frag layout; parts K-slice partial sums */
     float *h, *q, *parts, *logits;
@@ -72,7 +75,7 @@ struct HipbEngine {
     int enc_cap;               /* frames */
     int sub_cap;               /* subsampling scratch floats */
     int *e_subtab;             /* packed subsampling group tables */
-    float *ex, *eln, *emid, *eq, *ek, *ev, *eo, *eg, *edw, *epe, *ep, *eh, *esub, *emel;
+    float *ex, *eln, *emid, *eq, *ek, *ev, *eo, *eg, *edw, *epe, *ep, *esub, *emel;
     uint16_t *eln_h, *eln_l, *emid_h, *emid_l, *eo_h, *eo_l, *edw_h, *edw_l;  /* pre-split GEMM inputs */
     size_t emel_cap;
     int *e_row_start, *e_row_len, *e_seq_off, *e_seq_T, *e_blk_seq, *e_blk_q0;
@@ -336,7 +339,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
                     e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
-                    e->eh, e->esub, e->emel, e->e_subtab, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
+                    e->esub, e->emel, e->e_subtab, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
                     e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
                     e->d_fb_lo, e->d_fb_hi, e->epcm, e->e_clips, e->e_frame_clip,
                     e->eln_h, e->eln_l, e->emid_h, e->emid_l, e->eo_h, e->eo_l, e->edw_h, e->edw_l};
@@ -361,6 +364,7 @@ void hipb_reset(HipbEngine *e) {
     }
     e->n_req = e->n_enc = 0;
     e->meta_lo = 0;
+    e->pool_frames = 0;
     e->fq_count = 0;
     e->bench_mode = 0;
     e->stepped = 0;
@@ -505,7 +509,7 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     if (sub < CT_SUB_PACK_FLOATS) sub = CT_SUB_PACK_FLOATS;
     if (frames <= e->enc_cap && sub <= e->sub_cap) return;
     ECHK(hipStreamSynchronize(e->enc_s));
-    float **bufs[] = {&e->ex, &e->eln, &e->emid, &e->eq, &e->ek, &e->ev, &e->eo, &e->eg, &e->edw, &e->eh};
+    float **bufs[] = {&e->ex, &e->eln, &e->emid, &e->eq, &e->ek, &e->ev, &e->eo, &e->eg, &e->edw};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
         if (*bufs[i]) { ECHK(hipFree(*bufs[i])); *bufs[i] = NULL; }
     uint16_t **hb[] = {&e->eln_h, &e->eln_l, &e->emid_h, &e->emid_l, &e->eo_h, &e->eo_l, &e->edw_h, &e->edw_l};
@@ -540,7 +544,6 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     e->eo = dmalloc(rows * ENC_D * 4);
     e->eg = dmalloc(rows * ENC_D * 4);
     e->edw = NULL;
-    e->eh = dmalloc(rows * DEC_D * 4);
     e->e_row_start = dmalloc(rows * sizeof(int));
     e->e_row_len = dmalloc(rows * sizeof(int));
     e->e_rowoff = dmalloc(rows * sizeof(long));
@@ -760,14 +763,14 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         gemm_sp(e, e->emid_h, e->emid_l, M, ENC_FF, L->ff2_w2, L->ff2_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
         ctk_layernorm(e->ex, e->ex, DW(L->out_lnw), DW(L->out_lnb), M, ENC_D, s);
     }
-    gemm(e, e->ex, M, ENC_D, W->prw, W->prb, e->eh, DEC_D, CT_EPI_STORE, 0, NULL);
-    /* keep enc_h per request; cross K/V straight into the head-major pool */
-    for (int i = 0; i < n; i++)
-        ECHK(hipMemcpyAsync(e->enc_pool + (size_t)(r0 + i) * e->d.tmax * DEC_D,
-                            e->eh + (size_t)seq_off[i] * DEC_D, (size_t)seq_T[i] * DEC_D * 4,
-                            hipMemcpyDeviceToDevice, s));
+    /* the encoder output stays in enc_pool, packed as encoded; cross K/V
+     * go straight into the head-major cross caches */
+    float *eh = e->enc_pool + (size_t)e->pool_frames * DEC_D;
+    gemm(e, e->ex, M, ENC_D, W->prw, W->prb, eh, DEC_D, CT_EPI_STORE, 0, NULL);
+    for (int i = 0; i < n; i++) e->req[r0 + i].pool_off = e->pool_frames + seq_off[i];
+    e->pool_frames += M;
     const size_t cross_l = (size_t)e->d.max_req * DEC_H * e->d.tmax * DEC_DK;
-    ctk_split(e->eln_h, e->eln_l, e->eh, (long)M * DEC_D, s);   /* LN planes are free now */
+    ctk_split(e->eln_h, e->eln_l, eh, (long)M * DEC_D, s);   /* LN planes are free now */
     for (int l = 0; l < DEC_N; l++) {
         CtGemm g;
         memset(&g, 0, sizeof g);
@@ -1147,7 +1150,7 @@ void hipb_logits(HipbEngine *e, int slot, float *out) {
 void hipb_enc_out(HipbEngine *e, int req, float *out) {
     if (req < 0 || req >= e->n_enc) CT_FATAL("hipb_enc_out: request not encoded");
     ECHK(hipStreamSynchronize(e->s));
-    ECHK(hipMemcpy(out, e->enc_pool + (size_t)req * e->d.tmax * DEC_D,
+    ECHK(hipMemcpy(out, e->enc_pool + (size_t)e->req[req].pool_off * DEC_D,
                    (size_t)e->req[req].T_enc * DEC_D * sizeof(float), hipMemcpyDeviceToHost));
 }
 
