@@ -136,7 +136,12 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
         for (int k = lane; k < T; k += 64) mx = fmaxf(mx, row[k]);
         mx = wave_max(mx);
         float sum = 0.0f;
-        for (int k = lane; k < T; k += 64) { const float e = expf(row[k] - mx); row[k] = e; sum += e; }
+        // e^(s - max) as 2^((s - max) log2 e) on the hardware exp2
+        for (int k = lane; k < T; k += 64) {
+            const float e = __builtin_amdgcn_exp2f((row[k] - mx) * 1.4426950408889634f);
+            row[k] = e;
+            sum += e;
+        }
         sum = wave_sum(sum);
         for (int k = lane; k < T; k += 64) row[k] /= sum;
     }
@@ -229,7 +234,7 @@ __global__ void dwconv_bn_silu_kernel(float *out, uint16_t *out_hi, uint16_t *ou
 #pragma unroll
     for (int e = 0; e < 8; e++) {
         const float v = (s[e] - bf2f(m8[e])) / sqrtf(bf2f(v8[e]) + 1e-5f) * bf2f(w8[e]) + bf2f(bb8[e]);
-        o[e] = v / (1.0f + expf(-v));
+        o[e] = v * sigmoid_hw(v);
     }
     const long oi = (long)r * ENC_D + c0;
     if (out_hi) {

@@ -66,7 +66,7 @@ __device__ __forceinline__ void store_out(const CtGemm &g, int m, int col, float
             reinterpret_cast<float *>(sg.base)[(long)m * sg.ld + c] = s;
         } else if (sg.mode == CT_OUT_SPLIT) {
             float v = s;
-            if (g.epi == CT_EPI_SILU) v = s / (1.0f + expf(-s));
+            if (g.epi == CT_EPI_SILU) v = s * sigmoid_hw(s);
             else if (g.epi == CT_EPI_RELU) v = s > 0.0f ? s : 0.0f;
             uint16_t h, l;
             split_bf16(v, h, l);
@@ -88,7 +88,7 @@ __device__ __forceinline__ void store_out(const CtGemm &g, int m, int col, float
         yrow = (long)m * g.row_stride + len - 1;
     }
     float *y = g.Y + yrow * g.ldy + col;
-    if (g.epi == CT_EPI_SILU) *y = s / (1.0f + expf(-s));
+    if (g.epi == CT_EPI_SILU) *y = s * sigmoid_hw(s);
     else if (g.epi == CT_EPI_RELU) *y = s > 0.0f ? s : 0.0f;
     else if (g.epi == CT_EPI_FMADD) *y += g.scale * s;
     else *y = s;
@@ -99,7 +99,7 @@ __device__ __forceinline__ void store_out(const CtGemm &g, int m, int col, float
 __device__ __forceinline__ void act8(const CtGemm &g, float (&v)[8]) {
     if (g.epi == CT_EPI_SILU) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = v[i] / (1.0f + expf(-v[i]));
+        for (int i = 0; i < 8; i++) v[i] = v[i] * sigmoid_hw(v[i]);
     } else if (g.epi == CT_EPI_RELU) {
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = v[i] > 0.0f ? v[i] : 0.0f;
@@ -413,7 +413,7 @@ __global__ __launch_bounds__(256) void gemm_big_kernel(CtGemm g, int n_mt, int n
                         if (m >= g.M) continue;
                         const float a = acc[rb][cb][j] + ba;
                         const float gt = sx[lrow * 64 + cb * 16 + r] + bg;
-                        g.Y[(long)m * g.ldy + col] = a / (1.0f + expf(-gt));
+                        g.Y[(long)m * g.ldy + col] = a * sigmoid_hw(gt);
                     }
             }
         }
@@ -621,7 +621,7 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
                         if (m >= g.M) continue;
                         const float a = acc[rb][cb][j] + ba;
                         const float gt = sx[lrow * 128 + lc] + bg;
-                        g.Y[(long)m * g.ldy + col] = a / (1.0f + expf(-gt));
+                        g.Y[(long)m * g.ldy + col] = a * sigmoid_hw(gt);
                     }
             }
         }
@@ -912,7 +912,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_kernel(CtGemm g, int n_mt, in
                 const float s = acc[rb][cb][j] + ba;
                 if (GLU) {
                     const float gt = acc[rb][cb + (GLU ? CO : 0)][j] + bg;
-                    g.Y[(long)m * g.ldy + col] = s / (1.0f + expf(-gt));
+                    g.Y[(long)m * g.ldy + col] = s * sigmoid_hw(gt);
                 } else {
                     store_out(g, m, col, s);
                 }
