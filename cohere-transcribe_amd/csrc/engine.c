@@ -681,21 +681,22 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         moff += (size_t)N_MELS * q->T_mel;
     }
     /* subsampling over groups of requests packed along time, each group as
-     * large as the scratch allows: conv0 -> ra, depthwise -> rb, pointwise ->
-     * ra, depthwise -> rb, pointwise -> ra, then the flattened frames go
+     * large as the scratch allows: conv0 + depthwise -> rb, pointwise -> ra,
+     * depthwise -> rb, pointwise -> ra (ra and rb each hold the group's
+     * first-stage output, [sum T2][32][256]), then the flattened frames go
      * pre-split into the packed rows (the FFN planes are free until layer 0)
      * for one projection GEMM.  The group tables (row offsets of the three
      * stages, mel lengths and offsets) are staged in distinct parts of the
      * pinned buffer, so no group overwrites one still to be copied. */
     int *tab_h = e->h_enc, *tab_d = e->e_subtab;
     for (int g0 = 0; g0 < n;) {
-        long s1 = 0, s2 = 0;
+        long s2 = 0;
         int g1 = g0;
         while (g1 < n) {
             const int tm = e->req[r0 + g1].T_mel, T1 = (tm + 1) / 2, T2 = (T1 + 1) / 2;
-            const long a = (long)T1 * 64 * SUB_CH, b = (long)T2 * 32 * SUB_CH;
-            if (g1 > g0 && s1 + a + s2 + b > e->sub_cap) break;
-            s1 += a; s2 += b; g1++;
+            const long b = (long)T2 * 32 * SUB_CH;
+            if (g1 > g0 && 2 * (s2 + b) > e->sub_cap) break;
+            s2 += b; g1++;
         }
         const int ng = g1 - g0, L = ng + 1;
         int *o1 = tab_h, *o2 = o1 + L, *o3 = o2 + L, *tm = o3 + L, *mo = tm + L;
@@ -711,9 +712,9 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         }
         ECHK(hipMemcpyAsync(tab_d, tab_h, (size_t)5 * L * sizeof(int), hipMemcpyHostToDevice, s));
         const int *d1 = tab_d, *d2 = d1 + L, *d3 = d2 + L, *dtm = d3 + L, *dmo = dtm + L;
-        float *ra = e->esub, *rb = e->esub + s1;
-        ctk_sub_conv0_packed(ra, e->emel, d1, dtm, dmo, ng, o1[ng], DW(W->s0w), DW(W->s0b), s);
-        ctk_sub_dwconv_packed(rb, ra, d1, d2, ng, o2[ng], 64, DW(W->s2w), DW(W->s2b), s);
+        float *ra = e->esub, *rb = e->esub + s2;
+        ctk_sub_conv0_dw_packed(rb, e->emel, d1, d2, dtm, dmo, ng, o2[ng], DW(W->s0w), DW(W->s0b),
+                                DW(W->s2w), DW(W->s2b), s);
         gemm(e, rb, o2[ng] * 32, SUB_CH, W->s3w, W->s3b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
         ctk_sub_dwconv_packed(rb, ra, d2, d3, ng, o3[ng], 32, DW(W->s5w), DW(W->s5b), s);
         gemm(e, rb, o3[ng] * 16, SUB_CH, W->s6w, W->s6b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);

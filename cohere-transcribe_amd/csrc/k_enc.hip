@@ -318,33 +318,67 @@ __device__ __forceinline__ int packed_owner(const int *off, int n, int tau) {
     return lo;
 }
 
-// sub_conv0_kernel over several requests at once: request r's mel
-// (N_MELS x tmel[r], row stride tmel[r]) sits at mel + moff[r], its output
-// rows at o1[r] .. o1[r + 1] of the packed [sum T1][64][256] output.  Same
-// per-element arithmetic as the one-request kernel.
-__global__ void sub_conv0_packed_kernel(float *out, const float *mel, const int *o1, const int *tmel,
-                                        const int *moff, int n, const uint16_t *w, const uint16_t *b) {
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)o1[n] * 64 * SUB_CH) return;
-    const int oc = (int)(i % SUB_CH);
-    const int ow = (int)((i / SUB_CH) % 64);
-    const int tau = (int)(i / (SUB_CH * 64));
-    const int r = packed_owner(o1, n, tau);
-    const int oh = tau - o1[r], T_mel = tmel[r];
+// The first two subsampling stages fused, over several requests packed
+// along time: conv 3x3 stride 2 (1 -> 256 channels, ReLU) then depthwise
+// 3x3 stride 2, without storing the conv output.  Workgroup = one output row
+// tau of the depthwise stage (request r, row oh = tau - o2[r]), thread =
+// channel c, looping over the 32 output columns.  The 7 mel frames the row
+// needs (4*oh - 3 .. 4*oh + 3, all 128 bins) are staged in LDS; each conv
+// value a depthwise tap needs is recomputed from them (9 products), in the
+// same order and with the same skips as sub_conv0 then sub_dwconv, so the
+// result is bit-identical to running the two stages
+// (backends/cpu/backend.c:201-221).
+constexpr int C0D_FRAMES = 7;
+__global__ __launch_bounds__(256) void sub_conv0_dw_packed_kernel(float *out, const float *mel,
+                                                                  const int *o1, const int *o2,
+                                                                  const int *tmel, const int *moff, int n,
+                                                                  const uint16_t *w0, const uint16_t *b0,
+                                                                  const uint16_t *wd, const uint16_t *bd) {
+    __shared__ float sm[C0D_FRAMES][N_MELS];
+    const int tau = blockIdx.x, c = threadIdx.x;
+    const int r = packed_owner(o2, n, tau);
+    const int oh = tau - o2[r], H1 = o1[r + 1] - o1[r], T_mel = tmel[r];
     const float *m = mel + moff[r];
-    float s = bf2f(b[oc]);
-#pragma unroll
-    for (int kh = 0; kh < 3; kh++) {
-        const int ih = oh * 2 - 1 + kh;
-        if (ih < 0 || ih >= T_mel) continue;
-#pragma unroll
-        for (int kw = 0; kw < 3; kw++) {
-            const int iw = ow * 2 - 1 + kw;
-            if (iw < 0 || iw >= N_MELS) continue;
-            s += m[(long)iw * T_mel + ih] * bf2f(w[oc * 9 + kh * 3 + kw]);
-        }
+    const int f0 = 4 * oh - 3;                 // first mel frame of the window
+    for (int e = c; e < C0D_FRAMES * N_MELS; e += 256) {
+        const int fr = e / N_MELS, bin = e % N_MELS, ih0 = f0 + fr;
+        sm[fr][bin] = (ih0 >= 0 && ih0 < T_mel) ? m[(long)bin * T_mel + ih0] : 0.0f;
     }
-    out[i] = s > 0.0f ? s : 0.0f;
+    float k0[9], kd[9];
+#pragma unroll
+    for (int k = 0; k < 9; k++) { k0[k] = bf2f(w0[c * 9 + k]); kd[k] = bf2f(wd[c * 9 + k]); }
+    const float bias0 = bf2f(b0[c]), biasd = bf2f(bd[c]);
+    __syncthreads();
+    float *orow = out + (long)tau * 32 * SUB_CH + c;
+    for (int ow = 0; ow < 32; ow++) {
+        float acc = biasd;
+#pragma unroll
+        for (int kh2 = 0; kh2 < 3; kh2++) {
+            const int ih1 = oh * 2 - 1 + kh2;
+            if (ih1 < 0 || ih1 >= H1) continue;
+#pragma unroll
+            for (int kw2 = 0; kw2 < 3; kw2++) {
+                const int iw1 = ow * 2 - 1 + kw2;
+                if (iw1 < 0 || iw1 >= 64) continue;
+                // conv value at (ih1, iw1, c)
+                float x = bias0;
+#pragma unroll
+                for (int kh = 0; kh < 3; kh++) {
+                    const int ih0 = ih1 * 2 - 1 + kh;
+                    if (ih0 < 0 || ih0 >= T_mel) continue;
+#pragma unroll
+                    for (int kw = 0; kw < 3; kw++) {
+                        const int iw0 = iw1 * 2 - 1 + kw;
+                        if (iw0 < 0 || iw0 >= N_MELS) continue;
+                        x += sm[ih0 - f0][iw0] * k0[kh * 3 + kw];
+                    }
+                }
+                x = x > 0.0f ? x : 0.0f;
+                acc += x * kd[kh2 * 3 + kw2];
+            }
+        }
+        orow[(long)ow * SUB_CH] = acc;
+    }
 }
 
 // sub_dwconv_kernel over several requests: request r's input rows
@@ -532,12 +566,13 @@ extern "C" void ctk_sub_dwconv(float *out, const float *in, int H, int Wd,
     hipLaunchKernelGGL(sub_dwconv_kernel, dim3(nblk(n)), dim3(256), 0, s, out, in, H, Wd, w, b);
 }
 
-extern "C" void ctk_sub_conv0_packed(float *out, const float *mel, const int *o1, const int *tmel,
-                                     const int *moff, int n, int rows1, const uint16_t *w,
-                                     const uint16_t *b, hipStream_t s) {
-    const long cnt = (long)rows1 * 64 * SUB_CH;
-    if (cnt <= 0 || n <= 0) return;
-    hipLaunchKernelGGL(sub_conv0_packed_kernel, dim3(nblk(cnt)), dim3(256), 0, s, out, mel, o1, tmel, moff, n, w, b);
+extern "C" void ctk_sub_conv0_dw_packed(float *out, const float *mel, const int *o1, const int *o2,
+                                        const int *tmel, const int *moff, int n, int rows2,
+                                        const uint16_t *w0, const uint16_t *b0, const uint16_t *wd,
+                                        const uint16_t *bd, hipStream_t s) {
+    if (rows2 <= 0 || n <= 0) return;
+    hipLaunchKernelGGL(sub_conv0_dw_packed_kernel, dim3(rows2), dim3(256), 0, s, out, mel, o1, o2, tmel, moff,
+                       n, w0, b0, wd, bd);
 }
 
 extern "C" void ctk_sub_dwconv_packed(float *out, const float *in, const int *oin, const int *oout, int n,
