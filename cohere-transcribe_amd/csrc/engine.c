@@ -75,7 +75,11 @@ struct HipbEngine {
     int enc_cap;               /* frames */
     int sub_cap;               /* subsampling scratch floats */
     int *e_subtab;             /* packed subsampling group tables */
-    float *ex, *eln, *emid, *eq, *ek, *ev, *eo, *eg, *edw, *epe, *ep, *esub, *emel;
+    float *ex, *eln, *emid, *eq, *ek, *ev, *eo, *eg, *edw, *epe, *esub, *emel;
+    /* relative-position projections of every layer for clips of up to tmax
+     * frames, [ENC_N][2 tmax - 1][ENC_D], built once: a clip of T frames
+     * reads rows tmax - T .. tmax + T - 2 */
+    float *ep_all;
     uint16_t *eln_h, *eln_l, *emid_h, *emid_l, *eo_h, *eo_l, *edw_h, *edw_l;  /* pre-split GEMM inputs */
     size_t emel_cap;
     int *e_row_start, *e_row_len, *e_seq_off, *e_seq_T, *e_blk_seq, *e_blk_q0;
@@ -338,7 +342,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->d.req_next, e->d.rq, e->d.pend, e->d.fq,
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
                     e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
-                    e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep,
+                    e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep_all,
                     e->esub, e->emel, e->e_subtab, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
                     e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
                     e->d_fb_lo, e->d_fb_hi, e->epcm, e->e_clips, e->e_frame_clip,
@@ -521,10 +525,6 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     if (e->e_rowoff) ECHK(hipFree(e->e_rowoff));
     if (e->e_subtab) ECHK(hipFree(e->e_subtab));
     if (e->esub) ECHK(hipFree(e->esub));
-    if (!e->epe) {
-        e->epe = dmalloc((size_t)(2 * e->d.tmax - 1) * ENC_D * 4);
-        e->ep = dmalloc((size_t)(2 * e->d.tmax - 1) * ENC_D * 4);
-    }
     const int M = frames > e->enc_cap ? frames : e->enc_cap;
     const size_t rows = (size_t)M;
     e->ex = dmalloc(rows * ENC_D * 4);
@@ -593,6 +593,22 @@ static void batch_buffers(HipbEngine *e, int r0, int r1) {
         e->e_frame_clip = dmalloc((size_t)nfr * sizeof(int));
         e->frames_cap = nfr;
     }
+}
+
+/* The position projections P_l = pos_emb W_pos_l of every layer, for the
+ * engine's longest clip (tmax frames).  Row p holds relative distance
+ * tmax - 1 - p, so any shorter clip's window is a contiguous slice and its
+ * rows equal those a table built for that clip would hold (the GEMM's rows
+ * do not depend on the row count). */
+static void pos_tables(HipbEngine *e) {
+    if (e->ep_all) return;
+    const int rows = 2 * e->d.tmax - 1;
+    e->epe = dmalloc((size_t)rows * ENC_D * 4);
+    e->ep_all = dmalloc((size_t)ENC_N * rows * ENC_D * 4);
+    ctk_rel_pos_emb(e->epe, e->d.tmax, ct_inv_freq(), e->enc_s);
+    for (int l = 0; l < ENC_N; l++)
+        gemm(e, e->epe, rows, ENC_D, e->W.enc[l].sa_pw, NULL, e->ep_all + (size_t)l * rows * ENC_D, ENC_D,
+             CT_EPI_STORE, 0, NULL);
 }
 
 static void encode_batch(HipbEngine *e, int r0, int r1) {
@@ -726,8 +742,8 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     }
     free(mel_off);
     gemm_sp(e, e->emid_h, e->emid_l, M, SUB_CH * 16, W->sow, W->sob, e->ex, ENC_D, CT_EPI_STORE, 0);
-    /* relative positions for T_max; each clip reads its shifted window */
-    ctk_rel_pos_emb(e->epe, T_max, ct_inv_freq(), s);
+    pos_tables(e);
+    const long pos_rows = 2L * e->d.tmax - 1;
     for (int l = 0; l < ENC_N; l++) {
         const ELayer *L = &W->enc[l];
         /* x += 0.5 FFN1(LN x) */
@@ -739,8 +755,8 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_qw, L->sa_qb, e->eq, ENC_D, CT_EPI_STORE, 0);
         gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_kw, L->sa_kb, e->ek, ENC_D, CT_EPI_STORE, 0);
         gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_vw, L->sa_vb, e->ev, ENC_D, CT_EPI_STORE, 0);
-        gemm(e, e->epe, 2 * T_max - 1, ENC_D, L->sa_pw, NULL, e->ep, ENC_D, CT_EPI_STORE, 0, NULL);
-        ctk_relpos_attn_packed(NULL, e->eo_h, e->eo_l, e->eq, e->ek, e->ev, e->ep, T_max, DW(L->sa_pbu),
+        ctk_relpos_attn_packed(NULL, e->eo_h, e->eo_l, e->eq, e->ek, e->ev,
+                               e->ep_all + (size_t)l * pos_rows * ENC_D, e->d.tmax, DW(L->sa_pbu),
                                DW(L->sa_pbv), e->e_seq_off, e->e_seq_T, e->e_blk_seq, e->e_blk_q0, nblk,
                                T_max, s);
         gemm_sp(e, e->eo_h, e->eo_l, M, ENC_D, L->sa_ow, L->sa_ob, e->ex, ENC_D, CT_EPI_FMADD, 1.0f);
@@ -1088,7 +1104,10 @@ long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
             batch_buffers(e, r, r1);
             r = r1;
         }
-        if (frames_max) enc_reserve(e, frames_max, tmel_max);
+        if (frames_max) {
+            enc_reserve(e, frames_max, tmel_max);
+            pos_tables(e);
+        }
     }
     ECHK(hipStreamSynchronize(e->s));
     e->enc_s = e->s2;
