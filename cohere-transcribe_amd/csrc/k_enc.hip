@@ -191,21 +191,41 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
 // Depthwise conv (k = 9, zero padding 4 inside the sequence) + inference
 // BatchNorm + SiLU (backends/cpu/backend.c:312-334).
 // ---------------------------------------------------------------------------
-// One thread per 8 consecutive channels of a row (16-byte loads of the
-// activations and of every per-channel parameter); the arithmetic per
-// element is the scalar form's.
-__global__ void dwconv_bn_silu_kernel(float *out, uint16_t *out_hi, uint16_t *out_lo,
-                                      const float *in, int M, const int *row_start,
-                                      const int *row_len, const uint16_t *dww,
-                                      const uint16_t *dwb, const uint16_t *bnw, const uint16_t *bnb,
-                                      const uint16_t *bnm, const uint16_t *bnv) {
-    constexpr int G = ENC_D / 8;
+// One thread per 8 consecutive channels of DW_RB consecutive rows: the
+// DW_RB + 8 input rows the taps reach are read once (16-byte pieces) and kept
+// in registers, so each input row is fetched about twice instead of once per
+// tap.  The arithmetic per element is the scalar form's (taps in order, taps
+// outside the row's sequence skipped, then BN and SiLU).
+#ifndef CT_DW_RB
+#define CT_DW_RB 8
+#endif
+constexpr int DW_RB = CT_DW_RB;
+__global__ __launch_bounds__(256) void dwconv_bn_silu_kernel(float *out, uint16_t *out_hi, uint16_t *out_lo,
+                                                             const float *in, int M, const int *row_start,
+                                                             const int *row_len, const uint16_t *dww,
+                                                             const uint16_t *dwb, const uint16_t *bnw,
+                                                             const uint16_t *bnb, const uint16_t *bnm,
+                                                             const uint16_t *bnv) {
+    constexpr int G = ENC_D / 8, HALO = (ENC_CK - 1) / 2, NX = DW_RB + ENC_CK - 1;
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)M * G) return;
-    const int r = (int)(i / G), c0 = (int)(i % G) * 8;
-    const int st = row_start ? row_start[r] : 0;       // this row's sequence: [st, st + T)
-    const int T = row_len ? row_len[r] : M;
-    const int t = r - st;
+    const int nrb = (M + DW_RB - 1) / DW_RB;
+    if (i >= (long)nrb * G) return;
+    const int r0 = (int)(i / G) * DW_RB, c0 = (int)(i % G) * 8;
+    // input rows r0 - 4 .. r0 + DW_RB + 3 of these 8 channels (zero outside [0, M))
+    float x[NX][8];
+#pragma unroll
+    for (int j = 0; j < NX; j++) {
+        const int rr = r0 - HALO + j;
+        if (rr >= 0 && rr < M) {
+            const float4 *p = reinterpret_cast<const float4 *>(in + (long)rr * ENC_D + c0);
+            const float4 x0 = p[0], x1 = p[1];
+            x[j][0] = x0.x; x[j][1] = x0.y; x[j][2] = x0.z; x[j][3] = x0.w;
+            x[j][4] = x1.x; x[j][5] = x1.y; x[j][6] = x1.z; x[j][7] = x1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[j][e] = 0.0f;
+        }
+    }
     // taps of the 8 channels: dww[c][k] for c0 <= c < c0 + 8, 72 contiguous values
     uint16_t wk[8 * ENC_CK];
 #pragma unroll
@@ -215,42 +235,48 @@ __global__ void dwconv_bn_silu_kernel(float *out, uint16_t *out_hi, uint16_t *ou
         for (int e = 0; e < 8; e++) wk[8 * v + e] = w8[e];
     }
     const u16x8 b8 = *reinterpret_cast<const u16x8 *>(dwb + c0);
-    float s[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) s[e] = bf2f(b8[e]);
-#pragma unroll
-    for (int k = 0; k < ENC_CK; k++) {
-        const int ti = t - (ENC_CK - 1) / 2 + k;
-        if (ti < 0 || ti >= T) continue;
-        const float4 *x = reinterpret_cast<const float4 *>(in + (long)(st + ti) * ENC_D + c0);
-        const float4 x0 = x[0], x1 = x[1];
-        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-        for (int e = 0; e < 8; e++) s[e] += bf2f(wk[e * ENC_CK + k]) * xv[e];
-    }
     const u16x8 m8 = *reinterpret_cast<const u16x8 *>(bnm + c0), v8 = *reinterpret_cast<const u16x8 *>(bnv + c0);
     const u16x8 w8 = *reinterpret_cast<const u16x8 *>(bnw + c0), bb8 = *reinterpret_cast<const u16x8 *>(bnb + c0);
-    float o[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float v = (s[e] - bf2f(m8[e])) / sqrtf(bf2f(v8[e]) + 1e-5f) * bf2f(w8[e]) + bf2f(bb8[e]);
-        o[e] = v * sigmoid_hw(v);
-    }
-    const long oi = (long)r * ENC_D + c0;
-    if (out_hi) {
-        u16x8 h8, l8;
+    for (int rb = 0; rb < DW_RB; rb++) {
+        const int r = r0 + rb;
+        if (r >= M) break;
+        const int st = row_start ? row_start[r] : 0;       // this row's sequence: [st, st + T)
+        const int T = row_len ? row_len[r] : M;
+        const int t = r - st;
+        float s[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) s[e] = bf2f(b8[e]);
+#pragma unroll
+        for (int k = 0; k < ENC_CK; k++) {
+            const int ti = t - HALO + k;
+            if (ti < 0 || ti >= T) continue;
+            // input row st + ti = r - HALO + k is x[rb + k]
+#pragma unroll
+            for (int e = 0; e < 8; e++) s[e] += bf2f(wk[e * ENC_CK + k]) * x[rb + k][e];
+        }
+        float o[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            uint16_t hh, ll;
-            split_bf16(o[e], hh, ll);
-            h8[e] = hh; l8[e] = ll;
+            const float v = (s[e] - bf2f(m8[e])) / sqrtf(bf2f(v8[e]) + 1e-5f) * bf2f(w8[e]) + bf2f(bb8[e]);
+            o[e] = v * sigmoid_hw(v);
         }
-        *reinterpret_cast<u16x8 *>(out_hi + oi) = h8;
-        *reinterpret_cast<u16x8 *>(out_lo + oi) = l8;
-    } else {
-        float4 *y = reinterpret_cast<float4 *>(out + oi);
-        y[0] = make_float4(o[0], o[1], o[2], o[3]);
-        y[1] = make_float4(o[4], o[5], o[6], o[7]);
+        const long oi = (long)r * ENC_D + c0;
+        if (out_hi) {
+            u16x8 h8, l8;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                uint16_t hh, ll;
+                split_bf16(o[e], hh, ll);
+                h8[e] = hh; l8[e] = ll;
+            }
+            *reinterpret_cast<u16x8 *>(out_hi + oi) = h8;
+            *reinterpret_cast<u16x8 *>(out_lo + oi) = l8;
+        } else {
+            float4 *y = reinterpret_cast<float4 *>(out + oi);
+            y[0] = make_float4(o[0], o[1], o[2], o[3]);
+            y[1] = make_float4(o[4], o[5], o[6], o[7]);
+        }
     }
 }
 
@@ -536,7 +562,7 @@ extern "C" void ctk_dwconv_bn_silu(float *out, const float *in, int T, const uin
                                    const uint16_t *bnm, const uint16_t *bnv, hipStream_t s) {
     if (T <= 0) return;
     dw_check(out, nullptr, in, dww, dwb, bnw, bnb, bnm, bnv);
-    hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)T * (ENC_D / 8))), dim3(256), 0, s,
+    hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)((T + DW_RB - 1) / DW_RB) * (ENC_D / 8))), dim3(256), 0, s,
                        out, nullptr, nullptr, in, T, nullptr, nullptr, dww, dwb, bnw, bnb, bnm, bnv);
 }
 
@@ -548,7 +574,7 @@ extern "C" void ctk_dwconv_bn_silu_packed(uint16_t *out_hi, uint16_t *out_lo, co
     if (M <= 0) return;
     dw_check(nullptr, out_hi, in, dww, dwb, bnw, bnb, bnm, bnv);
     if ((uintptr_t)out_lo & 15) { fprintf(stderr, "dwconv: outputs must be 16-byte aligned\n"); exit(1); }
-    hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)M * (ENC_D / 8))), dim3(256), 0, s,
+    hipLaunchKernelGGL(dwconv_bn_silu_kernel, dim3(nblk((long)((M + DW_RB - 1) / DW_RB) * (ENC_D / 8))), dim3(256), 0, s,
                        nullptr, out_hi, out_lo, in, M, row_start, row_len, dww, dwb, bnw, bnb, bnm, bnv);
 }
 
