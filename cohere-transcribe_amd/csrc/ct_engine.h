@@ -61,7 +61,8 @@ typedef struct {
     int  *fq;
     /* q[0] next successor to admit, q[1] successors written, q[2] requests
      * finished, q[3] prompt tokens not yet fed after the last step, q[4] next
-     * fresh request to admit, q[5] fresh requests published */
+     * fresh request to admit, q[5] fresh requests published, q[6] rows the
+     * current step uses (the slots' rows plus the spare rows dealt out) */
     int  *q;
 } CtEngDev;
 

@@ -100,9 +100,14 @@ typedef struct {
     long hstride;
     int kv_bf16;
     int wtile;                /* 1: W in the tile layout of ctk_tile_w                 */
+    const int *m_active;      /* device int or NULL: rows at or past *m_active are
+                                 unused this launch (workgroups of only such rows
+                                 exit, their row blocks are not computed)           */
 } CtGemv;
 /* Requires N % 16 == 0 (N % 64 == 0 when N >= 8192), K % (256 * steps) == 0. */
 void ctk_gemv(const CtGemv *g, hipStream_t s);
+/* sizeof(CtGemv), for callers that mirror the struct (ctypes). */
+int ctk_gemv_sizeof(void);
 /* Tile layout of a decode-GEMM weight W[N][K] (N % 16 == 0, K % 32 == 0):
  * one 1024-entry tile per (16 output rows, K-step of 32), tiles ordered
  * row block major; lane l of a tile holds W[16*rb + (l & 15)][32*st +

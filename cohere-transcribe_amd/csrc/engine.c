@@ -68,8 +68,6 @@ struct HipbEngine {
     int fq_count;
     int proc_batch;            /* encoder batch frames of hipb_process */
     atomic_int enc_done;       /* the encoder thread has published every batch */
-    long stepped;              /* steps launched since creation or reset */
-    int prefill_min;           /* unfed prompt tokens that select the wide step */
     uint16_t *lnf, *attf, *midf;
     /* encoder workspace (lazy) */
     int enc_cap;               /* frames */
@@ -318,9 +316,6 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->req = calloc(R, sizeof(HostReq));
     const char *eg = getenv("HIPB_EAGER");
     e->eager = eg && eg[0] == '1';
-    const char *pm = getenv("HIPB_PREFILL_MIN");
-    e->prefill_min = pm ? atoi(pm) : 1;
-    if (e->prefill_min < 1) e->prefill_min = 1;
     mel_tables_init(e);
     ECHK(hipHostMalloc((void **)&e->h_tmp, (size_t)(R + 8) * (MAX_SEQ + 8) * sizeof(int), 0));
     ECHK(hipHostMalloc((void **)&e->h_meta, (size_t)R * (5 + CT_PROMPT_MAX) * sizeof(int), 0));
@@ -371,7 +366,6 @@ void hipb_reset(HipbEngine *e) {
     e->pool_frames = 0;
     e->fq_count = 0;
     e->bench_mode = 0;
-    e->stepped = 0;
     ECHK(hipMemsetAsync(e->d.slot_req, 0xff, e->d.slots * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.slot_S, 0, e->d.slots * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.req_ngen, 0, e->d.max_req * sizeof(int), e->s));
@@ -923,6 +917,7 @@ static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint1
     memset(&g, 0, sizeof g);
     g.A = A; g.W = Wd; g.bias = bd; g.wtile = CT_ENG_WTILE;
     g.M = e->M; g.N = N; g.K = K;
+    g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
     g.out = out; g.relu = relu;
     g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, K) : 1;
     g.Y = out == CT_GV_PARTIAL ? e->parts : Y;
@@ -956,6 +951,7 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         g.W = WT(e->wt_qkv[l], e->wqkv + (size_t)3 * l * DEC_D * DEC_D); g.wtile = CT_ENG_WTILE;
         g.bias = e->bqkv + (size_t)3 * l * DEC_D;
         g.M = B; g.N = 3 * DEC_D; g.K = DEC_D; g.ksplit = 1; g.out = CT_GV_QKV;
+        g.m_active = B > e->d.slots ? e->d.q + 6 : NULL;
         g.Y = e->q; g.ldy = DEC_D;
         g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)e->d.kv_rows * DEC_DK;
         g.kv_bf16 = e->esz == 2;
@@ -984,21 +980,16 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
 
 static void step_launch(HipbEngine *e, int wide) { step_kernels(e, 1, wide); }
 
-/* The wide step while prompt tokens wait to be fed, or before the first
- * step while requests wait for admission. */
-static int want_wide(const HipbEngine *e, const int *q) {
-    return e->d.rows > e->d.slots &&
-           (q[3] >= e->prefill_min || (e->stepped == 0 && (q[1] > q[0] || q[5] > q[4])));
-}
+/* With spare prompt rows every step is the wide one: a request admitted by
+ * any step has its prompt fed at once, and while no spare row is in use the
+ * GEMM workgroups past the slots' rows exit at once (q[6]). */
+static int want_wide(const HipbEngine *e) { return e->d.rows > e->d.slots; }
 
 static void read_queue(HipbEngine *e, int *q);
 
 void hipb_step(HipbEngine *e) {
     flush_meta(e);
-    int q[8];
-    read_queue(e, q);
-    step_launch(e, want_wide(e, q));
-    e->stepped++;
+    step_launch(e, want_wide(e));
 }
 
 void hipb_attention_only(HipbEngine *e) {
@@ -1056,10 +1047,10 @@ long hipb_run(HipbEngine *e, int chunk) {
         read_queue(e, q);
         if (q[2] >= e->n_enc) break;
         if (steps > bound) CT_FATAL("hipb_run: requests did not finish within the step bound");
-        const int wide = want_wide(e, q);
+        const int wide = want_wide(e);
         for (int i = 0; i < chunk; i++) launch_step(e, wide);
         steps += chunk;
-        e->stepped += chunk;
+
     }
     return steps;
 }
@@ -1130,10 +1121,10 @@ long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
             continue;
         }
         if (steps > bound) CT_FATAL("hipb_process: requests did not finish within the step bound");
-        const int wide = want_wide(e, q);
+        const int wide = want_wide(e);
         for (int i = 0; i < chunk; i++) launch_step(e, wide);
         steps += chunk;
-        e->stepped += chunk;
+
     }
     pthread_join(th, NULL);
     e->enc_s = e->s;

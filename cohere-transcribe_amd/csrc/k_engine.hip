@@ -133,7 +133,10 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     for (int o = 32; o > 0; o >>= 1) left += __shfl_xor(left, o, 64);
     if ((tid & 63) == 0) s_left[tid >> 6] = left;
     __syncthreads();
-    if (tid == 0) d.q[3] = s_left[0] + s_left[1] + s_left[2] + s_left[3];
+    if (tid == 0) {
+        d.q[3] = s_left[0] + s_left[1] + s_left[2] + s_left[3];
+        d.q[6] = d.slots + min(wanted, extra);
+    }
 }
 
 __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {

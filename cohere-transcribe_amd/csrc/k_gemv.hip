@@ -31,7 +31,13 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
     const int c0 = blockIdx.x * 16 * CB, ks = blockIdx.y, z = blockIdx.z, m0 = z * 64;
     const int nsteps = g.K >> 5;
     const int s0 = ks * (GV_WAVES * SPW);
-    const int nrb = min(4, (g.M - m0 + 15) >> 4);
+    int nrb = min(4, (g.M - m0 + 15) >> 4);
+    if (g.m_active && m0 > 0) {
+        // rows past the first block may be unused spare rows this step
+        const int ma = *g.m_active;
+        if (m0 >= ma) return;
+        nrb = min(nrb, (ma - m0 + 15) >> 4);
+    }
     const uint16_t *ablk = g.A + ((long)z * nsteps << 12);
     u16x8 ah[SPW][4], al[SPW][4], wv[SPW][CB];
 #pragma unroll
@@ -156,6 +162,8 @@ extern "C" void ctk_tile_w(const uint16_t *W, uint16_t *Wt, int N, int K, hipStr
     const long pieces = (long)N * K / 8;
     hipLaunchKernelGGL(tile_w_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, W, Wt, N, K);
 }
+
+extern "C" int ctk_gemv_sizeof(void) { return (int)sizeof(CtGemv); }
 
 extern "C" int ctk_gemv_ksplit(int N, int K) {
     if (N <= DEC_D && K == DEC_D) return 4;       // 256-column slices, one K-step per wave

@@ -1,0 +1,16 @@
+"""ctypes mirrors of the C structs the tests pass to libct_hip.so's kernel
+entry points (cohere-transcribe_amd/csrc/ct_launch.h).  The library reports
+each struct's size (ctk_gemv_sizeof), and tests/test_abi_exports.py checks
+the mirror against it on the CPU, so a field added on one side only fails
+there before any kernel reads past a mirror."""
+import ctypes as C
+
+
+class CtGemv(C.Structure):
+    _fields_ = [("A", C.c_void_p), ("W", C.c_void_p), ("bias", C.c_void_p),
+                ("M", C.c_int), ("N", C.c_int), ("K", C.c_int), ("ksplit", C.c_int),
+                ("out", C.c_int), ("relu", C.c_int),
+                ("Y", C.c_void_p), ("ldy", C.c_long), ("F", C.c_void_p),
+                ("kc", C.c_void_p), ("vc", C.c_void_p), ("rowoff", C.c_void_p),
+                ("hstride", C.c_long), ("kv_bf16", C.c_int), ("wtile", C.c_int),
+                ("m_active", C.c_void_p)]

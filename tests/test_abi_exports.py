@@ -46,3 +46,11 @@ def test_product_does_not_link_the_oracle():
     assert "orc_" not in syms
     deps = subprocess.run(["ldd", cb.HIP_LIB], capture_output=True, text=True).stdout
     assert "oracle" not in deps and "ref_cpu" not in deps
+
+
+def test_kernel_struct_mirrors_match():
+    """The tests' ctypes mirror of CtGemv has the C struct's size."""
+    from structs import CtGemv
+    lib = C.CDLL(cb.HIP_LIB)
+    lib.ctk_gemv_sizeof.restype = C.c_int
+    assert C.sizeof(CtGemv) == lib.ctk_gemv_sizeof()

@@ -14,6 +14,7 @@ import pytest
 
 import ctbind as cb
 import kernel_suite as ks
+from structs import CtGemv
 
 pytestmark = pytest.mark.gpu
 
@@ -21,13 +22,6 @@ PARTIAL, DENSE, FRAG, QKV = 0, 1, 2, 3
 TOL = 1e-5
 
 
-class CtGemv(C.Structure):
-    _fields_ = [("A", C.c_void_p), ("W", C.c_void_p), ("bias", C.c_void_p),
-                ("M", C.c_int), ("N", C.c_int), ("K", C.c_int), ("ksplit", C.c_int),
-                ("out", C.c_int), ("relu", C.c_int),
-                ("Y", C.c_void_p), ("ldy", C.c_long), ("F", C.c_void_p),
-                ("kc", C.c_void_p), ("vc", C.c_void_p), ("rowoff", C.c_void_p),
-                ("hstride", C.c_long), ("kv_bf16", C.c_int), ("wtile", C.c_int)]
 
 
 def frag_index(M, K):
@@ -79,6 +73,9 @@ def split(x):
 @pytest.fixture(scope="module")
 def lib(hip):
     L = C.CDLL(cb.HIP_LIB)
+    L.ctk_gemv_sizeof.restype = C.c_int
+    # the mirror must match the C struct before any kernel reads it
+    assert C.sizeof(CtGemv) == L.ctk_gemv_sizeof()
     L.ctk_gemv.argtypes = [C.POINTER(CtGemv), C.c_void_p]
     L.ctk_gemv_ksplit.argtypes = [C.c_int, C.c_int]
     L.ctk_gemv_ksplit.restype = C.c_int
@@ -183,21 +180,24 @@ def test_gemv_matches_float64(lib, hip, N, K):
         assert e <= tol, (M, e)
 
 
-@pytest.mark.parametrize("N,K", [(1024, 1024), (1024, 4096), (4096, 1024), (16384, 1024)])
-def test_gemv_rows_independent_of_batch(lib, hip, N, K):
-    """Row r of a 130-row launch equals the same row launched alone, bit for bit."""
+@pytest.mark.parametrize("N,K,rows", [(1024, 1024, 130), (1024, 4096, 130), (4096, 1024, 130),
+                                      (16384, 1024, 130), (3072, 1024, 80), (1024, 4096, 80)])
+def test_gemv_rows_independent_of_batch(lib, hip, N, K, rows):
+    """Row r of a 130-row launch (64-row blocks) or an 80-row launch (one
+    80-row block: a step's slots plus its prompt rows) equals the same row
+    launched alone, bit for bit."""
     dev = Dev(hip)
     rng = np.random.default_rng(7)
     W = f32_to_bf16(rng.standard_normal((N, K)).astype(np.float32) * 0.03)
     b = f32_to_bf16(rng.standard_normal(N).astype(np.float32) * 0.1)
-    A = rng.standard_normal((130, K)).astype(np.float32)
+    A = rng.standard_normal((rows, K)).astype(np.float32)
     ksplit = lib.ctk_gemv_ksplit(N, K)
     out = PARTIAL if ksplit > 1 else DENSE
     pw = dev.put(W)
     pb = dev.put(b) if out == DENSE else None
     full = run_gemv(lib, dev, A, pw, N, pb, out, ksplit=ksplit)
-    for r in (0, 17, 63, 64, 129):
-        print(f"case: gemv row {r} alone N={N} K={K}", flush=True)
+    for r in (0, 17, 63, 64, rows - 1):
+        print(f"case: gemv row {r} of {rows} alone N={N} K={K}", flush=True)
         one = run_gemv(lib, dev, A[r:r + 1], pw, N, pb, out, ksplit=ksplit)
         if out == PARTIAL:
             assert np.array_equal(full[:, r].view(np.uint32), one[:, 0].view(np.uint32))
