@@ -221,17 +221,19 @@ void ctk_sub_dwconv(float *out, const float *in, int H, int Wd,
 void ctk_sub_flatten(float *out, const float *in, int T, hipStream_t s);
 /* The subsampling convolutions over n requests packed along time: request r
  * owns rows off[r] .. off[r + 1] (off: n + 1 ascending device ints from 0) of
- * each stage; rows_out = off[n] of the output stage.  conv0_dw runs the 3x3
- * stride-2 conv (1 -> 256, ReLU) and the first depthwise stage in one pass
- * (rows2 = o2[n] output rows of [.][32][256]); it reads request r's mel
- * (N_MELS x tmel[r], row stride tmel[r]) at mel + moff[r]. */
-void ctk_sub_conv0_dw_packed(float *out, const float *mel, const int *o1, const int *o2,
-                             const int *tmel, const int *moff, int n, int rows2,
+ * each stage; rows2 / rows_out = off[n] of the output stage.  Outputs are
+ * written split hi/lo (bf16 planes) for the pointwise GEMM after each.
+ * conv0_dw runs the 3x3 stride-2 conv (1 -> 256, ReLU) and the first
+ * depthwise stage in one pass ([.][32][256] rows); it reads request r's mel
+ * (N_MELS x tmel[r], row stride tmel[r]) at mel + moff[r].  dw_split is a
+ * depthwise stage over [.][Wd][256] input rows. */
+void ctk_sub_conv0_dw_packed(uint16_t *out_hi, uint16_t *out_lo, const float *mel, const int *o1,
+                             const int *o2, const int *tmel, const int *moff, int n, int rows2,
                              const uint16_t *w0, const uint16_t *b0, const uint16_t *wd,
                              const uint16_t *bd, hipStream_t s);
-void ctk_sub_dwconv_packed(float *out, const float *in, const int *oin, const int *oout, int n,
-                           int rows_out, int Wd, const uint16_t *w, const uint16_t *b,
-                           hipStream_t s);
+void ctk_sub_dw_split_packed(uint16_t *out_hi, uint16_t *out_lo, const float *in, const int *oin,
+                             const int *oout, int n, int rows_out, int Wd, const uint16_t *w,
+                             const uint16_t *b, hipStream_t s);
 /* The same, written as hi/lo bf16 planes (row stride 4096). */
 void ctk_sub_flatten_split(uint16_t *hi, uint16_t *lo, const float *in, int T, hipStream_t s);
 

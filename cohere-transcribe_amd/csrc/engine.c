@@ -691,9 +691,10 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         moff += (size_t)N_MELS * q->T_mel;
     }
     /* subsampling over groups of requests packed along time, each group as
-     * large as the scratch allows: conv0 + depthwise -> rb, pointwise -> ra,
-     * depthwise -> rb, pointwise -> ra (ra and rb each hold the group's
-     * first-stage output, [sum T2][32][256]), then the flattened frames go
+     * large as the scratch allows: conv0 + depthwise -> rb (split), pointwise
+     * -> ra, depthwise -> rb (split), pointwise -> ra (ra and rb each hold the
+     * group's first-stage output, [sum T2][32][256] floats or its two bf16
+     * planes), then the flattened frames go
      * pre-split into the packed rows (the FFN planes are free until layer 0)
      * for one projection GEMM.  The group tables (row offsets of the three
      * stages, mel lengths and offsets) are staged in distinct parts of the
@@ -722,12 +723,13 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         }
         ECHK(hipMemcpyAsync(tab_d, tab_h, (size_t)5 * L * sizeof(int), hipMemcpyHostToDevice, s));
         const int *d1 = tab_d, *d2 = d1 + L, *d3 = d2 + L, *dtm = d3 + L, *dmo = dtm + L;
-        float *ra = e->esub, *rb = e->esub + s2;
-        ctk_sub_conv0_dw_packed(rb, e->emel, d1, d2, dtm, dmo, ng, o2[ng], DW(W->s0w), DW(W->s0b),
+        float *ra = e->esub;
+        uint16_t *rb_h = (uint16_t *)(e->esub + s2), *rb_l = rb_h + s2;
+        ctk_sub_conv0_dw_packed(rb_h, rb_l, e->emel, d1, d2, dtm, dmo, ng, o2[ng], DW(W->s0w), DW(W->s0b),
                                 DW(W->s2w), DW(W->s2b), s);
-        gemm(e, rb, o2[ng] * 32, SUB_CH, W->s3w, W->s3b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
-        ctk_sub_dwconv_packed(rb, ra, d2, d3, ng, o3[ng], 32, DW(W->s5w), DW(W->s5b), s);
-        gemm(e, rb, o3[ng] * 16, SUB_CH, W->s6w, W->s6b, ra, SUB_CH, CT_EPI_RELU, 0, NULL);
+        gemm_sp(e, rb_h, rb_l, o2[ng] * 32, SUB_CH, W->s3w, W->s3b, ra, SUB_CH, CT_EPI_RELU, 0);
+        ctk_sub_dw_split_packed(rb_h, rb_l, ra, d2, d3, ng, o3[ng], 32, DW(W->s5w), DW(W->s5b), s);
+        gemm_sp(e, rb_h, rb_l, o3[ng] * 16, SUB_CH, W->s6w, W->s6b, ra, SUB_CH, CT_EPI_RELU, 0);
         ctk_sub_flatten_split(e->emid_h + (size_t)seq_off[g0] * SUB_CH * 16,
                               e->emid_l + (size_t)seq_off[g0] * SUB_CH * 16, ra, o3[ng], s);
         tab_h += 5 * L;

@@ -353,9 +353,11 @@ __device__ __forceinline__ int packed_owner(const int *off, int n, int tau) {
 // value a depthwise tap needs is recomputed from them (9 products), in the
 // same order and with the same skips as sub_conv0 then sub_dwconv, so the
 // result is bit-identical to running the two stages
-// (backends/cpu/backend.c:201-221).
+// (backends/cpu/backend.c:201-221).  The output is written split hi/lo for
+// the pointwise GEMM that reads it.
 constexpr int C0D_FRAMES = 7;
-__global__ __launch_bounds__(256) void sub_conv0_dw_packed_kernel(float *out, const float *mel,
+__global__ __launch_bounds__(256) void sub_conv0_dw_packed_kernel(uint16_t *out_hi, uint16_t *out_lo,
+                                                                  const float *mel,
                                                                   const int *o1, const int *o2,
                                                                   const int *tmel, const int *moff, int n,
                                                                   const uint16_t *w0, const uint16_t *b0,
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(256) void sub_conv0_dw_packed_kernel(float *out, co
     for (int k = 0; k < 9; k++) { k0[k] = bf2f(w0[c * 9 + k]); kd[k] = bf2f(wd[c * 9 + k]); }
     const float bias0 = bf2f(b0[c]), biasd = bf2f(bd[c]);
     __syncthreads();
-    float *orow = out + (long)tau * 32 * SUB_CH + c;
+    const long orow = (long)tau * 32 * SUB_CH + c;
     for (int ow = 0; ow < 32; ow++) {
         float acc = biasd;
 #pragma unroll
@@ -403,37 +405,51 @@ __global__ __launch_bounds__(256) void sub_conv0_dw_packed_kernel(float *out, co
                 acc += x * kd[kh2 * 3 + kw2];
             }
         }
-        orow[(long)ow * SUB_CH] = acc;
+        uint16_t hh, ll;
+        split_bf16(acc, hh, ll);
+        out_hi[orow + (long)ow * SUB_CH] = hh;
+        out_lo[orow + (long)ow * SUB_CH] = ll;
     }
 }
 
-// sub_dwconv_kernel over several requests: request r's input rows
-// oin[r] .. oin[r + 1] of [sum H][Wd][256], output rows oout[r] .. oout[r+1]
-// of [sum (H+1)/2][(Wd+1)/2][256].
-__global__ void sub_dwconv_packed_kernel(float *out, const float *in, const int *oin, const int *oout,
-                                         int n, int Wd, const uint16_t *w, const uint16_t *b) {
+// sub_dwconv_kernel over several requests, written split hi/lo for the
+// pointwise GEMM: request r's input rows oin[r] .. oin[r + 1] of
+// [sum H][Wd][256], output rows oout[r] .. oout[r + 1] of
+// [sum (H+1)/2][(Wd+1)/2][256].  Workgroup = one output row, thread =
+// channel, looping over the output columns; each sum is the scalar form's
+// (taps in order, skips at the edges).
+__global__ __launch_bounds__(256) void sub_dw_split_packed_kernel(uint16_t *out_hi, uint16_t *out_lo,
+                                                                  const float *in, const int *oin,
+                                                                  const int *oout, int n, int Wd,
+                                                                  const uint16_t *w, const uint16_t *b) {
     const int Wo = (Wd + 1) / 2;
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)oout[n] * Wo * SUB_CH) return;
-    const int c = (int)(i % SUB_CH);
-    const int ow = (int)((i / SUB_CH) % Wo);
-    const int tau = (int)(i / ((long)SUB_CH * Wo));
+    const int tau = blockIdx.x, c = threadIdx.x;
     const int r = packed_owner(oout, n, tau);
     const int oh = tau - oout[r], H = oin[r + 1] - oin[r];
-    const float *x = in + (long)oin[r] * Wd * SUB_CH;
-    float s = bf2f(b[c]);
+    const float *x = in + (long)oin[r] * Wd * SUB_CH + c;
+    float k[9];
 #pragma unroll
-    for (int kh = 0; kh < 3; kh++) {
-        const int ih = oh * 2 - 1 + kh;
-        if (ih < 0 || ih >= H) continue;
+    for (int j = 0; j < 9; j++) k[j] = bf2f(w[c * 9 + j]);
+    const float bias = bf2f(b[c]);
+    for (int ow = 0; ow < Wo; ow++) {
+        float s = bias;
 #pragma unroll
-        for (int kw = 0; kw < 3; kw++) {
-            const int iw = ow * 2 - 1 + kw;
-            if (iw < 0 || iw >= Wd) continue;
-            s += x[((long)ih * Wd + iw) * SUB_CH + c] * bf2f(w[c * 9 + kh * 3 + kw]);
+        for (int kh = 0; kh < 3; kh++) {
+            const int ih = oh * 2 - 1 + kh;
+            if (ih < 0 || ih >= H) continue;
+#pragma unroll
+            for (int kw = 0; kw < 3; kw++) {
+                const int iw = ow * 2 - 1 + kw;
+                if (iw < 0 || iw >= Wd) continue;
+                s += x[((long)ih * Wd + iw) * SUB_CH] * k[kh * 3 + kw];
+            }
         }
+        uint16_t hh, ll;
+        split_bf16(s, hh, ll);
+        const long o = ((long)tau * Wo + ow) * SUB_CH + c;
+        out_hi[o] = hh;
+        out_lo[o] = ll;
     }
-    out[i] = s;
 }
 
 // [T][16][256] -> [T][ch*16 + f] (backends/cpu/backend.c:222-226).
@@ -592,21 +608,22 @@ extern "C" void ctk_sub_dwconv(float *out, const float *in, int H, int Wd,
     hipLaunchKernelGGL(sub_dwconv_kernel, dim3(nblk(n)), dim3(256), 0, s, out, in, H, Wd, w, b);
 }
 
-extern "C" void ctk_sub_conv0_dw_packed(float *out, const float *mel, const int *o1, const int *o2,
+extern "C" void ctk_sub_conv0_dw_packed(uint16_t *out_hi, uint16_t *out_lo, const float *mel, const int *o1,
+                                        const int *o2,
                                         const int *tmel, const int *moff, int n, int rows2,
                                         const uint16_t *w0, const uint16_t *b0, const uint16_t *wd,
                                         const uint16_t *bd, hipStream_t s) {
     if (rows2 <= 0 || n <= 0) return;
-    hipLaunchKernelGGL(sub_conv0_dw_packed_kernel, dim3(rows2), dim3(256), 0, s, out, mel, o1, o2, tmel, moff,
-                       n, w0, b0, wd, bd);
+    hipLaunchKernelGGL(sub_conv0_dw_packed_kernel, dim3(rows2), dim3(256), 0, s, out_hi, out_lo, mel, o1, o2,
+                       tmel, moff, n, w0, b0, wd, bd);
 }
 
-extern "C" void ctk_sub_dwconv_packed(float *out, const float *in, const int *oin, const int *oout, int n,
-                                      int rows_out, int Wd, const uint16_t *w, const uint16_t *b,
-                                      hipStream_t s) {
-    const long cnt = (long)rows_out * ((Wd + 1) / 2) * SUB_CH;
-    if (cnt <= 0 || n <= 0) return;
-    hipLaunchKernelGGL(sub_dwconv_packed_kernel, dim3(nblk(cnt)), dim3(256), 0, s, out, in, oin, oout, n, Wd, w, b);
+extern "C" void ctk_sub_dw_split_packed(uint16_t *out_hi, uint16_t *out_lo, const float *in, const int *oin,
+                                        const int *oout, int n, int rows_out, int Wd, const uint16_t *w,
+                                        const uint16_t *b, hipStream_t s) {
+    if (rows_out <= 0 || n <= 0) return;
+    hipLaunchKernelGGL(sub_dw_split_packed_kernel, dim3(rows_out), dim3(256), 0, s, out_hi, out_lo, in, oin, oout,
+                       n, Wd, w, b);
 }
 
 extern "C" void ctk_sub_flatten_split(uint16_t *hi, uint16_t *lo, const float *in, int T, hipStream_t s) {
