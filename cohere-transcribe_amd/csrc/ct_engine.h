@@ -16,6 +16,13 @@ extern "C" {
 #define CT_CARRY_MAX 64
 #define CT_PROMPT_MAX (CT_PROMPT_SUBMIT_MAX + CT_CARRY_MAX)
 #define CT_ENG_MAX_SLOTS 256  /* slots an engine may have (the ABI's MAX_BATCH) */
+/* Steps of at least this many rows deal their attention items to CUs by
+ * length rank (long with short): with >= 3 items per CU position the balance
+ * outweighs the extra dependent load per workgroup; at 64 slots + 16 prompt
+ * rows it measured even (the 128-slot step: 27.8 -> 24.0 us per launch). */
+#ifndef CT_RANK_MIN_ROWS
+#define CT_RANK_MIN_ROWS 96
+#endif
 #define CT_MAX_KSPLIT 8    /* largest ctk_gemv_ksplit() of a decoder weight */
 /* Spare rows per (slot, head) of the self caches: without them every
  * (slot, head) block starts on the same 256-KB boundary and the workgroups
@@ -41,6 +48,9 @@ typedef struct {
     int  *cross_len;   /* encoder frames of the row's request (0 when idle)    */
     int  *cross_idx;   /* request whose cross K/V the row reads                */
     int  *row_slot;    /* slot whose self cache the row writes and reads       */
+    /* rows of this step by descending self / cross length (ties by row):
+     * the attention launches deal them to CUs so long and short rows pair */
+    int  *rank_self, *rank_cross;
     long *kv_rowoff;   /* element offset of the row's self K/V entry, -1 idle  */
     /* requests */
     int  *req_T, *req_limit, *req_flags, *req_np, *req_ngen;

@@ -163,6 +163,9 @@ typedef struct {
     int   lens_step;
     int   len_const;          /* ... or this when lens == NULL                          */
     const int   *kv_index;    /* optional: item b reads K/V block kv_index[b]          */
+    const int   *rank;        /* optional (T_q == 1): items by descending length; launch
+                                 position p takes item rank[snake(p)], so the items that
+                                 share a CU pair long with short                      */
     int   kv_rows;            /* key rows allocated per item (0: unknown); with at least
                                  one key trip's rows (32) of bf16 the first keys are
                                  read before the length                                */

@@ -236,6 +236,8 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     d->cross_len = dmalloc(NR * sizeof(int));
     d->cross_idx = dmalloc(NR * sizeof(int));
     d->row_slot = dmalloc(NR * sizeof(int));
+    d->rank_self = dmalloc(NR * sizeof(int));
+    d->rank_cross = dmalloc(NR * sizeof(int));
     d->kv_rowoff = dmalloc(NR * sizeof(long));
     d->req_T = dmalloc(R * sizeof(int));
     d->req_limit = dmalloc(R * sizeof(int));
@@ -311,6 +313,15 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     ECHK(hipMemsetAsync(d->cross_len, 0, NR * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->cross_idx, 0, NR * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->row_slot, 0, NR * sizeof(int), e->s));
+    {
+        /* identity until a step ranks the rows */
+        int *ident = malloc((size_t)NR * sizeof(int));
+        if (!ident) CT_FATAL("out of host memory");
+        for (int i = 0; i < NR; i++) ident[i] = i;
+        ECHK(hipMemcpy(d->rank_self, ident, NR * sizeof(int), hipMemcpyHostToDevice));
+        ECHK(hipMemcpy(d->rank_cross, ident, NR * sizeof(int), hipMemcpyHostToDevice));
+        free(ident);
+    }
     ECHK(hipMemsetAsync(d->kv_rowoff, 0xff, NR * sizeof(long), e->s));
     e->M = S;
     e->req = calloc(R, sizeof(HostReq));
@@ -331,7 +342,7 @@ void hipb_destroy(HipbEngine *e) {
     for (int w = 0; w < 2; w++)
         if (e->have_graph[w]) { hipGraphExecDestroy(e->exec[w]); hipGraphDestroy(e->graph[w]); }
     void *ptrs[] = {e->d.slot_req, e->d.slot_S, e->d.act, e->d.tok, e->d.pos_len, e->d.cross_len,
-                    e->d.row_slot,
+                    e->d.row_slot, e->d.rank_self, e->d.rank_cross,
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
                     e->d.req_next, e->d.rq, e->d.pend, e->d.fq,
@@ -859,13 +870,14 @@ void hipb_encode(HipbEngine *e, int max_batch_frames) {
  * layout) for the out-projection.  The query is q (self) or the Q
  * projection's K-slice partials plus bias (cross). */
 static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, long head_stride,
-                 int rows, const int *lens, const int *kv_index, const uint16_t *q_bias) {
+                 int rows, const int *lens, const int *kv_index, const int *rank, const uint16_t *q_bias) {
     CtAttn a;
     memset(&a, 0, sizeof a);
     a.Q = e->q; a.q_sb = DEC_D; a.q_st = DEC_D;
     a.K = K; a.V = V; a.kv_bf16 = e->esz == 2;
     a.kv_sb = item_stride; a.kv_st = DEC_DK; a.kv_sh = head_stride;
     a.lens = lens; a.lens_step = 1; a.kv_index = kv_index; a.kv_rows = rows;
+    a.rank = e->M >= CT_RANK_MIN_ROWS ? rank : NULL;
     a.T_q = 1; a.B = e->M; a.H = DEC_H;
     a.scale = 0.08838834764831845f;   /* 1/sqrt(128) */
     if (q_bias) {
@@ -897,11 +909,11 @@ static void step_attention(HipbEngine *e, int l, int cross) {
         /* row s is slot s's own row: only the spare rows of a wide step
          * need the row -> slot table */
         attn(e, k, v, (long)DEC_H * e->d.kv_rows * DEC_DK, (long)e->d.kv_rows * DEC_DK, e->d.kv_rows,
-             e->d.pos_len, e->M > e->d.slots ? e->d.row_slot : NULL, NULL);
+             e->d.pos_len, e->M > e->d.slots ? e->d.row_slot : NULL, e->d.rank_self, NULL);
     } else {
         cross_kv(e, l, &k, &v);
         attn(e, k, v, (long)DEC_H * e->d.tmax * DEC_DK, (long)e->d.tmax * DEC_DK, e->d.tmax,
-             e->d.cross_len, e->d.cross_idx, DW(e->W.dec[l].ca_qb));
+             e->d.cross_len, e->d.cross_idx, e->d.rank_cross, DW(e->W.dec[l].ca_qb));
     }
 }
 

@@ -97,7 +97,19 @@ __device__ __forceinline__ float group_sum(float v) {
 template <bool BF16, bool VEC, int LPK, bool MASK, int NT, bool EARLY>
 __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
     constexpr int DPL = DEC_DK / LPK, NV = DPL / 8, NG = NT / LPK;
-    const int bq = blockIdx.x, h = blockIdx.y;
+    // heads vary fastest in launch order: workgroup i runs on XCD i % 8, so
+    // an item's 8 heads spread over all XCDs and every CU gets several items
+    // (with items fastest, a CU held 2 heads of one item and the longest
+    // item's CUs set the launch's duration)
+    const int h = blockIdx.x;
+    int bq = blockIdx.y;
+    if (a.rank) {
+        // positions p, p + 32, ... share a CU (32 per XCD); in alternate
+        // blocks of 32 positions the ranks run backwards, so a CU's items
+        // pair long with short
+        const int p = blockIdx.y, blk = p >> 5, o = p & 31, w = min(32, a.B - (blk << 5));
+        bq = a.rank[(blk << 5) + ((blk & 1) ? w - 1 - o : o)];
+    }
     const int b = bq / a.T_q, qi = bq % a.T_q;
     const int tid = threadIdx.x, g = tid / LPK, ls = tid % LPK;
     const long qoff = (long)b * a.q_sb + (long)qi * a.q_st + h * DEC_DK;
@@ -287,13 +299,17 @@ __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
 
 extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
     if (a->B <= 0 || a->T_q <= 0) return;
+    if (a->rank && a->T_q != 1) {
+        fprintf(stderr, "ctk_attn: a rank permutation needs one query per item\n");
+        exit(1);
+    }
     if (a->q_parts && (a->q_nparts < 1 || a->q_nparts > CT_ATTN_QPARTS || a->q_pstride % 4 ||
                        ((uintptr_t)a->q_parts & 15) || (a->q_bias && ((uintptr_t)a->q_bias & 15)) ||
                        a->q_sb % 4 || a->q_st % 4)) {
         fprintf(stderr, "ctk_attn: query partials need 1..4 slices and 16-byte aligned rows\n");
         exit(1);
     }
-    const dim3 grid(a->B * a->T_q, a->H);
+    const dim3 grid(a->H, a->B * a->T_q);
     // 16-byte vector loads need every 8-element K/V segment aligned.
     const long esz = a->kv_bf16 ? 2 : 4, need = 16 / esz;
     const bool vec = ((uintptr_t)a->K % 16 == 0) && ((uintptr_t)a->V % 16 == 0) &&

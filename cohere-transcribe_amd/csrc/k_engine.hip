@@ -54,6 +54,7 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     const int tid = threadIdx.x, s = tid;
     __shared__ int s_req[CT_ENG_MAX_SLOTS], s_pend[CT_ENG_MAX_SLOTS], s_new[CT_ENG_MAX_SLOTS];
     __shared__ int s_wsum[4], s_left[4];
+    __shared__ int s_pl[2 * CT_ENG_MAX_SLOTS], s_cl[2 * CT_ENG_MAX_SLOTS];   // row lengths this step
     int r = -1, S = 0, np = 0, ng = 0, T = 0, pend = -1, q0 = 0, q1 = 0, f0 = 0, f1 = 0;
     if (s < d.slots) {
         r = d.slot_req[s];
@@ -116,18 +117,27 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     int left = 0;
     if (s < d.slots && r >= 0) {
         const int k = 1 + granted;
-        for (int j = 0; j < granted; j++)
+        for (int j = 0; j < granted; j++) {
             set_row(d, d.slots + base + j, s, r, T, d.req_prompt[r * CT_PROMPT_MAX + S + j], S + j);
+            s_pl[d.slots + base + j] = S + j + 1;
+            s_cl[d.slots + base + j] = T;
+        }
         const int p = S + k - 1;
         const int t = p < np ? d.req_prompt[r * CT_PROMPT_MAX + p] : d.req_out[(long)r * d.smax + ng - 1];
         set_row(d, s, s, r, T, t, p);
+        s_pl[s] = p + 1;
+        s_cl[s] = T;
         d.slot_S[s] = S + k;
         left = max(0, np - (S + k));
     } else if (s < d.slots) {
         clear_row(d, s);
+        s_pl[s] = s_cl[s] = 0;
     }
     // spare rows nobody took this step
-    for (int i = min(wanted, extra) + tid; i < extra; i += 256) clear_row(d, d.slots + i);
+    for (int i = min(wanted, extra) + tid; i < extra; i += 256) {
+        clear_row(d, d.slots + i);
+        s_pl[d.slots + i] = s_cl[d.slots + i] = 0;
+    }
     // prompt tokens still to feed, summed over slots
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) left += __shfl_xor(left, o, 64);
@@ -136,6 +146,20 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     if (tid == 0) {
         d.q[3] = s_left[0] + s_left[1] + s_left[2] + s_left[3];
         d.q[6] = d.slots + min(wanted, extra);
+    }
+    // the step's rows by descending self and cross length (ties by row),
+    // for steps large enough that the attention deals its items by them
+    const int B = d.slots + extra;
+    for (int row = tid; B >= CT_RANK_MIN_ROWS && row < B; row += 256) {
+        const int lp = s_pl[row], lc = s_cl[row];
+        int rp = 0, rc = 0;
+        for (int j = 0; j < B; j++) {
+            const int pj = s_pl[j], cj = s_cl[j];
+            rp += (pj > lp) || (pj == lp && j < row);
+            rc += (cj > lc) || (cj == lc && j < row);
+        }
+        d.rank_self[rp] = row;
+        d.rank_cross[rc] = row;
     }
 }
 
