@@ -106,6 +106,30 @@ typedef struct {
 } CtGemv;
 /* Requires N % 16 == 0 (N % 64 == 0 when N >= 8192), K % (256 * steps) == 0. */
 void ctk_gemv(const CtGemv *g, hipStream_t s);
+/* The weight tiles one decode-GEMM launch reads, by workgroup: workgroup i
+ * (of gx * gy, i = column block + gx * K-slice) reads, for each of its cb
+ * column blocks c, the per consecutive 1-KB tiles from tile
+ * ((i % gx) * cb + c) * nsteps + (i / gx) * per of W (tile layout).  Workgroup
+ * i runs on XCD i % 8, like every launch's workgroup i. */
+typedef struct {
+    const uint16_t *W;
+    int gx, gy, cb, per, nsteps;
+} CtWarm;
+/* Fills w for the launch ctk_gemv(g) makes; w->gx = 0 when g's weights are
+ * not in the tile layout. */
+void ctk_gemv_warm(const CtGemv *g, CtWarm *w);
+/* sizeof(CtWarmSet), for callers that mirror the struct (ctypes). */
+int ctk_warmset_sizeof(void);
+/* Read-ahead a launch carries for the next n decode GEMMs: 8 * rows more
+ * workgroups, rows of them on each XCD, read the weight tiles each GEMM
+ * workgroup will read into the L2 of that workgroup's XCD.  sink (>= 1 KB) is
+ * written only if the tiles' XOR equals magic (so the reads stay). */
+typedef struct {
+    CtWarm t[4];
+    int n, rows;
+    unsigned magic;
+    unsigned *sink;
+} CtWarmSet;
 /* sizeof(CtGemv), for callers that mirror the struct (ctypes). */
 int ctk_gemv_sizeof(void);
 /* Tile layout of a decode-GEMM weight W[N][K] (N % 16 == 0, K % 32 == 0):
@@ -123,6 +147,10 @@ int  ctk_gemv_ksplit(int N, int K);
 /* Decoder residual + LayerNorm (D = DEC_D): h[m] += sum_{p<nparts} parts[p][m]
  * + pbias (in that order; skipped when nparts == 0), then frag = LN(h[m]) in
  * frag layout (K = DEC_D). */
+/* ctk_ln_frag plus the read-ahead warm (NULL or warm->n == 0: none). */
+void ctk_ln_frag_warm(float *h, uint16_t *frag, const float *parts, int nparts,
+                      const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,
+                      const CtWarmSet *warm, hipStream_t s);
 void ctk_ln_frag(float *h, uint16_t *frag, const float *parts, int nparts,
                  const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M, hipStream_t s);
 
@@ -181,6 +209,9 @@ typedef struct {
     /* optional: write the output split hi/lo in frag layout (K = H*128),
      * row b*T_q + qi, instead of out */
     uint16_t       *out_frag;
+    /* optional read-ahead of the next decode GEMMs' weights (warm.n > 0,
+     * H % 8 == 0): warm.rows more rows of H workgroups */
+    CtWarmSet       warm;
 } CtAttn;
 /* Head dim fixed at DEC_DK (128). */
 void ctk_attn(const CtAttn *a, hipStream_t s);

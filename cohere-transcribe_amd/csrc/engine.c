@@ -60,6 +60,10 @@ struct HipbEngine {
      * GEMMs' inputs in frag layout; parts K-slice partial sums */
     float *h, *q, *parts, *logits;
     int M;                     /* rows of the step being launched */
+    /* decode GEMMs whose weight tiles the next attention launch reads ahead
+     * into the L2 their workgroups will read from */
+    CtWarmSet warm;
+    unsigned *warm_sink;
     /* encoder side: its stream (the engine stream, or a second stream while
      * hipb_process overlaps encoding with decoding), pinned staging of its
      * own, and the host count of requests published to the fresh queue */
@@ -238,6 +242,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     d->row_slot = dmalloc(NR * sizeof(int));
     d->rank_self = dmalloc(NR * sizeof(int));
     d->rank_cross = dmalloc(NR * sizeof(int));
+    e->warm_sink = dmalloc(1024);
     d->kv_rowoff = dmalloc(NR * sizeof(long));
     d->req_T = dmalloc(R * sizeof(int));
     d->req_limit = dmalloc(R * sizeof(int));
@@ -342,7 +347,7 @@ void hipb_destroy(HipbEngine *e) {
     for (int w = 0; w < 2; w++)
         if (e->have_graph[w]) { hipGraphExecDestroy(e->exec[w]); hipGraphDestroy(e->graph[w]); }
     void *ptrs[] = {e->d.slot_req, e->d.slot_S, e->d.act, e->d.tok, e->d.pos_len, e->d.cross_len,
-                    e->d.row_slot, e->d.rank_self, e->d.rank_cross,
+                    e->d.row_slot, e->d.rank_self, e->d.rank_cross, e->warm_sink,
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
                     e->d.req_next, e->d.rq, e->d.pend, e->d.fq,
@@ -869,6 +874,53 @@ void hipb_encode(HipbEngine *e, int max_batch_frames) {
 /* Decode attention of every slot; the output goes split into attf (frag
  * layout) for the out-projection.  The query is q (self) or the Q
  * projection's K-slice partials plus bias (cross). */
+/* Decode GEMMs read the tiled weight copies (one contiguous 1 KB per
+ * wavefront load); CT_ENG_WTILE=0 builds the row-major reads instead. */
+#ifndef CT_ENG_WTILE
+#define CT_ENG_WTILE 1
+#endif
+#define WT(tiled, rowmajor) (CT_ENG_WTILE ? (tiled) : (rowmajor))
+
+/* Launches that read the next decode GEMMs' weight tiles ahead into the L2
+ * their workgroups read from (CT_WARM_ROWS read-ahead workgroups per XCD):
+ * the LayerNorm before each layer's QKV projection reads that projection's;
+ * the self attention the out- and cross-query projections'; the cross
+ * attention the FFN's.  CT_WARM=0 turns it off. */
+#ifndef CT_WARM
+#define CT_WARM 1
+#endif
+#ifndef CT_WARM_ROWS
+#define CT_WARM_ROWS 32
+#endif
+/* Queues the weight tiles of the launch gv() makes for (Wd, N, K, out) for
+ * the next attention or LayerNorm launch to read ahead. */
+static void warm_add(HipbEngine *e, const uint16_t *Wd, int N, int K, int out) {
+    if (e->warm.n >= 4) return;
+    CtGemv g;
+    memset(&g, 0, sizeof g);
+    g.W = Wd; g.wtile = CT_ENG_WTILE; g.N = N; g.K = K;
+    g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, K) : 1;
+    ctk_gemv_warm(&g, &e->warm.t[e->warm.n++]);
+}
+
+/* Hands the queued read-ahead to a launch and clears the queue. */
+static void warm_take(HipbEngine *e, CtWarmSet *ws) {
+    memset(ws, 0, sizeof *ws);
+    if (!e->warm.n) return;
+    *ws = e->warm;
+    ws->rows = CT_WARM_ROWS;
+    ws->magic = 0x5bd1e995u;
+    ws->sink = e->warm_sink;
+    e->warm.n = 0;
+}
+
+/* Residual LayerNorm into frag, carrying the queued read-ahead. */
+static void ln_frag(HipbEngine *e, int np, const uint16_t *pb, const uint16_t *w, const uint16_t *b) {
+    CtWarmSet ws;
+    warm_take(e, &ws);
+    ctk_ln_frag_warm(e->h, e->lnf, e->parts, np, pb, w, b, e->M, &ws, e->s);
+}
+
 static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, long head_stride,
                  int rows, const int *lens, const int *kv_index, const int *rank, const uint16_t *q_bias) {
     CtAttn a;
@@ -887,6 +939,7 @@ static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, 
         a.q_bias = q_bias;
     }
     a.out_frag = e->attf;
+    warm_take(e, &a.warm);
     ctk_attn(&a, e->s);
 }
 
@@ -918,12 +971,6 @@ static void step_attention(HipbEngine *e, int l, int cross) {
 }
 
 /* Decode GEMM over all slots; CT_GV_PARTIAL outputs go to parts. */
-/* Decode GEMMs read the tiled weight copies (one contiguous 1 KB per
- * wavefront load); CT_ENG_WTILE=0 builds the row-major reads instead. */
-#ifndef CT_ENG_WTILE
-#define CT_ENG_WTILE 1
-#endif
-#define WT(tiled, rowmajor) (CT_ENG_WTILE ? (tiled) : (rowmajor))
 
 static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint16_t *bd, int N, int K,
                int out, int relu, float *Y, long ldy, uint16_t *F) {
@@ -958,11 +1005,16 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         const DLayer *L = &W->dec[l];
         void *ks, *vs;
         self_kv(e, l, &ks, &vs);
-        if (full) ctk_ln_frag(e->h, e->lnf, e->parts, np, pb, DW(L->sa_lnw), DW(L->sa_lnb), B, s);
+        const uint16_t *w_qkv = WT(e->wt_qkv[l], e->wqkv + (size_t)3 * l * DEC_D * DEC_D);
+        const uint16_t *w_o = WT(e->wt_o[l], DW(L->sa_ow)), *w_cq = WT(e->wt_cq[l], DW(L->ca_qw));
+        const uint16_t *w_co = WT(e->wt_co[l], DW(L->ca_ow)), *w_f1 = WT(e->wt_f1[l], DW(L->ffn_w1));
+        const uint16_t *w_f2 = WT(e->wt_f2[l], DW(L->ffn_w2));
+        if (full && CT_WARM) warm_add(e, w_qkv, 3 * DEC_D, DEC_D, CT_GV_QKV);
+        if (full) ln_frag(e, np, pb, DW(L->sa_lnw), DW(L->sa_lnb));
         CtGemv g;
         memset(&g, 0, sizeof g);
         g.A = e->lnf;
-        g.W = WT(e->wt_qkv[l], e->wqkv + (size_t)3 * l * DEC_D * DEC_D); g.wtile = CT_ENG_WTILE;
+        g.W = w_qkv; g.wtile = CT_ENG_WTILE;
         g.bias = e->bqkv + (size_t)3 * l * DEC_D;
         g.M = B; g.N = 3 * DEC_D; g.K = DEC_D; g.ksplit = 1; g.out = CT_GV_QKV;
         g.m_active = B > e->d.slots ? e->d.q + 6 : NULL;
@@ -970,21 +1022,25 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)e->d.kv_rows * DEC_DK;
         g.kv_bf16 = e->esz == 2;
         ctk_gemv(&g, s);
+        if (full && CT_WARM) warm_add(e, w_o, DEC_D, DEC_D, CT_GV_PARTIAL);
+        if (full && CT_WARM) warm_add(e, w_cq, DEC_D, DEC_D, CT_GV_PARTIAL);
         if (full) step_attention(e, l, 0);
-        gv(e, e->attf, WT(e->wt_o[l], DW(L->sa_ow)), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        gv(e, e->attf, w_o, NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
 
-        if (full) ctk_ln_frag(e->h, e->lnf, e->parts, ks_o, DW(L->sa_ob), DW(L->ca_lnw), DW(L->ca_lnb), B, s);
-        gv(e, e->lnf, WT(e->wt_cq[l], DW(L->ca_qw)), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        if (full) ln_frag(e, ks_o, DW(L->sa_ob), DW(L->ca_lnw), DW(L->ca_lnb));
+        gv(e, e->lnf, w_cq, NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        if (full && CT_WARM) warm_add(e, w_f1, DEC_FF, DEC_D, CT_GV_FRAG);
+        if (full && CT_WARM) warm_add(e, w_f2, DEC_D, DEC_FF, CT_GV_PARTIAL);
         if (full) step_attention(e, l, 1);
-        gv(e, e->attf, WT(e->wt_co[l], DW(L->ca_ow)), NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        gv(e, e->attf, w_co, NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
 
-        if (full) ctk_ln_frag(e->h, e->lnf, e->parts, ks_o, DW(L->ca_ob), DW(L->ffn_lnw), DW(L->ffn_lnb), B, s);
-        gv(e, e->lnf, WT(e->wt_f1[l], DW(L->ffn_w1)), DW(L->ffn_b1), DEC_FF, DEC_D, CT_GV_FRAG, 1, NULL, 0, e->midf);
-        gv(e, e->midf, WT(e->wt_f2[l], DW(L->ffn_w2)), NULL, DEC_D, DEC_FF, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        if (full) ln_frag(e, ks_o, DW(L->ca_ob), DW(L->ffn_lnw), DW(L->ffn_lnb));
+        gv(e, e->lnf, w_f1, DW(L->ffn_b1), DEC_FF, DEC_D, CT_GV_FRAG, 1, NULL, 0, e->midf);
+        gv(e, e->midf, w_f2, NULL, DEC_D, DEC_FF, CT_GV_PARTIAL, 0, NULL, 0, NULL);
         np = ks_ff;
         pb = DW(L->ffn_b2);
     }
-    if (full) ctk_ln_frag(e->h, e->lnf, e->parts, np, pb, DW(W->dlnw), DW(W->dlnb), B, s);
+    if (full) ln_frag(e, np, pb, DW(W->dlnw), DW(W->dlnb));
     /* logits only for the slots' own rows */
     e->M = e->d.slots;
     gv(e, e->lnf, WT(e->wt_lm, DW(W->etw)), DW(W->hdb), VOCAB, DEC_D, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);

@@ -18,6 +18,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include "ct_launch.h"
+#include "ct_warm.h"
 #include "../../include/model_types.h"
 
 namespace {
@@ -97,6 +98,11 @@ __device__ __forceinline__ float group_sum(float v) {
 template <bool BF16, bool VEC, int LPK, bool MASK, int NT, bool EARLY>
 __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
     constexpr int DPL = DEC_DK / LPK, NV = DPL / 8, NG = NT / LPK;
+    if ((int)blockIdx.y >= a.B * a.T_q) {
+        // read-ahead rows: launch position h + H * row runs on XCD h (H % 8 == 0)
+        ct_warm_tiles<NT>(a.warm, blockIdx.x, blockIdx.y - a.B * a.T_q);
+        return;
+    }
     // heads vary fastest in launch order: workgroup i runs on XCD i % 8, so
     // an item's 8 heads spread over all XCDs and every CU gets several items
     // (with items fastest, a CU held 2 heads of one item and the longest
@@ -309,7 +315,12 @@ extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
         fprintf(stderr, "ctk_attn: query partials need 1..4 slices and 16-byte aligned rows\n");
         exit(1);
     }
-    const dim3 grid(a->H, a->B * a->T_q);
+    const int wrows = ct_warm_rows(&a->warm, "ctk_attn");
+    if (wrows && (a->H != 8)) {
+        fprintf(stderr, "ctk_attn: read-ahead rows need H == 8 (one workgroup per XCD)\n");
+        exit(1);
+    }
+    const dim3 grid(a->H, a->B * a->T_q + wrows);
     // 16-byte vector loads need every 8-element K/V segment aligned.
     const long esz = a->kv_bf16 ? 2 : 4, need = 16 / esz;
     const bool vec = ((uintptr_t)a->K % 16 == 0) && ((uintptr_t)a->V % 16 == 0) &&

@@ -164,11 +164,24 @@ extern "C" void ctk_tile_w(const uint16_t *W, uint16_t *Wt, int N, int K, hipStr
 }
 
 extern "C" int ctk_gemv_sizeof(void) { return (int)sizeof(CtGemv); }
+extern "C" int ctk_warmset_sizeof(void) { return (int)sizeof(CtWarmSet); }
 
 extern "C" int ctk_gemv_ksplit(int N, int K) {
     if (N <= DEC_D && K == DEC_D) return 4;       // 256-column slices, one K-step per wave
     if (N <= DEC_D && K == DEC_FF) return 8;      // 512-column slices
     return 1;
+}
+
+// columns per workgroup: 64 for the LM head; 32 for the long-K projection
+// (its 512-column K-slices leave 256 workgroups); else 16
+static int gv_cb(int N, int K) { return (N >= 8192 && N % 64 == 0) ? 4 : (K >= 4096 && N % 32 == 0) ? 2 : 1; }
+
+extern "C" void ctk_gemv_warm(const CtGemv *g, CtWarm *w) {
+    const int ksplit = g->ksplit < 1 ? 1 : g->ksplit, cb = gv_cb(g->N, g->K);
+    w->W = g->W;
+    w->gx = g->wtile ? g->N / (16 * cb) : 0;
+    w->gy = ksplit; w->cb = cb;
+    w->per = g->K / ksplit / 32; w->nsteps = g->K / 32;
 }
 
 extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
@@ -181,9 +194,7 @@ extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
         (g->out == CT_GV_FRAG && ((uintptr_t)g->F & 15)))
         gv_fatal("operands must be 16-byte aligned", g);
     const int spw = g->K / ksplit / 256;
-    // columns per workgroup: 64 for the LM head; 32 for the long-K
-    // projection (its 512-column K-slices leave 256 workgroups); else 16
-    const int cb = (g->N >= 8192 && g->N % 64 == 0) ? 4 : (g->K >= 4096 && g->N % 32 == 0) ? 2 : 1;
+    const int cb = gv_cb(g->N, g->K);
     const dim3 grid(g->N / (16 * cb), ksplit, (g->M + 63) / 64);
     const dim3 block(64 * GV_WAVES);
 #define GV_CASE(CB, SPW)                                                          \

@@ -7,6 +7,8 @@
 #include <limits.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
+#include "ct_warm.h"
 
 namespace {
 
@@ -259,8 +261,14 @@ __global__ void inc_kernel(int *p) {
 template <int NP>
 __global__ __launch_bounds__(256) void ln_frag_kernel(float *h, uint16_t *frag, const float *parts,
                                                       long pstride, const uint16_t *pbias,
-                                                      const uint16_t *w, const uint16_t *b) {
+                                                      const uint16_t *w, const uint16_t *b, int M,
+                                                      CtWarmSet warm) {
     constexpr int D = DEC_D;
+    if ((int)blockIdx.x >= M) {
+        // read-ahead workgroups: launch position q runs on XCD q % 8
+        ct_warm_tiles<256>(warm, blockIdx.x & 7, (blockIdx.x - M) >> 3);
+        return;
+    }
     const int row = blockIdx.x, t = threadIdx.x, wv = t >> 6, lane = t & 63;
     float4 *x = reinterpret_cast<float4 *>(h + (long)row * D);
     const int d0 = 4 * t;
@@ -344,10 +352,14 @@ extern "C" void ctk_layernorm_split(uint16_t *hi, uint16_t *lo, const float *src
         hipLaunchKernelGGL(layernorm_split_kernel<5>, dim3((T + 3) / 4), dim3(256), 0, s, hi, lo, src, w, b, T);
 }
 
-extern "C" void ctk_ln_frag(float *h, uint16_t *frag, const float *parts, int nparts,
-                            const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,
-                            hipStream_t s) {
+extern "C" void ctk_ln_frag_warm(float *h, uint16_t *frag, const float *parts, int nparts,
+                                 const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,
+                                 const CtWarmSet *warm, hipStream_t s) {
     if (M <= 0) return;
+    CtWarmSet ws;
+    memset(&ws, 0, sizeof ws);
+    if (warm) ws = *warm;
+    const int G = M + 8 * ct_warm_rows(&ws, "ctk_ln_frag");
     if ((uintptr_t)h % 16 || (uintptr_t)frag % 16 || (nparts > 0 && (uintptr_t)parts % 16)) {
         fprintf(stderr, "ctk_ln_frag: needs 16-byte aligned buffers\n");
         exit(1);
@@ -358,15 +370,21 @@ extern "C" void ctk_ln_frag(float *h, uint16_t *frag, const float *parts, int np
     }
     const long ps = (long)M * DEC_D;
     switch (nparts) {
-    case 0: hipLaunchKernelGGL(ln_frag_kernel<0>, dim3(M), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b); break;
-    case 1: hipLaunchKernelGGL(ln_frag_kernel<1>, dim3(M), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b); break;
-    case 2: hipLaunchKernelGGL(ln_frag_kernel<2>, dim3(M), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b); break;
-    case 4: hipLaunchKernelGGL(ln_frag_kernel<4>, dim3(M), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b); break;
-    case 8: hipLaunchKernelGGL(ln_frag_kernel<8>, dim3(M), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b); break;
+    case 0: hipLaunchKernelGGL(ln_frag_kernel<0>, dim3(G), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b, M, ws); break;
+    case 1: hipLaunchKernelGGL(ln_frag_kernel<1>, dim3(G), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b, M, ws); break;
+    case 2: hipLaunchKernelGGL(ln_frag_kernel<2>, dim3(G), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b, M, ws); break;
+    case 4: hipLaunchKernelGGL(ln_frag_kernel<4>, dim3(G), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b, M, ws); break;
+    case 8: hipLaunchKernelGGL(ln_frag_kernel<8>, dim3(G), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b, M, ws); break;
     default:
         fprintf(stderr, "ctk_ln_frag: %d partial slices not supported (0, 1, 2, 4, 8)\n", nparts);
         exit(1);
     }
+}
+
+extern "C" void ctk_ln_frag(float *h, uint16_t *frag, const float *parts, int nparts,
+                            const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,
+                            hipStream_t s) {
+    ctk_ln_frag_warm(h, frag, parts, nparts, pbias, w, b, M, NULL, s);
 }
 
 extern "C" void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, const int *pos_len,

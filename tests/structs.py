@@ -1,6 +1,6 @@
 """ctypes mirrors of the C structs the tests pass to libct_hip.so's kernel
 entry points (cohere-transcribe_amd/csrc/ct_launch.h).  The library reports
-each struct's size (ctk_gemv_sizeof), and tests/test_abi_exports.py checks
+each struct's size (ctk_gemv_sizeof, ctk_warmset_sizeof), and tests/test_abi_exports.py checks
 the mirror against it on the CPU, so a field added on one side only fails
 there before any kernel reads past a mirror."""
 import ctypes as C
@@ -14,3 +14,13 @@ class CtGemv(C.Structure):
                 ("kc", C.c_void_p), ("vc", C.c_void_p), ("rowoff", C.c_void_p),
                 ("hstride", C.c_long), ("kv_bf16", C.c_int), ("wtile", C.c_int),
                 ("m_active", C.c_void_p)]
+
+
+class CtWarm(C.Structure):
+    _fields_ = [("W", C.c_void_p), ("gx", C.c_int), ("gy", C.c_int), ("cb", C.c_int),
+                ("per", C.c_int), ("nsteps", C.c_int)]
+
+
+class CtWarmSet(C.Structure):
+    _fields_ = [("t", CtWarm * 4), ("n", C.c_int), ("rows", C.c_int), ("magic", C.c_uint),
+                ("sink", C.c_void_p)]

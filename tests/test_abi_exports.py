@@ -49,8 +49,10 @@ def test_product_does_not_link_the_oracle():
 
 
 def test_kernel_struct_mirrors_match():
-    """The tests' ctypes mirror of CtGemv has the C struct's size."""
-    from structs import CtGemv
+    """The tests' ctypes mirrors of CtGemv and CtWarmSet have the C structs' sizes."""
+    from structs import CtGemv, CtWarmSet
     lib = C.CDLL(cb.HIP_LIB)
     lib.ctk_gemv_sizeof.restype = C.c_int
+    lib.ctk_warmset_sizeof.restype = C.c_int
     assert C.sizeof(CtGemv) == lib.ctk_gemv_sizeof()
+    assert C.sizeof(CtWarmSet) == lib.ctk_warmset_sizeof()

@@ -14,7 +14,7 @@ import pytest
 
 import ctbind as cb
 import kernel_suite as ks
-from structs import CtGemv
+from structs import CtGemv, CtWarm, CtWarmSet
 
 pytestmark = pytest.mark.gpu
 
@@ -74,8 +74,14 @@ def split(x):
 def lib(hip):
     L = C.CDLL(cb.HIP_LIB)
     L.ctk_gemv_sizeof.restype = C.c_int
-    # the mirror must match the C struct before any kernel reads it
+    L.ctk_warmset_sizeof.restype = C.c_int
+    # the mirrors must match the C structs before any kernel reads them
     assert C.sizeof(CtGemv) == L.ctk_gemv_sizeof()
+    assert C.sizeof(CtWarmSet) == L.ctk_warmset_sizeof()
+    L.ctk_gemv_warm.argtypes = [C.POINTER(CtGemv), C.POINTER(CtWarm)]
+    L.ctk_ln_frag_warm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                   C.c_void_p, C.c_void_p, C.c_int, C.POINTER(CtWarmSet),
+                                   C.c_void_p]
     L.ctk_gemv.argtypes = [C.POINTER(CtGemv), C.c_void_p]
     L.ctk_gemv_ksplit.argtypes = [C.c_int, C.c_int]
     L.ctk_gemv_ksplit.restype = C.c_int
@@ -277,6 +283,48 @@ def test_ln_frag(lib, hip):
         hi, lo = from_frag(dev.get(pf, np.uint16, frag_elems(M, D)), M, D)
         got = bf16_to_f32(hi).astype(np.float64) + bf16_to_f32(lo)
         assert rel(got, ref) <= 1e-5
+
+
+def test_ln_frag_read_ahead_leaves_results(lib, hip):
+    """Read-ahead workgroups appended to the LayerNorm launch (the tiles of a
+    QKV-shaped and an FFN-down-shaped decode GEMM) change nothing it writes:
+    h and the frag output are bit-identical to the plain launch, and the GEMM
+    that follows on those weights gives the same bits as without."""
+    dev = Dev(hip)
+    rng = np.random.default_rng(11)
+    D, M, nparts = 1024, 80, 4
+    h = rng.standard_normal((M, D)).astype(np.float32)
+    parts = rng.standard_normal((nparts, M, D)).astype(np.float32)
+    pb = f32_to_bf16(rng.standard_normal(D).astype(np.float32) * 0.1)
+    w = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32))
+    bb = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
+    pp, ppb, pw, pbb = dev.put(parts), dev.put(pb), dev.put(w), dev.put(bb)
+    shapes = ((3 * D, D, 1), (D, 4 * D, lib.ctk_gemv_ksplit(D, 4 * D)))
+    ws = CtWarmSet()
+    tiled = []
+    for t, (N, K, ksplit) in enumerate(shapes):
+        wt = f32_to_bf16(0.05 * rng.standard_normal((N, K)).astype(np.float32))
+        praw, ptile = dev.put(wt), dev.zeros(N * K * 2)
+        lib.ctk_tile_w(praw, ptile, N, K, None)
+        g = CtGemv(W=ptile, N=N, K=K, ksplit=ksplit, wtile=1)
+        lib.ctk_gemv_warm(C.byref(g), C.byref(ws.t[t]))
+        assert (ws.t[t].gx * ws.t[t].gy, ws.t[t].per * ws.t[t].gy) == (256 if t else 192, K // 32)
+        tiled.append((ptile, N, K))
+    ws.n, ws.rows, ws.magic, ws.sink = 2, 32, 0x5BD1E995, dev.zeros(1024)
+    outs = []
+    for warm in (None, C.byref(ws)):
+        print(f"case: ln_frag M={M} read-ahead={warm is not None}", flush=True)
+        ph, pf = dev.put(h), dev.zeros(frag_elems(M, D) * 2)
+        dev.ev.sync()
+        lib.ctk_ln_frag_warm(ph, pf, pp, nparts, ppb, pw, pbb, M, warm, None)
+        ptile, N, K = tiled[0]
+        py = dev.zeros(M * N * 4)
+        g = CtGemv(A=pf, W=ptile, M=M, N=N, K=K, ksplit=1, out=1, Y=py, ldy=N, wtile=1)
+        lib.ctk_gemv(C.byref(g), None)
+        outs.append((dev.get(ph, np.uint32, M * D), dev.get(pf, np.uint16, frag_elems(M, D)),
+                     dev.get(py, np.uint32, M * N)))
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
 
 
 def wtile_index(N, K):
