@@ -40,6 +40,10 @@ typedef struct {
     /* slot table */
     int  *slot_req;    /* request in the slot, -1 when free                    */
     int  *slot_S;      /* tokens already in the slot's self cache              */
+    /* the slot's request fields, copied at admission so the step kernels
+     * read them beside the slot table: prompt ids, encoder frames, flags,
+     * token limit, tokens generated, and the last token generated */
+    int  *slot_np, *slot_T, *slot_flags, *slot_lim, *slot_ng, *slot_tok;
     /* step rows [rows]: row s < slots is slot s's row, rows past `slots`
      * carry extra prompt tokens of a slot (row_slot) */
     int  *act;         /* 1 if the row decodes this step                       */

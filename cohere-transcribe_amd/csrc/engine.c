@@ -234,6 +234,12 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     d->kv_rows = d->smax + CT_KV_PAD;
     d->slot_req = dmalloc(S * sizeof(int));
     d->slot_S = dmalloc(S * sizeof(int));
+    d->slot_np = dmalloc(S * sizeof(int));
+    d->slot_T = dmalloc(S * sizeof(int));
+    d->slot_flags = dmalloc(S * sizeof(int));
+    d->slot_lim = dmalloc(S * sizeof(int));
+    d->slot_ng = dmalloc(S * sizeof(int));
+    d->slot_tok = dmalloc(S * sizeof(int));
     d->act = dmalloc(NR * sizeof(int));
     d->tok = dmalloc(NR * sizeof(int));
     d->pos_len = dmalloc(NR * sizeof(int));
@@ -346,7 +352,8 @@ void hipb_destroy(HipbEngine *e) {
     ECHK(hipStreamSynchronize(e->s));
     for (int w = 0; w < 2; w++)
         if (e->have_graph[w]) { hipGraphExecDestroy(e->exec[w]); hipGraphDestroy(e->graph[w]); }
-    void *ptrs[] = {e->d.slot_req, e->d.slot_S, e->d.act, e->d.tok, e->d.pos_len, e->d.cross_len,
+    void *ptrs[] = {e->d.slot_req, e->d.slot_S, e->d.slot_np, e->d.slot_T, e->d.slot_flags,
+                    e->d.slot_lim, e->d.slot_ng, e->d.slot_tok, e->d.act, e->d.tok, e->d.pos_len, e->d.cross_len,
                     e->d.row_slot, e->d.rank_self, e->d.rank_cross, e->warm_sink,
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
@@ -1264,6 +1271,13 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
     ECHK(hipMemcpy(e->d.req_ngen, buf, B * sizeof(int), hipMemcpyHostToDevice));
     for (int s = 0; s < B; s++)
         ECHK(hipMemcpy(e->d.req_out + (size_t)s * e->d.smax, &(int){100 + s}, sizeof(int), hipMemcpyHostToDevice));
+    /* the slots' copies of those fields, as admission would have made them */
+    int *const sf[6] = {e->d.slot_np, e->d.slot_T, e->d.slot_flags, e->d.slot_lim, e->d.slot_ng, e->d.slot_tok};
+    for (int f = 0; f < 6; f++) {
+        for (int s = 0; s < B; s++)
+            buf[s] = f == 0 ? 0 : f == 1 ? T_enc[s] : f == 2 ? HIPB_SUPPRESS_EOS : f == 3 ? e->d.smax : f == 4 ? 1 : 100 + s;
+        ECHK(hipMemcpy(sf[f], buf, B * sizeof(int), hipMemcpyHostToDevice));
+    }
     int q[8] = {B, B, 0, 0, 0, 0, 0, 0};
     ECHK(hipMemcpy(e->d.q, q, sizeof q, hipMemcpyHostToDevice));
     const long self_el = (long)DEC_N * B * DEC_H * e->d.kv_rows * DEC_DK;

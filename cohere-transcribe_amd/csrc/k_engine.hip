@@ -47,57 +47,89 @@ __device__ __forceinline__ void clear_row(const CtEngDev &d, int row) {
 // spare rows dealt in slot order; each row is an ordinary decode row at its
 // own position, so a prompt fed k tokens per step gives the same bits as one
 // per step.  q[3] receives the prompt tokens still unfed after this step.
-// Thread s serves slot s (slots <= 256).  Everything a slot that keeps its
-// request needs is loaded in the first phase, beside the slot table and the
-// queue words, so only newly admitted slots wait for a second round.
+// Thread s serves slot s (slots <= 256).  A slot that keeps its request finds
+// everything it needs in the slot table (the request's fields are copied there
+// at admission, the last generated token by eng_end), so a step with no
+// admission and no prompt ids to feed makes one round of loads; newly
+// admitted slots load their request's fields, prompt-feeding slots their ids.
+// Exclusive prefix of v over the workgroup's 256 threads in thread order
+// (one barrier); total receives the sum.  sums: 4 ints of LDS for this call.
+__device__ __forceinline__ int block_prefix(int v, int *sums, int &total) {
+    const int tid = threadIdx.x;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if ((tid & 63) >= o) x += y;
+    }
+    if ((tid & 63) == 63) sums[tid >> 6] = x;
+    __syncthreads();
+    int base = x - v;
+    for (int w = 0; w < (tid >> 6); w++) base += sums[w];
+    total = (sums[0] + sums[1]) + (sums[2] + sums[3]);
+    return base;
+}
+
 __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     const int tid = threadIdx.x, s = tid;
-    __shared__ int s_req[CT_ENG_MAX_SLOTS], s_pend[CT_ENG_MAX_SLOTS], s_new[CT_ENG_MAX_SLOTS];
+    __shared__ int s_app[CT_ENG_MAX_SLOTS], s_q[4], s_asum[4];
     __shared__ int s_wsum[4], s_left[4];
     __shared__ int s_pl[2 * CT_ENG_MAX_SLOTS], s_cl[2 * CT_ENG_MAX_SLOTS];   // row lengths this step
-    int r = -1, S = 0, np = 0, ng = 0, T = 0, pend = -1, q0 = 0, q1 = 0, f0 = 0, f1 = 0;
+    int r = -1, S = 0, np = 0, T = 0, tok = 0, pend = -1, q0 = 0, q1 = 0, f0 = 0, f1 = 0;
     if (s < d.slots) {
         r = d.slot_req[s];
         pend = d.pend[s];
         S = d.slot_S[s];
+        np = d.slot_np[s];
+        T = d.slot_T[s];
+        tok = d.slot_tok[s];
     }
     if (tid == 0) {
         q0 = d.q[0]; q1 = d.q[1]; f0 = d.q[4];
         f1 = __hip_atomic_load(&d.q[5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_q[0] = q0; s_q[1] = q1; s_q[2] = f0; s_q[3] = f1;
     }
-    if (r >= 0) { np = d.req_np[r]; ng = d.req_ngen[r]; T = d.req_T[r]; }
-    if (s < d.slots) {
-        s_req[s] = r;
-        s_pend[s] = pend;
-        s_new[s] = 0;
+    // Released successors join the ring rq in slot order, then the free
+    // slots, in slot order, take the waiting successors (rq[q0..), the ones
+    // joining now last), then fresh requests (fq[q4..q5)): the c-th free slot
+    // takes the c-th of them.  One prefix counts both (pending in the low 16
+    // bits, free in the high).
+    const bool is_p = s < d.slots && pend >= 0, is_f = s < d.slots && r < 0;
+    int tot;
+    const int pre = block_prefix((int)is_p | ((int)is_f << 16), s_asum, tot);
+    const int pidx = pre & 0xffff, fidx = pre >> 16, npend = tot & 0xffff, nfree = tot >> 16;
+    q0 = s_q[0]; q1 = s_q[1]; f0 = s_q[2]; f1 = s_q[3];
+    if (is_p) {
+        d.rq[q1 + pidx] = pend;
+        s_app[pidx] = pend;
     }
     __syncthreads();
-    // released successors join the ring in slot order, then free slots take
-    // waiting successors, then fresh requests, in slot order
-    if (tid == 0) {
-        int nxt = q0, ready = q1, fn = f0;
-        for (int x = 0; x < d.slots; x++)
-            if (s_pend[x] >= 0) d.rq[ready++] = s_pend[x];
-        for (int x = 0; x < d.slots; x++) {
-            if (s_req[x] >= 0) continue;
-            if (nxt < ready) s_req[x] = d.rq[nxt++];
-            else if (fn < f1) s_req[x] = __hip_atomic_load(&d.fq[fn++], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else continue;
-            s_new[x] = 1;
+    const int waiting = q1 - q0, avail = waiting + npend;
+    bool fresh = false;
+    if (is_f) {
+        if (fidx < waiting) { r = d.rq[q0 + fidx]; fresh = true; }
+        else if (fidx < avail) { r = s_app[fidx - waiting]; fresh = true; }
+        else if (fidx - avail < f1 - f0) {
+            r = __hip_atomic_load(&d.fq[f0 + fidx - avail], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            fresh = true;
         }
-        d.q[0] = nxt;
-        d.q[1] = ready;
-        d.q[4] = fn;
     }
-    __syncthreads();
+    if (tid == 0) {
+        const int from_rq = min(nfree, avail);
+        d.q[0] = q0 + from_rq;
+        d.q[1] = q1 + npend;
+        d.q[4] = f0 + min(nfree - from_rq, f1 - f0);
+    }
     int want = 0;
     if (s < d.slots) {
         if (pend >= 0) d.pend[s] = -1;
-        r = s_req[s];
         d.slot_req[s] = r;
-        if (s_new[s]) {
+        if (fresh) {
             S = 0;
-            np = d.req_np[r]; ng = d.req_ngen[r]; T = d.req_T[r];
+            np = d.req_np[r]; T = d.req_T[r];
+            const int fl = d.req_flags[r], lim = d.req_limit[r], ng = d.req_ngen[r];
+            d.slot_np[s] = np; d.slot_T[s] = T;
+            d.slot_flags[s] = fl; d.slot_lim[s] = lim; d.slot_ng[s] = ng;
         }
         if (r >= 0 && S < np) want = min(np - S, 1 + extra) - 1;
     }
@@ -123,7 +155,7 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
             s_cl[d.slots + base + j] = T;
         }
         const int p = S + k - 1;
-        const int t = p < np ? d.req_prompt[r * CT_PROMPT_MAX + p] : d.req_out[(long)r * d.smax + ng - 1];
+        const int t = p < np ? d.req_prompt[r * CT_PROMPT_MAX + p] : tok;
         set_row(d, s, s, r, T, t, p);
         s_pl[s] = p + 1;
         s_cl[s] = T;
@@ -171,19 +203,18 @@ __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
 // sequential scan of backends/cpu/backend.c:446-456), optionally skipping EOS.
 __global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *logits) {
     const int s = blockIdx.x;
-    if (!d.act[s]) return;
-    const int r = d.slot_req[s];
-    const int S = d.slot_S[s];
-    if (S < d.req_np[r]) return;                 // still feeding the prompt
-    const int flags = d.req_flags[r];
-    const int skip = (flags & 1) ? EOS_ID : -1;
+    // one round of loads: the slot's state and its logits row
     const float *x = logits + (long)s * VOCAB;
-    float bv = -INFINITY;
-    int bi = INT_MAX;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     float4 v[VOCAB / 1024];
 #pragma unroll
     for (int k = 0; k < VOCAB / 1024; k++) v[k] = x4[threadIdx.x + 256 * k];
+    const int act = d.act[s], r = d.slot_req[s], S = d.slot_S[s], np = d.slot_np[s];
+    const int flags = d.slot_flags[s], lim = d.slot_lim[s], ng = d.slot_ng[s];
+    if (!act || S < np) return;                  // idle, or still feeding the prompt
+    const int skip = (flags & 1) ? EOS_ID : -1;
+    float bv = -INFINITY;
+    int bi = INT_MAX;
 #pragma unroll
     for (int k = 0; k < VOCAB / 1024; k++) {
         const int i = 4 * (threadIdx.x + 256 * k);
@@ -207,10 +238,11 @@ __global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *l
     for (int k = 1; k < 4; k++) better(bv, bi, sv[k], si[k]);
     const int first = skip == 0 ? 1 : 0;
     int best = (x[first] != x[first] || bi == INT_MAX) ? first : bi;
-    const int ng = d.req_ngen[r], lim = d.req_limit[r];
     if ((flags & 2) && ng == lim - 1) best = EOS_ID;
     d.req_out[(long)r * d.smax + ng] = best;
     d.req_ngen[r] = ng + 1;
+    d.slot_ng[s] = ng + 1;
+    d.slot_tok[s] = best;
     const bool fin = (best == EOS_ID && !(flags & 1)) || ng + 1 >= lim || S >= d.smax;
     if (fin) {
         d.slot_req[s] = -1;
