@@ -147,6 +147,14 @@ int  ctk_gemv_ksplit(int N, int K);
 /* Decoder residual + LayerNorm (D = DEC_D): h[m] += sum_{p<nparts} parts[p][m]
  * + pbias (in that order; skipped when nparts == 0), then frag = LN(h[m]) in
  * frag layout (K = DEC_D). */
+/* The decode step's embedding + first LayerNorm: for active rows r < M,
+ * h[r] = LN_e(etw[tokens[r]] + epw[pos_len[r] - 1]) (as ctk_embed_ln); then
+ * every row's LN(h[r]) with (w, b) into frag (as ctk_ln_frag with no
+ * slices), carrying the read-ahead warm (NULL: none). */
+void ctk_embed_ln_frag(float *h, uint16_t *frag, const int *tokens, const int *pos_len,
+                       const int *active, const uint16_t *etw, const uint16_t *epw,
+                       const uint16_t *elnw, const uint16_t *elnb, const uint16_t *w,
+                       const uint16_t *b, int M, const CtWarmSet *warm, hipStream_t s);
 /* ctk_ln_frag plus the read-ahead warm (NULL or warm->n == 0: none). */
 void ctk_ln_frag_warm(float *h, uint16_t *frag, const float *parts, int nparts,
                       const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,

@@ -1003,8 +1003,6 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
     const int ks_o = ctk_gemv_ksplit(DEC_D, DEC_D), ks_ff = ctk_gemv_ksplit(DEC_D, DEC_FF);
     e->M = B;
     if (full) ctk_eng_begin(&e->d, B - e->d.slots, s);
-    if (full) ctk_embed_ln(e->h, e->d.tok, B, 0, e->d.pos_len, e->d.act, DW(W->etw), DW(W->epw),
-                 DW(W->elnw), DW(W->elnb), s);
     /* each LayerNorm first adds the previous projection's K-slices + bias to h */
     int np = 0;
     const uint16_t *pb = NULL;
@@ -1017,7 +1015,15 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         const uint16_t *w_co = WT(e->wt_co[l], DW(L->ca_ow)), *w_f1 = WT(e->wt_f1[l], DW(L->ffn_w1));
         const uint16_t *w_f2 = WT(e->wt_f2[l], DW(L->ffn_w2));
         if (full && CT_WARM) warm_add(e, w_qkv, 3 * DEC_D, DEC_D, CT_GV_QKV);
-        if (full) ln_frag(e, np, pb, DW(L->sa_lnw), DW(L->sa_lnb));
+        if (full && l == 0) {
+            /* the embedding LayerNorm and this one in one launch */
+            CtWarmSet ws;
+            warm_take(e, &ws);
+            ctk_embed_ln_frag(e->h, e->lnf, e->d.tok, e->d.pos_len, e->d.act, DW(W->etw), DW(W->epw),
+                              DW(W->elnw), DW(W->elnb), DW(L->sa_lnw), DW(L->sa_lnb), B, &ws, s);
+        } else if (full) {
+            ln_frag(e, np, pb, DW(L->sa_lnw), DW(L->sa_lnb));
+        }
         CtGemv g;
         memset(&g, 0, sizeof g);
         g.A = e->lnf;

@@ -237,7 +237,8 @@ __global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *l
     if (threadIdx.x != 0) return;
     for (int k = 1; k < 4; k++) better(bv, bi, sv[k], si[k]);
     const int first = skip == 0 ? 1 : 0;
-    int best = (x[first] != x[first] || bi == INT_MAX) ? first : bi;
+    const float xf = first ? v[0].y : v[0].x;   // thread 0 holds logits 0..3
+    int best = (xf != xf || bi == INT_MAX) ? first : bi;
     if ((flags & 2) && ng == lim - 1) best = EOS_ID;
     d.req_out[(long)r * d.smax + ng] = best;
     d.req_ngen[r] = ng + 1;

@@ -258,43 +258,11 @@ __global__ void inc_kernel(int *p) {
 // variance of the centred values, eps 1e-5), each output split hi/lo and
 // stored where the decode GEMM's lanes read it.  NP (the number of slices)
 // is a template parameter so every load is issued before the first add.
-template <int NP>
-__global__ __launch_bounds__(256) void ln_frag_kernel(float *h, uint16_t *frag, const float *parts,
-                                                      long pstride, const uint16_t *pbias,
-                                                      const uint16_t *w, const uint16_t *b, int M,
-                                                      CtWarmSet warm) {
+// The two-pass LayerNorm of one row held as one float4 per thread (thread t:
+// elements 4t..4t+3; 256 threads), then split hi/lo into frag rows.
+__device__ __forceinline__ void ln_frag_tail(float4 v, ushort4 w4, ushort4 b4, uint16_t *frag, int row) {
     constexpr int D = DEC_D;
-    if ((int)blockIdx.x >= M) {
-        // read-ahead workgroups: launch position q runs on XCD q % 8
-        ct_warm_tiles<256>(warm, blockIdx.x & 7, (blockIdx.x - M) >> 3);
-        return;
-    }
-    const int row = blockIdx.x, t = threadIdx.x, wv = t >> 6, lane = t & 63;
-    float4 *x = reinterpret_cast<float4 *>(h + (long)row * D);
-    const int d0 = 4 * t;
-    // every load first: the row, its partial slices, then the three bf16
-    // vectors (4 entries = 8 bytes each)
-    float4 v = x[t];
-    float4 pr[NP > 0 ? NP : 1];
-#pragma unroll
-    for (int p = 0; p < NP; p++)
-        pr[p] = reinterpret_cast<const float4 *>(parts + p * pstride + (long)row * D)[t];
-    const ushort4 pb4 = (NP > 0 && pbias) ? reinterpret_cast<const ushort4 *>(pbias)[t] : make_ushort4(0, 0, 0, 0);
-    const ushort4 w4 = reinterpret_cast<const ushort4 *>(w)[t];
-    const ushort4 b4 = reinterpret_cast<const ushort4 *>(b)[t];
-    if (NP > 0) {
-        float4 a = pr[0];
-#pragma unroll
-        for (int p = 1; p < NP; p++) {
-            a.x += pr[p].x; a.y += pr[p].y; a.z += pr[p].z; a.w += pr[p].w;
-        }
-        if (pbias) {
-            a.x += bf2f(pb4.x); a.y += bf2f(pb4.y);
-            a.z += bf2f(pb4.z); a.w += bf2f(pb4.w);
-        }
-        v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
-        x[t] = v;
-    }
+    const int t = threadIdx.x, wv = t >> 6, lane = t & 63, d0 = 4 * t;
     __shared__ float red[2][4];
     const float s = wave_sum((v.x + v.y) + (v.z + v.w));
     if (lane == 0) red[0][wv] = s;
@@ -319,6 +287,83 @@ __global__ __launch_bounds__(256) void ln_frag_kernel(float *h, uint16_t *frag, 
     const long off = ct_frag_off(row, d0, D);
     *reinterpret_cast<ushort4 *>(frag + off) = h4;
     *reinterpret_cast<ushort4 *>(frag + off + 512) = l4;
+}
+
+template <int NP>
+__global__ __launch_bounds__(256) void ln_frag_kernel(float *h, uint16_t *frag, const float *parts,
+                                                      long pstride, const uint16_t *pbias,
+                                                      const uint16_t *w, const uint16_t *b, int M,
+                                                      CtWarmSet warm) {
+    constexpr int D = DEC_D;
+    if ((int)blockIdx.x >= M) {
+        // read-ahead workgroups: launch position q runs on XCD q % 8
+        ct_warm_tiles<256>(warm, blockIdx.x & 7, (blockIdx.x - M) >> 3);
+        return;
+    }
+    const int row = blockIdx.x, t = threadIdx.x;
+    float4 *x = reinterpret_cast<float4 *>(h + (long)row * D);
+    // every load first: the row, its partial slices, then the three bf16
+    // vectors (4 entries = 8 bytes each)
+    float4 v = x[t];
+    float4 pr[NP > 0 ? NP : 1];
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+        pr[p] = reinterpret_cast<const float4 *>(parts + p * pstride + (long)row * D)[t];
+    const ushort4 pb4 = (NP > 0 && pbias) ? reinterpret_cast<const ushort4 *>(pbias)[t] : make_ushort4(0, 0, 0, 0);
+    const ushort4 w4 = reinterpret_cast<const ushort4 *>(w)[t];
+    const ushort4 b4 = reinterpret_cast<const ushort4 *>(b)[t];
+    if (NP > 0) {
+        float4 a = pr[0];
+#pragma unroll
+        for (int p = 1; p < NP; p++) {
+            a.x += pr[p].x; a.y += pr[p].y; a.z += pr[p].z; a.w += pr[p].w;
+        }
+        if (pbias) {
+            a.x += bf2f(pb4.x); a.y += bf2f(pb4.y);
+            a.z += bf2f(pb4.z); a.w += bf2f(pb4.w);
+        }
+        v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+        x[t] = v;
+    }
+    ln_frag_tail(v, w4, b4, frag, row);
+}
+
+// The decode step's first two launches in one: row r's embedding LayerNorm
+// (wave 0, the arithmetic of embed_ln_kernel), written to h for active rows,
+// then the first layer's LayerNorm of h into frag (ln_frag_kernel<0>'s
+// arithmetic; inactive rows normalise their stale h, as there).
+__global__ __launch_bounds__(256) void embed_ln_frag_kernel(float *h, uint16_t *frag, const int *tokens,
+                                                            const int *pos_len, const int *active,
+                                                            const uint16_t *etw, const uint16_t *epw,
+                                                            const uint16_t *elnw, const uint16_t *elnb,
+                                                            const uint16_t *w, const uint16_t *b, int M,
+                                                            CtWarmSet warm) {
+    if ((int)blockIdx.x >= M) {
+        ct_warm_tiles<256>(warm, blockIdx.x & 7, (blockIdx.x - M) >> 3);
+        return;
+    }
+    const int row = blockIdx.x, t = threadIdx.x;
+    __shared__ float4 s_h[DEC_D / 4];
+    const ushort4 w4 = reinterpret_cast<const ushort4 *>(w)[t];
+    const ushort4 b4 = reinterpret_cast<const ushort4 *>(b)[t];
+    const bool act = active[row] != 0;
+    float4 *x = reinterpret_cast<float4 *>(h + (long)row * DEC_D);
+    if (!act) {
+        s_h[t] = x[t];
+    } else if (t < 64) {
+        const long tok = tokens[row], pos = (long)pos_len[row] - 1;
+        float v[LN_MAXV];
+#pragma unroll
+        for (int i = 0; i < LN_MAXV; i++) {
+            const int d = t + i * 64;
+            v[i] = d < DEC_D ? bf2f(etw[tok * DEC_D + d]) + bf2f(epw[pos * DEC_D + d]) : 0.0f;
+        }
+        ln_row(v, DEC_D, t, elnw, elnb, reinterpret_cast<float *>(s_h));
+    }
+    __syncthreads();
+    const float4 v = s_h[t];
+    if (act) x[t] = v;
+    ln_frag_tail(v, w4, b4, frag, row);
 }
 
 }  // namespace
@@ -393,6 +438,23 @@ extern "C" void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, 
     if (R <= 0) return;
     hipLaunchKernelGGL(embed_ln_kernel, dim3((R + 3) / 4), dim3(256), 0, s, h, tokens, R, pos_start,
                        pos_len, active, etw, epw, lnw, lnb);
+}
+
+extern "C" void ctk_embed_ln_frag(float *h, uint16_t *frag, const int *tokens, const int *pos_len,
+                                  const int *active, const uint16_t *etw, const uint16_t *epw,
+                                  const uint16_t *elnw, const uint16_t *elnb, const uint16_t *w,
+                                  const uint16_t *b, int M, const CtWarmSet *warm, hipStream_t s) {
+    if (M <= 0) return;
+    if ((uintptr_t)h % 16 || (uintptr_t)frag % 16 || (uintptr_t)w % 8 || (uintptr_t)b % 8) {
+        fprintf(stderr, "ctk_embed_ln_frag: needs 16-byte aligned rows and 8-byte aligned gain/bias\n");
+        exit(1);
+    }
+    CtWarmSet ws;
+    memset(&ws, 0, sizeof ws);
+    if (warm) ws = *warm;
+    const int G = M + 8 * ct_warm_rows(&ws, "ctk_embed_ln_frag");
+    hipLaunchKernelGGL(embed_ln_frag_kernel, dim3(G), dim3(256), 0, s, h, frag, tokens, pos_len, active,
+                       etw, epw, elnw, elnb, w, b, M, ws);
 }
 
 extern "C" void ctk_argmax(int *out, const float *logits, int R, int n, const int *active,
