@@ -88,6 +88,46 @@ def run_stepwise(eng, n_req, max_steps=64):
     return hist
 
 
+def test_engine_admission_order(hip, hot, mels):
+    """Admission follows the policy step by step: before each step the free
+    slots, in slot order, take the waiting requests in submission order; a
+    request then holds its slot for len(prompt) + limit - 1 steps (one prompt
+    id a step, the last one yielding the first token) and frees it after the
+    step that generates its limit-th token.  Checked against a host model of
+    that policy after every step, with more requests than slots."""
+    limits = [3, 7, 2, 5, 4, 1, 6]
+    n, S, npr = len(limits), 3, len(cb.PROMPT)
+    eng = cb.Engine(hot, slots=S, max_requests=n, max_frames=64, kv_bf16=True, prefill_rows=0)
+    try:
+        for i, lim in enumerate(limits):
+            eng.submit(mels[i % len(mels)], lim, FLAGS)
+        eng.encode()
+        slots, left, waiting = [None] * S, {}, list(range(n))
+        for step in range(200):
+            for s in range(S):
+                if slots[s] is None and waiting:
+                    r = waiting.pop(0)
+                    slots[s], left[r] = r, npr + limits[r] - 1
+            for s in range(S):
+                if slots[s] is not None:
+                    left[slots[s]] -= 1
+                    if left[slots[s]] == 0:
+                        slots[s] = None
+            want = {r: s for s, r in enumerate(slots) if r is not None}
+            eng.step()
+            got = {r: eng.slot_of(r) for r in range(n)}
+            print(f"case: step {step} slots {slots}", flush=True)
+            for r in range(n):
+                assert got[r] == want.get(r, -1), (step, r, got[r], want.get(r, -1))
+            if not waiting and all(x is None for x in slots):
+                break
+        assert eng.finished() == n
+        for r, lim in enumerate(limits):
+            assert len(eng.tokens(r)) == lim, r
+    finally:
+        eng.close()
+
+
 def test_engine_batch_vs_single_bitexact(hip, hot, mels):
     packed = cb.Engine(hot, slots=4, max_requests=8, max_frames=64, kv_bf16=True)
     try:
