@@ -35,6 +35,7 @@ extern "C" {
  * request-major arrays `max_req`. */
 typedef struct {
     int slots, max_req, smax, tmax;
+    int rank_min;      /* steps of at least this many rows rank their rows    */
     int rows;          /* step rows: slots + spare prompt rows                  */
     int kv_rows;       /* rows per (slot, head) of the self caches (>= smax)    */
     /* slot table */

@@ -100,6 +100,7 @@ struct HipbEngine {
     hipGraphExec_t exec[2];
     int have_graph[2];
     int eager;           /* HIPB_EAGER=1: launch steps without a graph */
+    int read_ahead;      /* HIPB_READ_AHEAD=0: no weight read-ahead rows */
     int bench_mode;
     int bench_gemm_M;    /* rows seeded by hipb_bench_encoder_gemm */
     /* log-mel front-end */
@@ -338,6 +339,10 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->req = calloc(R, sizeof(HostReq));
     const char *eg = getenv("HIPB_EAGER");
     e->eager = eg && eg[0] == '1';
+    /* scheduling knobs (the results are the same bits either way) */
+    const char *rm = getenv("HIPB_RANK_MIN_ROWS"), *ra = getenv("HIPB_READ_AHEAD");
+    d->rank_min = rm && rm[0] ? atoi(rm) : CT_RANK_MIN_ROWS;
+    e->read_ahead = !(ra && ra[0] == '0');
     mel_tables_init(e);
     ECHK(hipHostMalloc((void **)&e->h_tmp, (size_t)(R + 8) * (MAX_SEQ + 8) * sizeof(int), 0));
     ECHK(hipHostMalloc((void **)&e->h_meta, (size_t)R * (5 + CT_PROMPT_MAX) * sizeof(int), 0));
@@ -936,7 +941,7 @@ static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, 
     a.K = K; a.V = V; a.kv_bf16 = e->esz == 2;
     a.kv_sb = item_stride; a.kv_st = DEC_DK; a.kv_sh = head_stride;
     a.lens = lens; a.lens_step = 1; a.kv_index = kv_index; a.kv_rows = rows;
-    a.rank = e->M >= CT_RANK_MIN_ROWS ? rank : NULL;
+    a.rank = e->M >= e->d.rank_min ? rank : NULL;
     a.T_q = 1; a.B = e->M; a.H = DEC_H;
     a.scale = 0.08838834764831845f;   /* 1/sqrt(128) */
     if (q_bias) {
@@ -1014,7 +1019,7 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         const uint16_t *w_o = WT(e->wt_o[l], DW(L->sa_ow)), *w_cq = WT(e->wt_cq[l], DW(L->ca_qw));
         const uint16_t *w_co = WT(e->wt_co[l], DW(L->ca_ow)), *w_f1 = WT(e->wt_f1[l], DW(L->ffn_w1));
         const uint16_t *w_f2 = WT(e->wt_f2[l], DW(L->ffn_w2));
-        if (full && CT_WARM) warm_add(e, w_qkv, 3 * DEC_D, DEC_D, CT_GV_QKV);
+        if (full && CT_WARM && e->read_ahead) warm_add(e, w_qkv, 3 * DEC_D, DEC_D, CT_GV_QKV);
         if (full && l == 0) {
             /* the embedding LayerNorm and this one in one launch */
             CtWarmSet ws;
@@ -1035,15 +1040,15 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)e->d.kv_rows * DEC_DK;
         g.kv_bf16 = e->esz == 2;
         ctk_gemv(&g, s);
-        if (full && CT_WARM) warm_add(e, w_o, DEC_D, DEC_D, CT_GV_PARTIAL);
-        if (full && CT_WARM) warm_add(e, w_cq, DEC_D, DEC_D, CT_GV_PARTIAL);
+        if (full && CT_WARM && e->read_ahead) warm_add(e, w_o, DEC_D, DEC_D, CT_GV_PARTIAL);
+        if (full && CT_WARM && e->read_ahead) warm_add(e, w_cq, DEC_D, DEC_D, CT_GV_PARTIAL);
         if (full) step_attention(e, l, 0);
         gv(e, e->attf, w_o, NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
 
         if (full) ln_frag(e, ks_o, DW(L->sa_ob), DW(L->ca_lnw), DW(L->ca_lnb));
         gv(e, e->lnf, w_cq, NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
-        if (full && CT_WARM) warm_add(e, w_f1, DEC_FF, DEC_D, CT_GV_FRAG);
-        if (full && CT_WARM) warm_add(e, w_f2, DEC_D, DEC_FF, CT_GV_PARTIAL);
+        if (full && CT_WARM && e->read_ahead) warm_add(e, w_f1, DEC_FF, DEC_D, CT_GV_FRAG);
+        if (full && CT_WARM && e->read_ahead) warm_add(e, w_f2, DEC_D, DEC_FF, CT_GV_PARTIAL);
         if (full) step_attention(e, l, 1);
         gv(e, e->attf, w_co, NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
 

@@ -182,7 +182,7 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     // the step's rows by descending self and cross length (ties by row),
     // for steps large enough that the attention deals its items by them
     const int B = d.slots + extra;
-    for (int row = tid; B >= CT_RANK_MIN_ROWS && row < B; row += 256) {
+    for (int row = tid; B >= d.rank_min && row < B; row += 256) {
         const int lp = s_pl[row], lc = s_cl[row];
         int rp = 0, rc = 0;
         for (int j = 0; j < B; j++) {

@@ -97,7 +97,10 @@ void hipb_step(HipbEngine *e);
 /* Runs decode steps until every encoded request has finished; steps are
  * replayed from one captured graph (launched one by one instead when the
  * environment sets HIPB_EAGER=1, e.g. under a tracing profiler), chunk steps
- * per host check.
+ * per host check.  Two scheduling knobs, read at hipb_create, change where
+ * work runs but not the results (same bits): HIPB_RANK_MIN_ROWS (steps of at
+ * least this many rows deal attention items to compute units by length rank;
+ * default 96) and HIPB_READ_AHEAD=0 (no weight read-ahead workgroups).
  * Returns the number of steps run. */
 long hipb_run(HipbEngine *e, int chunk);
 /* hipb_encode and hipb_run overlapped: a worker thread encodes the requests

@@ -128,6 +128,33 @@ def test_engine_admission_order(hip, hot, mels):
         eng.close()
 
 
+def test_engine_scheduling_knobs_keep_bits(hip, hot, monkeypatch):
+    """Dealing attention items to compute units by length rank (steps of at
+    least HIPB_RANK_MIN_ROWS rows) and the weight read-ahead workgroups change
+    only where work runs: one step over 128 slots at the microbench's shapes
+    (S ~ U(1,448), T_enc ~ U(25,375), seeded bf16 caches) gives the same
+    logits bits with each of them off.  A rank table that skipped or repeated
+    an item would leave some slot's attention output stale."""
+    rng = np.random.default_rng(21)
+    S, T = rng.integers(1, 449, 128), rng.integers(25, 376, 128)
+    outs = []
+    for rank_min, read_ahead in (("96", "1"), ("100000", "1"), ("96", "0")):
+        print(f"case: 128 slots, rank from {rank_min} rows, read-ahead {read_ahead}", flush=True)
+        monkeypatch.setenv("HIPB_RANK_MIN_ROWS", rank_min)
+        monkeypatch.setenv("HIPB_READ_AHEAD", read_ahead)
+        eng = cb.Engine(hot, slots=128, max_requests=128, max_frames=376, kv_bf16=True,
+                        max_tokens=512)
+        try:
+            eng.bench_fill(S, T, seed=9)
+            eng.step()
+            outs.append(np.stack([eng.logits(s) for s in range(128)]))
+        finally:
+            eng.close()
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+
+
 def test_engine_batch_vs_single_bitexact(hip, hot, mels):
     packed = cb.Engine(hot, slots=4, max_requests=8, max_frames=64, kv_bf16=True)
     try:
