@@ -128,26 +128,28 @@ def test_engine_admission_order(hip, hot, mels):
         eng.close()
 
 
-def test_engine_scheduling_knobs_keep_bits(hip, hot, monkeypatch):
+@pytest.mark.parametrize("slots,max_tokens", [(128, 512), (256, 1024)])
+def test_engine_scheduling_knobs_keep_bits(hip, hot, monkeypatch, slots, max_tokens):
     """Dealing attention items to compute units by length rank (steps of at
     least HIPB_RANK_MIN_ROWS rows) and the weight read-ahead workgroups change
     only where work runs: one step over 128 slots at the microbench's shapes
-    (S ~ U(1,448), T_enc ~ U(25,375), seeded bf16 caches) gives the same
-    logits bits with each of them off.  A rank table that skipped or repeated
-    an item would leave some slot's attention output stale."""
+    (S ~ U(1,448), T_enc ~ U(25,375), seeded bf16 caches), and over the
+    largest engine (256 slots, 1024-token caches, S up to 960), gives the
+    same logits bits with each of them off.  A rank table that skipped or
+    repeated an item would leave some slot's attention output stale."""
     rng = np.random.default_rng(21)
-    S, T = rng.integers(1, 449, 128), rng.integers(25, 376, 128)
+    S, T = rng.integers(1, max_tokens - 63, slots), rng.integers(25, 376, slots)
     outs = []
     for rank_min, read_ahead in (("96", "1"), ("100000", "1"), ("96", "0")):
-        print(f"case: 128 slots, rank from {rank_min} rows, read-ahead {read_ahead}", flush=True)
+        print(f"case: {slots} slots, rank from {rank_min} rows, read-ahead {read_ahead}", flush=True)
         monkeypatch.setenv("HIPB_RANK_MIN_ROWS", rank_min)
         monkeypatch.setenv("HIPB_READ_AHEAD", read_ahead)
-        eng = cb.Engine(hot, slots=128, max_requests=128, max_frames=376, kv_bf16=True,
-                        max_tokens=512)
+        eng = cb.Engine(hot, slots=slots, max_requests=slots, max_frames=376, kv_bf16=True,
+                        max_tokens=max_tokens)
         try:
             eng.bench_fill(S, T, seed=9)
             eng.step()
-            outs.append(np.stack([eng.logits(s) for s in range(128)]))
+            outs.append(np.stack([eng.logits(s) for s in range(slots)]))
         finally:
             eng.close()
     assert np.isfinite(outs[0]).all()
