@@ -26,9 +26,10 @@ extern "C" {
 #define CT_MAX_KSPLIT 8    /* largest ctk_gemv_ksplit() of a decoder weight */
 /* Spare rows per (slot, head) of the self caches: without them every
  * (slot, head) block starts on the same 256-KB boundary and the workgroups
- * of a step stream from the same memory channels at the same time. */
+ * of a step stream from the same memory channels at the same time (16 rows:
+ * stream RTFx +0.1% over none, 8 rows +0.05%). */
 #ifndef CT_KV_PAD
-#define CT_KV_PAD 0
+#define CT_KV_PAD 16
 #endif
 
 /* All pointers are device memory.  Slot-major arrays have `slots` entries,
