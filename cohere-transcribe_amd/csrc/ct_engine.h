@@ -16,8 +16,8 @@ extern "C" {
 #define CT_CARRY_MAX 64
 #define CT_PROMPT_MAX (CT_PROMPT_SUBMIT_MAX + CT_CARRY_MAX)
 #define CT_ENG_MAX_SLOTS 256  /* slots an engine may have (the ABI's MAX_BATCH) */
-/* Steps of at least this many rows deal their attention items to CUs by
- * length rank (long with short): with >= 3 items per CU position the balance
+/* Default of HIPB_RANK_MIN_ROWS: steps of at least this many rows deal their
+ * attention items to CUs by length rank (long with short): with >= 3 items per CU position the balance
  * outweighs the extra dependent load per workgroup; at 64 slots + 16 prompt
  * rows it measured even (the 128-slot step: 27.8 -> 24.0 us per launch). */
 #ifndef CT_RANK_MIN_ROWS

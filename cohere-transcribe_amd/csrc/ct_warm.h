@@ -37,7 +37,8 @@ static inline int ct_warm_rows(const CtWarmSet *ws, const char *who) {
     bool ok = ws->n > 0 && ws->n <= 4 && ws->rows >= 1 && ws->rows <= 128 && ws->sink;
     for (int t = 0; ok && t < ws->n; t++)
         ok = ws->t[t].gx >= 0 && ws->t[t].gy >= 1 && ws->t[t].cb >= 1 && ws->t[t].per >= 1 &&
-             ((uintptr_t)ws->t[t].W & 15) == 0;
+             ws->t[t].per * ws->t[t].gy <= ws->t[t].nsteps &&
+             (ws->t[t].gx == 0 || ws->t[t].W) && ((uintptr_t)ws->t[t].W & 15) == 0;
     if (!ok) {
         fprintf(stderr, "%s: read-ahead needs 1..4 tiled GEMMs, 1..128 rows and a sink\n", who);
         exit(1);
