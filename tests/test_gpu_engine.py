@@ -264,7 +264,15 @@ def test_engine_pcm_path(hip, hot, oracle_runs):
         eng.close()
 
 
-def test_packed_encoder_bitexact_vs_abi_encoder(hip, hot):
+# four short clips packed into ~300 rows, and 24 clips of ~20 s packed into
+# ~6000 rows, where the FFN projections take the 256-row tile kernel while
+# each clip alone (<= 376 rows) takes the 128-row one
+ENC_CLIPS = {"small": [(4000, 101), (33000, 104), (7200, 102), (161 * 160, 105)],
+             "large": [(320000 + 1600 * i, 200 + i) for i in range(24)]}
+
+
+@pytest.mark.parametrize("batch", ["small", "large"])
+def test_packed_encoder_bitexact_vs_abi_encoder(hip, hot, batch):
     """The engine's packed encoder (pre-split activations, DMA-fed GEMM,
     ragged attention/conv kernels) gives the same bits per request as the
     reference host graph (model.h encoder_forward) driving the ABI one clip
@@ -278,13 +286,12 @@ def test_packed_encoder_bitexact_vs_abi_encoder(hip, hot):
     ref.ref_set_weights.argtypes = [C.c_void_p]
     ref.ref_encoder.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
     ref.ref_set_weights(hot.weights_ref())
-    clips = [(4000, 101), (33000, 104), (7200, 102), (161 * 160, 105)]
-    mels = [ob.compute_mel(cb.synth_audio(n, s)) for n, s in clips]
-    eng = cb.Engine(hot, slots=2, max_requests=8, max_frames=400, kv_bf16=True)
+    mels = [ob.compute_mel(cb.synth_audio(n, s)) for n, s in ENC_CLIPS[batch]]
+    eng = cb.Engine(hot, slots=2, max_requests=len(mels), max_frames=400, kv_bf16=True)
     try:
         for m in mels:
             eng.submit(m, 2, FLAGS)
-        eng.encode(max_batch_frames=4096)     # one packed batch
+        eng.encode(max_batch_frames=8192)     # one packed batch
         for i, m in enumerate(mels):
             want = np.zeros((cb.t_enc(m.shape[1]), cb.DEC_D), np.float32)
             ref.ref_encoder(m.ctypes.data, m.shape[1], want.ctypes.data)
