@@ -264,11 +264,12 @@ def test_engine_pcm_path(hip, hot, oracle_runs):
         eng.close()
 
 
-# four short clips packed into ~300 rows, and 24 clips of ~20 s packed into
-# ~6000 rows, where the FFN projections take the 256-row tile kernel while
-# each clip alone (<= 376 rows) takes the 128-row one
+# four short clips packed into ~300 rows, and 23 clips of ~20 s plus one of
+# 30 s (the longest, 376 encoder frames) packed into ~6100 rows, where the FFN
+# projections take the 256-row tile kernel while each clip alone (<= 376
+# rows) takes the 128-row one
 ENC_CLIPS = {"small": [(4000, 101), (33000, 104), (7200, 102), (161 * 160, 105)],
-             "large": [(320000 + 1600 * i, 200 + i) for i in range(24)]}
+             "large": [(320000 + 1600 * i, 200 + i) for i in range(23)] + [(480000, 230)]}
 
 
 @pytest.mark.parametrize("batch", ["small", "large"])
