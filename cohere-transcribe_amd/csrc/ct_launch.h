@@ -107,9 +107,9 @@ typedef struct {
 /* Requires N % 16 == 0 (N % 64 == 0 when N >= 8192), K % (256 * steps) == 0. */
 void ctk_gemv(const CtGemv *g, hipStream_t s);
 /* The weight tiles one decode-GEMM launch reads, by workgroup: workgroup i
- * (of gx * gy, i = column block + gx * K-slice) reads, for each of its cb
+ * (of gx * gy, i = K-slice + gy * column block) reads, for each of its cb
  * column blocks c, the per consecutive 1-KB tiles from tile
- * ((i % gx) * cb + c) * nsteps + (i / gx) * per of W (tile layout).  Workgroup
+ * ((i / gy) * cb + c) * nsteps + (i % gy) * per of W (tile layout).  Workgroup
  * i runs on XCD i % 8, like every launch's workgroup i. */
 typedef struct {
     const uint16_t *W;

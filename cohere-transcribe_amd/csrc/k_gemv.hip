@@ -23,12 +23,18 @@
 namespace {
 
 constexpr int GV_WAVES = 8;
+// 1: K-slices vary fastest in launch order, so with 8 K-slices each XCD (its
+// own L2) serves one slice and fetches only that slice's activations
+#ifndef CT_GV_KFAST
+#define CT_GV_KFAST 1
+#endif
 
 template <int CB, int SPW>
 __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int r = lane & 15, kg = lane >> 4;
-    const int c0 = blockIdx.x * 16 * CB, ks = blockIdx.y, z = blockIdx.z, m0 = z * 64;
+    const int c0 = (CT_GV_KFAST ? blockIdx.y : blockIdx.x) * 16 * CB;
+    const int ks = CT_GV_KFAST ? blockIdx.x : blockIdx.y, z = blockIdx.z, m0 = z * 64;
     const int nsteps = g.K >> 5;
     const int s0 = ks * (GV_WAVES * SPW);
     int nrb = min(4, (g.M - m0 + 15) >> 4);
@@ -195,7 +201,8 @@ extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
         gv_fatal("operands must be 16-byte aligned", g);
     const int spw = g->K / ksplit / 256;
     const int cb = gv_cb(g->N, g->K);
-    const dim3 grid(g->N / (16 * cb), ksplit, (g->M + 63) / 64);
+    const dim3 grid(CT_GV_KFAST ? ksplit : g->N / (16 * cb), CT_GV_KFAST ? g->N / (16 * cb) : ksplit,
+                    (g->M + 63) / 64);
     const dim3 block(64 * GV_WAVES);
 #define GV_CASE(CB, SPW)                                                          \
     if (cb == CB && spw == SPW) {                                                 \
