@@ -56,3 +56,34 @@ def test_kernel_struct_mirrors_match():
     lib.ctk_warmset_sizeof.restype = C.c_int
     assert C.sizeof(CtGemv) == lib.ctk_gemv_sizeof()
     assert C.sizeof(CtWarmSet) == lib.ctk_warmset_sizeof()
+
+
+def test_gemv_read_ahead_descriptor_covers_each_tile_once():
+    """ctk_gemv_warm (host code) describes the tiles each decode-GEMM
+    workgroup reads: workgroup i (K-slice i % gy, column position i / gy)
+    reads cb column blocks x per K-steps.  For every decoder shape the
+    workgroups' tiles together are each weight tile exactly once, and the
+    split matches ctk_gemv_ksplit."""
+    import numpy as np
+    from structs import CtGemv, CtWarm
+    lib = C.CDLL(cb.HIP_LIB)
+    lib.ctk_gemv_warm.argtypes = [C.POINTER(CtGemv), C.POINTER(CtWarm)]
+    lib.ctk_gemv_ksplit.argtypes = [C.c_int, C.c_int]
+    lib.ctk_gemv_ksplit.restype = C.c_int
+    for N, K, partial in ((3072, 1024, False), (1024, 1024, True), (4096, 1024, False),
+                          (1024, 4096, True), (16384, 1024, False)):
+        ks = lib.ctk_gemv_ksplit(N, K) if partial else 1
+        g = CtGemv(W=1 << 20, N=N, K=K, ksplit=ks, wtile=1)
+        w = CtWarm()
+        lib.ctk_gemv_warm(C.byref(g), C.byref(w))
+        assert (w.gy, w.nsteps, w.per * w.gy, w.gx * w.cb * 16) == (ks, K // 32, K // 32, N), (N, K)
+        seen = np.zeros((N // 16) * (K // 32), np.int32)
+        for i in range(w.gx * w.gy):
+            cx, k = i // w.gy, i % w.gy
+            for c in range(w.cb):
+                t0 = (cx * w.cb + c) * w.nsteps + k * w.per
+                seen[t0:t0 + w.per] += 1
+        assert np.all(seen == 1), (N, K)
+        g.wtile = 0
+        lib.ctk_gemv_warm(C.byref(g), C.byref(w))
+        assert w.gx == 0
