@@ -114,7 +114,15 @@ void ctk_gemv(const CtGemv *g, hipStream_t s);
 typedef struct {
     const uint16_t *W;
     int gx, gy, cb, per, nsteps;
+    int heads;                /* 1: a QKV launch, column positions dealt by head */
 } CtWarm;
+/* Column block of a QKV launch's workgroup at position p (192 blocks of 16):
+ * positions p % 8 == h take head h's 8 query, 8 key and 8 value blocks, so
+ * they run on XCD h, where the attention's workgroups of head h read them. */
+static inline CT_HD int ct_qkv_col(int p) {
+    const int j = p >> 3;
+    return (j >> 3) * 64 + (p & 7) * 8 + (j & 7);
+}
 /* Fills w for the launch ctk_gemv(g) makes; w->gx = 0 when g's weights are
  * not in the tile layout. */
 void ctk_gemv_warm(const CtGemv *g, CtWarm *w);

@@ -16,7 +16,7 @@ __device__ __forceinline__ void ct_warm_tiles(const CtWarmSet &ws, int x, int j)
         const CtWarm w = ws.t[t];
         const int G = w.gx * w.gy;
         for (int i = x + 8 * j; i < G; i += 8 * ws.rows) {
-            const int cx = i / w.gy, ks = i % w.gy;
+            const int cx = w.heads ? ct_qkv_col(i / w.gy) : i / w.gy, ks = i % w.gy;
             for (int c = 0; c < w.cb; c++) {
                 const uint4 *p = reinterpret_cast<const uint4 *>(
                     w.W + ((((long)cx * w.cb + c) * w.nsteps + (long)ks * w.per) << 9));

@@ -23,6 +23,10 @@
 namespace {
 
 constexpr int GV_WAVES = 8;
+// 1: a QKV launch's column blocks are dealt head by head over the XCDs
+#ifndef CT_GV_QKV_HEADS
+#define CT_GV_QKV_HEADS 1
+#endif
 // 1: K-slices vary fastest in launch order, so with 8 K-slices each XCD (its
 // own L2) serves one slice and fetches only that slice's activations
 #ifndef CT_GV_KFAST
@@ -33,7 +37,8 @@ template <int CB, int SPW>
 __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int r = lane & 15, kg = lane >> 4;
-    const int c0 = (CT_GV_KFAST ? blockIdx.y : blockIdx.x) * 16 * CB;
+    const int pos = CT_GV_KFAST ? blockIdx.y : blockIdx.x;
+    const int c0 = (CT_GV_QKV_HEADS && g.out == CT_GV_QKV ? ct_qkv_col(pos) : pos) * 16 * CB;
     const int ks = CT_GV_KFAST ? blockIdx.x : blockIdx.y, z = blockIdx.z, m0 = z * 64;
     const int nsteps = g.K >> 5;
     const int s0 = ks * (GV_WAVES * SPW);
@@ -188,6 +193,7 @@ extern "C" void ctk_gemv_warm(const CtGemv *g, CtWarm *w) {
     w->gx = g->wtile ? g->N / (16 * cb) : 0;
     w->gy = ksplit; w->cb = cb;
     w->per = g->K / ksplit / 32; w->nsteps = g->K / 32;
+    w->heads = CT_GV_QKV_HEADS && g->out == CT_GV_QKV;
 }
 
 extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {

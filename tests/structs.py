@@ -18,7 +18,7 @@ class CtGemv(C.Structure):
 
 class CtWarm(C.Structure):
     _fields_ = [("W", C.c_void_p), ("gx", C.c_int), ("gy", C.c_int), ("cb", C.c_int),
-                ("per", C.c_int), ("nsteps", C.c_int)]
+                ("per", C.c_int), ("nsteps", C.c_int), ("heads", C.c_int)]
 
 
 class CtWarmSet(C.Structure):

@@ -70,16 +70,20 @@ def test_gemv_read_ahead_descriptor_covers_each_tile_once():
     lib.ctk_gemv_warm.argtypes = [C.POINTER(CtGemv), C.POINTER(CtWarm)]
     lib.ctk_gemv_ksplit.argtypes = [C.c_int, C.c_int]
     lib.ctk_gemv_ksplit.restype = C.c_int
-    for N, K, partial in ((3072, 1024, False), (1024, 1024, True), (4096, 1024, False),
-                          (1024, 4096, True), (16384, 1024, False)):
+    def qkv_col(p):          # ct_qkv_col: head-by-head positions of a QKV launch
+        j = p >> 3
+        return (j >> 3) * 64 + (p & 7) * 8 + (j & 7)
+    for N, K, partial, out in ((3072, 1024, False, 3), (3072, 1024, False, 1), (1024, 1024, True, 0),
+                               (4096, 1024, False, 2), (1024, 4096, True, 0), (16384, 1024, False, 1)):
         ks = lib.ctk_gemv_ksplit(N, K) if partial else 1
-        g = CtGemv(W=1 << 20, N=N, K=K, ksplit=ks, wtile=1)
+        g = CtGemv(W=1 << 20, N=N, K=K, ksplit=ks, wtile=1, out=out)
         w = CtWarm()
         lib.ctk_gemv_warm(C.byref(g), C.byref(w))
         assert (w.gy, w.nsteps, w.per * w.gy, w.gx * w.cb * 16) == (ks, K // 32, K // 32, N), (N, K)
         seen = np.zeros((N // 16) * (K // 32), np.int32)
+        assert w.heads == (out == 3)
         for i in range(w.gx * w.gy):
-            cx, k = i // w.gy, i % w.gy
+            cx, k = (qkv_col(i // w.gy) if w.heads else i // w.gy), i % w.gy
             for c in range(w.cb):
                 t0 = (cx * w.cb + c) * w.nsteps + k * w.per
                 seen[t0:t0 + w.per] += 1
