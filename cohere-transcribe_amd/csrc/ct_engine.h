@@ -62,13 +62,17 @@ typedef struct {
     int  *req_T, *req_limit, *req_flags, *req_np, *req_ngen;
     int  *req_prompt;  /* [max_req][CT_PROMPT_MAX]                             */
     int  *req_out;     /* [max_req][smax] generated tokens                     */
+    float *req_score;  /* [max_req][smax] the largest logit the argmax weighed
+                          for each token (EOS left out when suppressed): the
+                          step's logits bits, for batch-vs-single checks      */
     /* chained chunks of one long recording: the request admitted after
      * this one finishes (its prompt then gets the carried tokens), or -1 */
     int  *req_next;
     /* successor ring: chained chunks released by their predecessors;
-     * rq[q[0]..q[1]) wait for a slot.  pend[slot] is a successor that eng_end
-     * released in that slot this step (-1 if none); eng_begin appends them in
-     * slot order.  Only the step kernels write rq and pend. */
+     * rq[q[0]..q[1]) wait for a slot and for their encoding (q[7]), in ring
+     * order.  pend[slot] is a successor that eng_end released in that slot
+     * this step (-1 if none); eng_begin appends them in slot order.  Only the
+     * step kernels write rq and pend. */
     int  *rq, *pend;
     /* fresh queue: requests that wait for no predecessor, in submission
      * order, published by the host once encoded (the ids, then the count
@@ -78,9 +82,17 @@ typedef struct {
     /* q[0] next successor to admit, q[1] successors written, q[2] requests
      * finished, q[3] prompt tokens not yet fed after the last step, q[4] next
      * fresh request to admit, q[5] fresh requests published, q[6] rows the
-     * current step uses (the slots' rows plus the spare rows dealt out) */
+     * current step uses (the slots' rows plus the spare rows dealt out),
+     * q[7] encoded watermark: requests with ids below it have their cross
+     * K/V written (host-published after each encoder batch; a released
+     * successor is admitted only once its id is below it), q[8] 1 when the
+     * successor at the head of rq waits for its encoding after the last
+     * admission, q[9] the watermark that admission saw, q[10] successors
+     * released so far (by eng_end; q[10] - q[0] wait in pend or rq) */
     int  *q;
 } CtEngDev;
+
+#define CT_Q_WORDS 16      /* ints in q */
 
 /* Admission + the step's rows (one workgroup; admission and spare-row
  * dealing go in slot order, so scheduling is deterministic).  extra: spare

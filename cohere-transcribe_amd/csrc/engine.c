@@ -72,6 +72,12 @@ struct HipbEngine {
     int fq_count;
     int proc_batch;            /* encoder batch frames of hipb_process */
     atomic_int enc_done;       /* the encoder thread has published every batch */
+    atomic_int published;      /* encoded watermark last published (q[7]) */
+    /* test support (hipb_test_hold_encoder): after publishing hold_batches
+     * batches the encoder thread waits until the decode loop has seen
+     * hold_finished requests finish */
+    int hold_batches, hold_finished, hold_expired;
+    atomic_int seen_finished;
     uint16_t *lnf, *attf, *midf;
     /* encoder workspace (lazy) */
     int enc_cap;               /* frames */
@@ -258,7 +264,8 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     d->req_ngen = dmalloc(R * sizeof(int));
     d->req_prompt = dmalloc((size_t)R * CT_PROMPT_MAX * sizeof(int));
     d->req_out = dmalloc((size_t)R * d->smax * sizeof(int));
-    d->q = dmalloc(8 * sizeof(int));
+    d->req_score = dmalloc((size_t)R * d->smax * sizeof(float));
+    d->q = dmalloc(CT_Q_WORDS * sizeof(int));
     d->fq = dmalloc(R * sizeof(int));
     d->req_next = dmalloc(R * sizeof(int));
     d->rq = dmalloc(R * sizeof(int));
@@ -266,7 +273,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     ECHK(hipMemsetAsync(d->slot_req, 0xff, S * sizeof(int), e->s));   /* -1: free */
     ECHK(hipMemsetAsync(d->slot_S, 0, S * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->req_ngen, 0, R * sizeof(int), e->s));
-    ECHK(hipMemsetAsync(d->q, 0, 8 * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->q, 0, CT_Q_WORDS * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->req_next, 0xff, R * sizeof(int), e->s));   /* -1: no successor */
     ECHK(hipMemsetAsync(d->pend, 0xff, S * sizeof(int), e->s));
 
@@ -361,7 +368,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->d.slot_lim, e->d.slot_ng, e->d.slot_tok, e->d.act, e->d.tok, e->d.pos_len, e->d.cross_len,
                     e->d.row_slot, e->d.rank_self, e->d.rank_cross, e->warm_sink,
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
-                    e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.q,
+                    e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.req_score, e->d.q,
                     e->d.req_next, e->d.rq, e->d.pend, e->d.fq,
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
                     e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
@@ -393,11 +400,12 @@ void hipb_reset(HipbEngine *e) {
     e->meta_lo = 0;
     e->pool_frames = 0;
     e->fq_count = 0;
+    atomic_store(&e->published, 0);
     e->bench_mode = 0;
     ECHK(hipMemsetAsync(e->d.slot_req, 0xff, e->d.slots * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.slot_S, 0, e->d.slots * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.req_ngen, 0, e->d.max_req * sizeof(int), e->s));
-    ECHK(hipMemsetAsync(e->d.q, 0, 8 * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(e->d.q, 0, CT_Q_WORDS * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.req_next, 0xff, e->d.max_req * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.pend, 0xff, e->d.slots * sizeof(int), e->s));
     ECHK(hipStreamSynchronize(e->s));
@@ -830,21 +838,29 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     free(row_start); free(row_len); free(rowoff); free(seq_off); free(seq_T); free(blk_seq); free(blk_q0);
 }
 
-/* Appends the requests of [r0, r1) that wait for no predecessor to the fresh
- * queue, in submission order: the ids first, then the new count, both copied
- * on the encoder stream, which is then drained (the step kernel reads them
- * with device-coherent loads, possibly while running on the other stream). */
+/* Publishes the encoded requests [r0, r1) (their cross K/V are written: the
+ * encoder stream has been drained): the encoded watermark q[7] = r1, which
+ * releases chained successors below it, then the requests that wait for no
+ * predecessor appended to the fresh queue in submission order (the ids
+ * first, then the new count).  All copies go on the encoder stream, which is
+ * then drained; the step kernel reads the words with acquire loads, possibly
+ * while running on the other stream. */
 static void publish(HipbEngine *e, int r0, int r1) {
     int *ids = e->h_enc + 10 * e->d.max_req + 16, k = 0;
+    int *words = e->h_enc + 10 * e->d.max_req + 8;   /* [0] watermark, [1] fresh count */
     for (int i = r0; i < r1; i++)
         if (!e->req[i].chained) ids[k++] = i;
-    if (!k) return;
-    ECHK(hipMemcpyAsync(e->d.fq + e->fq_count, ids, (size_t)k * sizeof(int), hipMemcpyHostToDevice, e->enc_s));
-    e->fq_count += k;
-    int *cnt = e->h_enc + 10 * e->d.max_req + 8;
-    *cnt = e->fq_count;
-    ECHK(hipMemcpyAsync(e->d.q + 5, cnt, sizeof(int), hipMemcpyHostToDevice, e->enc_s));
+    words[0] = r1;
+    ECHK(hipMemcpyAsync(e->d.q + 7, &words[0], sizeof(int), hipMemcpyHostToDevice, e->enc_s));
+    if (k) {
+        ECHK(hipMemcpyAsync(e->d.fq + e->fq_count, ids, (size_t)k * sizeof(int), hipMemcpyHostToDevice,
+                            e->enc_s));
+        e->fq_count += k;
+        words[1] = e->fq_count;
+        ECHK(hipMemcpyAsync(e->d.q + 5, &words[1], sizeof(int), hipMemcpyHostToDevice, e->enc_s));
+    }
     ECHK(hipStreamSynchronize(e->enc_s));
+    atomic_store(&e->published, r1);
 }
 
 static void release_inputs(HipbEngine *e, int r0, int r1) {
@@ -1087,15 +1103,15 @@ void hipb_attention_only(HipbEngine *e) {
     }
 }
 
-/* Reads the queue words (synchronises): q[0..3]. */
+/* Reads the queue words (synchronises). */
 static void read_queue(HipbEngine *e, int *q) {
-    ECHK(hipMemcpyAsync(e->h_tmp, e->d.q, 8 * sizeof(int), hipMemcpyDeviceToHost, e->s));
+    ECHK(hipMemcpyAsync(e->h_tmp, e->d.q, CT_Q_WORDS * sizeof(int), hipMemcpyDeviceToHost, e->s));
     ECHK(hipStreamSynchronize(e->s));
-    memcpy(q, e->h_tmp, 8 * sizeof(int));
+    memcpy(q, e->h_tmp, CT_Q_WORDS * sizeof(int));
 }
 
 int hipb_finished(HipbEngine *e) {
-    int q[8];
+    int q[CT_Q_WORDS];
     read_queue(e, q);
     return q[2];
 }
@@ -1131,7 +1147,7 @@ long hipb_run(HipbEngine *e, int chunk) {
      * a slot frees up */
     const long bound = (long)(e->n_enc + 2) * (MAX_SEQ + CT_PROMPT_MAX + 1);
     for (;;) {
-        int q[8];
+        int q[CT_Q_WORDS];
         read_queue(e, q);
         if (q[2] >= e->n_enc) break;
         if (steps > bound) CT_FATAL("hipb_run: requests did not finish within the step bound");
@@ -1150,12 +1166,22 @@ static void *enc_worker(void *arg) {
     HipbEngine *e = arg;
     ECHK(hipSetDevice(e->dev));
     ct_t.dev = e->dev;                 /* weight pointers translate per device */
+    int batches = 0;
     for (int r = e->n_enc; r < e->n_req;) {
         const int r1 = next_batch(e, r, e->proc_batch);
         encode_batch(e, r, r1);
         release_inputs(e, r, r1);
         publish(e, r, r1);
         r = r1;
+        if (++batches == e->hold_batches) {
+            /* test support: a bounded host-side wait (60 s) */
+            int waited = 0;
+            while (atomic_load(&e->seen_finished) < e->hold_finished && waited < 600000) {
+                usleep(100);
+                waited++;
+            }
+            e->hold_expired = atomic_load(&e->seen_finished) < e->hold_finished;
+        }
     }
     atomic_store(&e->enc_done, 1);
     return NULL;
@@ -1192,19 +1218,25 @@ long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
     e->enc_s = e->s2;
     e->proc_batch = max_batch_frames;
     atomic_store(&e->enc_done, 0);
+    atomic_store(&e->seen_finished, 0);
+    e->hold_expired = 0;
     pthread_t th;
     if (pthread_create(&th, NULL, enc_worker, e)) CT_FATAL("hipb_process: cannot start the encoder thread");
     long steps = 0;
     const long bound = (long)(e->n_req + 2) * (MAX_SEQ + CT_PROMPT_MAX + 1);
     for (;;) {
-        int q[8];
+        int q[CT_Q_WORDS];
         read_queue(e, q);
+        atomic_store(&e->seen_finished, q[2]);
         const int done = atomic_load(&e->enc_done);
         if (done && q[2] >= e->n_req) break;
-        /* every admitted request finished and none waits: wait for the
-         * encoder instead of stepping empty slots (a released successor
-         * joins at the next step once the encoder has published or ended) */
-        if (!done && q[2] >= q[0] + q[4] && q[0] >= q[1] && q[4] >= q[5]) {
+        /* every admitted request finished and none can be admitted: wait
+         * for the encoder instead of stepping empty slots.  No successor
+         * waits (released q[10] = admitted q[0]), or the one at the ring's
+         * head waits for its encoding (q[8]) and nothing was published since
+         * that admission saw the watermark (q[9]). */
+        const int ring_idle = q[10] <= q[0] || (q[8] && q[9] >= atomic_load(&e->published));
+        if (!done && q[2] >= q[0] + q[4] && ring_idle && q[4] >= q[5]) {
             usleep(50);
             continue;
         }
@@ -1220,6 +1252,13 @@ long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
     return steps;
 }
 
+void hipb_test_hold_encoder(HipbEngine *e, int after_batches, int until_finished) {
+    e->hold_batches = after_batches;
+    e->hold_finished = until_finished;
+}
+
+int hipb_test_hold_expired(HipbEngine *e) { return e->hold_expired; }
+
 /* ------------------------------------------------------------------ */
 /* Results                                                             */
 /* ------------------------------------------------------------------ */
@@ -1230,6 +1269,17 @@ int hipb_tokens(HipbEngine *e, int req, int *out, int cap) {
     ECHK(hipMemcpy(&n, e->d.req_ngen + req, sizeof(int), hipMemcpyDeviceToHost));
     if (n > cap) n = cap;
     if (n > 0) ECHK(hipMemcpy(out, e->d.req_out + (size_t)req * e->d.smax, n * sizeof(int), hipMemcpyDeviceToHost));
+    return n;
+}
+
+int hipb_token_scores(HipbEngine *e, int req, float *out, int cap) {
+    if (req < 0 || req >= e->n_req) return 0;
+    int n = 0;
+    ECHK(hipStreamSynchronize(e->s));
+    ECHK(hipMemcpy(&n, e->d.req_ngen + req, sizeof(int), hipMemcpyDeviceToHost));
+    if (n > cap) n = cap;
+    if (n > 0)
+        ECHK(hipMemcpy(out, e->d.req_score + (size_t)req * e->d.smax, n * sizeof(float), hipMemcpyDeviceToHost));
     return n;
 }
 
@@ -1289,7 +1339,9 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
             buf[s] = f == 0 ? 0 : f == 1 ? T_enc[s] : f == 2 ? HIPB_SUPPRESS_EOS : f == 3 ? e->d.smax : f == 4 ? 1 : 100 + s;
         ECHK(hipMemcpy(sf[f], buf, B * sizeof(int), hipMemcpyHostToDevice));
     }
-    int q[8] = {B, B, 0, 0, 0, 0, 0, 0};
+    int q[CT_Q_WORDS] = {B, B, 0, 0, 0, 0, 0, B};
+    q[9] = B;
+    q[10] = B;
     ECHK(hipMemcpy(e->d.q, q, sizeof q, hipMemcpyHostToDevice));
     const long self_el = (long)DEC_N * B * DEC_H * e->d.kv_rows * DEC_DK;
     const long cross_el = (long)DEC_N * e->d.max_req * DEC_H * e->d.tmax * DEC_DK;

@@ -24,10 +24,6 @@
 namespace {
 
 constexpr int CT_ATTN_QPARTS = 4;   // most query partial slices a launch may pass
-// 1: two key trips in flight per lane group (software pipelined)
-#ifndef CT_ATTN_PIPE
-#define CT_ATTN_PIPE 1
-#endif
 // lanes per key (16: 8 head dims a lane, 8: 16 a lane)
 #ifndef CT_ATTN_LPK
 #define CT_ATTN_LPK 16
@@ -258,7 +254,6 @@ __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
             }
         m = mn;
     };
-#if CT_ATTN_PIPE
     // two trips in flight: the next trip's loads are issued before the
     // current trip is used (register sets A and B alternate)
     Raw kB[KPI][NV], vB[KPI][NV];
@@ -272,13 +267,6 @@ __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
         load_trip(k1 + STEP, kA, vA);
         use_trip(k1, kB, vB);
     }
-#else
-    for (int k0 = kb + g; k0 < ke; k0 += STEP) {
-        Raw kr[KPI][NV], vr[KPI][NV];
-        load_trip(k0, kr, vr);
-        use_trip(k0, kr, vr);
-    }
-#endif
 
     __shared__ float sm[NG], sl[NG], so[NG][DEC_DK];
     if (ls == 0) { sm[g] = m; sl[g] = l; }

@@ -72,10 +72,10 @@ __device__ __forceinline__ int block_prefix(int v, int *sums, int &total) {
 
 __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     const int tid = threadIdx.x, s = tid;
-    __shared__ int s_app[CT_ENG_MAX_SLOTS], s_q[4], s_asum[4];
+    __shared__ int s_app[CT_ENG_MAX_SLOTS], s_cand[CT_ENG_MAX_SLOTS], s_q[6], s_asum[4];
     __shared__ int s_wsum[4], s_left[4];
     __shared__ int s_pl[2 * CT_ENG_MAX_SLOTS], s_cl[2 * CT_ENG_MAX_SLOTS];   // row lengths this step
-    int r = -1, S = 0, np = 0, T = 0, tok = 0, pend = -1, q0 = 0, q1 = 0, f0 = 0, f1 = 0;
+    int r = -1, S = 0, np = 0, T = 0, tok = 0, pend = -1, q0 = 0, q1 = 0, f0 = 0, f1 = 0, wm = 0;
     if (s < d.slots) {
         r = d.slot_req[s];
         pend = d.pend[s];
@@ -86,39 +86,58 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     }
     if (tid == 0) {
         q0 = d.q[0]; q1 = d.q[1]; f0 = d.q[4];
-        f1 = __hip_atomic_load(&d.q[5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_q[0] = q0; s_q[1] = q1; s_q[2] = f0; s_q[3] = f1;
+        // host-published words (possibly written while this step runs on
+        // another stream): acquire, so the queue entries read after them are
+        // at least as new
+        f1 = __hip_atomic_load(&d.q[5], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+        wm = __hip_atomic_load(&d.q[7], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+        s_q[0] = q0; s_q[1] = q1; s_q[2] = f0; s_q[3] = f1; s_q[4] = wm;
     }
     // Released successors join the ring rq in slot order, then the free
     // slots, in slot order, take the waiting successors (rq[q0..), the ones
-    // joining now last), then fresh requests (fq[q4..q5)): the c-th free slot
-    // takes the c-th of them.  One prefix counts both (pending in the low 16
-    // bits, free in the high).
+    // joining now last) up to the first one not yet encoded (ring order is
+    // kept: it and those behind it wait), then fresh requests (fq[q4..q5),
+    // all encoded when published): the c-th free slot takes the c-th of them.
+    // One prefix counts both (pending in the low 16 bits, free in the high).
     const bool is_p = s < d.slots && pend >= 0, is_f = s < d.slots && r < 0;
     int tot;
     const int pre = block_prefix((int)is_p | ((int)is_f << 16), s_asum, tot);
     const int pidx = pre & 0xffff, fidx = pre >> 16, npend = tot & 0xffff, nfree = tot >> 16;
-    q0 = s_q[0]; q1 = s_q[1]; f0 = s_q[2]; f1 = s_q[3];
+    q0 = s_q[0]; q1 = s_q[1]; f0 = s_q[2]; f1 = s_q[3]; wm = s_q[4];
     if (is_p) {
         d.rq[q1 + pidx] = pend;
         s_app[pidx] = pend;
     }
+    if (tid == 0) s_q[5] = INT_MAX;
     __syncthreads();
     const int waiting = q1 - q0, avail = waiting + npend;
+    // the first lim ring entries (one past what the free slots can take, so
+    // the head left behind is checked too): the admissible prefix ends at
+    // the first entry whose encoder batch is not published
+    const int lim = min(min(avail, nfree + 1), (int)CT_ENG_MAX_SLOTS);
+    if (tid < lim) {
+        const int c = tid < waiting ? d.rq[q0 + tid] : s_app[tid - waiting];
+        s_cand[tid] = c;
+        if (c >= wm) atomicMin(&s_q[5], tid);
+    }
+    __syncthreads();
+    const int blocked = s_q[5];                  // INT_MAX: none of the lim
+    const int ready = min(blocked, avail);       // admissible successors
+    const int from_rq = min(nfree, ready);
     bool fresh = false;
     if (is_f) {
-        if (fidx < waiting) { r = d.rq[q0 + fidx]; fresh = true; }
-        else if (fidx < avail) { r = s_app[fidx - waiting]; fresh = true; }
-        else if (fidx - avail < f1 - f0) {
-            r = __hip_atomic_load(&d.fq[f0 + fidx - avail], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (fidx < from_rq) { r = s_cand[fidx]; fresh = true; }
+        else if (fidx - from_rq < f1 - f0) {
+            r = __hip_atomic_load(&d.fq[f0 + fidx - from_rq], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             fresh = true;
         }
     }
     if (tid == 0) {
-        const int from_rq = min(nfree, avail);
         d.q[0] = q0 + from_rq;
         d.q[1] = q1 + npend;
         d.q[4] = f0 + min(nfree - from_rq, f1 - f0);
+        d.q[8] = blocked < lim ? 1 : 0;
+        d.q[9] = wm;
     }
     int want = 0;
     if (s < d.slots) {
@@ -241,6 +260,7 @@ __global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *l
     int best = (xf != xf || bi == INT_MAX) ? first : bi;
     if ((flags & 2) && ng == lim - 1) best = EOS_ID;
     d.req_out[(long)r * d.smax + ng] = best;
+    d.req_score[(long)r * d.smax + ng] = bv;
     d.req_ngen[r] = ng + 1;
     d.slot_ng[s] = ng + 1;
     d.slot_tok[s] = best;
@@ -262,6 +282,7 @@ __global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *l
             for (int i = 0; i < nc; i++) pp[2 + i] = og[gen - 1 - nc + i];
             d.req_np[nx] = np + nc;
             d.pend[s] = nx;
+            atomicAdd(&d.q[10], 1);
         }
         atomicAdd(&d.q[2], 1);
     }

@@ -496,11 +496,7 @@ __device__ __forceinline__ void lds_dma16(const void *g, uint16_t *lds_wave_base
 // 16-byte chunk c of a 64-byte LDS row R sits at chunk swz(R, c).  The 16 rows
 // a fragment read touches then cover every bank once whether the LDS serves
 // 16 lanes over 64 banks or 8 lanes over 32 banks per cycle.
-#ifndef CT_SWZ_OLD
 __device__ __forceinline__ int swz(int R, int c) { return c ^ (((R >> 1) ^ (R >> 2)) & 3); }
-#else
-__device__ __forceinline__ int swz(int R, int c) { return c ^ ((R >> 2) & 3); }
-#endif
 
 template <bool GLU>
 __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int n_nt, int vepi) {

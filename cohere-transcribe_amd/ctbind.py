@@ -120,6 +120,15 @@ class SynthModel:
         raw = np.ctypeslib.as_array(C.cast(self.ptr(field), C.POINTER(C.c_uint16)), shape=(n,))
         return (raw.astype(np.uint32) << 16).view(np.float32)
 
+    def set_bf16(self, field, index, value):
+        """Overwrites one bf16 value of a tensor in the host image (value must
+        be exactly representable); upload the blob again afterwards."""
+        f = np.float32(value)
+        raw = int(f.view(np.uint32))
+        if raw & 0xFFFF:
+            raise ValueError(f"{value} is not a bf16 value")
+        C.cast(self.ptr(field), C.POINTER(C.c_uint16))[index] = raw >> 16
+
     def weights_ref(self):
         return C.byref(self.W)
 
@@ -229,6 +238,7 @@ _ENGINE_SIGS = {
     "hipb_process": ([C.c_void_p, C.c_int, C.c_int], C.c_long),
     "hipb_finished": ([C.c_void_p], C.c_int),
     "hipb_tokens": ([C.c_void_p, C.c_int, C.c_void_p, C.c_int], C.c_int),
+    "hipb_token_scores": ([C.c_void_p, C.c_int, C.c_void_p, C.c_int], C.c_int),
     "hipb_slot_of": ([C.c_void_p, C.c_int], C.c_int),
     "hipb_logits": ([C.c_void_p, C.c_int, C.c_void_p], None),
     "hipb_enc_out": ([C.c_void_p, C.c_int, C.c_void_p], None),
@@ -293,6 +303,12 @@ class Engine:
         n = self.L.hipb_tokens(self.e, req, out.ctypes.data, MAX_SEQ)
         return out[:n].copy()
 
+    def scores(self, req):
+        """Per generated token, the largest logit the argmax weighed."""
+        out = np.zeros(MAX_SEQ, np.float32)
+        n = self.L.hipb_token_scores(self.e, req, out.ctypes.data, MAX_SEQ)
+        return out[:n].copy()
+
     def slot_of(self, req):
         return self.L.hipb_slot_of(self.e, req)
 
@@ -342,6 +358,8 @@ _ENGINE_SIGS.update({
                                  C.c_float, C.c_float, C.c_float, C.POINTER(C.c_int)], C.c_int),
     "hipb_chunk_bounds": ([C.c_void_p, C.c_int, C.c_float, C.c_float, C.c_float, C.c_void_p, C.c_int],
                           C.c_int),
+    "hipb_test_hold_encoder": ([C.c_void_p, C.c_int, C.c_int], None),
+    "hipb_test_hold_expired": ([C.c_void_p], C.c_int),
 })
 
 
@@ -387,6 +405,8 @@ def _engine_mel(self, pcm):
 
 
 Engine.submit_pcm = _engine_extra
+Engine.hold_encoder = lambda self, batches, finished: self.L.hipb_test_hold_encoder(self.e, batches, finished)
+Engine.hold_expired = lambda self: bool(self.L.hipb_test_hold_expired(self.e))
 Engine.mel = _engine_mel
 Engine.reset = lambda self: self.L.hipb_reset(self.e)
 

@@ -81,7 +81,8 @@ int  hipb_submit_pcm_chunked(HipbEngine *e, const float *pcm, int n_samples, con
 int  hipb_chunk_bounds(const float *pcm, int n_samples, float silence_db, float silence_dur,
                        float target_sec, int *bounds, int cap);
 /* The same with the samples already in device memory (not copied; they must
- * stay valid until hipb_encode returns). */
+ * stay valid until the hipb_encode or hipb_process call that encodes them
+ * returns). */
 int  hipb_submit_pcm_device(HipbEngine *e, const float *dev_pcm, int n_samples, const int *prompt,
                             int n_prompt, int limit, int flags);
 /* Log-mel of one clip on the GPU, synchronously (N_MELS x (1 + n/160)). */
@@ -108,14 +109,30 @@ long hipb_run(HipbEngine *e, int chunk);
  * max_batch_frames encoder frames, each published to the slot table as soon
  * as its cross-attention K/V are written, while the calling thread runs
  * decode steps (chunk per host check) until every submitted request has
- * finished.  Same tokens as hipb_encode then hipb_run.  Returns the number
- * of steps. */
+ * finished.  A chained chunk released by its predecessor is admitted only
+ * once its own batch has been published (requests are encoded in submission
+ * order; the published watermark gates it), so the tokens are those of
+ * hipb_encode then hipb_run.  Device PCM passed to hipb_submit_pcm_device
+ * must stay valid until hipb_process returns.  Returns the number of
+ * steps. */
 long hipb_process(HipbEngine *e, int max_batch_frames, int chunk);
+/* Test support for hipb_process: after publishing `after_batches` encoder
+ * batches the encoder thread waits (host-side, at most 60 s) until the decode
+ * loop has seen `until_finished` requests finish, so a test can make a
+ * chained chunk's predecessor retire before the chunk is encoded.  0
+ * batches: no hold.  hipb_test_hold_expired reports whether the last hold
+ * ran out of time. */
+void hipb_test_hold_encoder(HipbEngine *e, int after_batches, int until_finished);
+int  hipb_test_hold_expired(HipbEngine *e);
 /* Number of requests finished so far (device counter, synchronises). */
 int  hipb_finished(HipbEngine *e);
 
 /* Results and inspection (synchronise the engine's stream). */
 int  hipb_tokens(HipbEngine *e, int req, int *out, int cap);        /* returns count */
+/* Per generated token, the largest logit the argmax weighed at that step (EOS
+ * left out when suppressed; also for a forced EOS): a request's logits bits
+ * in compact form, for batch-vs-single checks.  Returns the count. */
+int  hipb_token_scores(HipbEngine *e, int req, float *out, int cap);
 int  hipb_slot_of(HipbEngine *e, int req);                          /* -1 if none    */
 void hipb_logits(HipbEngine *e, int slot, float *out);              /* VOCAB floats  */
 void hipb_enc_out(HipbEngine *e, int req, float *out);              /* T_enc x DEC_D */

@@ -33,6 +33,11 @@ static float round_bf16(float x) {
     return r;
 }
 
+/* In-place rounding of n values (exported for the rounding-mode test). */
+void orc_round_bf16_n(float *x, long n) {
+    for (long i = 0; i < n; i++) x[i] = round_bf16(x[i]);
+}
+
 /* ------------------------------------------------------------------ */
 /* Kernel-boundary functions                                           */
 /* ------------------------------------------------------------------ */

@@ -66,6 +66,7 @@ typedef struct {
     int S;                    /* tokens already in the self cache */
     int kv_bf16;              /* round K/V to bf16 when cached (bf16-KV mode) */
 } OrcSeq;
+void orc_round_bf16_n(float *x, long n);
 void orc_seq_init(OrcSeq *s, const float *ca_k, const float *ca_v, int T_enc, int kv_bf16);
 void orc_seq_free(OrcSeq *s);
 /* Feeds S_q new tokens at positions s->S .. s->S+S_q-1 through the decoder

@@ -202,3 +202,50 @@ void ref_transcribe_batch(const float *mel_batch, int B, const int *T_mel, int T
     backend_arena_free(g_base);
     free(toks); free(S); free(Sd); free(act); free(cur); free(nxt); free(Te);
 }
+
+/* ------------------------------------------------------------------ */
+/* Timing support for the CPU baseline: pieces of the reference's own  */
+/* host graph, run on whatever backend this file is linked with.       */
+/* ------------------------------------------------------------------ */
+
+/* n_layers Conformer layers (model.h conformer_layer, layers 0..n-1) over
+ * T frames: x_io [T][ENC_D] in, out. */
+void ref_encoder_layers(float *x_io, int T, int n_layers) {
+    const int T_mel = 8 * T;           /* any T_mel whose T_enc is T sizes the scratch */
+    arena_begin((size_t)T * ENC_D + (size_t)(2 * T - 1) * ENC_D + work_floats(T_mel) + 4096);
+    float *x = take((size_t)T * ENC_D), *pe = take((size_t)(2 * T - 1) * ENC_D);
+    float *work = take(work_floats(T_mel));
+    backend_htod(x, x_io, (size_t)T * ENC_D);
+    backend_make_rel_pos_emb(pe, T);
+    for (int l = 0; l < n_layers; l++) conformer_layer(x, pe, T, &W.enc[l % ENC_N], work);
+    backend_dtoh(x_io, x, (size_t)T * ENC_D * sizeof(float));
+    backend_arena_free(g_base);
+}
+
+/* n_steps single-sequence decode steps (model.h decoder_step_decode) from
+ * S0 tokens already in the self caches, over T_enc frames of cross K/V; the
+ * caches hold a fixed pattern.  Returns the last token id. */
+int ref_decode_steps(int T_enc, int S0, int n_steps) {
+    const int T_mel = 8 * T_enc;
+    arena_begin(2 * (size_t)DEC_N * T_enc * DEC_D + 2 * (size_t)DEC_N * MAX_SEQ * DEC_D
+                + (size_t)MAX_SEQ * DEC_D + work_floats(T_mel) + 65536);
+    float *ck[DEC_N], *cv[DEC_N], *sk[DEC_N], *sv[DEC_N];
+    for (int l = 0; l < DEC_N; l++) { ck[l] = take((size_t)T_enc * DEC_D); cv[l] = take((size_t)T_enc * DEC_D); }
+    for (int l = 0; l < DEC_N; l++) { sk[l] = take((size_t)MAX_SEQ * DEC_D); sv[l] = take((size_t)MAX_SEQ * DEC_D); }
+    float *h = take((size_t)MAX_SEQ * DEC_D), *work = take(work_floats(T_mel));
+    const size_t nfill = (size_t)(MAX_SEQ > T_enc ? MAX_SEQ : T_enc) * DEC_D;
+    float *pat = malloc(nfill * sizeof(float));
+    for (size_t i = 0; i < nfill; i++) pat[i] = (float)((int)(i * 2654435761u >> 20) % 201 - 100) * 1e-3f;
+    for (int l = 0; l < DEC_N; l++) {
+        backend_htod(ck[l], pat, (size_t)T_enc * DEC_D);
+        backend_htod(cv[l], pat, (size_t)T_enc * DEC_D);
+        backend_htod(sk[l], pat, (size_t)MAX_SEQ * DEC_D);
+        backend_htod(sv[l], pat, (size_t)MAX_SEQ * DEC_D);
+    }
+    free(pat);
+    backend_decode_set_S(S0);
+    int id = 100;
+    for (int i = 0; i < n_steps; i++) id = decoder_step_decode(id, T_mel, T_enc, ck, cv, sk, sv, h, work);
+    backend_arena_free(g_base);
+    return id;
+}

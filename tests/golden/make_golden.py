@@ -14,6 +14,11 @@ Run in the container that holds the reference sources, after
                             and batched (weights seed 5, spec init).
   model_small_hot.npz       the same with the decoder-hot weight variant, where
                             greedy decoding is input-dependent.
+  config_c0c1_v{0,2}.npz    `configs`: the single-sequence path at benchmark
+                            lengths (one 8 s clip with 48 tokens, two 10 s
+                            clips with 96 tokens), fp32 KV, EOS suppressed:
+                            encoder outputs, token ids, three logits rows per
+                            clip and every step's top-1/top-2 margin.
 
 Only data is written (inputs are regenerated from the stated seeds; their
 checksums are stored to detect drift).
@@ -119,6 +124,74 @@ def model_small(variant, fname):
     np.savez_compressed(os.path.join(HERE, fname), **res)
 
 
+# Benchmark-configuration fixtures: the reference host graph (model.h
+# transcribe_chunk path, transcribe.c:264-390) on the reference CPU backend,
+# fp32 KV, greedy with EOS suppressed, at the lengths of the single-clip
+# configuration (one 8 s clip, 48 tokens) and two clips of the uniform batch
+# configuration (10 s, 96 tokens).  Spec weights (variant 0: greedy repeats one
+# token) and decoder-hot weights (variant 2: input-dependent tokens).
+CONFIG_SEED = MODEL_SEED
+CONFIG_JOBS = {"c0": [(8 * 16000, 800, 48)],
+               "c1": [(10 * 16000, 1000, 96), (10 * 16000, 1001, 96)]}
+CONFIG_VARIANTS = (0, 2)
+
+
+def config_fname(variant):
+    return f"config_c0c1_v{variant}.npz"
+
+
+def margins(lg):
+    """(top1 - top2) / |top1| of each logits row with EOS excluded, the
+    row's gap between the chosen token and the runner-up."""
+    x = np.asarray(lg, np.float64).copy()
+    x[:, cb.EOS] = -np.inf
+    top = -np.sort(-x, axis=1)[:, :2]
+    return (top[:, 0] - top[:, 1]) / np.abs(top[:, 0])
+
+
+def config_job(args):
+    variant, name, idx, n, seed, limit = args
+    lib = C.CDLL(os.path.join(REF, "libref_model.so"))
+    P, I = C.c_void_p, C.c_int
+    lib.ref_set_weights.argtypes = [P]
+    lib.ref_transcribe_single.argtypes = [P, I, P, I, I, I, I, P, P, P]
+    lib.ref_transcribe_single.restype = I
+    model = cb.SynthModel(seed=CONFIG_SEED, variant=variant, nthreads=2)
+    lib.ref_set_weights(model.weights_ref())
+    mel = ob.compute_mel(cb.synth_audio(n, seed))
+    prompt = np.asarray(cb.PROMPT, np.int32)
+    toks = np.zeros(limit, np.int32)
+    lg = np.zeros((limit, cb.VOCAB), np.float32)
+    eh = np.zeros((cb.t_enc(mel.shape[1]), cb.DEC_D), np.float32)
+    t0 = time.time()
+    got = lib.ref_transcribe_single(mel.ctypes.data, mel.shape[1], prompt.ctypes.data, len(prompt),
+                                    limit, 1, 0, toks.ctypes.data, lg.ctypes.data, eh.ctypes.data)
+    assert got == limit
+    rows = np.asarray([0, limit // 2, limit - 1], np.int32)
+    key = f"{name}_{idx}"
+    print(f"v{variant} {key}: T_enc {eh.shape[0]}, {time.time() - t0:.0f} s, tokens {toks[:8]}...",
+          flush=True)
+    return variant, {f"{key}_samples": np.int64(n), f"{key}_seed": np.int64(seed),
+                     f"{key}_mel_sum": np.float64(checksum(mel)), f"{key}_tokens": toks,
+                     f"{key}_enc_h": eh, f"{key}_rows": rows, f"{key}_logits": lg[rows],
+                     f"{key}_margin": margins(lg).astype(np.float32),
+                     f"{key}_logit_absmax": np.abs(lg).max(axis=1).astype(np.float32)}
+
+
+def configs():
+    import multiprocessing as mp
+    jobs = [(v, name, i, n, s, lim) for v in CONFIG_VARIANTS for name, js in CONFIG_JOBS.items()
+            for i, (n, s, lim) in enumerate(js)]
+    with mp.get_context("fork").Pool(len(jobs)) as pool:
+        res = pool.map(config_job, jobs)
+    for v in CONFIG_VARIANTS:
+        out = {"weight_seed": np.int64(CONFIG_SEED), "variant": np.int64(v)}
+        for vv, d in res:
+            if vv == v:
+                out.update(d)
+        np.savez_compressed(os.path.join(HERE, config_fname(v)), **out)
+
+
 if __name__ == "__main__":
     which = sys.argv[1:] or ["bin", "ext", "model"]
     if "bin" in which:
@@ -128,3 +201,5 @@ if __name__ == "__main__":
     if "model" in which:
         for var, fname in MODEL_FIXTURES.items():
             model_small(var, fname)
+    if "configs" in which:
+        configs()

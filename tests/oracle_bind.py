@@ -45,6 +45,7 @@ _SIGS = {
     "orc_compute_mel": [_P, _I, _P],
     "orc_mel_filterbank": [_P],
     "orc_chunk_bounds": [_P, _I, _F, _F, _F, _P, _I],
+    "orc_round_bf16_n": [_P, C.c_long],
 }
 _RET = {"orc_argmax": _I, "orc_T_enc": _I, "orc_T_mel": _I, "orc_transcribe": _I,
         "orc_chunk_bounds": _I}

@@ -250,3 +250,46 @@ def test_reference_host_on_hip(hip, variant, fname):
                              lim.ctypes.data, 1, 1, max(BATCH_LIMITS), bt.ctypes.data, nb.ctypes.data, None)
     assert np.array_equal(nb, g["batch_n"])
     assert np.array_equal(bt, g["batch_tokens"])
+
+
+ENC_T = [17, 37, 101, 376]
+
+
+@pytest.mark.parametrize("T", ENC_T)
+def test_encoder_ops_long_T_vs_oracle(hip, kmodel, T):
+    """Rel-pos MHSA and the conformer conv module at encoder lengths of 1.3 to
+    30 s (T = 17, 37, 101, 376 frames: several 16-query blocks, multi-tile
+    score loops, the 32-key PV loop), through the ABI against the oracle
+    (backends/cpu/backend.c:244-337): own position table and the batch form
+    whose table is built for the longest clip (376) and read from row
+    376 - T (model.h:586-592).  <= 1e-4 relative per tensor."""
+    dev = ks.ArenaDev(hip)
+    o = ob.oracle()
+    rng = np.random.default_rng(1000 + T)
+    x0 = rng.standard_normal((T, cb.ENC_D)).astype(np.float32)
+    D = cb.ENC_D
+    work = dev.zeros((5 * T - 1) * D + max(T * (3 * T - 1), 2 * T * D))
+    pe_own = dev.zeros(2 * T - 1, D)
+    hip.backend_make_rel_pos_emb(pe_own[0], T)
+    TM = 376
+    pe_max = dev.zeros(2 * TM - 1, D)
+    hip.backend_make_rel_pos_emb(pe_max[0], TM)
+    pe_ref = np.zeros((2 * T - 1, D), np.float32)
+    o.orc_make_rel_pos_emb(pe_ref.ctypes.data, T)
+    assert relerr(dev.get(pe_own), pe_ref) <= 1e-6
+    for layer in (0, 7):
+        want = x0.copy()
+        o.orc_rel_pos_mhsa(want.ctypes.data, pe_ref.ctypes.data, T, kmodel.elayer_ptr(layer), None)
+        for form, pe_ptr in (("own", pe_own[0]), ("shifted", pe_max[0] + (TM - T) * D * 4)):
+            x = dev.put(x0)
+            hip.backend_rel_pos_mhsa(x[0], pe_ptr, T, kmodel.elayer_ptr(layer), work[0])
+            e = relerr(dev.get(x), want)
+            print(f"case: rel_pos_mhsa T={T} layer {layer} {form} table: relerr {e:.2e}", flush=True)
+            assert e <= TOL, (T, layer, form, e)
+        want = x0.copy()
+        o.orc_conformer_conv(want.ctypes.data, T, kmodel.elayer_ptr(layer), None)
+        x = dev.put(x0)
+        hip.backend_conformer_conv(x[0], T, kmodel.elayer_ptr(layer), dev.zeros(3 * T * D)[0])
+        e = relerr(dev.get(x), want)
+        print(f"case: conformer_conv T={T} layer {layer}: relerr {e:.2e}", flush=True)
+        assert e <= TOL, (T, layer, e)

@@ -453,3 +453,50 @@ def test_engine_process_overlapped(hip, hot, mels, oracle_runs, chunked_oracle):
                 assert np.array_equal(eng.tokens(r), toks), (rnd, r)
     finally:
         eng.close()
+
+
+def test_engine_process_chain_waits_for_its_encoding(hip, hot, mels):
+    """A chained chunk whose predecessor retires before the chunk's encoder
+    batch is published waits for that batch: a long plain request and the
+    first chunk of a recording form encoder batch 0, the second chunk starts
+    batch 1, and the encoder thread is held after batch 0 until the first
+    chunk has finished.  Tokens equal hipb_encode + hipb_run bit for bit
+    (admitting the chunk early would attend over cross K/V not written yet)."""
+    rec = long_recording(REC_SEEDS[0])
+    bounds = cb.chunk_bounds(rec, **SPLIT)
+    assert len(bounds) >= 2
+    frames = [cb.t_enc(cb.t_mel(b - a)) for a, b in bounds]
+    long_mel = mels[1]
+    t_long = cb.t_enc(long_mel.shape[1])
+    batch0 = t_long + frames[0]
+    assert batch0 + frames[1] > batch0 >= max([t_long] + frames)
+    limit_chain, limit_long = 3, 40
+    max_frames = max([t_long] + frames)            # tmax <= batch0 keeps the batch cut there
+
+    def submit_all(eng):
+        plain = eng.submit(long_mel, limit_long, FLAGS)
+        chain = eng.submit_pcm_chunked(rec, limit_chain, FLAGS, **SPLIT)
+        return plain, chain
+
+    kw = dict(slots=2, max_requests=16, max_frames=max_frames, kv_bf16=True,
+              max_tokens=len(cb.PROMPT) + 64 + limit_long)
+    ref = cb.Engine(hot, **kw)
+    try:
+        plain, chain = submit_all(ref)
+        ref.encode()
+        ref.run(chunk=1)
+        want = [ref.tokens(r) for r in [plain] + chain]
+    finally:
+        ref.close()
+    eng = cb.Engine(hot, **kw)
+    try:
+        plain, chain = submit_all(eng)
+        eng.hold_encoder(1, 1)
+        print(f"case: chain {frames} frames, batch 0 = {batch0} frames, hold after batch 0", flush=True)
+        eng.process(max_batch_frames=batch0, chunk=1)
+        assert not eng.hold_expired()
+        assert eng.finished() == 1 + len(chain)
+        for r, w in zip([plain] + chain, want):
+            assert np.array_equal(eng.tokens(r), w), r
+    finally:
+        eng.close()

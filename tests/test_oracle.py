@@ -368,3 +368,142 @@ def test_oracle_matches_reference_model(variant):
         tb, _, eh_b = ob.transcribe(m, mel, lim, suppress=True, force=True)
         assert np.array_equal(tb, g["batch_tokens"][b, :g["batch_n"][b]])
         assert relerr(eh_b, g[f"enc_h{b}" if b else "enc_h0_batch"]) < 1e-5
+
+
+def test_oracle_matches_reference_at_single_clip_config():
+    """The benchmark's single-clip configuration (8 s, 101 encoder frames,
+    48 tokens) on the decoder-hot weights: the oracle reproduces the
+    reference fixture bit for bit (encoder output, every token, the stored
+    logits rows)."""
+    g = np.load(os.path.join(GOLD, "config_c0c1_v2.npz"))
+    m = cb.SynthModel(seed=int(g["weight_seed"]), variant=2)
+    mel = ob.compute_mel(cb.synth_audio(int(g["c0_0_samples"]), int(g["c0_0_seed"])))
+    toks, lg, eh = ob.transcribe(m, mel, len(g["c0_0_tokens"]), suppress=True, want_logits=True)
+    assert np.array_equal(eh.view(np.uint32), g["c0_0_enc_h"].view(np.uint32))
+    assert np.array_equal(toks, g["c0_0_tokens"])
+    assert np.array_equal(lg[g["c0_0_rows"]].view(np.uint32), g["c0_0_logits"].view(np.uint32))
+
+
+def _torch_decoder(m, enc_h, prompt, n_new, kv_bf16):
+    """Independent float64 restatement of the decoder (model.h:376-503 for
+    the prompt, 517-554 per token) in torch; K/V written to the caches, and
+    the cross K/V, are rounded to bf16 (round to nearest even, torch's
+    float32 -> bfloat16 conversion) when kv_bf16.  Greedy with EOS
+    suppressed.  Returns the logits of each generated token."""
+    import torch
+    t = lambda f, *shape: torch.from_numpy(m.tensor(f, int(np.prod(shape))).reshape(shape)).double()  # noqa: E731
+    D, H, DK = cb.DEC_D, cb.DEC_H, cb.DEC_DK
+
+    def rnd(x):
+        return x.float().to(torch.bfloat16).double() if kv_bf16 else x
+
+    def ln(x, w, b):
+        mu = x.mean(-1, keepdim=True)
+        var = ((x - mu) ** 2).mean(-1, keepdim=True)
+        return (x - mu) / torch.sqrt(var + 1e-5) * w + b
+
+    def attend(q, K, V, causal_from=None):
+        n, S = q.shape[0], K.shape[0]
+        qh = q.view(n, H, DK).transpose(0, 1)
+        kh, vh = K.view(S, H, DK).transpose(0, 1), V.view(S, H, DK).transpose(0, 1)
+        sc = qh @ kh.transpose(1, 2) / np.sqrt(DK)
+        if causal_from is not None:
+            j = torch.arange(S).view(1, S)
+            i = torch.arange(n).view(n, 1)
+            sc = sc.masked_fill(j > causal_from + i, -1e9)
+        return (torch.softmax(sc, -1) @ vh).transpose(0, 1).reshape(n, D)
+
+    L = [{f: None for f in cb.DLAYER_FIELDS} for _ in range(cb.DEC_N)]
+    for l in range(cb.DEC_N):
+        for f in cb.DLAYER_FIELDS:
+            if f.endswith("w") and not f.endswith("lnw") and f.startswith(("sa_", "ca_")):
+                L[l][f] = t(f"dec{l}.{f}", D, D)
+            elif f == "ffn_w1":
+                L[l][f] = t(f"dec{l}.{f}", cb.DEC_FF, D)
+            elif f == "ffn_w2":
+                L[l][f] = t(f"dec{l}.{f}", D, cb.DEC_FF)
+            elif f == "ffn_b1":
+                L[l][f] = t(f"dec{l}.{f}", cb.DEC_FF)
+            else:
+                L[l][f] = t(f"dec{l}.{f}", D)
+    etw, epw = t("etw", cb.VOCAB, D), t("epw", cb.MAX_SEQ, D)
+    eh = torch.from_numpy(enc_h).double()
+    ck = [rnd(eh @ L[l]["ca_kw"].T + L[l]["ca_kb"]) for l in range(cb.DEC_N)]
+    cv = [rnd(eh @ L[l]["ca_vw"].T + L[l]["ca_vb"]) for l in range(cb.DEC_N)]
+    sk = [torch.zeros(0, D, dtype=torch.float64) for _ in range(cb.DEC_N)]
+    sv = [torch.zeros(0, D, dtype=torch.float64) for _ in range(cb.DEC_N)]
+    toks, out = list(prompt), []
+    feed = list(prompt)
+    for _ in range(n_new):
+        S0, n = sum(1 for _ in range(sk[0].shape[0])), len(feed)
+        pos = torch.arange(S0, S0 + n)
+        h = ln(etw[torch.tensor(feed)] + epw[pos], t("elnw", D), t("elnb", D))
+        for l in range(cb.DEC_N):
+            P = L[l]
+            x = ln(h, P["sa_lnw"], P["sa_lnb"])
+            q = x @ P["sa_qw"].T + P["sa_qb"]
+            sk[l] = torch.cat([sk[l], rnd(x @ P["sa_kw"].T + P["sa_kb"])])
+            sv[l] = torch.cat([sv[l], rnd(x @ P["sa_vw"].T + P["sa_vb"])])
+            h = h + attend(q, sk[l], sv[l], causal_from=S0 if n > 1 else None) @ P["sa_ow"].T + P["sa_ob"]
+            x = ln(h, P["ca_lnw"], P["ca_lnb"])
+            q = x @ P["ca_qw"].T + P["ca_qb"]
+            h = h + attend(q, ck[l], cv[l]) @ P["ca_ow"].T + P["ca_ob"]
+            x = ln(h, P["ffn_lnw"], P["ffn_lnb"])
+            h = h + torch.relu(x @ P["ffn_w1"].T + P["ffn_b1"]) @ P["ffn_w2"].T + P["ffn_b2"]
+        last = ln(h[-1], t("dlnw", D), t("dlnb", D))
+        lg = t("hdb", cb.VOCAB) + etw @ last
+        out.append(lg.numpy())
+        x = lg.clone()
+        x[cb.EOS] = -np.inf
+        nxt = int(torch.argmax(x))
+        toks.append(nxt)
+        feed = [nxt]
+    return np.stack(out), toks[len(prompt):]
+
+
+# Same-mode bounds: fp32 caches agree to ~1e-6; with bf16 caches an
+# element whose fp32 value lies within the two computations' rounding noise
+# of a bf16 rounding boundary rounds differently, and those one-ulp flips
+# cascade through the layers (measured 2.5-3.5e-5, against ~2e-4 between
+# the two modes).
+KV_MODE_BOUND = {0: 5e-6, 1: 1e-4}
+
+
+@pytest.mark.parametrize("kv_bf16", [0, 1])
+def test_oracle_decoder_kv_modes_independent(kv_bf16):
+    """The oracle's decoder with fp32 and with bf16-rounded K/V caches
+    against an independent float64 torch restatement, on the oracle's own
+    encoder output for a short clip (perturbed weights, 6 tokens, EOS
+    suppressed).  The rounding matters: the restatement in the other mode
+    differs from the oracle several times more than in the same mode."""
+    m = cb.SynthModel(seed=5, variant=1)
+    mel = ob.compute_mel(cb.synth_audio(7200, 102))
+    toks, lg, eh = ob.transcribe(m, mel, 6, suppress=True, kv_bf16=bool(kv_bf16), want_logits=True)
+    same, tt = _torch_decoder(m, eh, cb.PROMPT, 6, kv_bf16)
+    other, _ = _torch_decoder(m, eh, cb.PROMPT, 6, 1 - kv_bf16)
+    assert tt == toks.tolist()
+    e_same, e_other = relerr(lg, same), relerr(lg, other)
+    print(f"kv_bf16={kv_bf16}: vs same-mode restatement {e_same:.2e}, other mode {e_other:.2e}")
+    assert e_same < KV_MODE_BOUND[kv_bf16]
+    assert e_other > 3 * e_same
+
+
+def test_oracle_bf16_rounding_is_nearest_even():
+    """The oracle's bf16 rounding of cached K/V is round-to-nearest-even
+    (torch's float32 -> bfloat16 conversion), checked bit for bit on random
+    values, exact ties both ways, the largest finite values and inf/nan."""
+    import torch
+    r = np.random.default_rng(7)
+    x = (r.standard_normal(100000) * np.exp(r.uniform(-20, 20, 100000))).astype(np.float32)
+    u = x.view(np.uint32)
+    ties = ((u[:2000] & 0xFFFF0000) | 0x8000).view(np.float32)          # exactly halfway
+    edge = np.array([3.3895314e38, -3.3895314e38, np.inf, -np.inf, 0.0, -0.0, 1e-45, 1.0],
+                    np.float32)
+    x = np.concatenate([x, ties, edge])
+    got = x.copy()
+    ob.oracle().orc_round_bf16_n(got.ctypes.data, len(got))
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    nan = np.array([np.nan], np.float32)
+    ob.oracle().orc_round_bf16_n(nan.ctypes.data, 1)
+    assert np.isnan(nan[0])
