@@ -263,6 +263,7 @@ def test_encoder_ops_long_T_vs_oracle(hip, kmodel, T):
     (backends/cpu/backend.c:244-337): own position table and the batch form
     whose table is built for the longest clip (376) and read from row
     376 - T (model.h:586-592).  <= 1e-4 relative per tensor."""
+    hip.backend_weights_upload_blob(kmodel.data_ptr, kmodel.data_bytes)
     dev = ks.ArenaDev(hip)
     o = ob.oracle()
     rng = np.random.default_rng(1000 + T)

@@ -188,8 +188,12 @@ def test_engine_batch_vs_single_bitexact(hip, hot, mels):
 @pytest.mark.parametrize("kv_bf16", [False, True])
 def test_engine_logits_match_oracle(hip, hot, mels, kv_bf16):
     """Logits behind every generated token, engine (4 slots, ragged) vs the
-    oracle's fp32 path: max relative error per row within 1e-2 (measured
-    ~1e-5: split-bf16 activations, fp32 accumulation)."""
+    oracle in the same KV mode: max relative error per row within the
+    specified 1e-2, and with fp32 KV within a regression bound of 1e-4
+    (measured 4e-5: split-bf16 activations, fp32 accumulation).  With bf16
+    KV two correct implementations differ by ~4e-3 on these decoder-hot
+    weights: an element whose fp32 value lies within rounding noise of a bf16
+    rounding boundary rounds the other way, and the flips cascade."""
     eng = cb.Engine(hot, slots=4, max_requests=8, max_frames=64, kv_bf16=kv_bf16)
     try:
         for i, mel in enumerate(mels):
@@ -213,6 +217,8 @@ def test_engine_logits_match_oracle(hip, hot, mels, kv_bf16):
             worst = max(worst, e)
             assert e <= 1e-2, (i, j, e)
     print(f"  worst logits relerr {worst:.2e}")
+    if not kv_bf16:
+        assert worst <= 1e-4
 
 
 def test_engine_continuous_batching(hip, hot, mels, oracle_runs):
