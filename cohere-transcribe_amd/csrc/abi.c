@@ -129,6 +129,7 @@ void backend_init(int device_id) {
         CHK(hipMalloc((void **)&g_inv_freq[device_id], sizeof w));
         CHK(hipMemcpy(g_inv_freq[device_id], w, sizeof w, hipMemcpyHostToDevice));
     }
+    ct_static_init(device_id);
     pthread_mutex_unlock(&g_lock);
 }
 
@@ -304,9 +305,10 @@ void backend_make_rel_pos_emb(float *pe, int T) {
 
 void backend_rel_pos_mhsa(float *x, const float *pos_emb, int T, const ELayer *L, float *work) {
     require_init();
-    /* Scratch: Q, K, V (T rows), P (2T-1 rows), O (T rows) — within the
-     * (5T-1)*ENC_D + max(T(3T-1), 2T*ENC_D) floats the host provides
-     * (transcribe.c:286-293). */
+    /* Scratch: Q, K, V (T rows), P (2T-1 rows), O (T rows), i.e.
+     * CT_MHSA_SCRATCH_FLOATS(T) = (6T-1)*ENC_D floats, within the
+     * (5T-1)*ENC_D + max(T(3T-1), 2T*ENC_D) >= (7T-1)*ENC_D floats the host
+     * provides (transcribe.c:286-293). */
     const size_t TD = (size_t)T * ENC_D;
     float *Q = work, *K = Q + TD, *V = K + TD, *P = V + TD, *O = P + (size_t)(2 * T - 1) * ENC_D;
     const float *Xs[4] = {x, x, x, pos_emb};
@@ -317,6 +319,21 @@ void backend_rel_pos_mhsa(float *x, const float *pos_emb, int T, const ELayer *L
         backend_linear(Ys[i], Xs[i], Ws[i], Bs[i], i == 3 ? 2 * T - 1 : T, ENC_D, ENC_D);
     ctk_relpos_attn(O, Q, K, V, P, CT_W(L->sa_pbu), CT_W(L->sa_pbv), T, ct_t.stream);
     backend_linear(x, O, L->sa_ow, L->sa_ob, T, ENC_D, ENC_D);
+}
+
+void backend_rel_pos_mhsa_noalloc(float *x, const float *pos_emb, int T, const ELayer *L) {
+    if (T < 1 || T > CT_STATIC_MHSA_MAX_T) {
+        fprintf(stderr, "hip backend: backend_rel_pos_mhsa_noalloc: T=%d outside [1, %d] frames "
+                        "(its scratch holds a 30 s clip; use backend_rel_pos_mhsa with a workspace)\n",
+                T, CT_STATIC_MHSA_MAX_T);
+        exit(1);
+    }
+    require_init();
+    float *work = ct_static_scratch(ct_t.dev);
+    if (!work) CT_FATAL("backend_rel_pos_mhsa_noalloc: device scratch not set up");
+    if (CT_MHSA_SCRATCH_FLOATS(T) > ct_static_scratch_floats())
+        CT_FATAL("backend_rel_pos_mhsa_noalloc: scratch smaller than the layout");
+    backend_rel_pos_mhsa(x, pos_emb, T, L, work);
 }
 
 void backend_conformer_conv(float *x, int T, const ELayer *L, float *work) {

@@ -9,6 +9,13 @@
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 
+/* Longest clip (encoder frames) backend_rel_pos_mhsa_noalloc serves: 30 s,
+ * the longest file the reference batches unchunked (transcribe.c:894). */
+#define CT_STATIC_MHSA_MAX_T 376
+/* Scratch floats of backend_rel_pos_mhsa at T frames: Q, K, V (T rows each),
+ * P (2T - 1 rows) and O (T rows) of ENC_D (1280) floats. */
+#define CT_MHSA_SCRATCH_FLOATS(T) ((size_t)(6 * (T) - 1) * 1280)
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -307,6 +314,12 @@ typedef struct {
  * frame f (n_frames = sum of T). */
 void ctk_mel(float *mel, const CtMelClip *clips, int n_clips,
              const int *frame_clip, int n_frames, const CtMelTables *tab, hipStream_t s);
+
+/* Device scratch of backend_rel_pos_mhsa_noalloc: looked up once per device
+ * (with that device current), then its address for that device. */
+void ct_static_init(int dev);
+float *ct_static_scratch(int dev);
+size_t ct_static_scratch_floats(void);
 
 #ifdef __cplusplus
 }

@@ -191,6 +191,10 @@ ABI_SIGS = {
     "backend_sdp_attn_batch_decode_ca": ([_P, _P, _P, _P, _I, _I, _P], None),
 }
 assert len(ABI_SIGS) == 40
+# This backend's addition to the ABI (include/backend.h, after the 40).
+ABI_EXT_SIGS = {
+    "backend_rel_pos_mhsa_noalloc": ([_P, _P, _I, _P], None),
+}
 
 
 def bind_abi(lib):
@@ -198,6 +202,11 @@ def bind_abi(lib):
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = ret
+    for name, (args, ret) in ABI_EXT_SIGS.items():
+        fn = getattr(lib, name, None)
+        if fn is not None:
+            fn.argtypes = args
+            fn.restype = ret
     return lib
 
 

@@ -136,6 +136,18 @@ void backend_sdp_attn_batch_decode_ca(float *out, const float *Q,
                                       const float *K, const float *V,
                                       int T_k_stride, int B, float *work);       /* :226 */
 
+/* ---- Beyond the reference ABI ------------------------------------------ */
+/* backend_rel_pos_mhsa without the workspace argument, for callers that
+ * cannot allocate device memory (code under graph capture, serving loops,
+ * harnesses that forbid allocation).  It has no counterpart in the
+ * reference.  Its scratch (Q, K, V, P, O: (6T - 1) x ENC_D floats) is a
+ * static device array of 11.5 MB per device, held until the process ends,
+ * so T must be at most 376 frames (a 30 s clip); larger T prints an error
+ * and exits.  Allocates nothing.  Every call on one device uses the same
+ * scratch: calls that overlap on one device (other threads, other streams)
+ * race.  Same results, bit for bit, as backend_rel_pos_mhsa. */
+void backend_rel_pos_mhsa_noalloc(float *x, const float *pos_emb, int T, const ELayer *L);
+
 #ifdef __cplusplus
 }
 #endif

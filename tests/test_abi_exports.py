@@ -23,9 +23,12 @@ def exported(lib):
 
 
 def test_backend_abi_exports():
+    """The reference's 40 functions, plus the one allocation-free variant
+    declared after them."""
     names = declared("backend.h")
-    assert len(names) == 40
-    assert names == set(cb.ABI_SIGS)
+    assert names - set(cb.ABI_SIGS) == set(cb.ABI_EXT_SIGS)
+    assert len(names - set(cb.ABI_EXT_SIGS)) == 40
+    assert set(cb.ABI_SIGS) <= names
     syms = exported(cb.HIP_LIB)
     assert names <= syms
     lib = C.CDLL(cb.HIP_LIB)
@@ -91,3 +94,15 @@ def test_gemv_read_ahead_descriptor_covers_each_tile_once():
         g.wtile = 0
         lib.ctk_gemv_warm(C.byref(g), C.byref(w))
         assert w.gx == 0
+
+
+def test_noalloc_variant_rejects_long_clips():
+    """backend_rel_pos_mhsa_noalloc refuses clips beyond its 376-frame scratch
+    with a clear error before touching any device (checked in a child
+    process: the backend exits like the reference's fatal errors)."""
+    import sys
+    code = ("import ctypes as C; L = C.CDLL(%r); "
+            "L.backend_rel_pos_mhsa_noalloc(None, None, 377, None)" % cb.HIP_LIB)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1
+    assert "T=377 outside [1, 376]" in r.stderr
