@@ -27,8 +27,9 @@ per-kernel averages of `bench.py --roofline-only` can be set beside them):
                           against the bf16 dense MFMA peak;
   roofline                the one of them whose kernels take the largest
                           share of the stream's GPU time;
-  cpu_baseline            the oracle (fp32 C restatement of the reference CPU
-                          backend) on the host's cores on a bounded sample,
+  cpu_baseline            the reference CPU path (its model.h on its CPU
+                          backend, compiled from its sources) on the host's
+                          cores, one process per core, on a bounded sample
                           extrapolated to this workload's audio/token mix.
 HBM traffic per launch (`traffic`) comes from rocprofv3 FETCH_SIZE and
 WRITE_SIZE counter runs recorded in profiles/traffic.json, when present.
@@ -236,10 +237,96 @@ def with_traffic(rooflines):
     return rooflines
 
 
-def cpu_baseline(samples, limits):
-    """Oracle (C fp32 restatement of the reference CPU backend) on this host.
-    Sample: one 2 s clip through mel + encoder, then 16 decode steps; the
-    config mix is extrapolated from the two measured rates."""
+REF_MODEL_LIB = os.path.join(REPO, "oracle", "_ref", "libref_model.so")
+# The CPU baseline's sample: per process, one Conformer layer over the
+# frames of an 8 s clip and a few decode steps at the stream's median shape.
+CPU_LAYER_T = 101
+CPU_DEC_T, CPU_DEC_S0, CPU_DEC_STEPS = 76, 74, 4
+
+
+def cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _ref_worker(args):
+    """One process of the CPU baseline: the reference host graph (model.h)
+    on the reference CPU backend (backends/cpu/backend.c), both compiled from
+    the reference's sources into oracle/_ref/libref_model.so.  Runs on the
+    weight image inherited from the parent.  Returns (layer s, decode s)."""
+    what, T, n_layers, dec_T, dec_S0, dec_steps = args
+    lib = C.CDLL(REF_MODEL_LIB)
+    lib.ref_set_weights.argtypes = [C.c_void_p]
+    lib.ref_encoder_layers.argtypes = [C.c_void_p, C.c_int, C.c_int]
+    lib.ref_decode_steps.argtypes = [C.c_int, C.c_int, C.c_int]
+    lib.ref_decode_steps.restype = C.c_int
+    lib.ref_set_weights(C.byref(_CPU_MODEL.W))
+    x = np.random.default_rng(T).standard_normal((T, cb.ENC_D)).astype(np.float32)
+    t0 = time.perf_counter()
+    lib.ref_encoder_layers(x.ctypes.data, T, n_layers)
+    t1 = time.perf_counter()
+    lib.ref_decode_steps(dec_T, dec_S0, dec_steps)
+    t2 = time.perf_counter()
+    return t1 - t0, t2 - t1
+
+
+_CPU_MODEL = None
+
+
+def cpu_baseline(samples, limits, procs=None):
+    """The reference CPU backend timed on this host's cores, before the GPU
+    is touched.  The reference runs one sequence per thread, with as many
+    CPU "devices" as cores (transcribe.c:947-984, backends/cpu/backend.c:
+    21-24); here one process per core, each timing a bounded sample of the
+    reference's own host graph: one Conformer layer over 101 frames (an 8 s
+    clip) and 4 decode steps (self length 74, 76 encoder frames).  The
+    per-frame and per-token costs are extrapolated to the stream's audio and
+    token rows (prompt rows are prefilled, so each costs about a decode
+    step); the aggregate is the per-process rate times the process count,
+    all processes running at once.  Falls back to the oracle (kind "port")
+    where the reference library is not built."""
+    global _CPU_MODEL
+    import multiprocessing as mp
+    procs = procs or min(16, len(os.sched_getaffinity(0)))
+    audio = float(np.sum(samples)) / cb.SR
+    T_enc = np.asarray([cb.t_enc(cb.t_mel(int(n))) for n in samples], np.float64)
+    rows = float(np.sum(limits)) + len(cb.PROMPT) * len(limits)
+    if not os.path.exists(REF_MODEL_LIB):
+        return cpu_baseline_port(samples, limits)
+    _CPU_MODEL = cb.SynthModel(seed=1234, variant=0)
+    job = ("sample", CPU_LAYER_T, 1, CPU_DEC_T, CPU_DEC_S0, CPU_DEC_STEPS)
+    t0 = time.perf_counter()
+    with mp.get_context("fork").Pool(procs) as pool:
+        res = pool.map(_ref_worker, [job] * procs)
+    wall = time.perf_counter() - t0
+    _CPU_MODEL = None
+    t_layer = float(np.mean([r[0] for r in res]))
+    t_step = float(np.mean([r[1] for r in res])) / CPU_DEC_STEPS
+    per_frame = t_layer * cb.ENC_N / CPU_LAYER_T          # s of one process per encoder frame
+    t_proc = float(np.sum(T_enc)) * per_frame + rows * t_step
+    per_proc = audio / t_proc
+    return {"value": round(per_proc * procs, 4), "unit": "audio-sec/sec", "cores": procs,
+            "kind": "reference",
+            "sample": f"{procs} processes at once, one per core (the reference's thread-per-device "
+                      f"pool), each running the reference's model.h on its CPU backend: one "
+                      f"Conformer layer over {CPU_LAYER_T} frames ({t_layer:.2f} s) and "
+                      f"{CPU_DEC_STEPS} decode steps at S={CPU_DEC_S0}, T_enc={CPU_DEC_T} "
+                      f"({t_step:.3f} s/step); extrapolated to the stream's {audio:.0f} audio-s "
+                      f"({int(np.sum(T_enc))} encoder frames) and {int(rows)} token rows: "
+                      f"{per_proc:.4f} audio-s/s per process; {wall:.1f} s wall",
+            "cpu_model": cpu_model_name(), "extrapolated": True}
+
+
+def cpu_baseline_port(samples, limits):
+    """The oracle (C fp32 restatement of the reference CPU backend, OpenMP),
+    used when the reference library is not built: one 2 s clip through mel +
+    encoder, then 16 decode steps, extrapolated to the stream's mix."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
     import oracle_bind as ob
     threads = min(16, os.cpu_count() or 1)
@@ -266,7 +353,46 @@ def cpu_baseline(samples, limits):
     return {"value": round(audio / t_est, 4), "unit": "audio-sec/sec", "cores": threads, "kind": "port",
             "sample": "one 2 s clip: mel + 48-layer encoder, then prompt + 16 greedy tokens; "
                       f"encoder {enc_rate:.3f} audio-s/s, decode {dec_rate:.2f} tok/s, "
-                      "extrapolated to the stream's audio/token mix"}
+                      "extrapolated to the stream's audio/token mix",
+            "cpu_model": cpu_model_name(), "extrapolated": True}
+
+
+def cpu_single_clip_full(procs):
+    """The single-clip configuration in full on the reference CPU path (8 s
+    clip, 48 tokens, EOS suppressed): one process alone, then `procs`
+    processes at once.  Minutes of CPU time: run on request only."""
+    global _CPU_MODEL
+    import multiprocessing as mp
+    _CPU_MODEL = cb.SynthModel(seed=1234, variant=0)
+    out = {}
+    for n in (1, procs):
+        t0 = time.perf_counter()
+        with mp.get_context("fork").Pool(n) as pool:
+            res = pool.map(_ref_single_clip, [8] * n)
+        wall = time.perf_counter() - t0
+        out[n] = {"wall_s": round(wall, 1), "per_clip_s": [round(r, 1) for r in res],
+                  "audio_sec_per_sec": round(8.0 * n / wall, 4)}
+    _CPU_MODEL = None
+    return {"config": "8 s clip, 48 tokens, EOS suppressed (reference model.h + CPU backend)",
+            "cpu_model": cpu_model_name(), "runs": out}
+
+
+def _ref_single_clip(secs):
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import oracle_bind as ob
+    lib = C.CDLL(REF_MODEL_LIB)
+    lib.ref_set_weights.argtypes = [C.c_void_p]
+    lib.ref_transcribe_single.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                          C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    lib.ref_transcribe_single.restype = C.c_int
+    lib.ref_set_weights(C.byref(_CPU_MODEL.W))
+    mel = ob.compute_mel(cb.synth_audio(secs * cb.SR, 800))
+    prompt = np.asarray(cb.PROMPT, np.int32)
+    toks = np.zeros(48, np.int32)
+    t0 = time.perf_counter()
+    lib.ref_transcribe_single(mel.ctypes.data, mel.shape[1], prompt.ctypes.data, len(prompt), 48, 1, 0,
+                              toks.ctypes.data, None, None)
+    return time.perf_counter() - t0
 
 
 def measure_rooflines(hip, model, ev, step_reps=5):
@@ -295,11 +421,24 @@ def main():
                     help="run only the per-kernel roofline microbenchmarks (for profiling)")
     ap.add_argument("--no-rooflines", action="store_true",
                     help="run only the stream (for profiling its kernel mix)")
+    ap.add_argument("--cpu-single-clip", type=int, default=0, metavar="PROCS",
+                    help="only time the single-clip configuration in full on the reference CPU "
+                         "path, alone and with PROCS processes at once (minutes), and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (requests shard "
               "across GPUs with no exchange, see the design notes).", file=sys.stderr)
         sys.exit(2)
+    if args.cpu_single_clip:
+        print(json.dumps(cpu_single_clip_full(args.cpu_single_clip)))
+        return
+
+    samples, limits = make_stream(args.requests, seed=3)
+    # the CPU baseline runs first, in forked processes, before this process
+    # touches the GPU
+    cpu = None
+    if not (args.no_cpu_baseline or args.roofline_only):
+        cpu = cpu_baseline(samples, limits)
 
     hip = cb.hip()
     model = cb.SynthModel(seed=1234, variant=0)
@@ -312,7 +451,6 @@ def main():
         print(json.dumps({"rooflines": roofs, "decode_microbench": micro}))
         return
 
-    samples, limits = make_stream(args.requests, seed=3)
     offs = np.concatenate([[0], np.cumsum(samples)[:-1]])
     total = int(np.sum(samples))
     pcm = np.concatenate([cb.synth_audio(int(n), 1000 + i) for i, n in enumerate(samples)])
@@ -348,7 +486,6 @@ def main():
     eng.close()
 
     roofs, micro = ({}, {}) if args.no_rooflines else measure_rooflines(hip, model, ev)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(samples, limits)
 
     out = {
         "metric": METRIC, "value": round(rtfx, 2), "unit": "audio-sec/sec", "n_gpus": 1,
