@@ -225,15 +225,25 @@ def copy_calibration(ev, stream, mib=256):
     return {"bytes": n}
 
 
+MFMA_FILE = os.path.join(REPO, "profiles", "mfma.json")
+
+
 def with_traffic(rooflines):
-    """Fills `traffic` (HBM bytes per launch) from the counter runs."""
-    if not os.path.exists(TRAFFIC_FILE):
-        return rooflines
-    with open(TRAFFIC_FILE) as f:
-        tr = json.load(f)
-    for k, r in rooflines.items():
-        if k in tr.get("per_launch_bytes", {}):
-            r["traffic"] = tr["per_launch_bytes"][k]
+    """Fills `traffic` (HBM bytes per launch) from the FETCH_SIZE/WRITE_SIZE
+    counter runs and, for the encoder GEMM, the counter-derived MFMA
+    utilisation (SQ_INSTS_VALU_MFMA_MOPS_BF16, SQ_VALU_MFMA_BUSY_CYCLES,
+    GRBM_GUI_ACTIVE), when those runs are recorded under profiles/."""
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            tr = json.load(f)
+        for k, r in rooflines.items():
+            if k in tr.get("per_launch_bytes", {}):
+                r["traffic"] = tr["per_launch_bytes"][k]
+    if os.path.exists(MFMA_FILE) and "encoder_gemm" in rooflines:
+        with open(MFMA_FILE) as f:
+            mf = json.load(f)
+        if "encoder_gemm" in mf:
+            rooflines["encoder_gemm"]["mfma_counters"] = dict(mf["encoder_gemm"], source=mf["source"])
     return rooflines
 
 
