@@ -32,10 +32,15 @@ extern "C" {
 #define CT_KV_PAD 16
 #endif
 
-/* All pointers are device memory.  Slot-major arrays have `slots` entries,
- * request-major arrays `max_req`. */
+/* All pointers are device memory.  Slot-major arrays have `slots` entries.
+ * Request-major arrays are rings of ring_mask + 1 entries: request id r
+ * lives at r & ring_mask while it is outstanding (submitted, results not
+ * yet collected).  Encoder state (cross K/V, encoder output) is held in
+ * max_req entries, taken when a request is encoded and recycled after it
+ * retires. */
 typedef struct {
     int slots, max_req, smax, tmax;
+    int ring_mask;     /* request ring size - 1 (a power of two minus one)    */
     int rank_min;      /* steps of at least this many rows rank their rows    */
     int rows;          /* step rows: slots + spare prompt rows                  */
     int kv_rows;       /* rows per (slot, head) of the self caches (>= smax)    */
@@ -46,23 +51,25 @@ typedef struct {
      * read them beside the slot table: prompt ids, encoder frames, flags,
      * token limit, tokens generated, and the last token generated */
     int  *slot_np, *slot_T, *slot_flags, *slot_lim, *slot_ng, *slot_tok;
+    int  *slot_ent;    /* encoder entry of the slot's request                 */
     /* step rows [rows]: row s < slots is slot s's row, rows past `slots`
      * carry extra prompt tokens of a slot (row_slot) */
     int  *act;         /* 1 if the row decodes this step                       */
     int  *tok;         /* token embedded in the row                            */
     int  *pos_len;     /* self length the row attends to (position + 1)        */
     int  *cross_len;   /* encoder frames of the row's request (0 when idle)    */
-    int  *cross_idx;   /* request whose cross K/V the row reads                */
+    int  *cross_idx;   /* encoder entry whose cross K/V the row reads          */
     int  *row_slot;    /* slot whose self cache the row writes and reads       */
     /* rows of this step by descending self / cross length (ties by row):
      * the attention launches deal them to CUs so long and short rows pair */
     int  *rank_self, *rank_cross;
     long *kv_rowoff;   /* element offset of the row's self K/V entry, -1 idle  */
-    /* requests */
+    /* requests (rings) */
     int  *req_T, *req_limit, *req_flags, *req_np, *req_ngen;
-    int  *req_prompt;  /* [max_req][CT_PROMPT_MAX]                             */
-    int  *req_out;     /* [max_req][smax] generated tokens                     */
-    float *req_score;  /* [max_req][smax] the largest logit the argmax weighed
+    int  *req_entry;   /* encoder entry, written when the request is published */
+    int  *req_prompt;  /* [ring][CT_PROMPT_MAX]                                */
+    int  *req_out;     /* [ring][smax] generated tokens                        */
+    float *req_score;  /* [ring][smax] the largest logit the argmax weighed
                           for each token (EOS left out when suppressed): the
                           step's logits bits, for batch-vs-single checks      */
     /* chained chunks of one long recording: the request admitted after
@@ -74,6 +81,9 @@ typedef struct {
      * this step (-1 if none); eng_begin appends them in slot order.  Only the
      * step kernels write rq and pend. */
     int  *rq, *pend;
+    /* retired request ids in retirement order: ret[k & ring_mask] is the
+     * k-th request to finish (q[2] counts them) */
+    int  *ret;
     /* fresh queue: requests that wait for no predecessor, in submission
      * order, published by the host once encoded (the ids, then the count
      * q[5]); fq[q[4]..q[5]) wait for a slot.  Read with device-coherent

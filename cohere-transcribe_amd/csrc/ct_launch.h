@@ -187,6 +187,8 @@ void ctk_layernorm_split(uint16_t *hi, uint16_t *lo, const float *src, const uin
 void ctk_layernorm(float *dst, const float *src, const uint16_t *w, const uint16_t *b,
                    int T, int D, hipStream_t s);
 void ctk_add(float *dst, const float *src, long n, hipStream_t s);
+/* dst row dst_row[m] = src row m, M rows of D floats. */
+void ctk_copy_rows(float *dst, const float *src, const int *dst_row, int M, int D, hipStream_t s);
 void ctk_causal_mask(float *mask, int S, hipStream_t s);
 /* pe rows p = 0..2T-2 hold relative position T-1-p; inv_freq[k] (ENC_D/2
  * entries) is exp(-2k ln(1e4)/ENC_D), computed on the host. */

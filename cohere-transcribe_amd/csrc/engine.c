@@ -32,7 +32,12 @@ typedef struct {
     int n;               /* samples of a PCM request                          */
     int T_mel, T_enc;
     int chained;         /* admitted only after its predecessor chunk ends    */
-    long pool_off;       /* first frame of its encoder output in enc_pool     */
+    int entry;           /* encoder-state entry once encoded, else -1         */
+    int done;            /* seen retired by the host (recycle)                */
+    /* results copied to the host when its request-ring slot was reused */
+    int collected, n_out;
+    int *out;
+    float *score;
 } HostReq;
 
 struct HipbEngine {
@@ -52,10 +57,21 @@ struct HipbEngine {
         *wt_f2[DEC_N], *wt_lm;
     /* caches */
     void *kself, *vself;       /* [L][slots][H][kv_rows][128] */
-    void *kcross, *vcross;     /* [L][max_req][H][tmax][128] */
-    float *enc_pool;           /* encoder outputs, packed batch after batch:
-                                  <= max_req * tmax frames of DEC_D floats */
-    long pool_frames;          /* frames of enc_pool in use */
+    void *kcross, *vcross;     /* [L][entries][H][tmax][128] */
+    float *enc_pool;           /* encoder outputs, [entries][tmax][DEC_D] */
+    /* encoder-state entries (cross K/V + encoder output, max_requests of
+     * them): a FIFO of free ones (free_ent[i % entries] for i in
+     * [free_head, free_tail)), the request holding each, and the retired
+     * requests already recycled; the encoder thread of hipb_process takes
+     * entries while the decode loop returns them, under mu/cv */
+    int *free_ent, *ent_owner;
+    long free_head, free_tail;
+    int ret_seen;
+    int *h_ret;                /* pinned: retired ids read back */
+    pthread_mutex_t mu;
+    pthread_cond_t cv;
+    atomic_int n_assigned;     /* requests [0, n_assigned) have entries */
+    atomic_int stop;           /* hipb_process ends: the encoder thread quits its wait */
     /* step activations: h residual rows (fp32); lnf/attf/midf the decode
      * GEMMs' inputs in frag layout; parts K-slice partial sums */
     float *h, *q, *parts, *logits;
@@ -71,6 +87,7 @@ struct HipbEngine {
     int *h_enc;
     int fq_count;
     int proc_batch;            /* encoder batch frames of hipb_process */
+    int batch_frames;          /* encoder batch frames of the last hipb_encode */
     atomic_int enc_done;       /* the encoder thread has published every batch */
     atomic_int published;      /* encoded watermark last published (q[7]) */
     /* test support (hipb_test_hold_encoder): after publishing hold_batches
@@ -91,9 +108,12 @@ struct HipbEngine {
     uint16_t *eln_h, *eln_l, *emid_h, *emid_l, *eo_h, *eo_l, *edw_h, *edw_l;  /* pre-split GEMM inputs */
     size_t emel_cap;
     int *e_row_start, *e_row_len, *e_seq_off, *e_seq_T, *e_blk_seq, *e_blk_q0;
+    int *e_dstrow;             /* encoder-output row of each packed row */
     long *e_rowoff;
-    /* requests */
+    /* requests: host records grow with submissions; device fields live in
+     * rings of `ring` slots (id & (ring - 1)) */
     HostReq *req;
+    int req_cap, ring;
     int n_req, n_enc;
     int *h_tmp;                /* pinned staging */
     /* request fields as submitted (pinned): length, limit, flags, prompt
@@ -121,6 +141,7 @@ struct HipbEngine {
 };
 
 #define ECHK(x) ct_hip_check((x), #x, __FILE__, __LINE__)
+#define CT_META_FIELDS 6   /* request fields mirrored on the host (meta_field) */
 
 static void *dmalloc(size_t bytes) {
     void *p = NULL;
@@ -233,6 +254,13 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     const int S = cfg->slots, R = cfg->max_requests;
     const int tmax = (cfg->max_frames + 7) / 8 * 8;
     CtEngDev *d = &e->d;
+    /* request ring: at least 4 entries' worth of requests outstanding, and
+     * room for the retirements of 8 steps over all slots 4 times over (the
+     * host reads the retirement ring at least every ring / 4 of them) */
+    int ring = 1024;
+    while (ring < 4 * R || ring < 32 * S) ring <<= 1;
+    e->ring = ring;
+    d->ring_mask = ring - 1;
     if (cfg->prefill_rows < 0 || cfg->prefill_rows > CT_MAX_BATCH)
         CT_FATAL("hipb_create: prefill_rows outside [0, 256]");
     const int NR = S + cfg->prefill_rows;   /* step rows */
@@ -247,6 +275,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     d->slot_lim = dmalloc(S * sizeof(int));
     d->slot_ng = dmalloc(S * sizeof(int));
     d->slot_tok = dmalloc(S * sizeof(int));
+    d->slot_ent = dmalloc(S * sizeof(int));
     d->act = dmalloc(NR * sizeof(int));
     d->tok = dmalloc(NR * sizeof(int));
     d->pos_len = dmalloc(NR * sizeof(int));
@@ -257,24 +286,27 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     d->rank_cross = dmalloc(NR * sizeof(int));
     e->warm_sink = dmalloc(1024);
     d->kv_rowoff = dmalloc(NR * sizeof(long));
-    d->req_T = dmalloc(R * sizeof(int));
-    d->req_limit = dmalloc(R * sizeof(int));
-    d->req_flags = dmalloc(R * sizeof(int));
-    d->req_np = dmalloc(R * sizeof(int));
-    d->req_ngen = dmalloc(R * sizeof(int));
-    d->req_prompt = dmalloc((size_t)R * CT_PROMPT_MAX * sizeof(int));
-    d->req_out = dmalloc((size_t)R * d->smax * sizeof(int));
-    d->req_score = dmalloc((size_t)R * d->smax * sizeof(float));
+    d->req_T = dmalloc(ring * sizeof(int));
+    d->req_limit = dmalloc(ring * sizeof(int));
+    d->req_flags = dmalloc(ring * sizeof(int));
+    d->req_np = dmalloc(ring * sizeof(int));
+    d->req_ngen = dmalloc(ring * sizeof(int));
+    d->req_entry = dmalloc(ring * sizeof(int));
+    d->req_prompt = dmalloc((size_t)ring * CT_PROMPT_MAX * sizeof(int));
+    d->req_out = dmalloc((size_t)ring * d->smax * sizeof(int));
+    d->req_score = dmalloc((size_t)ring * d->smax * sizeof(float));
     d->q = dmalloc(CT_Q_WORDS * sizeof(int));
-    d->fq = dmalloc(R * sizeof(int));
-    d->req_next = dmalloc(R * sizeof(int));
-    d->rq = dmalloc(R * sizeof(int));
+    d->fq = dmalloc(ring * sizeof(int));
+    d->req_next = dmalloc(ring * sizeof(int));
+    d->rq = dmalloc(ring * sizeof(int));
+    d->ret = dmalloc(ring * sizeof(int));
     d->pend = dmalloc(S * sizeof(int));
     ECHK(hipMemsetAsync(d->slot_req, 0xff, S * sizeof(int), e->s));   /* -1: free */
     ECHK(hipMemsetAsync(d->slot_S, 0, S * sizeof(int), e->s));
-    ECHK(hipMemsetAsync(d->req_ngen, 0, R * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->slot_ent, 0, S * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(d->req_ngen, 0, ring * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->q, 0, CT_Q_WORDS * sizeof(int), e->s));
-    ECHK(hipMemsetAsync(d->req_next, 0xff, R * sizeof(int), e->s));   /* -1: no successor */
+    ECHK(hipMemsetAsync(d->req_next, 0xff, ring * sizeof(int), e->s));   /* -1: no successor */
     ECHK(hipMemsetAsync(d->pend, 0xff, S * sizeof(int), e->s));
 
     /* repack [Wq;Wk;Wv] and cross [Wk;Wv] contiguously (device to device) */
@@ -343,7 +375,16 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     }
     ECHK(hipMemsetAsync(d->kv_rowoff, 0xff, NR * sizeof(long), e->s));
     e->M = S;
+    e->req_cap = R;
     e->req = calloc(R, sizeof(HostReq));
+    e->free_ent = malloc((size_t)R * sizeof(int));
+    e->ent_owner = malloc((size_t)R * sizeof(int));
+    if (!e->req || !e->free_ent || !e->ent_owner) CT_FATAL("out of host memory");
+    for (int i = 0; i < R; i++) { e->free_ent[i] = i; e->ent_owner[i] = -1; }
+    e->free_head = 0;
+    e->free_tail = R;
+    pthread_mutex_init(&e->mu, NULL);
+    pthread_cond_init(&e->cv, NULL);
     const char *eg = getenv("HIPB_EAGER");
     e->eager = eg && eg[0] == '1';
     /* scheduling knobs (the results are the same bits either way) */
@@ -352,9 +393,11 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->read_ahead = !(ra && ra[0] == '0');
     mel_tables_init(e);
     ECHK(hipHostMalloc((void **)&e->h_tmp, (size_t)(R + 8) * (MAX_SEQ + 8) * sizeof(int), 0));
-    ECHK(hipHostMalloc((void **)&e->h_meta, (size_t)R * (5 + CT_PROMPT_MAX) * sizeof(int), 0));
-    /* subsampling group tables (<= 10 (R + 1) ints per batch) + published ids */
-    ECHK(hipHostMalloc((void **)&e->h_enc, (size_t)(11 * R + 64) * sizeof(int), 0));
+    ECHK(hipHostMalloc((void **)&e->h_meta, (size_t)ring * (CT_META_FIELDS + CT_PROMPT_MAX) * sizeof(int), 0));
+    ECHK(hipHostMalloc((void **)&e->h_ret, (size_t)ring * sizeof(int), 0));
+    /* per batch (at most R requests): subsampling group tables (<= 10 R
+     * ints), queue words, published ids, their entries */
+    ECHK(hipHostMalloc((void **)&e->h_enc, (size_t)(12 * R + 64) * sizeof(int), 0));
     ECHK(hipStreamSynchronize(e->s));
     return e;
 }
@@ -365,7 +408,8 @@ void hipb_destroy(HipbEngine *e) {
     for (int w = 0; w < 2; w++)
         if (e->have_graph[w]) { hipGraphExecDestroy(e->exec[w]); hipGraphDestroy(e->graph[w]); }
     void *ptrs[] = {e->d.slot_req, e->d.slot_S, e->d.slot_np, e->d.slot_T, e->d.slot_flags,
-                    e->d.slot_lim, e->d.slot_ng, e->d.slot_tok, e->d.act, e->d.tok, e->d.pos_len, e->d.cross_len,
+                    e->d.slot_lim, e->d.slot_ng, e->d.slot_tok, e->d.slot_ent, e->d.act, e->d.tok, e->d.pos_len,
+                    e->d.cross_len, e->d.req_entry, e->d.ret, e->e_dstrow,
                     e->d.row_slot, e->d.rank_self, e->d.rank_cross, e->warm_sink,
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.req_score, e->d.q,
@@ -379,10 +423,17 @@ void hipb_destroy(HipbEngine *e) {
                     e->eln_h, e->eln_l, e->emid_h, e->emid_l, e->eo_h, e->eo_l, e->edw_h, e->edw_l};
     for (size_t i = 0; i < sizeof ptrs / sizeof ptrs[0]; i++)
         if (ptrs[i]) ECHK(hipFree(ptrs[i]));
-    for (int r = 0; r < e->n_req; r++) { free(e->req[r].mel); free(e->req[r].pcm); }
+    for (int r = 0; r < e->n_req; r++) {
+        free(e->req[r].mel); free(e->req[r].pcm); free(e->req[r].out); free(e->req[r].score);
+    }
     free(e->req);
+    free(e->free_ent);
+    free(e->ent_owner);
+    pthread_mutex_destroy(&e->mu);
+    pthread_cond_destroy(&e->cv);
     ECHK(hipHostFree(e->h_tmp));
     ECHK(hipHostFree(e->h_meta));
+    ECHK(hipHostFree(e->h_ret));
     ECHK(hipHostFree(e->h_enc));
     ECHK(hipStreamDestroy(e->s2));
     free(e);
@@ -393,20 +444,24 @@ void *hipb_stream(HipbEngine *e) { return (void *)e->s; }
 void hipb_reset(HipbEngine *e) {
     ECHK(hipStreamSynchronize(e->s));
     for (int r = 0; r < e->n_req; r++) {
-        free(e->req[r].mel); free(e->req[r].pcm);
+        free(e->req[r].mel); free(e->req[r].pcm); free(e->req[r].out); free(e->req[r].score);
         memset(&e->req[r], 0, sizeof e->req[r]);
     }
     e->n_req = e->n_enc = 0;
+    atomic_store(&e->n_assigned, 0);
     e->meta_lo = 0;
-    e->pool_frames = 0;
     e->fq_count = 0;
+    e->ret_seen = 0;
+    for (int i = 0; i < e->d.max_req; i++) { e->free_ent[i] = i; e->ent_owner[i] = -1; }
+    e->free_head = 0;
+    e->free_tail = e->d.max_req;
     atomic_store(&e->published, 0);
     e->bench_mode = 0;
     ECHK(hipMemsetAsync(e->d.slot_req, 0xff, e->d.slots * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.slot_S, 0, e->d.slots * sizeof(int), e->s));
-    ECHK(hipMemsetAsync(e->d.req_ngen, 0, e->d.max_req * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(e->d.req_ngen, 0, e->ring * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.q, 0, CT_Q_WORDS * sizeof(int), e->s));
-    ECHK(hipMemsetAsync(e->d.req_next, 0xff, e->d.max_req * sizeof(int), e->s));
+    ECHK(hipMemsetAsync(e->d.req_next, 0xff, e->ring * sizeof(int), e->s));
     ECHK(hipMemsetAsync(e->d.pend, 0xff, e->d.slots * sizeof(int), e->s));
     ECHK(hipStreamSynchronize(e->s));
 }
@@ -422,26 +477,36 @@ static int t_enc_of(int T_mel) {
 static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prompt, int limit,
                          int flags);
 
-/* Host mirror of the request fields: field f (0 length, 1 limit, 2 flags,
- * 3 prompt length, 4 successor) of request r, and r's prompt. */
-static int *meta_field(HipbEngine *e, int f) { return e->h_meta + (size_t)f * e->d.max_req; }
+/* Host mirror of the request ring: field f (0 length, 1 limit, 2 flags,
+ * 3 prompt length, 4 successor, 5 tokens generated = 0) at ring slot i,
+ * then the prompts. */
+static int *meta_field(HipbEngine *e, int f) { return e->h_meta + (size_t)f * e->ring; }
 static int *meta_prompt(HipbEngine *e, int r) {
-    return e->h_meta + (size_t)5 * e->d.max_req + (size_t)r * CT_PROMPT_MAX;
+    return e->h_meta + (size_t)CT_META_FIELDS * e->ring + (size_t)(r & (e->ring - 1)) * CT_PROMPT_MAX;
 }
 
-/* Uploads the fields of the requests submitted since the last upload, in
- * one copy per field, on the engine stream: ahead of every step that could
+/* Copies `width` ints per request for the ids [lo, lo + n) from the host
+ * ring `src` into the device ring `dst`, on stream s (at most two pieces:
+ * the ids' slots wrap around once at most, n <= ring). */
+static void ring_put(HipbEngine *e, int *dst, const int *src, int lo, int n, int width, hipStream_t s) {
+    const int mask = e->ring - 1, a = lo & mask, n1 = n < e->ring - a ? n : e->ring - a;
+    ECHK(hipMemcpyAsync(dst + (size_t)a * width, src + (size_t)a * width, (size_t)n1 * width * sizeof(int),
+                        hipMemcpyHostToDevice, s));
+    if (n > n1)
+        ECHK(hipMemcpyAsync(dst, src, (size_t)(n - n1) * width * sizeof(int), hipMemcpyHostToDevice, s));
+}
+
+/* Uploads the fields of the requests submitted since the last upload to
+ * their ring slots, on the engine stream: ahead of every step that could
  * admit them (the device edits a chained request's prompt only after its
  * predecessor, uploaded with it, has decoded). */
 static void flush_meta(HipbEngine *e) {
     const int lo = e->meta_lo, n = e->n_req - lo;
     if (n <= 0) return;
-    int *const dst[5] = {e->d.req_T, e->d.req_limit, e->d.req_flags, e->d.req_np, e->d.req_next};
-    for (int f = 0; f < 5; f++)
-        ECHK(hipMemcpyAsync(dst[f] + lo, meta_field(e, f) + lo, (size_t)n * sizeof(int),
-                            hipMemcpyHostToDevice, e->s));
-    ECHK(hipMemcpyAsync(e->d.req_prompt + (size_t)lo * CT_PROMPT_MAX, meta_prompt(e, lo),
-                        (size_t)n * CT_PROMPT_MAX * sizeof(int), hipMemcpyHostToDevice, e->s));
+    int *const dst[CT_META_FIELDS] = {e->d.req_T, e->d.req_limit, e->d.req_flags, e->d.req_np,
+                                      e->d.req_next, e->d.req_ngen};
+    for (int f = 0; f < CT_META_FIELDS; f++) ring_put(e, dst[f], meta_field(e, f), lo, n, 1, e->s);
+    ring_put(e, e->d.req_prompt, e->h_meta + (size_t)CT_META_FIELDS * e->ring, lo, n, CT_PROMPT_MAX, e->s);
     e->meta_lo = e->n_req;
 }
 
@@ -477,7 +542,6 @@ int hipb_submit_pcm_chunked(HipbEngine *e, const float *pcm, int n_samples, cons
     int *b = malloc((size_t)2 * cap * sizeof(int));
     if (!b) CT_FATAL("out of host memory");
     const int nc = hipb_chunk_bounds(pcm, n_samples, silence_db, silence_dur, target_sec, b, cap);
-    if (e->n_req + nc > e->cfg.max_requests) CT_FATAL("hipb_submit_pcm_chunked: request pool full");
     const int r0 = e->n_req;
     for (int c = 0; c < nc; c++) {
         const int r = hipb_submit_pcm(e, pcm + b[2 * c], b[2 * c + 1] - b[2 * c], prompt, n_prompt,
@@ -486,7 +550,7 @@ int hipb_submit_pcm_chunked(HipbEngine *e, const float *pcm, int n_samples, cons
     }
     free(b);
     /* link chunk c to chunk c + 1 */
-    for (int c = 0; c + 1 < nc; c++) meta_field(e, 4)[r0 + c] = r0 + c + 1;
+    for (int c = 0; c + 1 < nc; c++) meta_field(e, 4)[(r0 + c) & (e->ring - 1)] = r0 + c + 1;
     if (first_req) *first_req = r0;
     return nc;
 }
@@ -500,27 +564,79 @@ int hipb_submit_pcm_device(HipbEngine *e, const float *dev_pcm, int n_samples, c
     return r;
 }
 
+static void read_queue(HipbEngine *e, int *q);
+static void recycle(HipbEngine *e, int finished);
+
+/* Copies a finished request's tokens and scores from its ring slot to the
+ * host (before the slot is reused). */
+static void collect(HipbEngine *e, int r) {
+    HostReq *q = &e->req[r];
+    if (q->collected) return;
+    const size_t slot = (size_t)(r & (e->ring - 1));
+    int n = 0;
+    ECHK(hipStreamSynchronize(e->s));
+    ECHK(hipMemcpy(&n, e->d.req_ngen + slot, sizeof(int), hipMemcpyDeviceToHost));
+    q->out = malloc((size_t)(n > 0 ? n : 1) * sizeof(int));
+    q->score = malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    if (!q->out || !q->score) CT_FATAL("out of host memory");
+    if (n > 0) {
+        ECHK(hipMemcpy(q->out, e->d.req_out + slot * e->d.smax, n * sizeof(int), hipMemcpyDeviceToHost));
+        ECHK(hipMemcpy(q->score, e->d.req_score + slot * e->d.smax, n * sizeof(float), hipMemcpyDeviceToHost));
+    }
+    q->n_out = n;
+    q->collected = 1;
+}
+
+/* Request r takes ring slot r & (ring - 1): the slot's previous request,
+ * r - ring, must have finished; its results move to the host first. */
+static void ring_slot_take(HipbEngine *e, int r) {
+    if (r < e->ring) return;
+    HostReq *o = &e->req[r - e->ring];
+    if (o->collected) return;
+    if (!o->done) {
+        int q[CT_Q_WORDS];
+        read_queue(e, q);
+        recycle(e, q[2]);
+    }
+    if (!o->done)
+        CT_FATAL("hipb_submit: more requests outstanding than the request ring holds (4 x max_requests, "
+                 "at least 1024): run the submitted ones first");
+    collect(e, r - e->ring);
+}
+
 static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prompt, int limit,
                          int flags) {
     if (e->bench_mode) CT_FATAL("hipb_submit: engine is in microbenchmark mode");
-    if (e->n_req >= e->cfg.max_requests) CT_FATAL("hipb_submit: request pool full");
     if (n_prompt < 1 || n_prompt > CT_PROMPT_SUBMIT_MAX) CT_FATAL("hipb_submit: prompt length outside [1, 16]");
     if (limit < 1) CT_FATAL("hipb_submit: limit < 1");
     if (n_prompt + limit > e->d.smax) CT_FATAL("hipb_submit: prompt + limit exceeds the engine's max_tokens");
     const int Te = t_enc_of(T_mel);
     if (T_mel < 1 || Te > e->d.tmax || Te > e->cfg.max_frames) CT_FATAL("hipb_submit: clip longer than max_frames");
-    const int r = e->n_req++;
+    if (e->n_req == e->req_cap) {
+        const int nc = 2 * e->req_cap;
+        HostReq *nr = realloc(e->req, (size_t)nc * sizeof(HostReq));
+        if (!nr) CT_FATAL("out of host memory");
+        memset(nr + e->req_cap, 0, (size_t)(nc - e->req_cap) * sizeof(HostReq));
+        e->req = nr;
+        e->req_cap = nc;
+    }
+    const int r = e->n_req;
+    ring_slot_take(e, r);
+    e->n_req++;
     HostReq *q = &e->req[r];
     memset(q, 0, sizeof *q);
     q->T_mel = T_mel;
     q->T_enc = Te;
-    /* request r's mirror entries are rewritten only after hipb_reset, which
-     * waits for the stream, so no upload is still reading them */
-    meta_field(e, 0)[r] = Te;
-    meta_field(e, 1)[r] = limit;
-    meta_field(e, 2)[r] = flags;
-    meta_field(e, 3)[r] = n_prompt;
-    meta_field(e, 4)[r] = -1;
+    q->entry = -1;
+    /* the ring slot's mirror entries were last uploaded for request
+     * r - ring, which has finished, so no upload is still reading them */
+    const int rs = r & (e->ring - 1);
+    meta_field(e, 0)[rs] = Te;
+    meta_field(e, 1)[rs] = limit;
+    meta_field(e, 2)[rs] = flags;
+    meta_field(e, 3)[rs] = n_prompt;
+    meta_field(e, 4)[rs] = -1;
+    meta_field(e, 5)[rs] = 0;
     int *pp = meta_prompt(e, r);
     memset(pp, 0, sizeof(int) * CT_PROMPT_MAX);
     memcpy(pp, prompt, (size_t)n_prompt * sizeof(int));
@@ -575,6 +691,8 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     e->eg = dmalloc(rows * ENC_D * 4);
     e->edw = NULL;
     e->e_row_start = dmalloc(rows * sizeof(int));
+    if (e->e_dstrow) ECHK(hipFree(e->e_dstrow));
+    e->e_dstrow = dmalloc(rows * sizeof(int));
     e->e_row_len = dmalloc(rows * sizeof(int));
     e->e_rowoff = dmalloc(rows * sizeof(long));
     /* at most M sequences (one frame each) and M query blocks */
@@ -653,17 +771,20 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     hipStream_t s = e->enc_s;
     /* host-side row tables */
     int *row_start = malloc(M * sizeof(int)), *row_len = malloc(M * sizeof(int));
+    int *dstrow = malloc(M * sizeof(int));
     long *rowoff = malloc(M * sizeof(long));
     int *seq_off = malloc(n * sizeof(int)), *seq_T = malloc(n * sizeof(int));
     int off = 0;
     for (int i = 0; i < n; i++) {
-        const int r = r0 + i, T = e->req[r].T_enc;
+        const int r = r0 + i, T = e->req[r].T_enc, ent = e->req[r].entry;
+        if (ent < 0) CT_FATAL("encode: request without an encoder entry");
         seq_off[i] = off;
         seq_T[i] = T;
         for (int t = 0; t < T; t++) {
             row_start[off + t] = off;
             row_len[off + t] = T;
-            rowoff[off + t] = ((long)r * DEC_H * e->d.tmax + t) * DEC_DK;
+            dstrow[off + t] = ent * e->d.tmax + t;
+            rowoff[off + t] = ((long)ent * DEC_H * e->d.tmax + t) * DEC_DK;
         }
         off += T;
     }
@@ -673,6 +794,7 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     if (nblk > e->enc_cap) CT_FATAL("encode: query-block table larger than the workspace");
     ECHK(hipMemcpyAsync(e->e_row_start, row_start, M * sizeof(int), hipMemcpyHostToDevice, s));
     ECHK(hipMemcpyAsync(e->e_row_len, row_len, M * sizeof(int), hipMemcpyHostToDevice, s));
+    ECHK(hipMemcpyAsync(e->e_dstrow, dstrow, M * sizeof(int), hipMemcpyHostToDevice, s));
     ECHK(hipMemcpyAsync(e->e_rowoff, rowoff, M * sizeof(long), hipMemcpyHostToDevice, s));
     ECHK(hipMemcpyAsync(e->e_seq_off, seq_off, n * sizeof(int), hipMemcpyHostToDevice, s));
     ECHK(hipMemcpyAsync(e->e_seq_T, seq_T, n * sizeof(int), hipMemcpyHostToDevice, s));
@@ -812,12 +934,12 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         gemm_sp(e, e->emid_h, e->emid_l, M, ENC_FF, L->ff2_w2, L->ff2_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
         ctk_layernorm(e->ex, e->ex, DW(L->out_lnw), DW(L->out_lnb), M, ENC_D, s);
     }
-    /* the encoder output stays in enc_pool, packed as encoded; cross K/V
-     * go straight into the head-major cross caches */
-    float *eh = e->enc_pool + (size_t)e->pool_frames * DEC_D;
+    /* the encoder output, packed (the Q workspace is free now), goes to
+     * each request's entry of enc_pool; cross K/V go straight into the
+     * head-major cross caches of the entries */
+    float *eh = e->eq;
     gemm(e, e->ex, M, ENC_D, W->prw, W->prb, eh, DEC_D, CT_EPI_STORE, 0, NULL);
-    for (int i = 0; i < n; i++) e->req[r0 + i].pool_off = e->pool_frames + seq_off[i];
-    e->pool_frames += M;
+    ctk_copy_rows(e->enc_pool, eh, e->e_dstrow, M, DEC_D, s);
     const size_t cross_l = (size_t)e->d.max_req * DEC_H * e->d.tmax * DEC_DK;
     ctk_split(e->eln_h, e->eln_l, eh, (long)M * DEC_D, s);   /* LN planes are free now */
     for (int l = 0; l < DEC_N; l++) {
@@ -835,29 +957,50 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         ctk_gemm(&g, s);
     }
     ECHK(hipStreamSynchronize(s));
-    free(row_start); free(row_len); free(rowoff); free(seq_off); free(seq_T); free(blk_seq); free(blk_q0);
+    free(row_start); free(row_len); free(dstrow); free(rowoff); free(seq_off); free(seq_T); free(blk_seq);
+    free(blk_q0);
+}
+
+/* Copies n ints src[0..n) into the device ring dst at positions [lo, lo + n)
+ * (wrapping), on stream s. */
+static void ring_put_seq(HipbEngine *e, int *dst, const int *src, long lo, int n, hipStream_t s) {
+    if (n <= 0) return;
+    const int mask = e->ring - 1, a = (int)(lo & mask), n1 = n < e->ring - a ? n : e->ring - a;
+    ECHK(hipMemcpyAsync(dst + a, src, (size_t)n1 * sizeof(int), hipMemcpyHostToDevice, s));
+    if (n > n1) ECHK(hipMemcpyAsync(dst, src + n1, (size_t)(n - n1) * sizeof(int), hipMemcpyHostToDevice, s));
 }
 
 /* Publishes the encoded requests [r0, r1) (their cross K/V are written: the
- * encoder stream has been drained): the encoded watermark q[7] = r1, which
- * releases chained successors below it, then the requests that wait for no
- * predecessor appended to the fresh queue in submission order (the ids
- * first, then the new count).  All copies go on the encoder stream, which is
- * then drained; the step kernel reads the words with acquire loads, possibly
- * while running on the other stream. */
+ * encoder stream has been drained): their encoder entries into the request
+ * ring, the encoded watermark q[7] = r1, which releases chained successors
+ * below it, then the requests that wait for no predecessor appended to the
+ * fresh queue in submission order (the ids first, then the new count).  All
+ * copies go on the encoder stream, which is then drained; the step kernel
+ * reads the words with acquire loads, possibly while running on the other
+ * stream. */
 static void publish(HipbEngine *e, int r0, int r1) {
-    int *ids = e->h_enc + 10 * e->d.max_req + 16, k = 0;
-    int *words = e->h_enc + 10 * e->d.max_req + 8;   /* [0] watermark, [1] fresh count */
-    for (int i = r0; i < r1; i++)
-        if (!e->req[i].chained) ids[k++] = i;
+    const int P = e->d.max_req;
+    int *words = e->h_enc + 10 * P + 8;   /* [0] watermark, [1] fresh count */
+    int *ids = e->h_enc + 10 * P + 16, *ents = ids + P, k = 0;
+    /* a publication covers at most P requests (each holds an entry) */
+    for (int lo = r0; lo < r1; lo += P) {
+        const int hi = r1 - lo > P ? lo + P : r1;
+        for (int i = lo; i < hi; i++) ents[i - lo] = e->req[i].entry;
+        ring_put_seq(e, e->d.req_entry, ents, lo, hi - lo, e->enc_s);
+        ECHK(hipStreamSynchronize(e->enc_s));
+    }
     words[0] = r1;
     ECHK(hipMemcpyAsync(e->d.q + 7, &words[0], sizeof(int), hipMemcpyHostToDevice, e->enc_s));
-    if (k) {
-        ECHK(hipMemcpyAsync(e->d.fq + e->fq_count, ids, (size_t)k * sizeof(int), hipMemcpyHostToDevice,
-                            e->enc_s));
-        e->fq_count += k;
-        words[1] = e->fq_count;
-        ECHK(hipMemcpyAsync(e->d.q + 5, &words[1], sizeof(int), hipMemcpyHostToDevice, e->enc_s));
+    for (int i = r0; i <= r1; i++) {
+        if (i < r1 && !e->req[i].chained) ids[k++] = i;
+        if (k && (k == P || i == r1)) {
+            ring_put_seq(e, e->d.fq, ids, e->fq_count, k, e->enc_s);
+            e->fq_count += k;
+            words[1] = e->fq_count;
+            ECHK(hipMemcpyAsync(e->d.q + 5, &words[1], sizeof(int), hipMemcpyHostToDevice, e->enc_s));
+            ECHK(hipStreamSynchronize(e->enc_s));
+            k = 0;
+        }
     }
     ECHK(hipStreamSynchronize(e->enc_s));
     atomic_store(&e->published, r1);
@@ -871,22 +1014,84 @@ static void release_inputs(HipbEngine *e, int r0, int r1) {
 }
 
 /* The next batch of not yet encoded requests: [r, *r1) with at most
- * max_batch_frames encoder frames (at least one request). */
-static int next_batch(const HipbEngine *e, int r, int max_batch_frames) {
+ * max_batch_frames encoder frames and at most max_n requests (at least
+ * one request). */
+static int next_batch(const HipbEngine *e, int r, int max_batch_frames, int max_n) {
     int frames = 0, r1 = r;
-    while (r1 < e->n_req && (r1 == r || frames + e->req[r1].T_enc <= max_batch_frames)) {
+    while (r1 < e->n_req && (r1 == r || (frames + e->req[r1].T_enc <= max_batch_frames && r1 - r < max_n))) {
         frames += e->req[r1].T_enc;
         r1++;
     }
     return r1;
 }
 
-void hipb_encode(HipbEngine *e, int max_batch_frames) {
-    flush_meta(e);
-    if (max_batch_frames < e->d.tmax) max_batch_frames = e->d.tmax;
+/* Encoder entries free right now (thread-safe). */
+static int free_entries(HipbEngine *e) {
+    pthread_mutex_lock(&e->mu);
+    const int n = (int)(e->free_tail - e->free_head);
+    pthread_mutex_unlock(&e->mu);
+    return n;
+}
+
+/* Gives requests [r0, r1) encoder entries from the free FIFO (the caller
+ * made sure there are enough). */
+static void take_entries(HipbEngine *e, int r0, int r1) {
+    const int P = e->d.max_req;
+    pthread_mutex_lock(&e->mu);
+    if (e->free_tail - e->free_head < r1 - r0) CT_FATAL("encode: fewer free encoder entries than requests");
+    for (int r = r0; r < r1; r++) {
+        const int ent = e->free_ent[e->free_head++ % P];
+        e->req[r].entry = ent;
+        e->ent_owner[ent] = r;
+    }
+    atomic_store(&e->n_assigned, r1);
+    pthread_mutex_unlock(&e->mu);
+}
+
+/* Marks the requests that retired since the last call (the device's
+ * retirement ring, up to `finished` of them) done and returns their
+ * encoder entries to the free FIFO.  Synchronises the engine stream. */
+static void recycle(HipbEngine *e, int finished) {
+    const int n = finished - e->ret_seen;
+    if (n <= 0) return;
+    if (n > e->ring)
+        CT_FATAL("recycle: more requests retired than the retirement ring holds since the host last "
+                 "looked (stepping with hipb_step alone: call hipb_finished between steps)");
+    const int mask = e->ring - 1, a = e->ret_seen & mask, n1 = n < e->ring - a ? n : e->ring - a;
+    ECHK(hipMemcpyAsync(e->h_ret, e->d.ret + a, (size_t)n1 * sizeof(int), hipMemcpyDeviceToHost, e->s));
+    if (n > n1)
+        ECHK(hipMemcpyAsync(e->h_ret + n1, e->d.ret, (size_t)(n - n1) * sizeof(int), hipMemcpyDeviceToHost, e->s));
+    ECHK(hipStreamSynchronize(e->s));
+    const int P = e->d.max_req;
+    pthread_mutex_lock(&e->mu);
+    for (int i = 0; i < n; i++) {
+        const int r = e->h_ret[i];
+        if (r < 0 || r >= e->n_req) CT_FATAL("recycle: bad retired request id");
+        HostReq *q = &e->req[r];
+        q->done = 1;
+        if (q->entry >= 0 && e->ent_owner[q->entry] == r) e->free_ent[e->free_tail++ % P] = q->entry;
+    }
+    pthread_cond_broadcast(&e->cv);
+    pthread_mutex_unlock(&e->mu);
+    e->ret_seen = finished;
+}
+
+/* True when requests without an entry outnumber the free entries, so that
+ * retired requests' entries should be recycled. */
+static int entries_short(HipbEngine *e) {
+    return e->n_req - atomic_load(&e->n_assigned) > free_entries(e);
+}
+
+/* Encodes (on the engine's encoder stream, synchronously) the submitted
+ * requests not yet encoded, as far as free encoder entries go, and
+ * publishes them. */
+static void encode_available(HipbEngine *e, int max_batch_frames) {
     int r = e->n_enc;
     while (r < e->n_req) {
-        const int r1 = next_batch(e, r, max_batch_frames);
+        const int avail = free_entries(e);
+        if (!avail) break;
+        const int r1 = next_batch(e, r, max_batch_frames, avail);
+        take_entries(e, r, r1);
         encode_batch(e, r, r1);
         release_inputs(e, r, r1);
         r = r1;
@@ -894,6 +1099,18 @@ void hipb_encode(HipbEngine *e, int max_batch_frames) {
     const int r0 = e->n_enc;
     e->n_enc = r;
     publish(e, r0, r);
+}
+
+void hipb_encode(HipbEngine *e, int max_batch_frames) {
+    flush_meta(e);
+    if (max_batch_frames < e->d.tmax) max_batch_frames = e->d.tmax;
+    e->batch_frames = max_batch_frames;
+    if (e->n_enc < e->n_req && entries_short(e)) {
+        int q[CT_Q_WORDS];
+        read_queue(e, q);
+        recycle(e, q[2]);
+    }
+    encode_available(e, max_batch_frames);
 }
 
 /* ------------------------------------------------------------------ */
@@ -1110,10 +1327,20 @@ static void read_queue(HipbEngine *e, int *q) {
     memcpy(q, e->h_tmp, CT_Q_WORDS * sizeof(int));
 }
 
+static void recycle(HipbEngine *e, int finished);
+
 int hipb_finished(HipbEngine *e) {
     int q[CT_Q_WORDS];
     read_queue(e, q);
+    recycle(e, q[2]);
     return q[2];
+}
+
+/* Steps a run or process loop may launch between two looks at the queue:
+ * fewer than a quarter of the retirement ring can fill meanwhile. */
+static int clamp_chunk(const HipbEngine *e, int chunk) {
+    const int most = e->ring / (4 * e->d.slots);
+    return chunk < 1 ? 1 : chunk > most ? most : chunk;
 }
 
 static void ensure_graph(HipbEngine *e, int wide) {
@@ -1137,38 +1364,57 @@ void hipb_bench_steps(HipbEngine *e, int n) {
 
 long hipb_run(HipbEngine *e, int chunk) {
     flush_meta(e);
-    if (chunk < 1) chunk = 1;
+    chunk = clamp_chunk(e, chunk);
     const int spare = e->d.rows - e->d.slots;
     ensure_graph(e, 0);
     if (spare) ensure_graph(e, 1);
+    if (e->batch_frames < e->d.tmax) e->batch_frames = 8192 > e->d.tmax ? 8192 : e->d.tmax;
     long steps = 0;
     /* every admitted request finishes within prompt + limit <= prompt +
      * MAX_SEQ steps of its admission, and some request is admitted whenever
      * a slot frees up */
-    const long bound = (long)(e->n_enc + 2) * (MAX_SEQ + CT_PROMPT_MAX + 1);
+    const long bound = (long)(e->n_req + 2) * (MAX_SEQ + CT_PROMPT_MAX + 1);
     for (;;) {
         int q[CT_Q_WORDS];
         read_queue(e, q);
-        if (q[2] >= e->n_enc) break;
+        if (q[2] - e->ret_seen >= e->ring / 4) recycle(e, q[2]);
+        if (e->n_enc < e->n_req) {
+            /* requests still waiting for an encoder entry: take those that
+             * retired requests returned */
+            recycle(e, q[2]);
+            const int before = e->n_enc;
+            encode_available(e, e->batch_frames);
+            if (e->n_enc > before) continue;
+        }
+        if (q[2] >= e->n_req) {
+            recycle(e, q[2]);
+            break;
+        }
         if (steps > bound) CT_FATAL("hipb_run: requests did not finish within the step bound");
         const int wide = want_wide(e);
         for (int i = 0; i < chunk; i++) launch_step(e, wide);
         steps += chunk;
-
     }
     return steps;
 }
 
 /* hipb_process: the encoder runs on a worker thread and the second stream,
  * publishing each batch to the fresh queue as soon as its cross K/V are
- * written, while the calling thread keeps launching decode steps. */
+ * written, while the calling thread keeps launching decode steps and
+ * returns retired requests' encoder entries to the free FIFO when the
+ * encoder is short of them. */
 static void *enc_worker(void *arg) {
     HipbEngine *e = arg;
     ECHK(hipSetDevice(e->dev));
     ct_t.dev = e->dev;                 /* weight pointers translate per device */
     int batches = 0;
     for (int r = e->n_enc; r < e->n_req;) {
-        const int r1 = next_batch(e, r, e->proc_batch);
+        pthread_mutex_lock(&e->mu);
+        while (e->free_tail == e->free_head) pthread_cond_wait(&e->cv, &e->mu);
+        const int avail = (int)(e->free_tail - e->free_head);
+        pthread_mutex_unlock(&e->mu);
+        const int r1 = next_batch(e, r, e->proc_batch, avail);
+        take_entries(e, r, r1);
         encode_batch(e, r, r1);
         release_inputs(e, r, r1);
         publish(e, r, r1);
@@ -1189,17 +1435,20 @@ static void *enc_worker(void *arg) {
 
 long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
     flush_meta(e);
-    if (chunk < 1) chunk = 1;
+    chunk = clamp_chunk(e, chunk);
     if (max_batch_frames < e->d.tmax) max_batch_frames = e->d.tmax;
     const int spare = e->d.rows - e->d.slots;
     /* graphs captured and every encoder buffer sized before the worker
-     * starts: no capture, allocation or free runs beside the other stream */
+     * starts: no capture, allocation or free runs beside the other stream.
+     * The worker's batches are cut by frames and by the free entries, so
+     * each lies inside the frames-only batch that starts where it starts:
+     * sizing for those from every start covers them all. */
     ensure_graph(e, 0);
     if (spare) ensure_graph(e, 1);
     {
         int frames_max = 0, tmel_max = 0;
-        for (int r = e->n_enc; r < e->n_req;) {
-            const int r1 = next_batch(e, r, max_batch_frames);
+        for (int r = e->n_enc; r < e->n_req; r++) {
+            const int r1 = next_batch(e, r, max_batch_frames, e->n_req);
             int f = 0;
             for (int i = r; i < r1; i++) {
                 f += e->req[i].T_enc;
@@ -1207,7 +1456,6 @@ long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
             }
             if (f > frames_max) frames_max = f;
             batch_buffers(e, r, r1);
-            r = r1;
         }
         if (frames_max) {
             enc_reserve(e, frames_max, tmel_max);
@@ -1228,8 +1476,12 @@ long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
         int q[CT_Q_WORDS];
         read_queue(e, q);
         atomic_store(&e->seen_finished, q[2]);
+        if (entries_short(e) || q[2] - e->ret_seen >= e->ring / 4) recycle(e, q[2]);
         const int done = atomic_load(&e->enc_done);
-        if (done && q[2] >= e->n_req) break;
+        if (done && q[2] >= e->n_req) {
+            recycle(e, q[2]);
+            break;
+        }
         /* every admitted request finished and none can be admitted: wait
          * for the encoder instead of stepping empty slots.  No successor
          * waits (released q[10] = admitted q[0]), or the one at the ring's
@@ -1244,7 +1496,6 @@ long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
         const int wide = want_wide(e);
         for (int i = 0; i < chunk; i++) launch_step(e, wide);
         steps += chunk;
-
     }
     pthread_join(th, NULL);
     e->enc_s = e->s;
@@ -1262,26 +1513,32 @@ int hipb_test_hold_expired(HipbEngine *e) { return e->hold_expired; }
 /* ------------------------------------------------------------------ */
 /* Results                                                             */
 /* ------------------------------------------------------------------ */
-int hipb_tokens(HipbEngine *e, int req, int *out, int cap) {
+/* Tokens (what = 0) or scores (what = 1) of request req: from the host copy
+ * once its ring slot was handed to a later request, else from the slot. */
+static int req_results(HipbEngine *e, int req, void *out, int cap, int what) {
     if (req < 0 || req >= e->n_req) return 0;
+    const HostReq *q = &e->req[req];
     int n = 0;
+    if (q->collected) {
+        n = q->n_out < cap ? q->n_out : cap;
+        if (n > 0) memcpy(out, what ? (const void *)q->score : (const void *)q->out, (size_t)n * 4);
+        return n;
+    }
+    const size_t slot = (size_t)(req & (e->ring - 1));
     ECHK(hipStreamSynchronize(e->s));
-    ECHK(hipMemcpy(&n, e->d.req_ngen + req, sizeof(int), hipMemcpyDeviceToHost));
+    ECHK(hipMemcpy(&n, e->d.req_ngen + slot, sizeof(int), hipMemcpyDeviceToHost));
     if (n > cap) n = cap;
-    if (n > 0) ECHK(hipMemcpy(out, e->d.req_out + (size_t)req * e->d.smax, n * sizeof(int), hipMemcpyDeviceToHost));
+    if (n > 0) {
+        const void *src = what ? (const void *)(e->d.req_score + slot * e->d.smax)
+                               : (const void *)(e->d.req_out + slot * e->d.smax);
+        ECHK(hipMemcpy(out, src, (size_t)n * 4, hipMemcpyDeviceToHost));
+    }
     return n;
 }
 
-int hipb_token_scores(HipbEngine *e, int req, float *out, int cap) {
-    if (req < 0 || req >= e->n_req) return 0;
-    int n = 0;
-    ECHK(hipStreamSynchronize(e->s));
-    ECHK(hipMemcpy(&n, e->d.req_ngen + req, sizeof(int), hipMemcpyDeviceToHost));
-    if (n > cap) n = cap;
-    if (n > 0)
-        ECHK(hipMemcpy(out, e->d.req_score + (size_t)req * e->d.smax, n * sizeof(float), hipMemcpyDeviceToHost));
-    return n;
-}
+int hipb_tokens(HipbEngine *e, int req, int *out, int cap) { return req_results(e, req, out, cap, 0); }
+
+int hipb_token_scores(HipbEngine *e, int req, float *out, int cap) { return req_results(e, req, out, cap, 1); }
 
 int hipb_slot_of(HipbEngine *e, int req) {
     ECHK(hipStreamSynchronize(e->s));
@@ -1298,8 +1555,11 @@ void hipb_logits(HipbEngine *e, int slot, float *out) {
 
 void hipb_enc_out(HipbEngine *e, int req, float *out) {
     if (req < 0 || req >= e->n_enc) CT_FATAL("hipb_enc_out: request not encoded");
+    const int ent = e->req[req].entry;
+    if (ent < 0 || e->ent_owner[ent] != req)
+        CT_FATAL("hipb_enc_out: the request's encoder entry was recycled for a later request");
     ECHK(hipStreamSynchronize(e->s));
-    ECHK(hipMemcpy(out, e->enc_pool + (size_t)e->req[req].pool_off * DEC_D,
+    ECHK(hipMemcpy(out, e->enc_pool + (size_t)ent * e->d.tmax * DEC_D,
                    (size_t)e->req[req].T_enc * DEC_D * sizeof(float), hipMemcpyDeviceToHost));
 }
 
@@ -1332,11 +1592,16 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
     ECHK(hipMemcpy(e->d.req_ngen, buf, B * sizeof(int), hipMemcpyHostToDevice));
     for (int s = 0; s < B; s++)
         ECHK(hipMemcpy(e->d.req_out + (size_t)s * e->d.smax, &(int){100 + s}, sizeof(int), hipMemcpyHostToDevice));
+    /* request s holds encoder entry s */
+    for (int s = 0; s < B; s++) buf[s] = s;
+    ECHK(hipMemcpy(e->d.req_entry, buf, B * sizeof(int), hipMemcpyHostToDevice));
     /* the slots' copies of those fields, as admission would have made them */
-    int *const sf[6] = {e->d.slot_np, e->d.slot_T, e->d.slot_flags, e->d.slot_lim, e->d.slot_ng, e->d.slot_tok};
-    for (int f = 0; f < 6; f++) {
+    int *const sf[7] = {e->d.slot_np, e->d.slot_T, e->d.slot_flags, e->d.slot_lim, e->d.slot_ng, e->d.slot_tok,
+                        e->d.slot_ent};
+    for (int f = 0; f < 7; f++) {
         for (int s = 0; s < B; s++)
-            buf[s] = f == 0 ? 0 : f == 1 ? T_enc[s] : f == 2 ? HIPB_SUPPRESS_EOS : f == 3 ? e->d.smax : f == 4 ? 1 : 100 + s;
+            buf[s] = f == 0 ? 0 : f == 1 ? T_enc[s] : f == 2 ? HIPB_SUPPRESS_EOS : f == 3 ? e->d.smax
+                   : f == 4 ? 1 : f == 5 ? 100 + s : s;
         ECHK(hipMemcpy(sf[f], buf, B * sizeof(int), hipMemcpyHostToDevice));
     }
     int q[CT_Q_WORDS] = {B, B, 0, 0, 0, 0, 0, B};

@@ -18,14 +18,15 @@
 
 namespace {
 
-// Writes row `row` of the step: token `tok` of slot s's request r (T_enc
-// frames) at position pos (0-based) of the slot's self cache.
-__device__ __forceinline__ void set_row(const CtEngDev &d, int row, int s, int r, int T, int tok, int pos) {
+// Writes row `row` of the step: token `tok` of slot s's request, whose
+// encoder state (T_enc frames of cross K/V) is in entry `ent`, at position
+// pos (0-based) of the slot's self cache.
+__device__ __forceinline__ void set_row(const CtEngDev &d, int row, int s, int ent, int T, int tok, int pos) {
     d.act[row] = 1;
     d.tok[row] = tok;
     d.pos_len[row] = pos + 1;
     d.cross_len[row] = T;
-    d.cross_idx[row] = r;
+    d.cross_idx[row] = ent;
     d.row_slot[row] = s;
     d.kv_rowoff[row] = ((long)s * DEC_H * d.kv_rows + pos) * DEC_DK;
 }
@@ -75,7 +76,8 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     __shared__ int s_app[CT_ENG_MAX_SLOTS], s_cand[CT_ENG_MAX_SLOTS], s_q[6], s_asum[4];
     __shared__ int s_wsum[4], s_left[4];
     __shared__ int s_pl[2 * CT_ENG_MAX_SLOTS], s_cl[2 * CT_ENG_MAX_SLOTS];   // row lengths this step
-    int r = -1, S = 0, np = 0, T = 0, tok = 0, pend = -1, q0 = 0, q1 = 0, f0 = 0, f1 = 0, wm = 0;
+    int r = -1, S = 0, np = 0, T = 0, tok = 0, ent = 0, pend = -1, q0 = 0, q1 = 0, f0 = 0, f1 = 0, wm = 0;
+    const int mk = d.ring_mask;
     if (s < d.slots) {
         r = d.slot_req[s];
         pend = d.pend[s];
@@ -83,6 +85,7 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
         np = d.slot_np[s];
         T = d.slot_T[s];
         tok = d.slot_tok[s];
+        ent = d.slot_ent[s];
     }
     if (tid == 0) {
         q0 = d.q[0]; q1 = d.q[1]; f0 = d.q[4];
@@ -105,7 +108,7 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     const int pidx = pre & 0xffff, fidx = pre >> 16, npend = tot & 0xffff, nfree = tot >> 16;
     q0 = s_q[0]; q1 = s_q[1]; f0 = s_q[2]; f1 = s_q[3]; wm = s_q[4];
     if (is_p) {
-        d.rq[q1 + pidx] = pend;
+        d.rq[(q1 + pidx) & mk] = pend;
         s_app[pidx] = pend;
     }
     if (tid == 0) s_q[5] = INT_MAX;
@@ -116,7 +119,7 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     // the first entry whose encoder batch is not published
     const int lim = min(min(avail, nfree + 1), (int)CT_ENG_MAX_SLOTS);
     if (tid < lim) {
-        const int c = tid < waiting ? d.rq[q0 + tid] : s_app[tid - waiting];
+        const int c = tid < waiting ? d.rq[(q0 + tid) & mk] : s_app[tid - waiting];
         s_cand[tid] = c;
         if (c >= wm) atomicMin(&s_q[5], tid);
     }
@@ -128,7 +131,8 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     if (is_f) {
         if (fidx < from_rq) { r = s_cand[fidx]; fresh = true; }
         else if (fidx - from_rq < f1 - f0) {
-            r = __hip_atomic_load(&d.fq[f0 + fidx - from_rq], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            r = __hip_atomic_load(&d.fq[(f0 + fidx - from_rq) & mk], __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
             fresh = true;
         }
     }
@@ -144,10 +148,11 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
         if (pend >= 0) d.pend[s] = -1;
         d.slot_req[s] = r;
         if (fresh) {
+            const int rs = r & mk;
             S = 0;
-            np = d.req_np[r]; T = d.req_T[r];
-            const int fl = d.req_flags[r], lim = d.req_limit[r], ng = d.req_ngen[r];
-            d.slot_np[s] = np; d.slot_T[s] = T;
+            np = d.req_np[rs]; T = d.req_T[rs]; ent = d.req_entry[rs];
+            const int fl = d.req_flags[rs], lim = d.req_limit[rs], ng = d.req_ngen[rs];
+            d.slot_np[s] = np; d.slot_T[s] = T; d.slot_ent[s] = ent;
             d.slot_flags[s] = fl; d.slot_lim[s] = lim; d.slot_ng[s] = ng;
         }
         if (r >= 0 && S < np) want = min(np - S, 1 + extra) - 1;
@@ -168,14 +173,15 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     int left = 0;
     if (s < d.slots && r >= 0) {
         const int k = 1 + granted;
+        const int *prompt = d.req_prompt + (long)(r & mk) * CT_PROMPT_MAX;
         for (int j = 0; j < granted; j++) {
-            set_row(d, d.slots + base + j, s, r, T, d.req_prompt[r * CT_PROMPT_MAX + S + j], S + j);
+            set_row(d, d.slots + base + j, s, ent, T, prompt[S + j], S + j);
             s_pl[d.slots + base + j] = S + j + 1;
             s_cl[d.slots + base + j] = T;
         }
         const int p = S + k - 1;
-        const int t = p < np ? d.req_prompt[r * CT_PROMPT_MAX + p] : tok;
-        set_row(d, s, s, r, T, t, p);
+        const int t = p < np ? prompt[p] : tok;
+        set_row(d, s, s, ent, T, t, p);
         s_pl[s] = p + 1;
         s_cl[s] = T;
         d.slot_S[s] = S + k;
@@ -259,15 +265,16 @@ __global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *l
     const float xf = first ? v[0].y : v[0].x;   // thread 0 holds logits 0..3
     int best = (xf != xf || bi == INT_MAX) ? first : bi;
     if ((flags & 2) && ng == lim - 1) best = EOS_ID;
-    d.req_out[(long)r * d.smax + ng] = best;
-    d.req_score[(long)r * d.smax + ng] = bv;
-    d.req_ngen[r] = ng + 1;
+    const int rs = r & d.ring_mask;
+    d.req_out[(long)rs * d.smax + ng] = best;
+    d.req_score[(long)rs * d.smax + ng] = bv;
+    d.req_ngen[rs] = ng + 1;
     d.slot_ng[s] = ng + 1;
     d.slot_tok[s] = best;
     const bool fin = (best == EOS_ID && !(flags & 1)) || ng + 1 >= lim || S >= d.smax;
     if (fin) {
         d.slot_req[s] = -1;
-        const int nx = d.req_next[r];
+        const int nx = d.req_next[rs];
         if (nx >= 0) {
             // The successor's prompt becomes pre + carry + post: its first two
             // ids, then the last <= CT_CARRY_MAX generated ids of this
@@ -275,16 +282,19 @@ __global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *l
             // (transcribe.c:382-387, 510-529).
             const int gen = ng + 1;
             const int nc = min(gen > 0 ? gen - 1 : 0, CT_CARRY_MAX);
-            int *pp = d.req_prompt + (long)nx * CT_PROMPT_MAX;
-            const int np = d.req_np[nx];
+            const int ns = nx & d.ring_mask;
+            int *pp = d.req_prompt + (long)ns * CT_PROMPT_MAX;
+            const int np = d.req_np[ns];
             for (int i = np - 1; i >= 2; i--) pp[i + nc] = pp[i];
-            const int *og = d.req_out + (long)r * d.smax;
+            const int *og = d.req_out + (long)rs * d.smax;
             for (int i = 0; i < nc; i++) pp[2 + i] = og[gen - 1 - nc + i];
-            d.req_np[nx] = np + nc;
+            d.req_np[ns] = np + nc;
             d.pend[s] = nx;
             atomicAdd(&d.q[10], 1);
         }
-        atomicAdd(&d.q[2], 1);
+        // retirement order, for the host to recycle the encoder entry
+        const int k = atomicAdd(&d.q[2], 1);
+        d.ret[k & d.ring_mask] = r;
     }
 }
 

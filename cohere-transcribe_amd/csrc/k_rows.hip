@@ -228,6 +228,14 @@ __global__ void add_kernel(float *dst, const float *src, long n) {
     if (i < n) dst[i] += src[i];
 }
 
+// Row m of src (D floats, D % 4 == 0) to row dst_row[m] of dst.
+__global__ void copy_rows_kernel(float *dst, const float *src, const int *dst_row, int M, int D) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x, per = D / 4;
+    if (i >= (long)M * per) return;
+    const int m = (int)(i / per), c = (int)(i % per);
+    reinterpret_cast<float4 *>(dst + (long)dst_row[m] * D)[c] = reinterpret_cast<const float4 *>(src + (long)m * D)[c];
+}
+
 __global__ void causal_mask_kernel(float *mask, int S) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)S * S) return;
@@ -466,6 +474,17 @@ extern "C" void ctk_argmax(int *out, const float *logits, int R, int n, const in
 extern "C" void ctk_add(float *dst, const float *src, long n, hipStream_t s) {
     if (n <= 0) return;
     hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst, src, n);
+}
+
+extern "C" void ctk_copy_rows(float *dst, const float *src, const int *dst_row, int M, int D, hipStream_t s) {
+    if (M <= 0) return;
+    if (D % 4 || ((uintptr_t)dst & 15) || ((uintptr_t)src & 15)) {
+        fprintf(stderr, "ctk_copy_rows: needs D %% 4 == 0 and 16-byte aligned rows\n");
+        exit(1);
+    }
+    const long n = (long)M * (D / 4);
+    hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst, src, dst_row,
+                       M, D);
 }
 
 extern "C" void ctk_causal_mask(float *mask, int S, hipStream_t s) {

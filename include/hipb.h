@@ -35,7 +35,13 @@ typedef struct HipbEngine HipbEngine;
 
 typedef struct {
     int slots;          /* concurrent KV slots (decode batch), 1..256          */
-    int max_requests;   /* request pool capacity                                */
+    int max_requests;   /* encoder-state entries: requests holding cross K/V and
+                           an encoder output at once (each ~16 MB at 376 frames,
+                           bf16 KV); an entry is taken when a request is
+                           encoded and recycled after it finishes, so any
+                           number of requests flows through.  Up to
+                           max(4 x max_requests, 32 x slots, 1024) may be
+                           outstanding (submitted, not finished)          */
     int max_frames;     /* largest encoder length a request may have (<= 2048) */
     int kv_bf16;        /* 1: bf16 KV caches, 0: fp32                           */
     int max_tokens;     /* longest prompt + limit of any request (sizes the self
@@ -57,7 +63,9 @@ void hipb_destroy(HipbEngine *e);
 
 /* Queues a request: mel (N_MELS x T_mel, row stride T_mel, host memory),
  * prompt ids, at most `limit` generated tokens.  Returns the request id
- * (0, 1, 2, ... in submission order). */
+ * (0, 1, 2, ... in submission order, until hipb_reset).  Fatal if more
+ * requests are outstanding than the request ring holds (see
+ * max_requests). */
 int  hipb_submit(HipbEngine *e, const float *mel, int T_mel, const int *prompt, int n_prompt,
                  int limit, int flags);
 /* Queues a request given 16 kHz mono PCM (host memory); its log-mel
@@ -89,16 +97,19 @@ int  hipb_submit_pcm_device(HipbEngine *e, const float *dev_pcm, int n_samples, 
 void hipb_mel(HipbEngine *e, const float *pcm, int n_samples, float *mel_out);
 /* Drops every request and frees all slots (caches and weights stay). */
 void hipb_reset(HipbEngine *e);
-/* Runs the encoder and cross-attention K/V for every submitted request not yet
- * encoded, in packed batches of at most max_batch_frames encoder frames. */
+/* Runs the encoder and cross-attention K/V for the submitted requests not yet
+ * encoded, in packed batches of at most max_batch_frames encoder frames, as
+ * far as free encoder entries go (hipb_run encodes the rest as entries are
+ * recycled). */
 void hipb_encode(HipbEngine *e, int max_batch_frames);
 /* One decode step over all slots (admission, embed, 8 layers, LM head,
  * argmax/policy).  Returns nothing; state stays on the device. */
 void hipb_step(HipbEngine *e);
-/* Runs decode steps until every encoded request has finished; steps are
- * replayed from one captured graph (launched one by one instead when the
- * environment sets HIPB_EAGER=1, e.g. under a tracing profiler), chunk steps
- * per host check.  Two scheduling knobs, read at hipb_create, change where
+/* Runs decode steps until every submitted request has finished, encoding
+ * the requests still waiting for an encoder entry as finished requests
+ * return theirs; steps are replayed from one captured graph (launched one by
+ * one instead when the environment sets HIPB_EAGER=1, e.g. under a tracing
+ * profiler), chunk steps per host check (at most ring / (4 x slots)).  Two scheduling knobs, read at hipb_create, change where
  * work runs but not the results (same bits): HIPB_RANK_MIN_ROWS (steps of at
  * least this many rows deal attention items to compute units by length rank;
  * default 96) and HIPB_READ_AHEAD=0 (no weight read-ahead workgroups).
@@ -124,7 +135,8 @@ long hipb_process(HipbEngine *e, int max_batch_frames, int chunk);
  * ran out of time. */
 void hipb_test_hold_encoder(HipbEngine *e, int after_batches, int until_finished);
 int  hipb_test_hold_expired(HipbEngine *e);
-/* Number of requests finished so far (device counter, synchronises). */
+/* Number of requests finished so far (device counter, synchronises; also
+ * returns the finished requests' encoder entries for reuse). */
 int  hipb_finished(HipbEngine *e);
 
 /* Results and inspection (synchronise the engine's stream). */
@@ -135,6 +147,8 @@ int  hipb_tokens(HipbEngine *e, int req, int *out, int cap);        /* returns c
 int  hipb_token_scores(HipbEngine *e, int req, float *out, int cap);
 int  hipb_slot_of(HipbEngine *e, int req);                          /* -1 if none    */
 void hipb_logits(HipbEngine *e, int slot, float *out);              /* VOCAB floats  */
+/* Encoder output of a request while it still holds its encoder entry
+ * (fatal once the entry went to a later request). */
 void hipb_enc_out(HipbEngine *e, int req, float *out);              /* T_enc x DEC_D */
 int  hipb_req_frames(HipbEngine *e, int req);
 

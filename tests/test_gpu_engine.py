@@ -506,3 +506,73 @@ def test_engine_process_chain_waits_for_its_encoding(hip, hot, mels):
             assert np.array_equal(eng.tokens(r), w), r
     finally:
         eng.close()
+
+
+def test_engine_entry_pool_recycles(hip, hot):
+    """max_requests bounds the encoder state held at once, not the requests
+    that flow through: 8 entries serve 32 requests (4x), among them a long
+    recording's chained chunks, on 3 slots, both overlapped (hipb_process)
+    and encode-then-run (hipb_run encoding the rest as entries come back).
+    Every request yields its limit, and sampled requests, including two
+    chunks, give the tokens and chosen-logit bits of the same audio alone."""
+    rng = np.random.default_rng(88)
+    n_plain, P = 28, 8
+    pcms = [cb.synth_audio(int(rng.integers(2400, 12000)), 4000 + i) for i in range(n_plain)]
+    limits = [int(x) for x in rng.integers(2, 14, n_plain)]
+    rec = long_recording(REC_SEEDS[1])
+    kw = dict(slots=3, max_requests=P, max_frames=80, kv_bf16=True,
+              max_tokens=len(cb.PROMPT) + 64 + CHUNK_LIMIT + 14, prefill_rows=2)
+    runs = {}
+    for mode in ("process", "run"):
+        eng = cb.Engine(hot, **kw)
+        try:
+            plain = [eng.submit_pcm(p, lim, FLAGS) for p, lim in zip(pcms[:14], limits[:14])]
+            chain = eng.submit_pcm_chunked(rec, CHUNK_LIMIT, FLAGS, **SPLIT)
+            plain += [eng.submit_pcm(p, lim, FLAGS) for p, lim in zip(pcms[14:], limits[14:])]
+            n = len(plain) + len(chain)
+            assert n >= 4 * P
+            print(f"case: {n} requests through {P} encoder entries, {mode}", flush=True)
+            if mode == "process":
+                eng.process(max_batch_frames=40, chunk=2)
+            else:
+                eng.encode(max_batch_frames=40)
+                eng.run(chunk=2)
+            assert eng.finished() == n
+            runs[mode] = ([eng.tokens(r) for r in plain], [eng.scores(r) for r in plain],
+                          [eng.tokens(r) for r in chain], [eng.scores(r) for r in chain])
+        finally:
+            eng.close()
+        toks = runs[mode][0]
+        assert [len(t) for t in toks] == limits, mode
+        assert all(len(t) == CHUNK_LIMIT for t in runs[mode][2]), mode
+    for a, b in zip(runs["process"], runs["run"]):
+        for x, y in zip(a, b):
+            assert np.array_equal(np.asarray(x).view(np.uint32), np.asarray(y).view(np.uint32))
+    ref = cb.chunk_bounds(rec, **SPLIT)
+    for i in (0, 9, 27):
+        alone = cb.Engine(hot, slots=1, max_requests=1, max_frames=80, kv_bf16=True,
+                          max_tokens=len(cb.PROMPT) + 14)
+        try:
+            alone.submit_pcm(pcms[i], limits[i], FLAGS)
+            alone.encode()
+            alone.run(chunk=4)
+            assert np.array_equal(alone.tokens(0), runs["process"][0][i]), i
+            assert np.array_equal(alone.scores(0).view(np.uint32), runs["process"][1][i].view(np.uint32)), i
+        finally:
+            alone.close()
+    # a chunk alone: its audio with the prompt its predecessor's tokens made
+    for c in (1, len(ref) - 1):
+        prev = runs["process"][2][c - 1]
+        nc = min(len(prev) - 1, 64)
+        prompt = list(cb.PROMPT[:2]) + [int(t) for t in prev[len(prev) - 1 - nc:len(prev) - 1]] + list(cb.PROMPT[2:])
+        a, b = ref[c]
+        alone = cb.Engine(hot, slots=1, max_requests=1, max_frames=80, kv_bf16=True,
+                          max_tokens=len(prompt) + CHUNK_LIMIT)
+        try:
+            alone.submit_pcm(rec[a:b], CHUNK_LIMIT, FLAGS, prompt=np.asarray(prompt, np.int32))
+            alone.encode()
+            alone.run(chunk=4)
+            assert np.array_equal(alone.tokens(0), runs["process"][2][c]), c
+            assert np.array_equal(alone.scores(0).view(np.uint32), runs["process"][3][c].view(np.uint32)), c
+        finally:
+            alone.close()
