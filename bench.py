@@ -4,7 +4,8 @@ Workload (one "step"): the continuous-batching stream of 256 requests —
 clip lengths log-normal (median 6 s, sigma 0.5) clipped to [1, 30] s, forced
 decode lengths uniform in [8, 256] (EOS suppressed until the limit, then
 EOS), at most 64 requests in flight; a freed KV slot is refilled from the
-queue on the device.  The PCM of all clips is resident in HBM when the timed
+queue on the device, the waiting requests taken largest token budget first
+(--admit-order 0: in submission order).  The PCM of all clips is resident in HBM when the timed
 region starts; a step runs the GPU log-mel front-end, the packed Conformer
 encoder, cross-attention K/V and the decode loop until every request has
 finished.  value = audio seconds transcribed per wall second (RTFx).
@@ -426,6 +427,8 @@ def main():
     ap.add_argument("--slots", type=int, default=64)
     ap.add_argument("--prefill-rows", type=int, default=16,
                     help="spare step rows that feed prompts several tokens a step")
+    ap.add_argument("--admit-order", type=int, default=1,
+                    help="0: encode and admit in submission order; 1: largest token budget first")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the per-kernel roofline microbenchmarks (for profiling)")
@@ -466,7 +469,8 @@ def main():
     pcm = np.concatenate([cb.synth_audio(int(n), 1000 + i) for i, n in enumerate(samples)])
     # self caches sized for the longest request (prompt + 256 tokens)
     eng = cb.Engine(model, slots=args.slots, max_requests=args.requests, max_frames=376, kv_bf16=True,
-                    max_tokens=len(cb.PROMPT) + 256, prefill_rows=args.prefill_rows)
+                    max_tokens=len(cb.PROMPT) + 256, prefill_rows=args.prefill_rows,
+                    admit_order=args.admit_order)
     # device-resident input: the PCM buffer lives in a second engine-independent
     # allocation (the backend arena)
     dev_pcm = hip.backend_arena_alloc(total)
@@ -508,7 +512,8 @@ def main():
                    "prefill_rows": args.prefill_rows, "audio_sec": round(audio, 1),
                    "encoder_batch_frames": OVERLAP_BATCH_FRAMES or 24576,
                    "encode_decode_overlap": bool(OVERLAP_BATCH_FRAMES),
-                   "generated_tokens": gen_tokens, "kv": "bf16", "parallelism": "single GPU"},
+                   "generated_tokens": gen_tokens, "kv": "bf16", "parallelism": "single GPU",
+                   "admission": "largest token budget first" if args.admit_order else "submission order"},
         "decode_tokens_per_s": round(dec_tps, 1),
         "decode_steps": int(np.mean(steps)),
         "roofline": dict(roofs[DOMINANT], name=DOMINANT) if roofs else None, "rooflines": roofs,

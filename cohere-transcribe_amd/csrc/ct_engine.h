@@ -93,11 +93,11 @@ typedef struct {
      * finished, q[3] prompt tokens not yet fed after the last step, q[4] next
      * fresh request to admit, q[5] fresh requests published, q[6] rows the
      * current step uses (the slots' rows plus the spare rows dealt out),
-     * q[7] encoded watermark: requests with ids below it have their cross
-     * K/V written (host-published after each encoder batch; a released
-     * successor is admitted only once its id is below it), q[8] 1 when the
-     * successor at the head of rq waits for its encoding after the last
-     * admission, q[9] the watermark that admission saw, q[10] successors
+     * q[7] publications of encoded batches so far (each writes its
+     * requests' encoder entries first: a released successor is admitted
+     * only once its entry is there), q[8] 1 when the successor at the head
+     * of rq waits for its encoding after the last admission, q[9] the
+     * publication count that admission saw, q[10] successors
      * released so far (by eng_end; q[10] - q[0] wait in pend or rq) */
     int  *q;
 } CtEngDev;
@@ -110,6 +110,8 @@ typedef struct {
 void ctk_eng_begin(const CtEngDev *d, int extra, hipStream_t s);
 /* Argmax with the request's policy, token append, retirement. */
 void ctk_eng_end(const CtEngDev *d, const float *logits, hipStream_t s);
+/* dst[pairs[2i] & mask] = pairs[2i + 1], i < n (request-ring writes). */
+void ctk_ring_scatter(int *dst, const int *pairs, int n, int mask, hipStream_t s);
 /* Seeded fill of n elements (N(0,1)*scale approx.), bf16 or fp32. */
 void ctk_fill_random(void *p, long n, int bf16, float scale, uint64_t seed, hipStream_t s);
 

@@ -33,6 +33,7 @@ typedef struct {
     int T_mel, T_enc;
     int chained;         /* admitted only after its predecessor chunk ends    */
     int entry;           /* encoder-state entry once encoded, else -1         */
+    int limit;           /* token budget                                      */
     int done;            /* seen retired by the host (recycle)                */
     /* results copied to the host when its request-ring slot was reused */
     int collected, n_out;
@@ -114,7 +115,10 @@ struct HipbEngine {
      * rings of `ring` slots (id & (ring - 1)) */
     HostReq *req;
     int req_cap, ring;
-    int n_req, n_enc;
+    int n_req, n_enc;          /* submitted; encoded (the first n_enc of order) */
+    int *order;                /* [req_cap] encode order: ids by position      */
+    int n_pub;                 /* publications so far (q[7])                   */
+    int *d_pairs;              /* device staging of (id, entry) pairs          */
     int *h_tmp;                /* pinned staging */
     /* request fields as submitted (pinned): length, limit, flags, prompt
      * length, successor, then the prompts; requests [meta_lo, n_req) are
@@ -141,7 +145,7 @@ struct HipbEngine {
 };
 
 #define ECHK(x) ct_hip_check((x), #x, __FILE__, __LINE__)
-#define CT_META_FIELDS 6   /* request fields mirrored on the host (meta_field) */
+#define CT_META_FIELDS 7   /* request fields mirrored on the host (meta_field) */
 
 static void *dmalloc(size_t bytes) {
     void *p = NULL;
@@ -377,9 +381,12 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->M = S;
     e->req_cap = R;
     e->req = calloc(R, sizeof(HostReq));
+    e->order = malloc((size_t)R * sizeof(int));
+    e->d_pairs = dmalloc((size_t)2 * R * sizeof(int));
+    if (cfg->admit_order < 0 || cfg->admit_order > 1) CT_FATAL("hipb_create: admit_order outside [0, 1]");
     e->free_ent = malloc((size_t)R * sizeof(int));
     e->ent_owner = malloc((size_t)R * sizeof(int));
-    if (!e->req || !e->free_ent || !e->ent_owner) CT_FATAL("out of host memory");
+    if (!e->req || !e->order || !e->free_ent || !e->ent_owner) CT_FATAL("out of host memory");
     for (int i = 0; i < R; i++) { e->free_ent[i] = i; e->ent_owner[i] = -1; }
     e->free_head = 0;
     e->free_tail = R;
@@ -397,7 +404,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     ECHK(hipHostMalloc((void **)&e->h_ret, (size_t)ring * sizeof(int), 0));
     /* per batch (at most R requests): subsampling group tables (<= 10 R
      * ints), queue words, published ids, their entries */
-    ECHK(hipHostMalloc((void **)&e->h_enc, (size_t)(12 * R + 64) * sizeof(int), 0));
+    ECHK(hipHostMalloc((void **)&e->h_enc, (size_t)(13 * R + 64) * sizeof(int), 0));
     ECHK(hipStreamSynchronize(e->s));
     return e;
 }
@@ -409,7 +416,7 @@ void hipb_destroy(HipbEngine *e) {
         if (e->have_graph[w]) { hipGraphExecDestroy(e->exec[w]); hipGraphDestroy(e->graph[w]); }
     void *ptrs[] = {e->d.slot_req, e->d.slot_S, e->d.slot_np, e->d.slot_T, e->d.slot_flags,
                     e->d.slot_lim, e->d.slot_ng, e->d.slot_tok, e->d.slot_ent, e->d.act, e->d.tok, e->d.pos_len,
-                    e->d.cross_len, e->d.req_entry, e->d.ret, e->e_dstrow,
+                    e->d.cross_len, e->d.req_entry, e->d.ret, e->e_dstrow, e->d_pairs,
                     e->d.row_slot, e->d.rank_self, e->d.rank_cross, e->warm_sink,
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.req_score, e->d.q,
@@ -427,6 +434,7 @@ void hipb_destroy(HipbEngine *e) {
         free(e->req[r].mel); free(e->req[r].pcm); free(e->req[r].out); free(e->req[r].score);
     }
     free(e->req);
+    free(e->order);
     free(e->free_ent);
     free(e->ent_owner);
     pthread_mutex_destroy(&e->mu);
@@ -451,6 +459,7 @@ void hipb_reset(HipbEngine *e) {
     atomic_store(&e->n_assigned, 0);
     e->meta_lo = 0;
     e->fq_count = 0;
+    e->n_pub = 0;
     e->ret_seen = 0;
     for (int i = 0; i < e->d.max_req; i++) { e->free_ent[i] = i; e->ent_owner[i] = -1; }
     e->free_head = 0;
@@ -478,8 +487,8 @@ static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prom
                          int flags);
 
 /* Host mirror of the request ring: field f (0 length, 1 limit, 2 flags,
- * 3 prompt length, 4 successor, 5 tokens generated = 0) at ring slot i,
- * then the prompts. */
+ * 3 prompt length, 4 successor, 5 tokens generated = 0, 6 encoder entry =
+ * -1 until published) at ring slot i, then the prompts. */
 static int *meta_field(HipbEngine *e, int f) { return e->h_meta + (size_t)f * e->ring; }
 static int *meta_prompt(HipbEngine *e, int r) {
     return e->h_meta + (size_t)CT_META_FIELDS * e->ring + (size_t)(r & (e->ring - 1)) * CT_PROMPT_MAX;
@@ -504,7 +513,7 @@ static void flush_meta(HipbEngine *e) {
     const int lo = e->meta_lo, n = e->n_req - lo;
     if (n <= 0) return;
     int *const dst[CT_META_FIELDS] = {e->d.req_T, e->d.req_limit, e->d.req_flags, e->d.req_np,
-                                      e->d.req_next, e->d.req_ngen};
+                                      e->d.req_next, e->d.req_ngen, e->d.req_entry};
     for (int f = 0; f < CT_META_FIELDS; f++) ring_put(e, dst[f], meta_field(e, f), lo, n, 1, e->s);
     ring_put(e, e->d.req_prompt, e->h_meta + (size_t)CT_META_FIELDS * e->ring, lo, n, CT_PROMPT_MAX, e->s);
     e->meta_lo = e->n_req;
@@ -618,6 +627,9 @@ static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prom
         if (!nr) CT_FATAL("out of host memory");
         memset(nr + e->req_cap, 0, (size_t)(nc - e->req_cap) * sizeof(HostReq));
         e->req = nr;
+        int *no = realloc(e->order, (size_t)nc * sizeof(int));
+        if (!no) CT_FATAL("out of host memory");
+        e->order = no;
         e->req_cap = nc;
     }
     const int r = e->n_req;
@@ -628,6 +640,8 @@ static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prom
     q->T_mel = T_mel;
     q->T_enc = Te;
     q->entry = -1;
+    q->limit = limit;
+    e->order[r] = r;
     /* the ring slot's mirror entries were last uploaded for request
      * r - ring, which has finished, so no upload is still reading them */
     const int rs = r & (e->ring - 1);
@@ -637,6 +651,7 @@ static int submit_common(HipbEngine *e, int T_mel, const int *prompt, int n_prom
     meta_field(e, 3)[rs] = n_prompt;
     meta_field(e, 4)[rs] = -1;
     meta_field(e, 5)[rs] = 0;
+    meta_field(e, 6)[rs] = -1;
     int *pp = meta_prompt(e, r);
     memset(pp, 0, sizeof(int) * CT_PROMPT_MAX);
     memcpy(pp, prompt, (size_t)n_prompt * sizeof(int));
@@ -708,12 +723,12 @@ static void enc_reserve(HipbEngine *e, int frames, int max_tmel) {
     e->sub_cap = sc;
 }
 
-/* Encodes requests [r0, r1) as one packed batch. */
-/* Grows the mel, PCM and clip-table buffers for the batch [r0, r1). */
-static void batch_buffers(HipbEngine *e, int r0, int r1) {
+/* Grows the mel, PCM and clip-table buffers for the batch ids[0..n). */
+static void batch_buffers(HipbEngine *e, const int *ids, int n) {
     size_t mel_need = 0, pcm_need = 0;
     int nclip = 0, nfr = 0;
-    for (int r = r0; r < r1; r++) {
+    for (int i = 0; i < n; i++) {
+        const int r = ids[i];
         mel_need += (size_t)N_MELS * e->req[r].T_mel;
         if (e->req[r].pcm || e->req[r].dpcm) {
             if (e->req[r].pcm) pcm_need += e->req[r].n;
@@ -759,10 +774,11 @@ static void pos_tables(HipbEngine *e) {
              CT_EPI_STORE, 0, NULL);
 }
 
-static void encode_batch(HipbEngine *e, int r0, int r1) {
-    const int n = r1 - r0;
+/* Encodes the requests ids[0..n) as one packed batch. */
+static void encode_batch(HipbEngine *e, const int *ids, int n) {
     int M = 0, tmel_max = 0, T_max = 0;
-    for (int r = r0; r < r1; r++) {
+    for (int i = 0; i < n; i++) {
+        const int r = ids[i];
         M += e->req[r].T_enc;
         if (e->req[r].T_mel > tmel_max) tmel_max = e->req[r].T_mel;
         if (e->req[r].T_enc > T_max) T_max = e->req[r].T_enc;
@@ -776,7 +792,7 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     int *seq_off = malloc(n * sizeof(int)), *seq_T = malloc(n * sizeof(int));
     int off = 0;
     for (int i = 0; i < n; i++) {
-        const int r = r0 + i, T = e->req[r].T_enc, ent = e->req[r].entry;
+        const int r = ids[i], T = e->req[r].T_enc, ent = e->req[r].entry;
         if (ent < 0) CT_FATAL("encode: request without an encoder entry");
         seq_off[i] = off;
         seq_T[i] = T;
@@ -802,22 +818,22 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     ECHK(hipMemcpyAsync(e->e_blk_q0, blk_q0, nblk * sizeof(int), hipMemcpyHostToDevice, s));
 
     /* mel for every request of the batch, then the subsampling */
-    batch_buffers(e, r0, r1);
+    batch_buffers(e, ids, n);
     /* log-mel on the GPU for PCM requests, uploaded mel otherwise */
     {
         int nclip = 0, nfr = 0;
-        for (int r = r0; r < r1; r++)
-            if (e->req[r].pcm || e->req[r].dpcm) {
+        for (int i = 0; i < n; i++)
+            if (e->req[ids[i]].pcm || e->req[ids[i]].dpcm) {
                 nclip++;
-                nfr += e->req[r].T_mel;
+                nfr += e->req[ids[i]].T_mel;
             }
         if (nclip) {
             CtMelClip *cl = malloc(nclip * sizeof *cl);
             int *fc = malloc(nfr * sizeof(int));
             size_t po = 0, mo = 0;
             int ci = 0, fo = 0;
-            for (int r = r0; r < r1; r++) {
-                HostReq *q = &e->req[r];
+            for (int i = 0; i < n; i++) {
+                HostReq *q = &e->req[ids[i]];
                 if (q->pcm || q->dpcm) {
                     const float *src = q->dpcm;
                     if (q->pcm) {
@@ -842,7 +858,7 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
     const Weights *W = &e->W;
     int *mel_off = malloc(n * sizeof(int));
     for (int i = 0; i < n; i++) {
-        HostReq *q = &e->req[r0 + i];
+        HostReq *q = &e->req[ids[i]];
         mel_off[i] = (int)moff;
         if (q->mel)
             ECHK(hipMemcpyAsync(e->emel + moff, q->mel, (size_t)N_MELS * q->T_mel * 4, hipMemcpyHostToDevice, s));
@@ -862,7 +878,7 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         long s2 = 0;
         int g1 = g0;
         while (g1 < n) {
-            const int tm = e->req[r0 + g1].T_mel, T1 = (tm + 1) / 2, T2 = (T1 + 1) / 2;
+            const int tm = e->req[ids[g1]].T_mel, T1 = (tm + 1) / 2, T2 = (T1 + 1) / 2;
             const long b = (long)T2 * 32 * SUB_CH;
             if (g1 > g0 && 2 * (s2 + b) > e->sub_cap) break;
             s2 += b; g1++;
@@ -871,7 +887,7 @@ static void encode_batch(HipbEngine *e, int r0, int r1) {
         int *o1 = tab_h, *o2 = o1 + L, *o3 = o2 + L, *tm = o3 + L, *mo = tm + L;
         o1[0] = o2[0] = o3[0] = 0;
         for (int j = 0; j < ng; j++) {
-            const HostReq *q = &e->req[r0 + g0 + j];
+            const HostReq *q = &e->req[ids[g0 + j]];
             const int T1 = (q->T_mel + 1) / 2, T2 = (T1 + 1) / 2;
             o1[j + 1] = o1[j] + T1;
             o2[j + 1] = o2[j] + T2;
@@ -970,59 +986,88 @@ static void ring_put_seq(HipbEngine *e, int *dst, const int *src, long lo, int n
     if (n > n1) ECHK(hipMemcpyAsync(dst, src + n1, (size_t)(n - n1) * sizeof(int), hipMemcpyHostToDevice, s));
 }
 
-/* Publishes the encoded requests [r0, r1) (their cross K/V are written: the
- * encoder stream has been drained): their encoder entries into the request
- * ring, the encoded watermark q[7] = r1, which releases chained successors
- * below it, then the requests that wait for no predecessor appended to the
- * fresh queue in submission order (the ids first, then the new count).  All
- * copies go on the encoder stream, which is then drained; the step kernel
- * reads the words with acquire loads, possibly while running on the other
- * stream. */
-static void publish(HipbEngine *e, int r0, int r1) {
+/* Publishes the encoded requests ids[0..n) (their cross K/V are written: the
+ * encoder stream has been drained): their encoder entries into their
+ * request-ring slots (an entry >= 0 marks a request encoded; a released
+ * chained successor is admitted only then), the publication count q[7],
+ * then the requests that wait for no predecessor appended to the fresh
+ * queue in the order given (the ids first, then the new count).  All copies
+ * go on the encoder stream, which is then drained; the step kernel reads the
+ * words with acquire loads, possibly while running on the other stream. */
+static void publish(HipbEngine *e, const int *ids, int n) {
     const int P = e->d.max_req;
-    int *words = e->h_enc + 10 * P + 8;   /* [0] watermark, [1] fresh count */
-    int *ids = e->h_enc + 10 * P + 16, *ents = ids + P, k = 0;
-    /* a publication covers at most P requests (each holds an entry) */
-    for (int lo = r0; lo < r1; lo += P) {
-        const int hi = r1 - lo > P ? lo + P : r1;
-        for (int i = lo; i < hi; i++) ents[i - lo] = e->req[i].entry;
-        ring_put_seq(e, e->d.req_entry, ents, lo, hi - lo, e->enc_s);
-        ECHK(hipStreamSynchronize(e->enc_s));
+    int *words = e->h_enc + 10 * P + 8;   /* [0] publications, [1] fresh count */
+    int *fresh = e->h_enc + 10 * P + 16, *pairs = fresh + P, k = 0;
+    /* at most P requests hold entries, so n <= P */
+    if (n > P) CT_FATAL("publish: more requests than encoder entries");
+    for (int i = 0; i < n; i++) {
+        pairs[2 * i] = ids[i];
+        pairs[2 * i + 1] = e->req[ids[i]].entry;
     }
-    words[0] = r1;
+    if (n) {
+        ECHK(hipMemcpyAsync(e->d_pairs, pairs, (size_t)2 * n * sizeof(int), hipMemcpyHostToDevice, e->enc_s));
+        ctk_ring_scatter(e->d.req_entry, e->d_pairs, n, e->ring - 1, e->enc_s);
+    }
+    words[0] = ++e->n_pub;
     ECHK(hipMemcpyAsync(e->d.q + 7, &words[0], sizeof(int), hipMemcpyHostToDevice, e->enc_s));
-    for (int i = r0; i <= r1; i++) {
-        if (i < r1 && !e->req[i].chained) ids[k++] = i;
-        if (k && (k == P || i == r1)) {
-            ring_put_seq(e, e->d.fq, ids, e->fq_count, k, e->enc_s);
-            e->fq_count += k;
-            words[1] = e->fq_count;
-            ECHK(hipMemcpyAsync(e->d.q + 5, &words[1], sizeof(int), hipMemcpyHostToDevice, e->enc_s));
-            ECHK(hipStreamSynchronize(e->enc_s));
-            k = 0;
-        }
+    for (int i = 0; i < n; i++)
+        if (!e->req[ids[i]].chained) fresh[k++] = ids[i];
+    if (k) {
+        ring_put_seq(e, e->d.fq, fresh, e->fq_count, k, e->enc_s);
+        e->fq_count += k;
+        words[1] = e->fq_count;
+        ECHK(hipMemcpyAsync(e->d.q + 5, &words[1], sizeof(int), hipMemcpyHostToDevice, e->enc_s));
     }
     ECHK(hipStreamSynchronize(e->enc_s));
-    atomic_store(&e->published, r1);
+    atomic_store(&e->published, e->n_pub);
 }
 
-static void release_inputs(HipbEngine *e, int r0, int r1) {
-    for (int i = r0; i < r1; i++) {
-        free(e->req[i].mel); e->req[i].mel = NULL;
-        free(e->req[i].pcm); e->req[i].pcm = NULL;
+static void release_inputs(HipbEngine *e, const int *ids, int n) {
+    for (int i = 0; i < n; i++) {
+        HostReq *q = &e->req[ids[i]];
+        free(q->mel); q->mel = NULL;
+        free(q->pcm); q->pcm = NULL;
     }
 }
 
-/* The next batch of not yet encoded requests: [r, *r1) with at most
- * max_batch_frames encoder frames and at most max_n requests (at least
- * one request). */
-static int next_batch(const HipbEngine *e, int r, int max_batch_frames, int max_n) {
-    int frames = 0, r1 = r;
-    while (r1 < e->n_req && (r1 == r || (frames + e->req[r1].T_enc <= max_batch_frames && r1 - r < max_n))) {
-        frames += e->req[r1].T_enc;
-        r1++;
+/* The next batch of not yet encoded requests in encode order: positions
+ * [p, p1) of e->order with at most max_batch_frames encoder frames and at
+ * most max_n requests (at least one request). */
+static int next_batch(const HipbEngine *e, int p, int max_batch_frames, int max_n) {
+    int frames = 0, p1 = p;
+    while (p1 < e->n_req &&
+           (p1 == p || (frames + e->req[e->order[p1]].T_enc <= max_batch_frames && p1 - p < max_n))) {
+        frames += e->req[e->order[p1]].T_enc;
+        p1++;
     }
-    return r1;
+    return p1;
+}
+
+typedef struct { int key, id; } OrderKey;
+
+static int order_cmp(const void *a, const void *b) {
+    const OrderKey *x = a, *y = b;
+    return x->key != y->key ? (x->key < y->key ? -1 : 1) : (x->id < y->id ? -1 : x->id > y->id);
+}
+
+/* Encode (and so admission) order of the requests not yet encoded: as
+ * submitted, or with admit_order 1 the largest token budget first (a
+ * recording's chunks keep their order, together, under the first chunk's
+ * budget).  Longest-first shortens the pass: fewer slots idle at its end. */
+static void plan_order(HipbEngine *e) {
+    const int p0 = e->n_enc, n = e->n_req - p0;
+    if (e->cfg.admit_order != 1 || n < 2) return;
+    OrderKey *k = malloc((size_t)n * sizeof *k);
+    if (!k) CT_FATAL("out of host memory");
+    for (int i = 0; i < n; i++) {
+        const int r = e->order[p0 + i];
+        int h = r;
+        while (e->req[h].chained) h--;
+        k[i] = (OrderKey){-e->req[h].limit, r};
+    }
+    qsort(k, (size_t)n, sizeof *k, order_cmp);
+    for (int i = 0; i < n; i++) e->order[p0 + i] = k[i].id;
+    free(k);
 }
 
 /* Encoder entries free right now (thread-safe). */
@@ -1033,18 +1078,18 @@ static int free_entries(HipbEngine *e) {
     return n;
 }
 
-/* Gives requests [r0, r1) encoder entries from the free FIFO (the caller
- * made sure there are enough). */
-static void take_entries(HipbEngine *e, int r0, int r1) {
+/* Gives the requests at encode positions [p0, p1) encoder entries from the
+ * free FIFO (the caller made sure there are enough). */
+static void take_entries(HipbEngine *e, int p0, int p1) {
     const int P = e->d.max_req;
     pthread_mutex_lock(&e->mu);
-    if (e->free_tail - e->free_head < r1 - r0) CT_FATAL("encode: fewer free encoder entries than requests");
-    for (int r = r0; r < r1; r++) {
-        const int ent = e->free_ent[e->free_head++ % P];
+    if (e->free_tail - e->free_head < p1 - p0) CT_FATAL("encode: fewer free encoder entries than requests");
+    for (int p = p0; p < p1; p++) {
+        const int r = e->order[p], ent = e->free_ent[e->free_head++ % P];
         e->req[r].entry = ent;
         e->ent_owner[ent] = r;
     }
-    atomic_store(&e->n_assigned, r1);
+    atomic_store(&e->n_assigned, p1);
     pthread_mutex_unlock(&e->mu);
 }
 
@@ -1086,19 +1131,20 @@ static int entries_short(HipbEngine *e) {
  * requests not yet encoded, as far as free encoder entries go, and
  * publishes them. */
 static void encode_available(HipbEngine *e, int max_batch_frames) {
-    int r = e->n_enc;
-    while (r < e->n_req) {
+    plan_order(e);
+    int p = e->n_enc;
+    while (p < e->n_req) {
         const int avail = free_entries(e);
         if (!avail) break;
-        const int r1 = next_batch(e, r, max_batch_frames, avail);
-        take_entries(e, r, r1);
-        encode_batch(e, r, r1);
-        release_inputs(e, r, r1);
-        r = r1;
+        const int p1 = next_batch(e, p, max_batch_frames, avail);
+        take_entries(e, p, p1);
+        encode_batch(e, e->order + p, p1 - p);
+        release_inputs(e, e->order + p, p1 - p);
+        p = p1;
     }
-    const int r0 = e->n_enc;
-    e->n_enc = r;
-    publish(e, r0, r);
+    const int p0 = e->n_enc;
+    e->n_enc = p;
+    publish(e, e->order + p0, p - p0);
 }
 
 void hipb_encode(HipbEngine *e, int max_batch_frames) {
@@ -1408,17 +1454,17 @@ static void *enc_worker(void *arg) {
     ECHK(hipSetDevice(e->dev));
     ct_t.dev = e->dev;                 /* weight pointers translate per device */
     int batches = 0;
-    for (int r = e->n_enc; r < e->n_req;) {
+    for (int p = e->n_enc; p < e->n_req;) {
         pthread_mutex_lock(&e->mu);
         while (e->free_tail == e->free_head) pthread_cond_wait(&e->cv, &e->mu);
         const int avail = (int)(e->free_tail - e->free_head);
         pthread_mutex_unlock(&e->mu);
-        const int r1 = next_batch(e, r, e->proc_batch, avail);
-        take_entries(e, r, r1);
-        encode_batch(e, r, r1);
-        release_inputs(e, r, r1);
-        publish(e, r, r1);
-        r = r1;
+        const int p1 = next_batch(e, p, e->proc_batch, avail);
+        take_entries(e, p, p1);
+        encode_batch(e, e->order + p, p1 - p);
+        release_inputs(e, e->order + p, p1 - p);
+        publish(e, e->order + p, p1 - p);
+        p = p1;
         if (++batches == e->hold_batches) {
             /* test support: a bounded host-side wait (60 s) */
             int waited = 0;
@@ -1445,17 +1491,18 @@ long hipb_process(HipbEngine *e, int max_batch_frames, int chunk) {
      * sizing for those from every start covers them all. */
     ensure_graph(e, 0);
     if (spare) ensure_graph(e, 1);
+    plan_order(e);
     {
         int frames_max = 0, tmel_max = 0;
-        for (int r = e->n_enc; r < e->n_req; r++) {
-            const int r1 = next_batch(e, r, max_batch_frames, e->n_req);
+        for (int p = e->n_enc; p < e->n_req; p++) {
+            const int p1 = next_batch(e, p, max_batch_frames, e->n_req);
             int f = 0;
-            for (int i = r; i < r1; i++) {
-                f += e->req[i].T_enc;
-                if (e->req[i].T_mel > tmel_max) tmel_max = e->req[i].T_mel;
+            for (int i = p; i < p1; i++) {
+                f += e->req[e->order[i]].T_enc;
+                if (e->req[e->order[i]].T_mel > tmel_max) tmel_max = e->req[e->order[i]].T_mel;
             }
             if (f > frames_max) frames_max = f;
-            batch_buffers(e, r, r1);
+            batch_buffers(e, e->order + p, p1 - p);
         }
         if (frames_max) {
             enc_reserve(e, frames_max, tmel_max);

@@ -98,9 +98,10 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     }
     // Released successors join the ring rq in slot order, then the free
     // slots, in slot order, take the waiting successors (rq[q0..), the ones
-    // joining now last) up to the first one not yet encoded (ring order is
-    // kept: it and those behind it wait), then fresh requests (fq[q4..q5),
-    // all encoded when published): the c-th free slot takes the c-th of them.
+    // joining now last) up to the first one not yet encoded, i.e. without an
+    // encoder entry published (ring order is kept: it and those behind it
+    // wait), then fresh requests (fq[q4..q5), all encoded when published):
+    // the c-th free slot takes the c-th of them.
     // One prefix counts both (pending in the low 16 bits, free in the high).
     const bool is_p = s < d.slots && pend >= 0, is_f = s < d.slots && r < 0;
     int tot;
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(256) void eng_begin_kernel(CtEngDev d, int extra) {
     if (tid < lim) {
         const int c = tid < waiting ? d.rq[(q0 + tid) & mk] : s_app[tid - waiting];
         s_cand[tid] = c;
-        if (c >= wm) atomicMin(&s_q[5], tid);
+        if (d.req_entry[c & mk] < 0) atomicMin(&s_q[5], tid);   // not published yet
     }
     __syncthreads();
     const int blocked = s_q[5];                  // INT_MAX: none of the lim
@@ -298,6 +299,12 @@ __global__ __launch_bounds__(256) void eng_end_kernel(CtEngDev d, const float *l
     }
 }
 
+// dst[pairs[2i] & mask] = pairs[2i + 1] for i < n.
+__global__ void ring_scatter_kernel(int *dst, const int *pairs, int n, int mask) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[pairs[2 * i] & mask] = pairs[2 * i + 1];
+}
+
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
     z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
@@ -331,6 +338,11 @@ extern "C" void ctk_eng_begin(const CtEngDev *d, int extra, hipStream_t s) {
 
 extern "C" void ctk_eng_end(const CtEngDev *d, const float *logits, hipStream_t s) {
     hipLaunchKernelGGL(eng_end_kernel, dim3(d->slots), dim3(256), 0, s, *d, logits);
+}
+
+extern "C" void ctk_ring_scatter(int *dst, const int *pairs, int n, int mask, hipStream_t s) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(ring_scatter_kernel, dim3((n + 255) / 256), dim3(256), 0, s, dst, pairs, n, mask);
 }
 
 extern "C" void ctk_fill_random(void *p, long n, int bf16, float scale, uint64_t seed, hipStream_t s) {

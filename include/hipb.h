@@ -50,6 +50,11 @@ typedef struct {
                            tokens wait, hipb_run launches a step of slots +
                            prefill_rows rows that feeds several prompt tokens
                            of a slot at once (same bits as one per step)       */
+    int admit_order;    /* 0: requests are encoded and admitted in submission
+                           order; 1: largest token budget (limit) first, a
+                           recording's chunks together in order under the
+                           first chunk's budget (shortens a pass: fewer slots
+                           idle at its end); results are the same bits      */
 } HipbConfig;
 
 /* Request policy flags. */

@@ -209,13 +209,15 @@ def test_ragged_batch32_vs_single(hip):
                       f"request {r} ({secs[r]:.1f} s, {limits[r]} tokens) alone vs batch of 32")
 
 
-def test_stream256_counts_and_samples_alone(hip):
+@pytest.mark.parametrize("admit_order", [0, 1])
+def test_stream256_counts_and_samples_alone(hip, admit_order):
     """The continuous-batching stream: 256 requests (clips lognormal, median
     6 s, in [1, 30] s; limits U[8, 256]), 64 slots, 16 spare prompt rows,
     encoding in batches of 6144 frames overlapped with decoding.  Every
     request yields exactly its limit; four requests (the longest clip, the
     longest limit, the last submitted, one more) rerun alone give the same
-    tokens and chosen-logit bits."""
+    tokens and chosen-logit bits.  In submission order, and largest token
+    budget first."""
     m = model(hip, 2)
     rng = np.random.default_rng(3)
     secs = np.clip(np.exp(rng.normal(np.log(6.0), 0.5, 256)), 1.0, 30.0)
@@ -223,7 +225,7 @@ def test_stream256_counts_and_samples_alone(hip):
     limits = rng.integers(8, 257, 256)
     pcms = [cb.synth_audio(int(n), 1000 + i) for i, n in enumerate(samples)]
     eng = cb.Engine(m, slots=64, max_requests=256, max_frames=376, kv_bf16=True,
-                    max_tokens=len(cb.PROMPT) + 256, prefill_rows=16)
+                    max_tokens=len(cb.PROMPT) + 256, prefill_rows=16, admit_order=admit_order)
     try:
         for p, lim in zip(pcms, limits):
             eng.submit_pcm(p, int(lim), cb.HIPB_SUPPRESS_EOS | cb.HIPB_FORCE_EOS)
@@ -232,7 +234,7 @@ def test_stream256_counts_and_samples_alone(hip):
         toks = [eng.tokens(r) for r in range(256)]
         sample = sorted({int(np.argmax(samples)), int(np.argmax(limits)), 255, 100})
         scores = {r: eng.scores(r) for r in sample}
-        print(f"case: stream of 256: {steps} steps", flush=True)
+        print(f"case: stream of 256, admit_order {admit_order}: {steps} steps", flush=True)
     finally:
         eng.close()
     assert [len(t) for t in toks] == [int(x) for x in limits]

@@ -88,21 +88,26 @@ def run_stepwise(eng, n_req, max_steps=64):
     return hist
 
 
-def test_engine_admission_order(hip, hot, mels):
+@pytest.mark.parametrize("admit_order", [0, 1])
+def test_engine_admission_order(hip, hot, mels, admit_order):
     """Admission follows the policy step by step: before each step the free
-    slots, in slot order, take the waiting requests in submission order; a
-    request then holds its slot for len(prompt) + limit - 1 steps (one prompt
-    id a step, the last one yielding the first token) and frees it after the
-    step that generates its limit-th token.  Checked against a host model of
-    that policy after every step, with more requests than slots."""
-    limits = [3, 7, 2, 5, 4, 1, 6]
+    slots, in slot order, take the waiting requests in submission order (or,
+    with admit_order 1, largest token budget first, ties in submission
+    order); a request then holds its slot for len(prompt) + limit - 1 steps
+    (one prompt id a step, the last one yielding the first token) and frees
+    it after the step that generates its limit-th token.  Checked against a
+    host model of that policy after every step, with more requests than
+    slots."""
+    limits = [3, 7, 2, 5, 4, 1, 6, 7]
     n, S, npr = len(limits), 3, len(cb.PROMPT)
-    eng = cb.Engine(hot, slots=S, max_requests=n, max_frames=64, kv_bf16=True, prefill_rows=0)
+    eng = cb.Engine(hot, slots=S, max_requests=n, max_frames=64, kv_bf16=True, prefill_rows=0,
+                    admit_order=admit_order)
     try:
         for i, lim in enumerate(limits):
             eng.submit(mels[i % len(mels)], lim, FLAGS)
         eng.encode()
-        slots, left, waiting = [None] * S, {}, list(range(n))
+        waiting = sorted(range(n), key=lambda r: (-limits[r], r)) if admit_order else list(range(n))
+        slots, left = [None] * S, {}
         for step in range(200):
             for s in range(S):
                 if slots[s] is None and waiting:
