@@ -180,9 +180,10 @@ def decode_gemm_roofline(model, ev, slots=64, reps=20):
             "workload": f"{slots} slots, one step's 49 GEMMs (268.4 MB of bf16 weights)"}
 
 
-def encoder_gemm_roofline(model, ev, M=16384, reps=10):
+def encoder_gemm_roofline(model, ev, ffn_bf16, M=16384, reps=10):
     K, N = cb.ENC_D, cb.ENC_FF
-    eng = cb.Engine(model, slots=1, max_requests=1, max_frames=8, kv_bf16=True)
+    eng = cb.Engine(model, slots=1, max_requests=1, max_frames=8, kv_bf16=True,
+                    enc_ffn_bf16=ffn_bf16)
     try:
         s = eng.stream()
         eng.encoder_gemm(M)
@@ -195,13 +196,20 @@ def encoder_gemm_roofline(model, ev, M=16384, reps=10):
     finally:
         eng.close()
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-    return {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
-            "kernel": "gemm_split256_kernel (encoder FFN up, SiLU, pre-split in/out)",
-            "avg_launch_us": round(ms * 1e3, 1), "flops_per_launch": 2 * M * N * K,
-            "workload": f"M={M} N={N} K={K}",
-            "note": "activations as hi+lo bf16 against exact bf16 weights: the MFMA pipe runs "
-                    "2x the algorithmic flops counted here"}
+    out = {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+           "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
+           "avg_launch_us": round(ms * 1e3, 1), "flops_per_launch": 2 * M * N * K,
+           "workload": f"M={M} N={N} K={K}"}
+    if ffn_bf16:
+        out.update(kernel="gemm_split256_kernel<false> (encoder FFN up, SiLU, single-pass bf16 "
+                          "in/out)",
+                   note="bf16 activations (rounded by the producer) against bf16 weights, fp32 "
+                        "accumulation: the MFMA pipe runs the algorithmic flops counted here")
+    else:
+        out.update(kernel="gemm_split256_kernel<true> (encoder FFN up, SiLU, pre-split in/out)",
+                   note="activations as hi+lo bf16 against exact bf16 weights: the MFMA pipe "
+                        "runs 2x the algorithmic flops counted here")
+    return out
 
 
 def copy_calibration(ev, stream, mib=256):
@@ -240,11 +248,12 @@ def with_traffic(rooflines):
         for k, r in rooflines.items():
             if k in tr.get("per_launch_bytes", {}):
                 r["traffic"] = tr["per_launch_bytes"][k]
-    if os.path.exists(MFMA_FILE) and "encoder_gemm" in rooflines:
+    if os.path.exists(MFMA_FILE):
         with open(MFMA_FILE) as f:
             mf = json.load(f)
-        if "encoder_gemm" in mf:
-            rooflines["encoder_gemm"]["mfma_counters"] = dict(mf["encoder_gemm"], source=mf["source"])
+        for k, r in rooflines.items():
+            if k in mf and mf[k].get("kernel") == r.get("kernel"):
+                r["mfma_counters"] = dict(mf[k], source=mf["source"])
     return rooflines
 
 
@@ -406,10 +415,15 @@ def _ref_single_clip(secs):
     return time.perf_counter() - t0
 
 
-def measure_rooflines(hip, model, ev, step_reps=5):
+def measure_rooflines(hip, model, ev, ffn_bf16, step_reps=5):
+    """Per-kernel rooflines; encoder_gemm is the FFN GEMM in the stream's
+    precision mode, encoder_gemm_split the fp32-accurate form beside it
+    when the stream runs the single-pass one."""
     att, micro = attention_roofline(hip, model, ev, step_reps=step_reps)
     roofs = {"attention": att, "decode_gemm": decode_gemm_roofline(model, ev),
-             "encoder_gemm": encoder_gemm_roofline(model, ev)}
+             "encoder_gemm": encoder_gemm_roofline(model, ev, ffn_bf16)}
+    if ffn_bf16:
+        roofs["encoder_gemm_split"] = encoder_gemm_roofline(model, ev, 0)
     tmp = cb.Engine(model, slots=1, max_requests=1, max_frames=8, kv_bf16=True)
     try:
         copy_calibration(ev, tmp.stream())
@@ -429,6 +443,9 @@ def main():
                     help="spare step rows that feed prompts several tokens a step")
     ap.add_argument("--admit-order", type=int, default=1,
                     help="0: encode and admit in submission order; 1: largest token budget first")
+    ap.add_argument("--enc-ffn-bf16", type=int, default=1,
+                    help="1: the encoder's FFN projections in single-pass bf16 (inputs rounded "
+                         "to bf16, fp32 accumulation); 0: fp32-accurate hi+lo split")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the per-kernel roofline microbenchmarks (for profiling)")
@@ -460,7 +477,7 @@ def main():
     ev = cb.HipEvents()
 
     if args.roofline_only:
-        roofs, micro = measure_rooflines(hip, model, ev, step_reps=0)
+        roofs, micro = measure_rooflines(hip, model, ev, args.enc_ffn_bf16, step_reps=0)
         print(json.dumps({"rooflines": roofs, "decode_microbench": micro}))
         return
 
@@ -470,7 +487,7 @@ def main():
     # self caches sized for the longest request (prompt + 256 tokens)
     eng = cb.Engine(model, slots=args.slots, max_requests=args.requests, max_frames=376, kv_bf16=True,
                     max_tokens=len(cb.PROMPT) + 256, prefill_rows=args.prefill_rows,
-                    admit_order=args.admit_order)
+                    admit_order=args.admit_order, enc_ffn_bf16=args.enc_ffn_bf16)
     # device-resident input: the PCM buffer lives in a second engine-independent
     # allocation (the backend arena)
     dev_pcm = hip.backend_arena_alloc(total)
@@ -499,7 +516,8 @@ def main():
         dec_tps = gen_tokens / (float(np.sum(dec_times)) / args.steps)
     eng.close()
 
-    roofs, micro = ({}, {}) if args.no_rooflines else measure_rooflines(hip, model, ev)
+    roofs, micro = ({}, {}) if args.no_rooflines else measure_rooflines(hip, model, ev,
+                                                                         args.enc_ffn_bf16)
 
     out = {
         "metric": METRIC, "value": round(rtfx, 2), "unit": "audio-sec/sec", "n_gpus": 1,
@@ -513,7 +531,8 @@ def main():
                    "encoder_batch_frames": OVERLAP_BATCH_FRAMES or 24576,
                    "encode_decode_overlap": bool(OVERLAP_BATCH_FRAMES),
                    "generated_tokens": gen_tokens, "kv": "bf16", "parallelism": "single GPU",
-                   "admission": "largest token budget first" if args.admit_order else "submission order"},
+                   "admission": "largest token budget first" if args.admit_order else "submission order",
+                   "encoder_ffn": "single-pass bf16" if args.enc_ffn_bf16 else "hi+lo split"},
         "decode_tokens_per_s": round(dec_tps, 1),
         "decode_steps": int(np.mean(steps)),
         "roofline": dict(roofs[DOMINANT], name=DOMINANT) if roofs else None, "rooflines": roofs,

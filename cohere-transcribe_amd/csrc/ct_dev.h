@@ -21,8 +21,6 @@ __device__ __forceinline__ uint16_t f2bf(float x) {
     return (uint16_t)(u >> 16);
 }
 
-// x = hi + lo + r with hi, lo bf16 and |r| <= 2^-17 |x|: the two-term split
-// that lets bf16 MFMA multiply an fp32 activation by an exact bf16 weight.
 // 1 / (1 + e^-x) on the hardware exp2 (e^-x = 2^(-x log2 e)) and
 // reciprocal, each about 1 ulp: within a few units in the last place of the
 // expf-and-divide forms of SiLU and the GLU gate (backends/cpu/backend.c:62,
@@ -32,6 +30,8 @@ __device__ __forceinline__ float sigmoid_hw(float x) {
     return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
 }
 
+// x = hi + lo + r with hi, lo bf16 and |r| <= 2^-17 |x|: the two-term split
+// that lets bf16 MFMA multiply an fp32 activation by an exact bf16 weight.
 __device__ __forceinline__ void split_bf16(float x, uint16_t &hi, uint16_t &lo) {
     hi = f2bf(x);
     lo = f2bf(x - bf2f(hi));

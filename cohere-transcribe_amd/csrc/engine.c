@@ -384,6 +384,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->order = malloc((size_t)R * sizeof(int));
     e->d_pairs = dmalloc((size_t)2 * R * sizeof(int));
     if (cfg->admit_order < 0 || cfg->admit_order > 1) CT_FATAL("hipb_create: admit_order outside [0, 1]");
+    if (cfg->enc_ffn_bf16 < 0 || cfg->enc_ffn_bf16 > 1) CT_FATAL("hipb_create: enc_ffn_bf16 outside [0, 1]");
     e->free_ent = malloc((size_t)R * sizeof(int));
     e->ent_owner = malloc((size_t)R * sizeof(int));
     if (!e->req || !e->order || !e->free_ent || !e->ent_owner) CT_FATAL("out of host memory");
@@ -914,12 +915,15 @@ static void encode_batch(HipbEngine *e, const int *ids, int n) {
     gemm_sp(e, e->emid_h, e->emid_l, M, SUB_CH * 16, W->sow, W->sob, e->ex, ENC_D, CT_EPI_STORE, 0);
     pos_tables(e);
     const long pos_rows = 2L * e->d.tmax - 1;
+    /* the FFN projections in single-pass bf16 when configured: their inputs
+     * (the LayerNorm and the SiLU outputs) as the hi plane alone */
+    uint16_t *const ffl = e->cfg.enc_ffn_bf16 ? NULL : e->eln_l, *const ffm = e->cfg.enc_ffn_bf16 ? NULL : e->emid_l;
     for (int l = 0; l < ENC_N; l++) {
         const ELayer *L = &W->enc[l];
         /* x += 0.5 FFN1(LN x) */
-        ctk_layernorm_split(e->eln_h, e->eln_l, e->ex, DW(L->ff1_lnw), DW(L->ff1_lnb), M, ENC_D, s);
-        gemm_sp_silu_split(e, e->eln_h, e->eln_l, M, L->ff1_w1, L->ff1_b1, e->emid_h, e->emid_l);
-        gemm_sp(e, e->emid_h, e->emid_l, M, ENC_FF, L->ff1_w2, L->ff1_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
+        ctk_layernorm_split(e->eln_h, ffl, e->ex, DW(L->ff1_lnw), DW(L->ff1_lnb), M, ENC_D, s);
+        gemm_sp_silu_split(e, e->eln_h, ffl, M, L->ff1_w1, L->ff1_b1, e->emid_h, ffm);
+        gemm_sp(e, e->emid_h, ffm, M, ENC_FF, L->ff1_w2, L->ff1_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
         /* x += MHSA(LN x) */
         ctk_layernorm_split(e->eln_h, e->eln_l, e->ex, DW(L->sa_lnw), DW(L->sa_lnb), M, ENC_D, s);
         gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_qw, L->sa_qb, e->eq, ENC_D, CT_EPI_STORE, 0);
@@ -945,9 +949,9 @@ static void encode_batch(HipbEngine *e, const int *ids, int n) {
                                   DW(L->cv_bnmean), DW(L->cv_bnvar), s);
         gemm_sp(e, e->edw_h, e->edw_l, M, ENC_D, L->cv_pw2w, L->cv_pw2b, e->ex, ENC_D, CT_EPI_FMADD, 1.0f);
         /* x += 0.5 FFN2(LN x); x = LN(x) */
-        ctk_layernorm_split(e->eln_h, e->eln_l, e->ex, DW(L->ff2_lnw), DW(L->ff2_lnb), M, ENC_D, s);
-        gemm_sp_silu_split(e, e->eln_h, e->eln_l, M, L->ff2_w1, L->ff2_b1, e->emid_h, e->emid_l);
-        gemm_sp(e, e->emid_h, e->emid_l, M, ENC_FF, L->ff2_w2, L->ff2_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
+        ctk_layernorm_split(e->eln_h, ffl, e->ex, DW(L->ff2_lnw), DW(L->ff2_lnb), M, ENC_D, s);
+        gemm_sp_silu_split(e, e->eln_h, ffl, M, L->ff2_w1, L->ff2_b1, e->emid_h, ffm);
+        gemm_sp(e, e->emid_h, ffm, M, ENC_FF, L->ff2_w2, L->ff2_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
         ctk_layernorm(e->ex, e->ex, DW(L->out_lnw), DW(L->out_lnb), M, ENC_D, s);
     }
     /* the encoder output, packed (the Q workspace is free now), goes to
@@ -1670,16 +1674,18 @@ void hipb_bench_decode_gemms(HipbEngine *e) { step_kernels(e, 0, 0); }
 
 void hipb_bench_encoder_gemm(HipbEngine *e, int M) {
     if (M < 1) CT_FATAL("hipb_bench_encoder_gemm: M < 1");
+    const int sp = e->cfg.enc_ffn_bf16;
     if (M > e->enc_cap || e->bench_gemm_M != M) {
         enc_reserve(e, M, 8);
         /* seeded operand, split as the producers write it: hi ~ N(0,1),
          * lo ~ N(0,1) * 2^-9 */
         ctk_fill_random(e->eln_h, (long)M * ENC_D, 1, 1.0f, 71, e->s);
-        ctk_fill_random(e->eln_l, (long)M * ENC_D, 1, 1.0f / 512.0f, 72, e->s);
+        if (!sp) ctk_fill_random(e->eln_l, (long)M * ENC_D, 1, 1.0f / 512.0f, 72, e->s);
         e->bench_gemm_M = M;
     }
     const ELayer *L = &e->W.enc[0];
-    gemm_sp_silu_split(e, e->eln_h, e->eln_l, M, L->ff1_w1, L->ff1_b1, e->emid_h, e->emid_l);
+    gemm_sp_silu_split(e, e->eln_h, sp ? NULL : e->eln_l, M, L->ff1_w1, L->ff1_b1, e->emid_h,
+                       sp ? NULL : e->emid_l);
 }
 
 void hipb_mel(HipbEngine *e, const float *pcm, int n_samples, float *mel_out) {

@@ -71,7 +71,7 @@ __device__ __forceinline__ void store_out(const CtGemm &g, int m, int col, float
             uint16_t h, l;
             split_bf16(v, h, l);
             reinterpret_cast<uint16_t *>(sg.base)[(long)m * sg.ld + c] = h;
-            reinterpret_cast<uint16_t *>(sg.base_lo)[(long)m * sg.ld + c] = l;
+            if (sg.base_lo) reinterpret_cast<uint16_t *>(sg.base_lo)[(long)m * sg.ld + c] = l;
         } else {
             const long ro = sg.rowoff[m];
             if (ro < 0) return;
@@ -124,7 +124,8 @@ __device__ __forceinline__ void store_out8(const CtGemm &g, int m, int col, floa
                 h8[i] = h; l8[i] = l;
             }
             *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(sg.base) + (long)m * sg.ld + c) = h8;
-            *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(sg.base_lo) + (long)m * sg.ld + c) = l8;
+            if (sg.base_lo)
+                *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(sg.base_lo) + (long)m * sg.ld + c) = l8;
             return;
         }
         if (sg.mode == CT_OUT_DENSE) {
@@ -475,6 +476,8 @@ __global__ __launch_bounds__(256) void gemm_big_kernel(CtGemm g, int n_mt, int n
 // the next), each XCD taking a contiguous range, so a group's A rows and the
 // W columns in use stay in that XCD's L2.
 // Per element: K-steps in order, hi then lo (as every other GEMM kernel).
+// Single-pass form (LO = false, no lo plane): A is bf16 (hi) alone, one MFMA
+// per K-step and fragment, two thirds of the DMA bytes, and a deeper ring.
 // ---------------------------------------------------------------------------
 constexpr int SBM = 128, SBN = 256, SBK = 32, SST = 4, SGM = 4;
 // rows from which the 256-row tile kernel takes pre-split GEMMs
@@ -482,9 +485,11 @@ constexpr int SBM = 128, SBN = 256, SBK = 32, SST = 4, SGM = 4;
 #define CT_SPLIT256_MIN_M 1024
 #endif
 constexpr int S_A = SBM * SBK, S_W = SBN * SBK;       // elements per operand tile
-constexpr int STAGE_ELEMS = 2 * S_A + S_W;            // Ahi, Alo, W
-constexpr int S_INSTR = STAGE_ELEMS / 512;            // 1-KB DMA instructions per stage (32)
-constexpr int S_PER_WAVE = S_INSTR / 8;               // 4
+template <bool LO> struct SplitCfg {
+    static constexpr int STAGE = (LO ? 2 : 1) * S_A + S_W;   // Ahi, (Alo,) W
+    static constexpr int PER_WAVE = STAGE / 512 / 8;          // 1-KB DMA instructions (4, 3)
+    static constexpr int STAGES = LO ? SST : 5;               // 128 KB, 120 KB of LDS
+};
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 typedef const __attribute__((address_space(1))) void *glb_ptr_t;
@@ -498,9 +503,13 @@ __device__ __forceinline__ void lds_dma16(const void *g, uint16_t *lds_wave_base
 // 16 lanes over 64 banks or 8 lanes over 32 banks per cycle.
 __device__ __forceinline__ int swz(int R, int c) { return c ^ (((R >> 1) ^ (R >> 2)) & 3); }
 
-template <bool GLU>
+template <bool GLU, bool LO>
 __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int n_nt, int vepi) {
-    __shared__ __attribute__((aligned(16))) uint16_t smem[SST * STAGE_ELEMS];
+    constexpr int STAGE_ELEMS = SplitCfg<LO>::STAGE, S_PER_WAVE = SplitCfg<LO>::PER_WAVE;
+    constexpr int NST = SplitCfg<LO>::STAGES;
+    // the ring, and the epilogue's 128 x 256 fp32 tile after it
+    constexpr int SMEM = NST * STAGE_ELEMS > SBM * SBN * 2 ? NST * STAGE_ELEMS : SBM * SBN * 2;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r = lane & 15, kg = lane >> 4;
     const int nt = n_mt * n_nt;
@@ -516,31 +525,32 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
     const int c0 = tn * (GLU ? SBN / 2 : SBN);
     const int nlim = GLU ? 2 * g.glu_half : g.N;
 
-    // DMA plan: instruction i (0..31) covers 16 rows x 64 B of one operand
-    // tile: i < 8 A-hi, i < 16 A-lo, else W.  Lane L lands at row
-    // 16*(i%8 or (i-16)) + L/4, chunk slot L%4, fetching global chunk
+    // DMA plan: instruction i covers 16 rows x 64 B of one operand tile:
+    // i < 8 A-hi, then (LO) i < 16 A-lo, then W.  Lane L lands at row
+    // 16*(i%8 or (i-NA)) + L/4, chunk slot L%4, fetching global chunk
     // swz(row, L%4).  Wave wv issues i = wv + 8*j.
+    constexpr int NA = LO ? 16 : 8;                      // A instructions per stage
     const uint16_t *src[S_PER_WAVE];
     int dst[S_PER_WAVE];
 #pragma unroll
     for (int j = 0; j < S_PER_WAVE; j++) {
         const int i = wv + 8 * j;
         const int Rl = lane >> 2, ch = lane & 3;
-        if (i < 16) {
+        if (i < NA) {
             const int R = (i & 7) * 16 + Rl;
             const int m = min(m0 + R, g.M - 1);            // rows >= M are never stored
             src[j] = (i < 8 ? g.Ahi : g.Alo) + (long)m * g.lda + swz(R, ch) * 8;
             dst[j] = (i < 8 ? 0 : S_A) + (i & 7) * 16 * SBK;
         } else {
-            const int R = (i - 16) * 16 + Rl;
+            const int R = (i - NA) * 16 + Rl;
             int n = GLU ? (R < SBN / 2 ? c0 + R : g.glu_half + c0 + R - SBN / 2) : c0 + R;
             n = min(n, nlim - 1);
             src[j] = g.W + (long)n * g.K + swz(R, ch) * 8;
-            dst[j] = 2 * S_A + (i - 16) * 16 * SBK;
+            dst[j] = (LO ? 2 : 1) * S_A + (i - NA) * 16 * SBK;
         }
     }
     auto issue = [&](int kt) {
-        uint16_t *stage = smem + (kt % SST) * STAGE_ELEMS;
+        uint16_t *stage = smem + (kt % NST) * STAGE_ELEMS;
 #pragma unroll
         for (int j = 0; j < S_PER_WAVE; j++) lds_dma16(src[j] + kt * SBK, stage + dst[j]);
     };
@@ -553,19 +563,20 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
     const int wm = (wv >> 2) * 64, wn = (wv & 3) * 64;
     const int nk = g.K / SBK;
 #pragma unroll
-    for (int p = 0; p < SST - 1; p++)
+    for (int p = 0; p < NST - 1; p++)
         if (p < nk) issue(p);
     for (int kt = 0; kt < nk; kt++) {
         // wait for this wave's part of stage kt; younger stages stay in flight
-        const int younger = min(nk - 1 - kt, SST - 2);
-        if (younger >= 2) __builtin_amdgcn_s_waitcnt((8 & 0xF) | (0x7 << 4) | (0xF << 8));
-        else if (younger == 1) __builtin_amdgcn_s_waitcnt((4 & 0xF) | (0x7 << 4) | (0xF << 8));
+        const int younger = min(nk - 1 - kt, NST - 2);
+        if (younger >= 3) __builtin_amdgcn_s_waitcnt(((3 * S_PER_WAVE) & 0xF) | (0x7 << 4) | (0xF << 8));
+        else if (younger == 2) __builtin_amdgcn_s_waitcnt(((2 * S_PER_WAVE) & 0xF) | (0x7 << 4) | (0xF << 8));
+        else if (younger == 1) __builtin_amdgcn_s_waitcnt((S_PER_WAVE & 0xF) | (0x7 << 4) | (0xF << 8));
         else __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
         __builtin_amdgcn_s_barrier();            // stage kt landed for every wave, and every
         asm volatile("" ::: "memory");           // wave is done reading stage kt-1
-        if (kt + SST - 1 < nk) issue(kt + SST - 1);
-        const uint16_t *st = smem + (kt % SST) * STAGE_ELEMS;
-        const uint16_t *sAh = st, *sAl = st + S_A, *sW = st + 2 * S_A;
+        if (kt + NST - 1 < nk) issue(kt + NST - 1);
+        const uint16_t *st = smem + (kt % NST) * STAGE_ELEMS;
+        const uint16_t *sAh = st, *sAl = st + S_A, *sW = st + (LO ? 2 : 1) * S_A;
         bf16x8 bfr[4];
 #pragma unroll
         for (int cb = 0; cb < 4; cb++) {
@@ -577,11 +588,16 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
             const int R = wm + rb * 16 + r;
             const int off = R * SBK + swz(R, kg) * 8;
             const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAh + off));
-            const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
+            if (LO) {
+                const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
 #pragma unroll
-            for (int cb = 0; cb < 4; cb++) {
-                acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
-                acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
+                for (int cb = 0; cb < 4; cb++) {
+                    acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
+                    acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
+                }
+            } else {
+#pragma unroll
+                for (int cb = 0; cb < 4; cb++) acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
             }
         }
     }
@@ -676,12 +692,18 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
 // 3-stage ring of 48 KB (A hi, A lo: 256 x 32 each; W: 256 x 32), 6 DMA
 // instructions per wave per stage.  Per element the sequence is unchanged.
 // ---------------------------------------------------------------------------
-constexpr int TBM = 256, TST = 3;
+constexpr int TBM = 256;
 constexpr int T_A = TBM * SBK;
-constexpr int T_STAGE = 2 * T_A + S_W;
-constexpr int T_PER_WAVE = T_STAGE / 512 / 8;     // 6
+template <bool LO> struct Split256Cfg {
+    static constexpr int STAGE = (LO ? 2 : 1) * T_A + S_W;    // 48 KB, 32 KB
+    static constexpr int PER_WAVE = STAGE / 512 / 8;          // 6, 4
+    static constexpr int STAGES = LO ? 3 : 4;                 // 144 KB, 128 KB of LDS
+};
 
+template <bool LO>
 __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, int n_nt, int vepi) {
+    constexpr int T_STAGE = Split256Cfg<LO>::STAGE, T_PER_WAVE = Split256Cfg<LO>::PER_WAVE;
+    constexpr int TST = Split256Cfg<LO>::STAGES;
     __shared__ __attribute__((aligned(16))) uint16_t smem[TST * T_STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r = lane & 15, kg = lane >> 4;
@@ -695,23 +717,25 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
     const int tn = rem / gm, tm = grp * SGM + rem % gm;
     const int m0 = tm * TBM, c0 = tn * SBN;
 
-    // instruction i = wv + 8*j: i < 16 A-hi rows 16i.., i < 32 A-lo, else W
+    // instruction i = wv + 8*j: i < 16 A-hi rows 16i.., then (LO) i < 32
+    // A-lo, then W
+    constexpr int NA = LO ? 32 : 16;
     const uint16_t *src[T_PER_WAVE];
     int dst[T_PER_WAVE];
 #pragma unroll
     for (int j = 0; j < T_PER_WAVE; j++) {
         const int i = wv + 8 * j;
         const int Rl = lane >> 2, ch = lane & 3;
-        if (i < 32) {
+        if (i < NA) {
             const int R = (i & 15) * 16 + Rl;
             const int m = min(m0 + R, g.M - 1);
             src[j] = (i < 16 ? g.Ahi : g.Alo) + (long)m * g.lda + swz(R, ch) * 8;
             dst[j] = (i < 16 ? 0 : T_A) + (i & 15) * 16 * SBK;
         } else {
-            const int R = (i - 32) * 16 + Rl;
+            const int R = (i - NA) * 16 + Rl;
             const int n = min(c0 + R, g.N - 1);
             src[j] = g.W + (long)n * g.K + swz(R, ch) * 8;
-            dst[j] = 2 * T_A + (i - 32) * 16 * SBK;
+            dst[j] = (LO ? 2 : 1) * T_A + (i - NA) * 16 * SBK;
         }
     }
     auto issue = [&](int kt) {
@@ -731,14 +755,16 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
     for (int p = 0; p < TST - 1; p++)
         if (p < nk) issue(p);
     for (int kt = 0; kt < nk; kt++) {
-        // this wave's part of stage kt landed; at most one younger stage in flight
-        if (kt + 1 < nk) __builtin_amdgcn_s_waitcnt((T_PER_WAVE & 0xF) | (0x7 << 4) | (0xF << 8));
+        // this wave's part of stage kt landed; younger stages stay in flight
+        const int younger = min(nk - 1 - kt, TST - 2);
+        if (younger >= 2) __builtin_amdgcn_s_waitcnt(((2 * T_PER_WAVE) & 0xF) | (0x7 << 4) | (0xF << 8));
+        else if (younger == 1) __builtin_amdgcn_s_waitcnt((T_PER_WAVE & 0xF) | (0x7 << 4) | (0xF << 8));
         else __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (kt + TST - 1 < nk) issue(kt + TST - 1);
         const uint16_t *st = smem + (kt % TST) * T_STAGE;
-        const uint16_t *sAh = st, *sAl = st + T_A, *sW = st + 2 * T_A;
+        const uint16_t *sAh = st, *sAl = st + T_A, *sW = st + (LO ? 2 : 1) * T_A;
         bf16x8 bfr[8];
 #pragma unroll
         for (int cb = 0; cb < 8; cb++) {
@@ -750,11 +776,16 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
             const int R = wm + rb * 16 + r;
             const int off = R * SBK + swz(R, kg) * 8;
             const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAh + off));
-            const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
+            if (LO) {
+                const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
 #pragma unroll
-            for (int cb = 0; cb < 8; cb++) {
-                acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
-                acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
+                for (int cb = 0; cb < 8; cb++) {
+                    acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
+                    acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
+                }
+            } else {
+#pragma unroll
+                for (int cb = 0; cb < 8; cb++) acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
             }
         }
     }
@@ -1005,13 +1036,17 @@ extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
         const int n_nt = glu ? (g->glu_half + SBN / 2 - 1) / (SBN / 2) : (g->N + SBN - 1) / SBN;
         const int nt = n_mt * n_nt, per = (nt + 7) / 8;
         const int vepi = vector_epilogue_ok(g);
+        const bool lo = g->Alo != NULL;     /* no lo plane: single-pass bf16 A */
         if (!glu && g->M >= CT_SPLIT256_MIN_M && prefer_256(g->M, n_nt)) {
             const int n_mt2 = (g->M + TBM - 1) / TBM, nt2 = n_mt2 * n_nt, per2 = (nt2 + 7) / 8;
-            hipLaunchKernelGGL(gemm_split256_kernel, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
+            if (lo) hipLaunchKernelGGL(gemm_split256_kernel<true>, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
+            else hipLaunchKernelGGL(gemm_split256_kernel<false>, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
             return;
         }
-        if (glu) hipLaunchKernelGGL(gemm_split_kernel<true>, dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, 0);
-        else hipLaunchKernelGGL(gemm_split_kernel<false>, dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, vepi);
+        if (glu && lo) hipLaunchKernelGGL((gemm_split_kernel<true, true>), dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, 0);
+        else if (glu) hipLaunchKernelGGL((gemm_split_kernel<true, false>), dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, 0);
+        else if (lo) hipLaunchKernelGGL((gemm_split_kernel<false, true>), dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, vepi);
+        else hipLaunchKernelGGL((gemm_split_kernel<false, false>), dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, vepi);
         return;
     }
     const bool vec = (g->K % 8 == 0) && (g->lda % 4 == 0) &&

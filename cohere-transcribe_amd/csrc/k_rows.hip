@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void layernorm_split_kernel(uint16_t *hi, uint
         h4.x = hh[0]; h4.y = hh[1]; h4.z = hh[2]; h4.w = hh[3];
         l4.x = ll[0]; l4.y = ll[1]; l4.z = ll[2]; l4.w = ll[3];
         reinterpret_cast<ushort4 *>(hi + (long)row * D)[lane + 64 * i] = h4;
-        reinterpret_cast<ushort4 *>(lo + (long)row * D)[lane + 64 * i] = l4;
+        if (lo) reinterpret_cast<ushort4 *>(lo + (long)row * D)[lane + 64 * i] = l4;
     }
 }
 

@@ -234,7 +234,7 @@ HIPB_FORCE_EOS = 2
 class HipbConfig(C.Structure):
     _fields_ = [("slots", C.c_int), ("max_requests", C.c_int),
                 ("max_frames", C.c_int), ("kv_bf16", C.c_int), ("max_tokens", C.c_int),
-                ("prefill_rows", C.c_int), ("admit_order", C.c_int)]
+                ("prefill_rows", C.c_int), ("admit_order", C.c_int), ("enc_ffn_bf16", C.c_int)]
 
 
 _ENGINE_SIGS = {
@@ -277,11 +277,11 @@ class Engine:
     backend_init and uploaded the model's blob)."""
 
     def __init__(self, model, slots, max_requests, max_frames, kv_bf16=True, max_tokens=0,
-                 prefill_rows=0, admit_order=0):
+                 prefill_rows=0, admit_order=0, enc_ffn_bf16=0):
         self.L = engine_lib()
         self.model = model
         cfg = HipbConfig(slots, max_requests, max_frames, int(kv_bf16), int(max_tokens),
-                         int(prefill_rows), int(admit_order))
+                         int(prefill_rows), int(admit_order), int(enc_ffn_bf16))
         self.e = self.L.hipb_create(C.byref(cfg), model.weights_ref())
         self.slots = slots
 

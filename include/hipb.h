@@ -55,6 +55,12 @@ typedef struct {
                            recording's chunks together in order under the
                            first chunk's budget (shortens a pass: fewer slots
                            idle at its end); results are the same bits      */
+    int enc_ffn_bf16;   /* 1: the encoder's FFN projections (70% of its flops)
+                           take their activations as bf16 (one MFMA pass)
+                           instead of the hi + lo pair (two passes): encoder
+                           output within ~4e-3 of the fp32 path instead of
+                           ~1e-5, logits ~6e-4 instead of ~3e-4 on the
+                           specified weights; 0: both passes              */
 } HipbConfig;
 
 /* Request policy flags. */
@@ -171,8 +177,9 @@ void hipb_attention_only(HipbEngine *e);
 void hipb_bench_decode_gemms(HipbEngine *e);
 /* Launches the packed encoder's FFN up-projection (layer 0 weights: M frames
  * x 1280 -> 5120, SiLU, pre-split input and output; the encoder runs this
- * GEMM twice per layer) once on the engine stream.  The input is seeded when
- * M changes. */
+ * GEMM twice per layer) once on the engine stream, in the engine's FFN
+ * precision mode (enc_ffn_bf16: bf16 input and output, no lo halves).  The
+ * input is seeded when M changes. */
 void hipb_bench_encoder_gemm(HipbEngine *e, int M);
 
 /* Launches n decode steps (graph replays, or eager steps under HIPB_EAGER=1)

@@ -368,14 +368,29 @@ int orc_T_enc(int T_mel) {
 }
 int orc_T_mel(int n_samples) { return 1 + n_samples / HOP_LEN; }
 
+/* Single-pass precision mode of the encoder FFN projections: the inputs of
+ * both FFN linears (the LayerNorm output and the SiLU output) are rounded to
+ * bf16 before the fp32 dot products.  Off by default (the reference's fp32
+ * arithmetic); not part of the reference. */
+static int g_enc_ffn_bf16 = 0;
+void orc_set_enc_ffn_bf16(int on) { g_enc_ffn_bf16 = on != 0; }
+
+static void ffn_half(float *x, float *ln, float *mid, int T, const uint16_t *lnw,
+                     const uint16_t *lnb, const uint16_t *w1, const uint16_t *b1,
+                     const uint16_t *w2, const uint16_t *b2) {
+    orc_layernorm(ln, x, lnw, lnb, T, ENC_D);
+    if (g_enc_ffn_bf16) orc_round_bf16_n(ln, (long)T * ENC_D);
+    orc_linear_silu(mid, ln, w1, b1, T, ENC_D, ENC_FF);
+    if (g_enc_ffn_bf16) orc_round_bf16_n(mid, (long)T * ENC_FF);
+    orc_linear_fmadd(x, 0.5f, mid, w2, b2, T, ENC_FF, ENC_D);
+}
+
 /* model.h:276-314: FFN/2, MHSA, conv module, FFN/2, final LN. */
 void orc_conformer_layer(float *x, const float *pos_emb, int T, const ELayer *L, float *work) {
     (void)work;
     float *ln = xmalloc((size_t)T * ENC_D * sizeof(float));
     float *mid = xmalloc((size_t)T * ENC_FF * sizeof(float));
-    orc_layernorm(ln, x, L->ff1_lnw, L->ff1_lnb, T, ENC_D);
-    orc_linear_silu(mid, ln, L->ff1_w1, L->ff1_b1, T, ENC_D, ENC_FF);
-    orc_linear_fmadd(x, 0.5f, mid, L->ff1_w2, L->ff1_b2, T, ENC_FF, ENC_D);
+    ffn_half(x, ln, mid, T, L->ff1_lnw, L->ff1_lnb, L->ff1_w1, L->ff1_b1, L->ff1_w2, L->ff1_b2);
 
     orc_layernorm(ln, x, L->sa_lnw, L->sa_lnb, T, ENC_D);
     orc_rel_pos_mhsa(ln, pos_emb, T, L, NULL);
@@ -385,9 +400,7 @@ void orc_conformer_layer(float *x, const float *pos_emb, int T, const ELayer *L,
     orc_conformer_conv(ln, T, L, NULL);
     orc_add_inplace(x, ln, T * ENC_D);
 
-    orc_layernorm(ln, x, L->ff2_lnw, L->ff2_lnb, T, ENC_D);
-    orc_linear_silu(mid, ln, L->ff2_w1, L->ff2_b1, T, ENC_D, ENC_FF);
-    orc_linear_fmadd(x, 0.5f, mid, L->ff2_w2, L->ff2_b2, T, ENC_FF, ENC_D);
+    ffn_half(x, ln, mid, T, L->ff2_lnw, L->ff2_lnb, L->ff2_w1, L->ff2_b1, L->ff2_w2, L->ff2_b2);
 
     orc_layernorm(x, x, L->out_lnw, L->out_lnb, T, ENC_D);
     free(ln); free(mid);

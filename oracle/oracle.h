@@ -51,6 +51,9 @@ int  orc_argmax(const float *x, int n, int skip);
 /* ---- graph level (model.h) ---- */
 int  orc_T_enc(int T_mel);
 void orc_conformer_layer(float *x, const float *pos_emb, int T, const ELayer *L, float *work);
+/* 1: round the inputs of the encoder FFN linears to bf16 (the single-pass
+ * precision mode of the HIP encoder); 0 (default): fp32 as the reference. */
+void orc_set_enc_ffn_bf16(int on);
 /* mel (N_MELS, T_mel) with row stride T_mel_stride -> enc_h (T_enc, DEC_D). */
 void orc_encoder_forward(const float *mel, int T_mel, int T_mel_stride,
                          const Weights *W, float *x_enc_out, float *enc_h);

@@ -46,6 +46,7 @@ _SIGS = {
     "orc_mel_filterbank": [_P],
     "orc_chunk_bounds": [_P, _I, _F, _F, _F, _P, _I],
     "orc_round_bf16_n": [_P, C.c_long],
+    "orc_set_enc_ffn_bf16": [_I],
 }
 _RET = {"orc_argmax": _I, "orc_T_enc": _I, "orc_T_mel": _I, "orc_transcribe": _I,
         "orc_chunk_bounds": _I}
@@ -69,6 +70,22 @@ def oracle():
             raise RuntimeError(f"{ORACLE_LIB} is not built")
         _oracle = _bind(C.CDLL(ORACLE_LIB), _SIGS, _RET)
     return _oracle
+
+
+class enc_ffn_bf16:
+    """Context: the oracle's encoder FFN linears take bf16-rounded inputs
+    (the HIP encoder's single-pass FFN mode) inside the block."""
+
+    def __init__(self, on=True):
+        self.on = bool(on)
+
+    def __enter__(self):
+        oracle().orc_set_enc_ffn_bf16(int(self.on))
+        return self
+
+    def __exit__(self, *exc):
+        oracle().orc_set_enc_ffn_bf16(0)
+        return False
 
 
 def ptr(a):

@@ -236,15 +236,8 @@ def test_rel_pos_mhsa_independent(kernel_model):
         assert abs(direct - (Q[q, sl] + v[h]) @ P[k + T - 1 - q, sl]) < 1e-3
 
 
-def test_conformer_conv_independent(kernel_model):
-    m, o = kernel_model, ob.oracle()
-    T = 11
-    rng = np.random.default_rng(4)
-    x = rng.standard_normal((T, 1280)).astype(np.float32)
-    y = x.copy()
-    o.orc_conformer_conv(y.ctypes.data, T, m.elayer_ptr(5), None)
-    p = "enc5."
-    xd = x.astype(np.float64)
+def conv_fp64(m, layer, xd):
+    p = f"enc{layer}."
     pw = xd @ bf(m, p + "cv_pw1w", (2560, 1280)).T + bf(m, p + "cv_pw1b", 2560)
     g = pw[:, :1280] / (1 + np.exp(-pw[:, 1280:]))
     w = bf(m, p + "cv_dww", (1280, 9))
@@ -253,8 +246,84 @@ def test_conformer_conv_independent(kernel_model):
     bn = (dw - bf(m, p + "cv_bnmean", 1280)) / np.sqrt(bf(m, p + "cv_bnvar", 1280) + 1e-5)
     bn = bn * bf(m, p + "cv_bnw", 1280) + bf(m, p + "cv_bnb", 1280)
     a = bn / (1 + np.exp(-bn))
-    ref = a @ bf(m, p + "cv_pw2w", (1280, 1280)).T + bf(m, p + "cv_pw2b", 1280)
-    assert relerr(y, ref) < 1e-4
+    return a @ bf(m, p + "cv_pw2w", (1280, 1280)).T + bf(m, p + "cv_pw2b", 1280)
+
+
+def test_conformer_conv_independent(kernel_model):
+    m, o = kernel_model, ob.oracle()
+    T = 11
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((T, 1280)).astype(np.float32)
+    y = x.copy()
+    o.orc_conformer_conv(y.ctypes.data, T, m.elayer_ptr(5), None)
+    assert relerr(y, conv_fp64(m, 5, x.astype(np.float64))) < 1e-4
+
+
+def ln_fp64(x, w, b):
+    mu = x.mean(-1, keepdims=True)
+    return (x - mu) / np.sqrt(((x - mu) ** 2).mean(-1, keepdims=True) + 1e-5) * w + b
+
+
+def round_bf16(x):
+    """float64 -> nearest fp32 -> bf16 round to nearest even (torch)."""
+    import torch
+    return torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16).double().numpy()
+
+
+def conformer_layer_fp64(m, layer, x, pe, T, ffn_bf16):
+    """model.h:276-314 in float64 from the pieces above; with ffn_bf16 the
+    inputs of the four FFN linears are rounded to bf16."""
+    p = f"enc{layer}."
+    v = lambda n, *sh: bf(m, p + n, sh)  # noqa: E731
+    rnd = round_bf16 if ffn_bf16 else (lambda a: a)  # noqa: E731
+
+    def ffn(x, k):
+        a = rnd(ln_fp64(x, v(f"ff{k}_lnw", 1280), v(f"ff{k}_lnb", 1280)))
+        s = a @ v(f"ff{k}_w1", 5120, 1280).T + v(f"ff{k}_b1", 5120)
+        mid = rnd(s / (1 + np.exp(-s)))
+        return x + 0.5 * (mid @ v(f"ff{k}_w2", 1280, 5120).T + v(f"ff{k}_b2", 1280))
+
+    x = ffn(x, 1)
+    x = x + mhsa_fp64(m, layer, ln_fp64(x, v("sa_lnw", 1280), v("sa_lnb", 1280)), pe, T)[0]
+    x = x + conv_fp64(m, layer, ln_fp64(x, v("cv_lnw", 1280), v("cv_lnb", 1280)))
+    x = ffn(x, 2)
+    return ln_fp64(x, v("out_lnw", 1280), v("out_lnb", 1280))
+
+
+# Same-mode bounds: with rounded FFN inputs, an input within the float32
+# and float64 computations' difference of a bf16 rounding boundary rounds
+# one ulp apart (measured 1.1e-4, against 9.8e-4 between the modes).
+FFN_MODE_BOUND = {0: 5e-6, 1: 2.5e-4}
+
+
+@pytest.mark.parametrize("ffn_bf16", [0, 1])
+def test_conformer_layer_ffn_modes_independent(kernel_model, ffn_bf16):
+    """The oracle's conformer layer with fp32 FFN inputs and with the
+    single-pass mode's bf16-rounded FFN inputs, against the float64
+    restatement in both modes: the same-mode restatement is several times
+    closer than the other mode's, and the mode switch restores the fp32
+    layer bit for bit."""
+    m, o = kernel_model, ob.oracle()
+    T = 7
+    x = np.random.default_rng(9).standard_normal((T, 1280)).astype(np.float32)
+    pe = np.zeros((2 * T - 1, 1280), np.float32)
+    o.orc_make_rel_pos_emb(pe.ctypes.data, T)
+
+    def layer():
+        y = x.copy()
+        o.orc_conformer_layer(y.ctypes.data, pe.ctypes.data, T, m.elayer_ptr(4), None)
+        return y
+
+    before = layer()
+    with ob.enc_ffn_bf16(bool(ffn_bf16)):
+        y = layer()
+    assert np.array_equal(layer().view(np.uint32), before.view(np.uint32))
+    xd, ped = x.astype(np.float64), pe.astype(np.float64)
+    e_same = relerr(y, conformer_layer_fp64(m, 4, xd, ped, T, ffn_bf16))
+    e_other = relerr(y, conformer_layer_fp64(m, 4, xd, ped, T, 1 - ffn_bf16))
+    print(f"ffn_bf16={ffn_bf16}: same mode {e_same:.2e}, other mode {e_other:.2e}")
+    assert e_same < FFN_MODE_BOUND[ffn_bf16]
+    assert e_other > 3 * e_same
 
 
 def test_subsampling_independent(kernel_model):
