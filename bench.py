@@ -246,7 +246,7 @@ def with_traffic(rooflines):
         with open(TRAFFIC_FILE) as f:
             tr = json.load(f)
         for k, r in rooflines.items():
-            if k in tr.get("per_launch_bytes", {}):
+            if k in tr.get("per_launch_bytes", {}) and tr.get("kernels", {}).get(k) == r.get("kernel"):
                 r["traffic"] = tr["per_launch_bytes"][k]
     if os.path.exists(MFMA_FILE):
         with open(MFMA_FILE) as f:
