@@ -50,6 +50,9 @@ struct HipbEngine {
     CtEngDev d;
     /* repacked weights: [Wq;Wk;Wv] per layer, [Wk;Wv] cross per layer */
     uint16_t *wqkv, *bqkv, *wckv, *bckv;
+    /* encoder self-attention [Wq;Wk;Wv] (3*ENC_D x ENC_D) and biases per
+     * layer: one GEMM launch for the three projections */
+    uint16_t *ew_qkv, *eb_qkv;
     /* decode-GEMM weights in the tile layout (ctk_tile_w), one allocation:
      * per layer [Wq;Wk;Wv], Wo, Wq_cross, Wo_cross, W_ffn1, W_ffn2; then the
      * tied LM head */
@@ -332,6 +335,21 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
         ECHK(hipMemcpyAsync((char *)e->bckv + (2 * l + 1) * bsz, DW(L->ca_vb), bsz, hipMemcpyDeviceToDevice, e->s));
     }
     {
+        const size_t ewsz = (size_t)ENC_D * ENC_D * 2, ebsz = (size_t)ENC_D * 2;
+        e->ew_qkv = dmalloc(ENC_N * 3 * ewsz);
+        e->eb_qkv = dmalloc(ENC_N * 3 * ebsz);
+        for (int l = 0; l < ENC_N; l++) {
+            const ELayer *L = &W->enc[l];
+            const uint16_t *ws[3] = {L->sa_qw, L->sa_kw, L->sa_vw}, *bs[3] = {L->sa_qb, L->sa_kb, L->sa_vb};
+            for (int i = 0; i < 3; i++) {
+                ECHK(hipMemcpyAsync((char *)e->ew_qkv + (3 * l + i) * ewsz, DW(ws[i]), ewsz,
+                                    hipMemcpyDeviceToDevice, e->s));
+                ECHK(hipMemcpyAsync((char *)e->eb_qkv + (3 * l + i) * ebsz, DW(bs[i]), ebsz,
+                                    hipMemcpyDeviceToDevice, e->s));
+            }
+        }
+    }
+    {
         const size_t DD = (size_t)DEC_D * DEC_D, per = 3 * DD + 3 * DD + 2 * (size_t)DEC_FF * DEC_D;
         e->wtile = dmalloc((DEC_N * per + (size_t)VOCAB * DEC_D) * 2);
         uint16_t *p = e->wtile;
@@ -422,7 +440,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->d.cross_idx, e->d.kv_rowoff, e->d.req_T, e->d.req_limit, e->d.req_flags,
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.req_score, e->d.q,
                     e->d.req_next, e->d.rq, e->d.pend, e->d.fq,
-                    e->wqkv, e->bqkv, e->wckv, e->bckv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
+                    e->wqkv, e->bqkv, e->wckv, e->bckv, e->ew_qkv, e->eb_qkv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
                     e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep_all,
                     e->esub, e->emel, e->e_subtab, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
@@ -926,9 +944,18 @@ static void encode_batch(HipbEngine *e, const int *ids, int n) {
         gemm_sp(e, e->emid_h, ffm, M, ENC_FF, L->ff1_w2, L->ff1_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
         /* x += MHSA(LN x) */
         ctk_layernorm_split(e->eln_h, e->eln_l, e->ex, DW(L->sa_lnw), DW(L->sa_lnb), M, ENC_D, s);
-        gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_qw, L->sa_qb, e->eq, ENC_D, CT_EPI_STORE, 0);
-        gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_kw, L->sa_kb, e->ek, ENC_D, CT_EPI_STORE, 0);
-        gemm_sp(e, e->eln_h, e->eln_l, M, ENC_D, L->sa_vw, L->sa_vb, e->ev, ENC_D, CT_EPI_STORE, 0);
+        {
+            /* Q, K, V in one launch: columns [0, 1280) to eq, then ek, ev */
+            CtGemm g;
+            memset(&g, 0, sizeof g);
+            g.Ahi = e->eln_h; g.Alo = e->eln_l; g.lda = ENC_D;
+            g.W = e->ew_qkv + (size_t)3 * l * ENC_D * ENC_D; g.bias = e->eb_qkv + (size_t)3 * l * ENC_D;
+            g.M = M; g.N = 3 * ENC_D; g.K = ENC_D; g.epi = CT_EPI_STORE;
+            g.nseg = 3; g.seg_w = ENC_D;
+            float *const qkv[3] = {e->eq, e->ek, e->ev};
+            for (int i = 0; i < 3; i++) g.seg[i] = (CtSeg){.mode = CT_OUT_DENSE, .base = qkv[i], .ld = ENC_D};
+            ctk_gemm(&g, s);
+        }
         ctk_relpos_attn_packed(NULL, e->eo_h, e->eo_l, e->eq, e->ek, e->ev,
                                e->ep_all + (size_t)l * pos_rows * ENC_D, e->d.tmax, DW(L->sa_pbu),
                                DW(L->sa_pbv), e->e_seq_off, e->e_seq_T, e->e_blk_seq, e->e_blk_q0, nblk,
