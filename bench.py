@@ -166,9 +166,18 @@ def decode_gemm_roofline(model, ev, slots=64, reps=20):
             eng.decode_gemms_only()
         ev.record(b, s)
         step_us = ev.ms(a, b) * 1e3 / reps
+        # the same launches reading their weight tiles alone
+        eng.decode_gemm_read_floor()
+        a2, b2 = ev.event(), ev.event()
+        ev.record(a2, s)
+        for _ in range(reps):
+            eng.decode_gemm_read_floor()
+        ev.record(b2, s)
+        floor_us = ev.ms(a2, b2) * 1e3 / reps
     finally:
         eng.close()
     n = len(DEC_GEMMS)
+    w_bytes = float(sum(N * K * 2 for N, K in DEC_GEMMS))
     # weights once, activations in (fp32-equivalent hi+lo), outputs (fp32)
     bytes_step = float(sum(N * K * 2 + slots * K * 4 + slots * N * 4 for N, K in DEC_GEMMS))
     per_launch_us = step_us / n
@@ -177,7 +186,12 @@ def decode_gemm_roofline(model, ev, slots=64, reps=20):
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": "gemv_kernel (decode GEMMs, all instances)", "avg_launch_us": round(per_launch_us, 3),
             "bytes_per_launch": int(bytes_step / n), "launches_per_step": n,
-            "workload": f"{slots} slots, one step's 49 GEMMs (268.4 MB of bf16 weights)"}
+            "workload": f"{slots} slots, one step's 49 GEMMs (268.4 MB of bf16 weights)",
+            "read_floor": {"avg_launch_us": round(floor_us / n, 3),
+                           "weight_GBs": round(w_bytes / (floor_us * 1e-6) / 1e9, 1),
+                           "gemm_over_floor": round(step_us / floor_us, 3),
+                           "what": "the same 49 launches (grids, weight tiles per workgroup) reading "
+                                   "their weights alone: no activations, no MFMAs, no outputs"}}
 
 
 def encoder_gemm_roofline(model, ev, ffn_bf16, M=16384, reps=10):

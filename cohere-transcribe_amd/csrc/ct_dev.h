@@ -52,6 +52,11 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, CT_WAVE));
     return v;
 }
+__device__ __forceinline__ unsigned wave_xor(unsigned v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v ^= (unsigned)__shfl_xor((int)v, o, CT_WAVE);
+    return v;
+}
 // Lane exchange within a row of 16 lanes (DPP): CTRL 0xB1 = quad_perm
 // [1,0,3,2], 0x4E = quad_perm [2,3,0,1], 0x141 = row_half_mirror (lane i of
 // each 8 reads 7-i), 0x140 = row_mirror (lane i reads 15-i).

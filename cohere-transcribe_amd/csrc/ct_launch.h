@@ -113,6 +113,11 @@ typedef struct {
 } CtGemv;
 /* Requires N % 16 == 0 (N % 64 == 0 when N >= 8192), K % (256 * steps) == 0. */
 void ctk_gemv(const CtGemv *g, hipStream_t s);
+/* The GEMM's weight reads alone (tiled weights, same grid as ctk_gemv for
+ * g): one value per workgroup to sink (ctk_gemv_read_floor_blocks(g)
+ * floats).  A floor for the GEMM's duration, for benchmarking. */
+void ctk_gemv_read_floor(const CtGemv *g, float *sink, hipStream_t s);
+long ctk_gemv_read_floor_blocks(const CtGemv *g);
 /* The weight tiles one decode-GEMM launch reads, by workgroup: workgroup i
  * (of gx * gy, i = K-slice + gy * column block) reads, for each of its cb
  * column blocks c, the per consecutive 1-KB tiles from tile

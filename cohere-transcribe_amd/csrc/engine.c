@@ -84,6 +84,11 @@ struct HipbEngine {
      * into the L2 their workgroups will read from */
     CtWarmSet warm;
     unsigned *warm_sink;
+    /* hipb_bench_read_floor: decode GEMM launches replaced by their weight
+     * reads alone, one value per workgroup to floor_sink */
+    int bench_floor;
+    float *floor_sink;
+    long floor_cap;
     /* encoder side: its stream (the engine stream, or a second stream while
      * hipb_process overlaps encoding with decoding), pinned staging of its
      * own, and the host count of requests published to the fresh queue */
@@ -446,7 +451,8 @@ void hipb_destroy(HipbEngine *e) {
                     e->esub, e->emel, e->e_subtab, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
                     e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
                     e->d_fb_lo, e->d_fb_hi, e->epcm, e->e_clips, e->e_frame_clip,
-                    e->eln_h, e->eln_l, e->emid_h, e->emid_l, e->eo_h, e->eo_l, e->edw_h, e->edw_l};
+                    e->eln_h, e->eln_l, e->emid_h, e->emid_l, e->eo_h, e->eo_l, e->edw_h, e->edw_l,
+                    e->floor_sink};
     for (size_t i = 0; i < sizeof ptrs / sizeof ptrs[0]; i++)
         if (ptrs[i]) ECHK(hipFree(ptrs[i]));
     for (int r = 0; r < e->n_req; r++) {
@@ -1292,6 +1298,16 @@ static void step_attention(HipbEngine *e, int l, int cross) {
     }
 }
 
+/* A decode GEMM launch, or (bench_floor) its weight reads alone. */
+static void launch_gemv(HipbEngine *e, const CtGemv *g) {
+    if (!e->bench_floor) {
+        ctk_gemv(g, e->s);
+        return;
+    }
+    if (ctk_gemv_read_floor_blocks(g) > e->floor_cap) CT_FATAL("hipb_bench_read_floor: sink too small");
+    ctk_gemv_read_floor(g, e->floor_sink, e->s);
+}
+
 /* Decode GEMM over all slots; CT_GV_PARTIAL outputs go to parts. */
 
 static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint16_t *bd, int N, int K,
@@ -1305,7 +1321,7 @@ static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint1
     g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, K) : 1;
     g.Y = out == CT_GV_PARTIAL ? e->parts : Y;
     g.ldy = ldy; g.F = F;
-    ctk_gemv(&g, e->s);
+    launch_gemv(e, &g);
 }
 
 /* One decode step over slots rows, or (wide) over slots + prefill_rows rows
@@ -1349,7 +1365,7 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         g.Y = e->q; g.ldy = DEC_D;
         g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)e->d.kv_rows * DEC_DK;
         g.kv_bf16 = e->esz == 2;
-        ctk_gemv(&g, s);
+        launch_gemv(e, &g);
         if (full && CT_WARM && e->read_ahead) warm_add(e, w_o, DEC_D, DEC_D, CT_GV_PARTIAL);
         if (full && CT_WARM && e->read_ahead) warm_add(e, w_cq, DEC_D, DEC_D, CT_GV_PARTIAL);
         if (full) step_attention(e, l, 0);
@@ -1698,6 +1714,19 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
 }
 
 void hipb_bench_decode_gemms(HipbEngine *e) { step_kernels(e, 0, 0); }
+
+void hipb_bench_read_floor(HipbEngine *e) {
+    if (!CT_ENG_WTILE) CT_FATAL("hipb_bench_read_floor: needs the tiled decode weights");
+    const long cap = 256L * ((e->d.rows + 63) / 64);
+    if (e->floor_cap < cap) {
+        if (e->floor_sink) ECHK(hipFree(e->floor_sink));
+        e->floor_sink = dmalloc((size_t)cap * sizeof(float));
+        e->floor_cap = cap;
+    }
+    e->bench_floor = 1;
+    step_kernels(e, 0, 0);
+    e->bench_floor = 0;
+}
 
 void hipb_bench_encoder_gemm(HipbEngine *e, int M) {
     if (M < 1) CT_FATAL("hipb_bench_encoder_gemm: M < 1");

@@ -146,6 +146,46 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
     }
 }
 
+// The weight reads of gemv_kernel alone (tiled weights): the same grid, and
+// workgroup (x, y, z) reads the same 1 KB tiles as the GEMM's workgroup, one
+// 16-byte piece per lane, wave w taking tiles w, w + 8, ... with four loads
+// in flight; no activations, no MFMAs.  The XOR of what a workgroup read
+// goes to sink[linear workgroup id] so the loads are not removed.  A floor
+// for the GEMM's duration at its grid, for benchmarking.
+template <int CB>
+__global__ __launch_bounds__(64 * GV_WAVES) void read_floor_kernel(CtGemv g, int ksplit, float *sink) {
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int pos = CT_GV_KFAST ? blockIdx.y : blockIdx.x;
+    const int cbk = (CT_GV_QKV_HEADS && g.out == CT_GV_QKV ? ct_qkv_col(pos) : pos) * CB;
+    const int ks = CT_GV_KFAST ? blockIdx.x : blockIdx.y;
+    const int nsteps = g.K >> 5, per = nsteps / ksplit, s0 = ks * per;
+    const int ntile = CB * per;
+    u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int t0 = w; t0 < ntile; t0 += 4 * GV_WAVES) {
+        u16x8 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t = min(t0 + u * GV_WAVES, ntile - 1);
+            const int cb = t / per, st = s0 + t % per;
+            v[u] = *reinterpret_cast<const u16x8 *>(g.W + ((((long)cbk + cb) * nsteps + st) << 9) + lane * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) x ^= v[u];
+    }
+    __shared__ unsigned red[GV_WAVES];
+    unsigned r = (unsigned)x[0] ^ x[1] ^ x[2] ^ x[3] ^ x[4] ^ x[5] ^ x[6] ^ x[7];
+    r = wave_xor(r);
+    if (lane == 0) red[w] = r;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned a = 0;
+#pragma unroll
+        for (int i = 0; i < GV_WAVES; i++) a ^= red[i];
+        const long b = ((long)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        sink[b] = __uint_as_float(a);
+    }
+}
+
 // One thread per 16-byte piece of the tiled weight.
 __global__ __launch_bounds__(256) void tile_w_kernel(const uint16_t *W, uint16_t *Wt, int N, int K) {
     const long piece = blockIdx.x * 256L + threadIdx.x, pieces = (long)N * K / 8;
@@ -186,6 +226,24 @@ extern "C" int ctk_gemv_ksplit(int N, int K) {
 // columns per workgroup: 64 for the LM head; 32 for the long-K projection
 // (its 512-column K-slices leave 256 workgroups); else 16
 static int gv_cb(int N, int K) { return (N >= 8192 && N % 64 == 0) ? 4 : (K >= 4096 && N % 32 == 0) ? 2 : 1; }
+
+extern "C" long ctk_gemv_read_floor_blocks(const CtGemv *g) {
+    const int ksplit = g->ksplit < 1 ? 1 : g->ksplit, cb = gv_cb(g->N, g->K);
+    return (long)ksplit * (g->N / (16 * cb)) * ((g->M + 63) / 64);
+}
+
+extern "C" void ctk_gemv_read_floor(const CtGemv *g, float *sink, hipStream_t s) {
+    if (g->M <= 0) return;
+    const int ksplit = g->ksplit < 1 ? 1 : g->ksplit, cb = gv_cb(g->N, g->K);
+    if (!g->wtile || g->K % (256 * ksplit) != 0 || g->N % (16 * cb) != 0 || ((uintptr_t)g->W & 15))
+        gv_fatal("read floor needs tiled, 16-byte aligned weights of a supported shape", g);
+    const dim3 grid(CT_GV_KFAST ? ksplit : g->N / (16 * cb), CT_GV_KFAST ? g->N / (16 * cb) : ksplit,
+                    (g->M + 63) / 64);
+    if (cb == 1) hipLaunchKernelGGL(read_floor_kernel<1>, grid, dim3(64 * GV_WAVES), 0, s, *g, ksplit, sink);
+    else if (cb == 2) hipLaunchKernelGGL(read_floor_kernel<2>, grid, dim3(64 * GV_WAVES), 0, s, *g, ksplit, sink);
+    else hipLaunchKernelGGL(read_floor_kernel<4>, grid, dim3(64 * GV_WAVES), 0, s, *g, ksplit, sink);
+}
+
 
 extern "C" void ctk_gemv_warm(const CtGemv *g, CtWarm *w) {
     const int ksplit = g->ksplit < 1 ? 1 : g->ksplit, cb = gv_cb(g->N, g->K);

@@ -255,6 +255,7 @@ _ENGINE_SIGS = {
     "hipb_bench_fill": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64], None),
     "hipb_attention_only": ([C.c_void_p], None),
     "hipb_bench_decode_gemms": ([C.c_void_p], None),
+    "hipb_bench_read_floor": ([C.c_void_p], None),
     "hipb_bench_encoder_gemm": ([C.c_void_p, C.c_int], None),
     "hipb_bench_steps": ([C.c_void_p, C.c_int], None),
     "hipb_stream": ([C.c_void_p], C.c_void_p),
@@ -342,6 +343,9 @@ class Engine:
 
     def decode_gemms_only(self):
         self.L.hipb_bench_decode_gemms(self.e)
+
+    def decode_gemm_read_floor(self):
+        self.L.hipb_bench_read_floor(self.e)
 
     def encoder_gemm(self, M):
         self.L.hipb_bench_encoder_gemm(self.e, M)

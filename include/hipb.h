@@ -175,6 +175,10 @@ void hipb_attention_only(HipbEngine *e);
  * cross out, FFN up, FFN down, then the LM head) over the current step
  * buffers on the engine stream, for per-kernel timing. */
 void hipb_bench_decode_gemms(HipbEngine *e);
+/* The same launches with each GEMM replaced by its weight reads alone (same
+ * grid, same 1 KB tiles per workgroup, no activations, no MFMAs): the floor
+ * the decode GEMMs are measured against. */
+void hipb_bench_read_floor(HipbEngine *e);
 /* Launches the packed encoder's FFN up-projection (layer 0 weights: M frames
  * x 1280 -> 5120, SiLU, pre-split input and output; the encoder runs this
  * GEMM twice per layer) once on the engine stream, in the engine's FFN
