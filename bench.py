@@ -56,8 +56,9 @@ TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 DOMINANT = "decode_gemm"
 BF16_PEAK_TFLOPS = 2500.0
 # Encoder frames per batch of the overlapped encode/decode (0: encode all,
-# then decode)
-OVERLAP_BATCH_FRAMES = int(os.environ.get("CT_BENCH_OVERLAP", "6144"))
+# then decode).  Measured on the stream: 4096 -> 3664 RTFx, 6144 -> 3770,
+# 9216 -> 3827, 12288 -> 3845, 16384 -> 3702, 20480 -> 3684, 0 -> 3708.
+OVERLAP_BATCH_FRAMES = int(os.environ.get("CT_BENCH_OVERLAP", "12288"))
 METRIC = "audio-sec/sec (RTFx) + decode tokens/s at ragged batch 64; % HBM/MFMA peak"
 
 
@@ -391,27 +392,40 @@ def cpu_baseline_port(samples, limits):
             "cpu_model": cpu_model_name(), "extrapolated": True}
 
 
-def cpu_single_clip_full(procs):
-    """The single-clip configuration in full on the reference CPU path (8 s
-    clip, 48 tokens, EOS suppressed): one process alone, then `procs`
-    processes at once.  Minutes of CPU time: run on request only."""
+def cpu_configs_full(procs):
+    """The single-clip and uniform-batch configurations in full on the
+    reference CPU path (its model.h on its CPU backend), one sequence per
+    process as the reference's thread-per-device pool runs them:
+      * single clip: an 8 s clip, 48 tokens, EOS suppressed; alone, then
+        `procs` copies at once (the CPU's aggregate);
+      * uniform batch: 8 clips of 10 s, 96 tokens each, 8 processes at once.
+    Minutes of CPU time: run on request only.  The reference prints each
+    finished encoder layer (its `verbose` flag) as progress."""
     global _CPU_MODEL
     import multiprocessing as mp
     _CPU_MODEL = cb.SynthModel(seed=1234, variant=0)
     out = {}
-    for n in (1, procs):
+    for name, jobs in (("single clip alone", [(8, 48, 800)]),
+                       (f"single clip x {procs}", [(8, 48, 800 + i) for i in range(procs)]),
+                       ("uniform batch (8 x 10 s, 96 tokens)", [(10, 96, 900 + i) for i in range(8)])):
         t0 = time.perf_counter()
-        with mp.get_context("fork").Pool(n) as pool:
-            res = pool.map(_ref_single_clip, [8] * n)
+        with mp.get_context("fork").Pool(len(jobs)) as pool:
+            res = pool.map(_ref_clip, jobs)
         wall = time.perf_counter() - t0
-        out[n] = {"wall_s": round(wall, 1), "per_clip_s": [round(r, 1) for r in res],
-                  "audio_sec_per_sec": round(8.0 * n / wall, 4)}
+        audio = float(sum(j[0] for j in jobs))
+        toks = sum(j[1] for j in jobs)
+        out[name] = {"processes": len(jobs), "wall_s": round(wall, 1),
+                     "per_clip_s": [round(r, 1) for r in res],
+                     "audio_sec_per_sec": round(audio / wall, 4),
+                     "tokens_per_s": round(toks / wall, 2)}
+        print(f"{name}: {out[name]['wall_s']} s", file=sys.stderr, flush=True)
     _CPU_MODEL = None
-    return {"config": "8 s clip, 48 tokens, EOS suppressed (reference model.h + CPU backend)",
+    return {"path": "reference model.h + backends/cpu/backend.c (oracle/_ref/libref_model.so)",
             "cpu_model": cpu_model_name(), "runs": out}
 
 
-def _ref_single_clip(secs):
+def _ref_clip(job):
+    secs, limit, seed = job
     sys.path.insert(0, os.path.join(REPO, "tests"))
     import oracle_bind as ob
     lib = C.CDLL(REF_MODEL_LIB)
@@ -419,13 +433,16 @@ def _ref_single_clip(secs):
     lib.ref_transcribe_single.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                           C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
     lib.ref_transcribe_single.restype = C.c_int
+    C.c_int.in_dll(lib, "verbose").value = 1
     lib.ref_set_weights(C.byref(_CPU_MODEL.W))
-    mel = ob.compute_mel(cb.synth_audio(secs * cb.SR, 800))
+    mel = ob.compute_mel(cb.synth_audio(secs * cb.SR, seed))
     prompt = np.asarray(cb.PROMPT, np.int32)
-    toks = np.zeros(48, np.int32)
+    toks = np.zeros(limit, np.int32)
     t0 = time.perf_counter()
-    lib.ref_transcribe_single(mel.ctypes.data, mel.shape[1], prompt.ctypes.data, len(prompt), 48, 1, 0,
-                              toks.ctypes.data, None, None)
+    n = lib.ref_transcribe_single(mel.ctypes.data, mel.shape[1], prompt.ctypes.data, len(prompt), limit,
+                                  1, 0, toks.ctypes.data, None, None)
+    if n != limit:
+        raise RuntimeError(f"reference produced {n} of {limit} tokens")
     return time.perf_counter() - t0
 
 
@@ -465,16 +482,16 @@ def main():
                     help="run only the per-kernel roofline microbenchmarks (for profiling)")
     ap.add_argument("--no-rooflines", action="store_true",
                     help="run only the stream (for profiling its kernel mix)")
-    ap.add_argument("--cpu-single-clip", type=int, default=0, metavar="PROCS",
-                    help="only time the single-clip configuration in full on the reference CPU "
-                         "path, alone and with PROCS processes at once (minutes), and exit")
+    ap.add_argument("--cpu-configs", type=int, default=0, metavar="PROCS",
+                    help="only time the single-clip (alone and PROCS at once) and uniform-batch "
+                         "configurations in full on the reference CPU path (minutes), and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (requests shard "
               "across GPUs with no exchange, see the design notes).", file=sys.stderr)
         sys.exit(2)
-    if args.cpu_single_clip:
-        print(json.dumps(cpu_single_clip_full(args.cpu_single_clip)))
+    if args.cpu_configs:
+        print(json.dumps(cpu_configs_full(args.cpu_configs)))
         return
 
     samples, limits = make_stream(args.requests, seed=3)
