@@ -97,6 +97,47 @@ def run_stream(hip, eng, ev, dev_pcm, offs, samples, limits, overlap=OVERLAP_BAT
     return t2 - t0, t2 - t1, steps
 
 
+def config_latency(hip, model, ev, ffn_bf16, reps=3):
+    """The single-clip (one 8 s clip, 48 tokens) and uniform-batch (8 x 10 s,
+    96 tokens) configurations end to end on the engine, PCM resident in HBM:
+    mel, encoder, cross K/V, prompt, decode, one slot per request.  Wall
+    seconds per run (mean of `reps` after one warm run), for comparison with
+    the reference CPU path's full runs of the same configurations."""
+    out = {}
+    prompt = np.asarray(cb.PROMPT, np.int32)
+    flags = cb.HIPB_SUPPRESS_EOS | cb.HIPB_FORCE_EOS
+    for name, secs, n, limit in (("single clip (8 s, 48 tokens)", 8, 1, 48),
+                                 ("uniform batch (8 x 10 s, 96 tokens)", 10, 8, 96)):
+        pcm = np.concatenate([cb.synth_audio(secs * cb.SR, 800 + i) for i in range(n)])
+        dev = hip.backend_arena_alloc(pcm.size)
+        hip.backend_htod(dev, pcm.ctypes.data, pcm.size)
+        eng = cb.Engine(model, slots=n, max_requests=n, max_frames=376, kv_bf16=True,
+                        max_tokens=len(prompt) + limit, prefill_rows=16, enc_ffn_bf16=ffn_bf16)
+        try:
+            times = []
+            for rep in range(reps + 1):
+                eng.reset()
+                ev.sync()
+                t0 = time.perf_counter()
+                for i in range(n):
+                    eng.L.hipb_submit_pcm_device(eng.e, dev + i * secs * cb.SR * 4, secs * cb.SR,
+                                                 prompt.ctypes.data, len(prompt), limit, flags)
+                eng.encode(max_batch_frames=24576)
+                eng.run(chunk=8)
+                ev.sync()
+                if rep:
+                    times.append(time.perf_counter() - t0)
+                if [len(eng.tokens(r)) for r in range(n)] != [limit] * n:
+                    raise RuntimeError(f"{name}: a request did not produce {limit} tokens")
+        finally:
+            eng.close()
+            hip.backend_arena_free(dev)
+        t = float(np.mean(times))
+        out[name] = {"seconds": round(t, 5), "audio_sec_per_sec": round(secs * n / t, 1),
+                     "tokens_per_s": round(limit * n / t, 1)}
+    return out
+
+
 def attention_roofline(hip, model, ev, reps=20, step_reps=0):
     """Decode-attention kernel at the 128-slot microbench shape; with
     step_reps > 0 also the whole decode step at that shape (eager steps)."""
@@ -549,6 +590,7 @@ def main():
 
     roofs, micro = ({}, {}) if args.no_rooflines else measure_rooflines(hip, model, ev,
                                                                          args.enc_ffn_bf16)
+    configs = None if args.no_rooflines else config_latency(hip, model, ev, args.enc_ffn_bf16)
 
     out = {
         "metric": METRIC, "value": round(rtfx, 2), "unit": "audio-sec/sec", "n_gpus": 1,
@@ -568,6 +610,7 @@ def main():
         "decode_steps": int(np.mean(steps)),
         "roofline": dict(roofs[DOMINANT], name=DOMINANT) if roofs else None, "rooflines": roofs,
         "decode_microbench": micro,
+        "config_runs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
