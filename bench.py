@@ -22,12 +22,17 @@ per-kernel averages of `bench.py --roofline-only` can be set beside them):
                           launch / average launch time, against 8 TB/s;
   rooflines.decode_gemm   the 49 decode GEMMs of one step at the stream's 64
                           slots: weight + activation-in + output bytes per
-                          launch / average launch time, against 8 TB/s;
+                          launch / average launch time, against 8 TB/s; with
+                          the same launches reading their weights alone
+                          (read_floor) beside it;
   rooflines.encoder_gemm  the packed encoder's FFN up-projection (M = 16384
-                          frames, 1280 -> 5120): 2*M*N*K per launch / time,
-                          against the bf16 dense MFMA peak;
+                          frames, 1280 -> 5120) in the stream's precision mode
+                          (encoder_gemm_split: the fp32-accurate form): 2*M*N*K
+                          per launch / time, against the bf16 dense MFMA peak;
   roofline                the one of them whose kernels take the largest
                           share of the stream's GPU time;
+  config_runs             the single-clip and uniform-batch configurations
+                          end to end on the engine (wall seconds);
   cpu_baseline            the reference CPU path (its model.h on its CPU
                           backend, compiled from its sources) on the host's
                           cores, one process per core, on a bounded sample
@@ -52,7 +57,7 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 # The kernel family with the largest share of the stream's GPU time (from the
 # eager rocprofv3 profile of the stream, encoding not overlapped: decode GEMMs
-# 30.9%, the encoder's pre-split GEMMs 27.6%, decode attention 20.1%).
+# 31.2%, the encoder's pre-split GEMMs 25.4%, decode attention 20.0%).
 DOMINANT = "decode_gemm"
 BF16_PEAK_TFLOPS = 2500.0
 # Encoder frames per batch of the overlapped encode/decode (0: encode all,
