@@ -252,17 +252,18 @@ def test_reference_host_on_hip(hip, variant, fname):
     assert np.array_equal(bt, g["batch_tokens"])
 
 
-ENC_T = [17, 37, 101, 376]
+ENC_T = [17, 37, 101, 376, 751, 2048]
 
 
 @pytest.mark.parametrize("T", ENC_T)
 def test_encoder_ops_long_T_vs_oracle(hip, kmodel, T):
-    """Rel-pos MHSA and the conformer conv module at encoder lengths of 1.3 to
-    30 s (T = 17, 37, 101, 376 frames: several 16-query blocks, multi-tile
-    score loops, the 32-key PV loop), through the ABI against the oracle
+    """Rel-pos MHSA and the conformer conv module at encoder lengths of 1.3 s
+    to the supported maximum (T = 17, 37, 101, 376, 751 and 2048 frames:
+    several 16-query blocks, multi-tile score loops, the 32-key PV loop, score
+    rows up to the 131 KB LDS bound), through the ABI against the oracle
     (backends/cpu/backend.c:244-337): own position table and the batch form
-    whose table is built for the longest clip (376) and read from row
-    376 - T (model.h:586-592).  <= 1e-4 relative per tensor."""
+    whose table is built for the longest clip (376, or T beyond it) and read
+    from row T_max - T (model.h:586-592).  <= 1e-4 relative per tensor."""
     hip.backend_weights_upload_blob(kmodel.data_ptr, kmodel.data_bytes)
     dev = ks.ArenaDev(hip)
     o = ob.oracle()
@@ -272,25 +273,27 @@ def test_encoder_ops_long_T_vs_oracle(hip, kmodel, T):
     work = dev.zeros((5 * T - 1) * D + max(T * (3 * T - 1), 2 * T * D))
     pe_own = dev.zeros(2 * T - 1, D)
     hip.backend_make_rel_pos_emb(pe_own[0], T)
-    TM = 376
+    TM = max(376, T)
     pe_max = dev.zeros(2 * TM - 1, D)
     hip.backend_make_rel_pos_emb(pe_max[0], TM)
     pe_ref = np.zeros((2 * T - 1, D), np.float32)
     o.orc_make_rel_pos_emb(pe_ref.ctypes.data, T)
     assert relerr(dev.get(pe_own), pe_ref) <= 1e-6
+    x = dev.zeros(T, D)
+    conv_work = dev.zeros(3 * T * D)
     for layer in (0, 7):
         want = x0.copy()
         o.orc_rel_pos_mhsa(want.ctypes.data, pe_ref.ctypes.data, T, kmodel.elayer_ptr(layer), None)
         for form, pe_ptr in (("own", pe_own[0]), ("shifted", pe_max[0] + (TM - T) * D * 4)):
-            x = dev.put(x0)
+            hip.backend_htod(x[0], x0.ctypes.data, x0.size)
             hip.backend_rel_pos_mhsa(x[0], pe_ptr, T, kmodel.elayer_ptr(layer), work[0])
             e = relerr(dev.get(x), want)
             print(f"case: rel_pos_mhsa T={T} layer {layer} {form} table: relerr {e:.2e}", flush=True)
             assert e <= TOL, (T, layer, form, e)
         want = x0.copy()
         o.orc_conformer_conv(want.ctypes.data, T, kmodel.elayer_ptr(layer), None)
-        x = dev.put(x0)
-        hip.backend_conformer_conv(x[0], T, kmodel.elayer_ptr(layer), dev.zeros(3 * T * D)[0])
+        hip.backend_htod(x[0], x0.ctypes.data, x0.size)
+        hip.backend_conformer_conv(x[0], T, kmodel.elayer_ptr(layer), conv_work[0])
         e = relerr(dev.get(x), want)
         print(f"case: conformer_conv T={T} layer {layer}: relerr {e:.2e}", flush=True)
         assert e <= TOL, (T, layer, e)
