@@ -279,11 +279,14 @@ def test_engine_pcm_path(hip, hot, oracle_runs):
 # 30 s (the longest, 376 encoder frames) packed into ~6100 rows, where the FFN
 # projections take the 256-row tile kernel while each clip alone (<= 376
 # rows) takes the 128-row one
+# "long": recordings of 60 s and 2 min left unchunked (751 and 1501 encoder
+# frames) beside a 5 s clip, in an engine sized for 2048 frames
 ENC_CLIPS = {"small": [(4000, 101), (33000, 104), (7200, 102), (161 * 160, 105)],
-             "large": [(320000 + 1600 * i, 200 + i) for i in range(23)] + [(480000, 230)]}
+             "large": [(320000 + 1600 * i, 200 + i) for i in range(23)] + [(480000, 230)],
+             "long": [(960000, 301), (1920000, 302), (80000, 303)]}
 
 
-@pytest.mark.parametrize("batch", ["small", "large"])
+@pytest.mark.parametrize("batch", ["small", "large", "long"])
 def test_packed_encoder_bitexact_vs_abi_encoder(hip, hot, batch):
     """The engine's packed encoder (pre-split activations, DMA-fed GEMM,
     ragged attention/conv kernels) gives the same bits per request as the
@@ -299,7 +302,8 @@ def test_packed_encoder_bitexact_vs_abi_encoder(hip, hot, batch):
     ref.ref_encoder.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
     ref.ref_set_weights(hot.weights_ref())
     mels = [ob.compute_mel(cb.synth_audio(n, s)) for n, s in ENC_CLIPS[batch]]
-    eng = cb.Engine(hot, slots=2, max_requests=len(mels), max_frames=400, kv_bf16=True)
+    eng = cb.Engine(hot, slots=2, max_requests=len(mels), max_frames=2048 if batch == "long" else 400,
+                    kv_bf16=True)
     try:
         for m in mels:
             eng.submit(m, 2, FLAGS)
