@@ -23,23 +23,19 @@
 namespace {
 
 constexpr int GV_WAVES = 8;
-// 1: a QKV launch's column blocks are dealt head by head over the XCDs
-#ifndef CT_GV_QKV_HEADS
-#define CT_GV_QKV_HEADS 1
-#endif
-// 1: K-slices vary fastest in launch order, so with 8 K-slices each XCD (its
-// own L2) serves one slice and fetches only that slice's activations
-#ifndef CT_GV_KFAST
-#define CT_GV_KFAST 1
-#endif
+// Launch order: K-slices vary fastest (grid x), so with 8 K-slices each XCD
+// (its own L2) serves one slice and fetches only that slice's activations;
+// column blocks follow (grid y), a QKV launch's dealt head by head over the
+// XCDs (ct_qkv_col) so that head h's blocks run where the attention's head-h
+// workgroups read them.
 
 template <int CB, int SPW>
 __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int r = lane & 15, kg = lane >> 4;
-    const int pos = CT_GV_KFAST ? blockIdx.y : blockIdx.x;
-    const int c0 = (CT_GV_QKV_HEADS && g.out == CT_GV_QKV ? ct_qkv_col(pos) : pos) * 16 * CB;
-    const int ks = CT_GV_KFAST ? blockIdx.x : blockIdx.y, z = blockIdx.z, m0 = z * 64;
+    const int pos = blockIdx.y;
+    const int c0 = (g.out == CT_GV_QKV ? ct_qkv_col(pos) : pos) * 16 * CB;
+    const int ks = blockIdx.x, z = blockIdx.z, m0 = z * 64;
     const int nsteps = g.K >> 5;
     const int s0 = ks * (GV_WAVES * SPW);
     int nrb = min(4, (g.M - m0 + 15) >> 4);
@@ -155,9 +151,9 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
 template <int CB>
 __global__ __launch_bounds__(64 * GV_WAVES) void read_floor_kernel(CtGemv g, int ksplit, float *sink) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int pos = CT_GV_KFAST ? blockIdx.y : blockIdx.x;
-    const int cbk = (CT_GV_QKV_HEADS && g.out == CT_GV_QKV ? ct_qkv_col(pos) : pos) * CB;
-    const int ks = CT_GV_KFAST ? blockIdx.x : blockIdx.y;
+    const int pos = blockIdx.y;
+    const int cbk = (g.out == CT_GV_QKV ? ct_qkv_col(pos) : pos) * CB;
+    const int ks = blockIdx.x;
     const int nsteps = g.K >> 5, per = nsteps / ksplit, s0 = ks * per;
     const int ntile = CB * per;
     u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -237,7 +233,7 @@ extern "C" void ctk_gemv_read_floor(const CtGemv *g, float *sink, hipStream_t s)
     const int ksplit = g->ksplit < 1 ? 1 : g->ksplit, cb = gv_cb(g->N, g->K);
     if (!g->wtile || g->K % (256 * ksplit) != 0 || g->N % (16 * cb) != 0 || ((uintptr_t)g->W & 15))
         gv_fatal("read floor needs tiled, 16-byte aligned weights of a supported shape", g);
-    const dim3 grid(CT_GV_KFAST ? ksplit : g->N / (16 * cb), CT_GV_KFAST ? g->N / (16 * cb) : ksplit,
+    const dim3 grid(ksplit, g->N / (16 * cb),
                     (g->M + 63) / 64);
     if (cb == 1) hipLaunchKernelGGL(read_floor_kernel<1>, grid, dim3(64 * GV_WAVES), 0, s, *g, ksplit, sink);
     else if (cb == 2) hipLaunchKernelGGL(read_floor_kernel<2>, grid, dim3(64 * GV_WAVES), 0, s, *g, ksplit, sink);
@@ -251,7 +247,7 @@ extern "C" void ctk_gemv_warm(const CtGemv *g, CtWarm *w) {
     w->gx = g->wtile ? g->N / (16 * cb) : 0;
     w->gy = ksplit; w->cb = cb;
     w->per = g->K / ksplit / 32; w->nsteps = g->K / 32;
-    w->heads = CT_GV_QKV_HEADS && g->out == CT_GV_QKV;
+    w->heads = g->out == CT_GV_QKV;
 }
 
 extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
@@ -265,7 +261,7 @@ extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
         gv_fatal("operands must be 16-byte aligned", g);
     const int spw = g->K / ksplit / 256;
     const int cb = gv_cb(g->N, g->K);
-    const dim3 grid(CT_GV_KFAST ? ksplit : g->N / (16 * cb), CT_GV_KFAST ? g->N / (16 * cb) : ksplit,
+    const dim3 grid(ksplit, g->N / (16 * cb),
                     (g->M + 63) / 64);
     const dim3 block(64 * GV_WAVES);
 #define GV_CASE(CB, SPW)                                                          \
