@@ -11,8 +11,9 @@
  *    round trip);
  *  - KV caches in HBM as [layer][slot][head][position][128] (self) and
  *    [layer][request][head][frame][128] (cross), bf16 or fp32;
- *  - the prompt is fed one token per step through the same kernels, so a
- *    request's numbers never depend on its slot or on the other requests;
+ *  - the prompt is fed through the same step kernels (one token per step,
+ *    or several per step in spare prompt rows), so a request's numbers
+ *    never depend on its slot, its step rows or the other requests;
  *  - the forced-length policy of the benchmark configurations on device:
  *    EOS excluded from the argmax and/or EOS forced at token `limit`;
  *  - the encoder on packed ragged batches (M = sum of frames).
@@ -36,7 +37,7 @@ typedef struct HipbEngine HipbEngine;
 typedef struct {
     int slots;          /* concurrent KV slots (decode batch), 1..256          */
     int max_requests;   /* encoder-state entries: requests holding cross K/V and
-                           an encoder output at once (each ~16 MB at 376 frames,
+                           an encoder output at once (each ~14 MB at 376 frames,
                            bf16 KV); an entry is taken when a request is
                            encoded and recycled after it finishes, so any
                            number of requests flows through.  Up to
@@ -59,8 +60,8 @@ typedef struct {
                            take their activations as bf16 (one MFMA pass)
                            instead of the hi + lo pair (two passes): encoder
                            output within ~4e-3 of the fp32 path instead of
-                           ~1e-5, logits ~6e-4 instead of ~3e-4 on the
-                           specified weights; 0: both passes              */
+                           ~1e-5; logits within ~6e-4 on the specified weights
+                           (bf16 KV alone: ~4e-4); 0: both passes          */
 } HipbConfig;
 
 /* Request policy flags. */
