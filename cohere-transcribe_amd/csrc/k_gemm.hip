@@ -503,6 +503,115 @@ __device__ __forceinline__ void lds_dma16(const void *g, uint16_t *lds_wave_base
 // 16 lanes over 64 banks or 8 lanes over 32 banks per cycle.
 __device__ __forceinline__ int swz(int R, int c) { return c ^ (((R >> 1) ^ (R >> 2)) & 3); }
 
+// The vector epilogue of a tile staged in LDS as fp32 rows of SBN floats
+// (16-column groups XOR-swizzled by row).  A thread finishes the 8 columns
+// col..col+7 (one segment, one head, col < N; local group g8) of NI rows 16
+// apart.  What is constant for the thread (bias, segment) is set up once per
+// tile (Epi8), and every global load the rows need (row mask, cache row
+// offset, the FMADD residual) is issued before the first store, so their
+// latencies overlap instead of adding up row after row.  Per element the
+// arithmetic is store_out8's.
+struct Epi8 {
+    float b[8];
+    int mode;               // CtSeg mode, or -1 for plain rows (nseg == 0)
+    void *base, *base_lo;
+    long ld;
+    const long *rowoff;
+    long off;               // column offset in a row (HEADS: head block + column)
+};
+
+__device__ __forceinline__ Epi8 epi8_setup(const CtGemm &g, int col) {
+    Epi8 e;
+    if (g.bias) {
+        const u16x8 b8 = *reinterpret_cast<const u16x8 *>(g.bias + col);
+#pragma unroll
+        for (int i = 0; i < 8; i++) e.b[i] = bf2f(b8[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) e.b[i] = 0.0f;
+    }
+    if (g.nseg > 0) {
+        const int si = col / g.seg_w, c = col - si * g.seg_w;
+        const CtSeg &sg = g.seg[si];
+        e.mode = sg.mode; e.base = sg.base; e.base_lo = sg.base_lo; e.ld = sg.ld; e.rowoff = sg.rowoff;
+        e.off = (sg.mode == CT_OUT_DENSE || sg.mode == CT_OUT_SPLIT) ? c : (long)(c >> 7) * sg.hstride + (c & 127);
+    } else {
+        e.mode = -1; e.base = g.Y; e.base_lo = nullptr; e.ld = g.ldy; e.rowoff = nullptr; e.off = col;
+    }
+    return e;
+}
+
+// Local rows lr0 + 16*i (i < NI) of the staged tile sc = output rows m0 + those.
+template <int NI>
+__device__ __forceinline__ void epi8_rows(const CtGemm &g, const Epi8 &e, const float *sc, int lr0, int m0, int g8) {
+    const bool fmadd = e.mode < 0 && g.epi == CT_EPI_FMADD;
+    const bool heads = e.mode == CT_OUT_HEADS_F32 || e.mode == CT_OUT_HEADS_BF16;
+    bool ok[NI];
+    long ro[NI];
+    float4 y0[NI], y1[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int m = m0 + lr0 + 16 * i;
+        ok[i] = m < g.M && (!g.row_mask || g.row_mask[m] != 0);
+        ro[i] = heads && ok[i] ? e.rowoff[m] : 0;
+        if (fmadd && ok[i]) {
+            const float4 *y4 = reinterpret_cast<const float4 *>(reinterpret_cast<float *>(e.base) + (long)m * e.ld + e.off);
+            y0[i] = y4[0]; y1[i] = y4[1];
+        } else {
+            y0[i] = y1[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int row = lr0 + 16 * i, m = m0 + row;
+        if (!ok[i] || ro[i] < 0) continue;
+        const float4 *pv = reinterpret_cast<const float4 *>(sc + row * SBN + ((g8 * 8) ^ (((row >> 2) & 3) << 4)));
+        const float4 v0 = pv[0], v1 = pv[1];
+        float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] += e.b[j];
+        if (heads) {
+            const long o = ro[i] + e.off;
+            if (e.mode == CT_OUT_HEADS_BF16) {
+                u16x8 b8;
+#pragma unroll
+                for (int j = 0; j < 8; j++) b8[j] = f2bf(v[j]);
+                *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base) + o) = b8;
+            } else {
+                float4 *y4 = reinterpret_cast<float4 *>(reinterpret_cast<float *>(e.base) + o);
+                y4[0] = make_float4(v[0], v[1], v[2], v[3]);
+                y4[1] = make_float4(v[4], v[5], v[6], v[7]);
+            }
+            continue;
+        }
+        if (e.mode == CT_OUT_SPLIT) {
+            act8(g, v);
+            u16x8 h8, l8;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                uint16_t h, l;
+                split_bf16(v[j], h, l);
+                h8[j] = h; l8[j] = l;
+            }
+            *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base) + (long)m * e.ld + e.off) = h8;
+            if (e.base_lo)
+                *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base_lo) + (long)m * e.ld + e.off) = l8;
+            continue;
+        }
+        if (e.mode < 0) act8(g, v);      // plain rows take the activation; DENSE segments do not
+        float4 *y4 = reinterpret_cast<float4 *>(reinterpret_cast<float *>(e.base) + (long)m * e.ld + e.off);
+        if (fmadd) {
+            float4 a = y0[i], b = y1[i];
+            a.x += g.scale * v[0]; a.y += g.scale * v[1]; a.z += g.scale * v[2]; a.w += g.scale * v[3];
+            b.x += g.scale * v[4]; b.y += g.scale * v[5]; b.z += g.scale * v[6]; b.w += g.scale * v[7];
+            y4[0] = a; y4[1] = b;
+        } else {
+            y4[0] = make_float4(v[0], v[1], v[2], v[3]);
+            y4[1] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+    }
+}
+
 template <bool GLU, bool LO>
 __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int n_nt, int vepi) {
     constexpr int STAGE_ELEMS = SplitCfg<LO>::STAGE, S_PER_WAVE = SplitCfg<LO>::PER_WAVE;
@@ -656,6 +765,15 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
                 sc[row * SBN + col] = acc[rb][cb][j];
             }
     __syncthreads();
+    if (vepi == 2) {
+        // thread tid finishes columns 8*(tid%32).. of rows tid/32 + 16*i
+        const int g8 = tid & 31, col = c0 + g8 * 8;
+        if (col < g.N) {
+            const Epi8 e = epi8_setup(g, col);
+            epi8_rows<SBM / 16>(g, e, sc, tid >> 5, m0, g8);
+        }
+        return;
+    }
     for (int it = tid; it < SBM * (SBN / 8); it += 512) {
         const int row = it / (SBN / 8), g8 = it % (SBN / 8);
         const int m = m0 + row, col = c0 + g8 * 8;
@@ -700,8 +818,8 @@ template <bool LO> struct Split256Cfg {
     static constexpr int STAGES = LO ? 3 : 4;                 // 144 KB, 128 KB of LDS
 };
 
-template <bool LO>
 __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, int n_nt, int vepi) {
+    constexpr bool LO = true;
     constexpr int T_STAGE = Split256Cfg<LO>::STAGE, T_PER_WAVE = Split256Cfg<LO>::PER_WAVE;
     constexpr int TST = Split256Cfg<LO>::STAGES;
     __shared__ __attribute__((aligned(16))) uint16_t smem[TST * T_STAGE];
@@ -776,16 +894,11 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
             const int R = wm + rb * 16 + r;
             const int off = R * SBK + swz(R, kg) * 8;
             const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAh + off));
-            if (LO) {
-                const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
+            const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
 #pragma unroll
-                for (int cb = 0; cb < 8; cb++) {
-                    acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
-                    acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
-                }
-            } else {
-#pragma unroll
-                for (int cb = 0; cb < 8; cb++) acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
+            for (int cb = 0; cb < 8; cb++) {
+                acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
+                acc[rb][cb] = mfma16(al, bfr[cb], acc[rb][cb]);
             }
         }
     }
@@ -796,6 +909,9 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
     // epilogue in two 128-row halves through the LDS ring (128 KB each); rows
     // finish 8 columns per thread (16-byte stores when vepi allows)
     float *sc = reinterpret_cast<float *>(smem);
+    const int eg8 = tid & 31, ecol = c0 + eg8 * 8;
+    Epi8 ep;
+    if (vepi == 2 && ecol < g.N) ep = epi8_setup(g, ecol);
 #pragma unroll
     for (int half = 0; half < 2; half++) {
         if ((wm >> 7) == half) {
@@ -811,6 +927,232 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
                     }
         }
         __syncthreads();
+        if (vepi == 2) {
+            if (ecol < g.N) {
+                // two batches of four rows: the other half's accumulators are still live
+                epi8_rows<4>(g, ep, sc, tid >> 5, m0 + 128 * half, eg8);
+                epi8_rows<4>(g, ep, sc, (tid >> 5) + 64, m0 + 128 * half, eg8);
+            }
+            __syncthreads();
+            continue;
+        }
+        for (int it = tid; it < 128 * (SBN / 8); it += 512) {
+            const int row = it / (SBN / 8), g8 = it % (SBN / 8);
+            const int m = m0 + 128 * half + row, col = c0 + g8 * 8;
+            if (m >= g.M || col >= g.N) continue;
+            if (g.row_mask && !g.row_mask[m]) continue;
+            const float4 *pv = reinterpret_cast<const float4 *>(sc + row * SBN + ((g8 * 8) ^ (((row >> 2) & 3) << 4)));
+            const float4 v0 = pv[0], v1 = pv[1];
+            float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            if (g.bias) {
+                if (vepi) {
+                    const u16x8 b8 = *reinterpret_cast<const u16x8 *>(g.bias + col);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] += bf2f(b8[i]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] += col + i < g.N ? bf2f(g.bias[col + i]) : 0.0f;
+                }
+            }
+            if (vepi) {
+                store_out8(g, m, col, v);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (col + i < g.N) store_out(g, m, col + i, v[i]);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// The same DMA as lds_dma16, issued from inline assembly.  The compiler counts
+// the builtin's LDS write as an LDS event of unknown order (it is not: the
+// hardware's lgkmcnt does not wait for the DMA's data), so with the builtin in
+// a loop every first use of an LDS fragment waits for all LDS reads in
+// flight.  Issued here, the DMA is invisible to that bookkeeping and the
+// fragment reads get in-order waits; the DMA itself is waited for explicitly
+// (vmcnt) before the barrier that publishes a stage.  M0 takes the wave's LDS
+// destination; one wait state separates its write from the load.  M0 is a
+// register the compiler reserves (an asm clobber of it is ignored): the kernel
+// that uses this helper has no other instruction that reads M0 (no LDS-DMA
+// builtin, no register-indexed moves), so nothing relies on its old value.
+__device__ __forceinline__ void lds_dma16_asm(const void *g, uint16_t *lds_wave_base) {
+    const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_ptr_t)lds_wave_base);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(l) : "memory");
+}
+
+// ---------------------------------------------------------------------------
+// The 256 x 256 tile, single-pass form (A is bf16 alone: one MFMA per K-step
+// and fragment; 4-stage ring of 32 KB, 4 DMA instructions per wave per stage),
+// software-pipelined: the W fragments of K-step kt + 1 are read while the
+// MFMAs of step kt run (two register sets), and each 16-row A fragment one
+// row block ahead of its MFMAs, so LDS latency sits under the MFMAs.  Stage
+// kt + 1 is made readable (its DMA waited for, one barrier) at the top of step
+// kt, which also frees the slot of stage kt - 1 for the next DMA.  The number
+// of K-steps must be even (K % 64 == 0): the last pair is peeled so that no
+// LDS read sits under a branch.  Per element the MFMA sequence is unchanged.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(512) void gemm_split256_sp_kernel(CtGemm g, int n_mt, int n_nt, int vepi) {
+    constexpr int T_STAGE = Split256Cfg<false>::STAGE, T_PER_WAVE = Split256Cfg<false>::PER_WAVE;
+    constexpr int TST = Split256Cfg<false>::STAGES;
+    static_assert(TST >= 3, "the ring needs a landed stage, a stage in use and a free slot");
+    __shared__ __attribute__((aligned(16))) uint16_t smem[TST * T_STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int r = lane & 15, kg = lane >> 4;
+    const int nt = n_mt * n_nt;
+    const int per = (nt + 7) / 8;
+    const int t = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (t >= nt) return;
+    const int gsize = SGM * n_nt;
+    const int grp = t / gsize, rem = t % gsize;
+    const int gm = min(SGM, n_mt - grp * SGM);
+    const int tn = rem / gm, tm = grp * SGM + rem % gm;
+    const int m0 = tm * TBM, c0 = tn * SBN;
+
+    // instruction i = wv + 8*j: i < 16 A rows 16i.., then W
+    const uint16_t *src[T_PER_WAVE];
+    int dst[T_PER_WAVE];
+#pragma unroll
+    for (int j = 0; j < T_PER_WAVE; j++) {
+        const int i = wv + 8 * j;
+        const int Rl = lane >> 2, ch = lane & 3;
+        if (i < 16) {
+            const int R = i * 16 + Rl;
+            const int m = min(m0 + R, g.M - 1);
+            src[j] = g.Ahi + (long)m * g.lda + swz(R, ch) * 8;
+            dst[j] = i * 16 * SBK;
+        } else {
+            const int R = (i - 16) * 16 + Rl;
+            const int n = min(c0 + R, g.N - 1);
+            src[j] = g.W + (long)n * g.K + swz(R, ch) * 8;
+            dst[j] = T_A + (i - 16) * 16 * SBK;
+        }
+    }
+    auto issue = [&](int kt) {
+        uint16_t *stage = smem + (kt % TST) * T_STAGE;
+#pragma unroll
+        for (int j = 0; j < T_PER_WAVE; j++) lds_dma16_asm(src[j] + kt * SBK, stage + dst[j]);
+    };
+    const int wm = (wv >> 1) * 64, wn = (wv & 1) * 128;
+    // fragment offsets within a stage: rows of one fragment share the swizzle
+    const int aoff = (wm + r) * SBK + swz(r, kg) * 8;
+    const int boff = T_A + (wn + r) * SBK + swz(r, kg) * 8;
+    // W fragments of a stage (8) double-buffered across steps; A fragments of
+    // a 16-row block read one block ahead (the last block's successor is
+    // block 0 of the next stage)
+    struct BFr { bf16x8 v[8]; };
+    struct AFr { bf16x8 h; };
+    auto read_b = [&](int kt, BFr &f) {
+        const uint16_t *st = smem + (kt % TST) * T_STAGE;
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++)
+            f.v[cb] = as_bf16x8(*reinterpret_cast<const u16x8 *>(st + boff + cb * 16 * SBK));
+    };
+    auto read_a = [&](int kt, int rb, AFr &f) {
+        const uint16_t *st = smem + (kt % TST) * T_STAGE + aoff + rb * 16 * SBK;
+        f.h = as_bf16x8(*reinterpret_cast<const u16x8 *>(st));
+    };
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    auto mma_row = [&](int rb, const AFr &a, const BFr &b) {
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++) acc[rb][cb] = mfma16(a.h, b.v[cb], acc[rb][cb]);
+    };
+    // vmcnt(n * T_PER_WAVE): this wave's DMA of all but the n youngest stages landed
+    auto wait_stages = [&](int n) {
+        if (n >= 2) __builtin_amdgcn_s_waitcnt(((2 * T_PER_WAVE) & 0xF) | (0x7 << 4) | (0xF << 8));
+        else if (n == 1) __builtin_amdgcn_s_waitcnt((T_PER_WAVE & 0xF) | (0x7 << 4) | (0xF << 8));
+        else __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
+    };
+    static_assert(TST - 3 <= 2 && 2 * T_PER_WAVE <= 15, "wait_stages covers at most two younger stages");
+    const int nk = g.K / SBK;
+#pragma unroll
+    for (int p = 0; p < TST - 1; p++)
+        if (p < nk) issue(p);
+    wait_stages(min(nk - 1, TST - 2));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    BFr b0, b1;
+    AFr a0, a1;
+    read_b(0, b0);
+    read_a(0, 0, a0);
+    // step kt (kt + 1 < nk): make stage kt + 1 readable and refill the freed
+    // slot, read W of kt + 1, then the row blocks of kt, each MFMA group with
+    // the next block's A read in flight.  No branch around the reads, so each
+    // wait leaves the younger reads in flight.
+    auto step = [&](int kt, const BFr &bc, BFr &bn) {
+        wait_stages(min(nk - 2 - kt, TST - 3));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + TST - 1 < nk) issue(kt + TST - 1);
+        read_b(kt + 1, bn);
+        read_a(kt, 1, a1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_row(0, a0, bc);
+        __builtin_amdgcn_sched_barrier(0);
+        read_a(kt, 2, a0);
+        mma_row(1, a1, bc);
+        __builtin_amdgcn_sched_barrier(0);
+        read_a(kt, 3, a1);
+        mma_row(2, a0, bc);
+        __builtin_amdgcn_sched_barrier(0);
+        read_a(kt + 1, 0, a0);
+        mma_row(3, a1, bc);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // the last step: no next stage
+    auto last = [&](int kt, const BFr &bc) {
+        read_a(kt, 1, a1);
+        mma_row(0, a0, bc);
+        read_a(kt, 2, a0);
+        mma_row(1, a1, bc);
+        read_a(kt, 3, a1);
+        mma_row(2, a0, bc);
+        mma_row(3, a1, bc);
+    };
+    // nk is even (the launch checks K % 64 == 0): the last pair is peeled
+    for (int kt = 0; kt + 2 < nk; kt += 2) {
+        step(kt, b0, b1);
+        step(kt + 1, b1, b0);
+    }
+    step(nk - 2, b0, b1);
+    last(nk - 1, b1);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    float *sc = reinterpret_cast<float *>(smem);
+    const int eg8 = tid & 31, ecol = c0 + eg8 * 8;
+    Epi8 ep;
+    if (vepi == 2 && ecol < g.N) ep = epi8_setup(g, ecol);
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+        if ((wm >> 7) == half) {
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                for (int cb = 0; cb < 8; cb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int row = wm - 128 * half + rb * 16 + kg * 4 + j;
+                        const int col = (wn + cb * 16 + r) ^ (((row >> 2) & 3) << 4);
+                        sc[row * SBN + col] = acc[rb][cb][j];
+                    }
+        }
+        __syncthreads();
+        if (vepi == 2) {
+            if (ecol < g.N) {
+                // two batches of four rows: the other half's accumulators are still live
+                epi8_rows<4>(g, ep, sc, tid >> 5, m0 + 128 * half, eg8);
+                epi8_rows<4>(g, ep, sc, (tid >> 5) + 64, m0 + 128 * half, eg8);
+            }
+            __syncthreads();
+            continue;
+        }
         for (int it = tid; it < 128 * (SBN / 8); it += 512) {
             const int row = it / (SBN / 8), g8 = it % (SBN / 8);
             const int m = m0 + 128 * half + row, col = c0 + g8 * 8;
@@ -1035,12 +1377,13 @@ extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
         const int n_mt = (g->M + SBM - 1) / SBM;
         const int n_nt = glu ? (g->glu_half + SBN / 2 - 1) / (SBN / 2) : (g->N + SBN - 1) / SBN;
         const int nt = n_mt * n_nt, per = (nt + 7) / 8;
-        const int vepi = vector_epilogue_ok(g);
+        // 2: the batched vector epilogue (no row scatter), 1: vector stores, 0: scalar
+        const int vepi = vector_epilogue_ok(g) ? (g->row_len ? 1 : 2) : 0;
         const bool lo = g->Alo != NULL;     /* no lo plane: single-pass bf16 A */
-        if (!glu && g->M >= CT_SPLIT256_MIN_M && prefer_256(g->M, n_nt)) {
+        if (!glu && g->M >= CT_SPLIT256_MIN_M && prefer_256(g->M, n_nt) && (lo || g->K % 64 == 0)) {
             const int n_mt2 = (g->M + TBM - 1) / TBM, nt2 = n_mt2 * n_nt, per2 = (nt2 + 7) / 8;
-            if (lo) hipLaunchKernelGGL(gemm_split256_kernel<true>, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
-            else hipLaunchKernelGGL(gemm_split256_kernel<false>, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
+            if (lo) hipLaunchKernelGGL(gemm_split256_kernel, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
+            else hipLaunchKernelGGL(gemm_split256_sp_kernel, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
             return;
         }
         if (glu && lo) hipLaunchKernelGGL((gemm_split_kernel<true, true>), dim3(per * 8), dim3(512), 0, s, *g, n_mt, n_nt, 0);
