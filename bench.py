@@ -262,12 +262,12 @@ def encoder_gemm_roofline(model, ev, ffn_bf16, M=16384, reps=10):
            "avg_launch_us": round(ms * 1e3, 1), "flops_per_launch": 2 * M * N * K,
            "workload": f"M={M} N={N} K={K}"}
     if ffn_bf16:
-        out.update(kernel="gemm_split256_kernel<false> (encoder FFN up, SiLU, single-pass bf16 "
+        out.update(kernel="gemm_split256_sp_kernel (encoder FFN up, SiLU, single-pass bf16 "
                           "in/out)",
                    note="bf16 activations (rounded by the producer) against bf16 weights, fp32 "
                         "accumulation: the MFMA pipe runs the algorithmic flops counted here")
     else:
-        out.update(kernel="gemm_split256_kernel<true> (encoder FFN up, SiLU, pre-split in/out)",
+        out.update(kernel="gemm_split256_kernel (encoder FFN up, SiLU, pre-split in/out)",
                    note="activations as hi+lo bf16 against exact bf16 weights: the MFMA pipe "
                         "runs 2x the algorithmic flops counted here")
     return out
