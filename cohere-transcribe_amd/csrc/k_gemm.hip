@@ -586,16 +586,17 @@ __device__ __forceinline__ void epi8_rows(const CtGemm &g, const Epi8 &e, const 
         }
         if (e.mode == CT_OUT_SPLIT) {
             act8(g, v);
-            u16x8 h8, l8;
+            u16x8 h8;
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                uint16_t h, l;
-                split_bf16(v[j], h, l);
-                h8[j] = h; l8[j] = l;
-            }
+            for (int j = 0; j < 8; j++) h8[j] = f2bf(v[j]);
             *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base) + (long)m * e.ld + e.off) = h8;
-            if (e.base_lo)
+            if (e.base_lo) {
+                // lo = the rounding remainder, as split_bf16
+                u16x8 l8;
+#pragma unroll
+                for (int j = 0; j < 8; j++) l8[j] = f2bf(v[j] - bf2f(h8[j]));
                 *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base_lo) + (long)m * e.ld + e.off) = l8;
+            }
             continue;
         }
         if (e.mode < 0) act8(g, v);      // plain rows take the activation; DENSE segments do not
