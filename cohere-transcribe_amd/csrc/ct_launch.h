@@ -66,6 +66,10 @@ typedef struct {
 } CtGemm;
 
 void ctk_gemm(const CtGemm *g, hipStream_t s);
+/* Tests: 128 or 256 forces the pre-split kernels' tile (0: the tile-count
+ * model); sizeof(CtGemm) for the tests' struct mirror. */
+void ctk_gemm_force_tile(int rows);
+int  ctk_gemm_sizeof(void);
 
 /* ---------------- decode GEMM on fragment-ordered activations ----------------
  * "Frag" layout of an activation matrix X[M][K] (K % 32 == 0), as the decode

@@ -1346,6 +1346,13 @@ static int vector_epilogue_ok(const CtGemm *g) {
     return 1;
 }
 
+// Tile choice of the pre-split kernels, for tests: 0 follows the tile-count
+// model below; 128 or 256 takes that tile wherever it applies (the two give
+// the same bits: the same per-element MFMA sequence).
+static int g_force_tile = 0;
+extern "C" void ctk_gemm_force_tile(int rows) { g_force_tile = rows; }
+extern "C" int ctk_gemm_sizeof(void) { return (int)sizeof(CtGemm); }
+
 // Tile-count model for the two pre-split kernels: a 256-row tile costs about
 // 1.74 128-row tiles (measured), and tiles run in rounds over the CUs.
 static int prefer_256(int M, int n_nt) {
@@ -1381,7 +1388,9 @@ extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
         // 2: the batched vector epilogue (no row scatter), 1: vector stores, 0: scalar
         const int vepi = vector_epilogue_ok(g) ? (g->row_len ? 1 : 2) : 0;
         const bool lo = g->Alo != NULL;     /* no lo plane: single-pass bf16 A */
-        if (!glu && g->M >= CT_SPLIT256_MIN_M && prefer_256(g->M, n_nt) && (lo || g->K % 64 == 0)) {
+        const bool t256 = g_force_tile ? g_force_tile == 256
+                                       : g->M >= CT_SPLIT256_MIN_M && prefer_256(g->M, n_nt);
+        if (!glu && t256 && (lo || g->K % 64 == 0)) {
             const int n_mt2 = (g->M + TBM - 1) / TBM, nt2 = n_mt2 * n_nt, per2 = (nt2 + 7) / 8;
             if (lo) hipLaunchKernelGGL(gemm_split256_kernel, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
             else hipLaunchKernelGGL(gemm_split256_sp_kernel, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);

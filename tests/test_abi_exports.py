@@ -52,13 +52,15 @@ def test_product_does_not_link_the_oracle():
 
 
 def test_kernel_struct_mirrors_match():
-    """The tests' ctypes mirrors of CtGemv and CtWarmSet have the C structs' sizes."""
-    from structs import CtGemv, CtWarmSet
+    """The tests' ctypes mirrors of CtGemv, CtWarmSet and CtGemm have the C structs' sizes."""
+    from structs import CtGemm, CtGemv, CtWarmSet
     lib = C.CDLL(cb.HIP_LIB)
     lib.ctk_gemv_sizeof.restype = C.c_int
     lib.ctk_warmset_sizeof.restype = C.c_int
+    lib.ctk_gemm_sizeof.restype = C.c_int
     assert C.sizeof(CtGemv) == lib.ctk_gemv_sizeof()
     assert C.sizeof(CtWarmSet) == lib.ctk_warmset_sizeof()
+    assert C.sizeof(CtGemm) == lib.ctk_gemm_sizeof()
 
 
 def test_gemv_read_ahead_descriptor_covers_each_tile_once():
