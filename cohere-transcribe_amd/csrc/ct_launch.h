@@ -123,21 +123,25 @@ void ctk_gemv(const CtGemv *g, hipStream_t s);
 void ctk_gemv_read_floor(const CtGemv *g, float *sink, hipStream_t s);
 long ctk_gemv_read_floor_blocks(const CtGemv *g);
 /* The weight tiles one decode-GEMM launch reads, by workgroup: workgroup i
- * (of gx * gy, i = K-slice + gy * column block) reads, for each of its cb
- * column blocks c, the per consecutive 1-KB tiles from tile
- * ((i / gy) * cb + c) * nsteps + (i % gy) * per of W (tile layout).  Workgroup
- * i runs on XCD i % 8, like every launch's workgroup i. */
+ * of its first row group (of gx * gy, i = K-slice + gy * column position,
+ * column block x = i / gy, or ct_qkv_col(i / gy, cb) for a QKV launch) reads,
+ * for each of its cb column blocks c, the per consecutive 1-KB tiles from
+ * tile (x * cb + c) * nsteps + (i % gy) * per of W (tile layout).  Workgroup
+ * i runs on XCD i % 8, like every launch's workgroup i; the other row groups'
+ * workgroups i + gx * gy * z read the same tiles on the same XCD (gx * gy is
+ * a multiple of 8 for every decoder shape). */
 typedef struct {
     const uint16_t *W;
     int gx, gy, cb, per, nsteps;
     int heads;                /* 1: a QKV launch, column positions dealt by head */
 } CtWarm;
-/* Column block of a QKV launch's workgroup at position p (192 blocks of 16):
- * positions p % 8 == h take head h's 8 query, 8 key and 8 value blocks, so
- * they run on XCD h, where the attention's workgroups of head h read them. */
-static inline CT_HD int ct_qkv_col(int p) {
-    const int j = p >> 3;
-    return (j >> 3) * 64 + (p & 7) * 8 + (j & 7);
+/* Column block of a QKV launch's workgroup at position p (blocks of 16*cb
+ * columns, cb in {1, 2, 4}): positions p % 8 == h take head h's 8/cb query,
+ * 8/cb key and 8/cb value blocks, so they run on XCD h, where the attention's
+ * workgroups of head h read them. */
+static inline CT_HD int ct_qkv_col(int p, int cb) {
+    const int j = p >> 3, bph = 8 / cb;
+    return (j / bph) * (64 / cb) + (p & 7) * bph + j % bph;
 }
 /* Fills w for the launch ctk_gemv(g) makes; w->gx = 0 when g's weights are
  * not in the tile layout. */

@@ -5,26 +5,28 @@
 #include "ct_dev.h"
 #include "ct_launch.h"
 
-// Read-ahead workgroup j of XCD x: reads the tiles of the GEMM workgroups
-// i = x + 8 j, x + 8 (j + rows), ... of each listed GEMM.  GEMM workgroup i
-// runs on XCD i % 8; the caller places this workgroup on XCD x, so the tiles
-// land in the L2 that GEMM workgroup reads them from.
+// Read-ahead workgroup j of XCD x.  The GEMM workgroups on XCD x are
+// i = x + 8 k (GEMM workgroup i runs on XCD i % 8), each reading cb column
+// blocks of per tiles; this workgroup reads the units (k, c) numbered
+// u = k * cb + c = j, j + rows, j + 2 rows, ...  Dealing 16-column units
+// rather than whole GEMM workgroups keeps each read-ahead workgroup's share
+// the same whatever columns per workgroup the GEMM takes.  The caller places
+// this workgroup on XCD x, so the tiles land in the L2 the GEMM reads them from.
 template <int NT>
 __device__ __forceinline__ void ct_warm_tiles(const CtWarmSet &ws, int x, int j) {
     unsigned acc = 0;
     for (int t = 0; t < ws.n; t++) {
         const CtWarm w = ws.t[t];
-        const int G = w.gx * w.gy;
-        for (int i = x + 8 * j; i < G; i += 8 * ws.rows) {
-            const int cx = w.heads ? ct_qkv_col(i / w.gy) : i / w.gy, ks = i % w.gy;
-            for (int c = 0; c < w.cb; c++) {
-                const uint4 *p = reinterpret_cast<const uint4 *>(
-                    w.W + ((((long)cx * w.cb + c) * w.nsteps + (long)ks * w.per) << 9));
+        const int U = (w.gx * w.gy - x + 7) / 8 * w.cb;      // units on XCD x
+        for (int u = j; u < U; u += ws.rows) {
+            const int i = x + 8 * (u / w.cb), c = u % w.cb;
+            const int cx = w.heads ? ct_qkv_col(i / w.gy, w.cb) : i / w.gy, ks = i % w.gy;
+            const uint4 *p = reinterpret_cast<const uint4 *>(
+                w.W + ((((long)cx * w.cb + c) * w.nsteps + (long)ks * w.per) << 9));
 #pragma unroll 8
-                for (int e = threadIdx.x; e < w.per * 64; e += NT) {
-                    const uint4 v = p[e];
-                    acc ^= v.x ^ v.y ^ v.z ^ v.w;
-                }
+            for (int e = threadIdx.x; e < w.per * 64; e += NT) {
+                const uint4 v = p[e];
+                acc ^= v.x ^ v.y ^ v.z ^ v.w;
             }
         }
     }

@@ -1226,7 +1226,7 @@ static void warm_add(HipbEngine *e, const uint16_t *Wd, int N, int K, int out) {
     if (e->warm.n >= 4) return;
     CtGemv g;
     memset(&g, 0, sizeof g);
-    g.W = Wd; g.wtile = CT_ENG_WTILE; g.N = N; g.K = K;
+    g.W = Wd; g.wtile = CT_ENG_WTILE; g.M = e->M; g.N = N; g.K = K; g.out = out;
     g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, K) : 1;
     ctk_gemv_warm(&g, &e->warm.t[e->warm.n++]);
 }
@@ -1717,7 +1717,7 @@ void hipb_bench_decode_gemms(HipbEngine *e) { step_kernels(e, 0, 0); }
 
 void hipb_bench_read_floor(HipbEngine *e) {
     if (!CT_ENG_WTILE) CT_FATAL("hipb_bench_read_floor: needs the tiled decode weights");
-    const long cap = 256L * ((e->d.rows + 63) / 64);
+    const long cap = 256L * ((e->d.rows + 15) / 16);     /* <= 256 workgroups per 16 rows */
     if (e->floor_cap < cap) {
         if (e->floor_sink) ECHK(hipFree(e->floor_sink));
         e->floor_sink = dmalloc((size_t)cap * sizeof(float));

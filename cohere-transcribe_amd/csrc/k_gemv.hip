@@ -4,13 +4,15 @@
 // Activations arrive pre-split (hi + lo bf16) in frag layout, so every load
 // a lane issues is one contiguous 16-byte piece of a 1-KB run: no strided row
 // reads, no split arithmetic in the GEMM.  A workgroup of 8 wavefronts owns
-// 16*CB output columns, one 64-row block and one K-slice of 256*SPW columns;
+// 16*CB output columns, 16*RB rows and one K-slice of 256*SPW columns;
 // wavefront w takes K-steps w, w+8, ... of the slice and issues all of its
 // loads before the first MFMA.  The 8 wave tiles are summed in LDS in wave
 // order.  With ksplit > 1 the slice sums are written as partial rows and the
 // consumer (the next LayerNorm, or the attention's query load) adds them in
-// slice order.  The split is a function of (N, K) only, so a row's bits never
-// depend on how many rows the step has.
+// slice order.  The split is a function of (N, K) only, and every tiling
+// gives an element the same MFMA sequence (its K-steps in order, hi then lo,
+// then the wave sum), so a row's bits never depend on how many rows the step
+// has or on the tiling chosen for them.
 //
 // Semantics per output: backends/cpu/backend.c:124-182 (y = x W^T + b, ReLU,
 // fmadd), with x = hi + lo exactly representable to 2^-17 relative.
@@ -29,31 +31,32 @@ constexpr int GV_WAVES = 8;
 // XCDs (ct_qkv_col) so that head h's blocks run where the attention's head-h
 // workgroups read them.
 
-template <int CB, int SPW>
+template <int CB, int SPW, int RB>
 __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int r = lane & 15, kg = lane >> 4;
     const int pos = blockIdx.y;
-    const int c0 = (g.out == CT_GV_QKV ? ct_qkv_col(pos) : pos) * 16 * CB;
-    const int ks = blockIdx.x, z = blockIdx.z, m0 = z * 64;
+    const int c0 = (g.out == CT_GV_QKV ? ct_qkv_col(pos, CB) : pos) * 16 * CB;
+    const int ks = blockIdx.x, q0 = blockIdx.z * RB, m0 = q0 * 16;   // first 16-row block, row
     const int nsteps = g.K >> 5;
     const int s0 = ks * (GV_WAVES * SPW);
-    int nrb = min(4, (g.M - m0 + 15) >> 4);
-    if (g.m_active && m0 > 0) {
-        // rows past the first block may be unused spare rows this step
+    int nrb = min(RB, (g.M - m0 + 15) >> 4);
+    if (g.m_active && m0 >= 64) {
+        // rows past the first 64 may be unused spare rows this step
         const int ma = *g.m_active;
         if (m0 >= ma) return;
         nrb = min(nrb, (ma - m0 + 15) >> 4);
     }
-    const uint16_t *ablk = g.A + ((long)z * nsteps << 12);
-    u16x8 ah[SPW][4], al[SPW][4], wv[SPW][CB];
+    u16x8 ah[SPW][RB], al[SPW][RB], wv[SPW][CB];
 #pragma unroll
     for (int j = 0; j < SPW; j++) {
         const int st = s0 + w + GV_WAVES * j;
 #pragma unroll
-        for (int rb = 0; rb < 4; rb++) {
+        for (int rb = 0; rb < RB; rb++) {
             if (rb < nrb) {
-                const uint16_t *p = ablk + ((long)(st * 4 + rb) << 10) + lane * 8;
+                // frag layout: per 64 rows and K-step, four 16-row pieces of 1 KB hi + 1 KB lo
+                const int q = q0 + rb;
+                const uint16_t *p = g.A + ((((long)(q >> 2) * nsteps + st) * 4 + (q & 3)) << 10) + lane * 8;
                 ah[j][rb] = *reinterpret_cast<const u16x8 *>(p);
                 al[j][rb] = *reinterpret_cast<const u16x8 *>(p + 512);
             } else {
@@ -66,15 +69,15 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
                 g.wtile ? g.W + ((((long)(c0 >> 4) + cb) * nsteps + st) << 9) + lane * 8
                         : g.W + (long)(c0 + cb * 16 + r) * g.K + st * 32 + kg * 8);
     }
-    f32x4 acc[4][CB];
+    f32x4 acc[RB][CB];
 #pragma unroll
-    for (int rb = 0; rb < 4; rb++)
+    for (int rb = 0; rb < RB; rb++)
 #pragma unroll
         for (int cb = 0; cb < CB; cb++) acc[rb][cb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < SPW; j++)
 #pragma unroll
-        for (int rb = 0; rb < 4; rb++) {
+        for (int rb = 0; rb < RB; rb++) {
             if (rb >= nrb) break;
 #pragma unroll
             for (int cb = 0; cb < CB; cb++) {
@@ -83,9 +86,9 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
                 acc[rb][cb] = mfma16(as_bf16x8(al[j][rb]), b, acc[rb][cb]);
             }
         }
-    __shared__ float part[GV_WAVES][64][16 * CB + 1];
+    __shared__ float part[GV_WAVES][16 * RB][16 * CB + 1];
 #pragma unroll
-    for (int rb = 0; rb < 4; rb++)
+    for (int rb = 0; rb < RB; rb++)
 #pragma unroll
         for (int cb = 0; cb < CB; cb++)
 #pragma unroll
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
 
     if (g.out == CT_GV_FRAG) {
         // one thread per (row, 8 consecutive columns): a 16-byte piece per plane
-        for (int e = tid; e < 64 * 2 * CB; e += 64 * GV_WAVES) {
+        for (int e = tid; e < 16 * RB * 2 * CB; e += 64 * GV_WAVES) {
             const int row = e / (2 * CB), grp = e % (2 * CB), m = m0 + row;
             if (m >= g.M) continue;
             u16x8 hv, lv;
@@ -116,7 +119,7 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
         }
         return;
     }
-    for (int e = tid; e < 64 * 16 * CB; e += 64 * GV_WAVES) {
+    for (int e = tid; e < 16 * RB * 16 * CB; e += 64 * GV_WAVES) {
         const int row = e / (16 * CB), cc = e % (16 * CB), m = m0 + row, col = c0 + cc;
         if (m >= g.M) continue;
         float s = part[0][row][cc];
@@ -152,7 +155,7 @@ template <int CB>
 __global__ __launch_bounds__(64 * GV_WAVES) void read_floor_kernel(CtGemv g, int ksplit, float *sink) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int pos = blockIdx.y;
-    const int cbk = (g.out == CT_GV_QKV ? ct_qkv_col(pos) : pos) * CB;
+    const int cbk = (g.out == CT_GV_QKV ? ct_qkv_col(pos, CB) : pos) * CB;
     const int ks = blockIdx.x;
     const int nsteps = g.K >> 5, per = nsteps / ksplit, s0 = ks * per;
     const int ntile = CB * per;
@@ -219,22 +222,36 @@ extern "C" int ctk_gemv_ksplit(int N, int K) {
     return 1;
 }
 
-// columns per workgroup: 64 for the LM head; 32 for the long-K projection
-// (its 512-column K-slices leave 256 workgroups); else 16
-static int gv_cb(int N, int K) { return (N >= 8192 && N % 64 == 0) ? 4 : (K >= 4096 && N % 32 == 0) ? 2 : 1; }
+// Tiling: 16-column blocks (cb) and 16-row blocks (rb) per workgroup.  A
+// workgroup pulls 16*rb*K*4 bytes of activations and 16*cb*K*2 of weights
+// through its CU's L2 port (≈ 64 B/clk), so the all-rows, 16-column tile
+// moved 8x more activation than weight bytes.  Measured over M = 16..80 with
+// weights streamed from HBM: one row block per workgroup and 32 columns (64
+// for the long-K projection) take 15-25% off the 64-row launches; 16 columns
+// stay best for the wide projections at M <= 16, and the LM head (32 MB of
+// weights, 256 workgroups) keeps all rows and 64 columns.
+static void gv_tile(int N, int K, int M, int *cb, int *rb) {
+    if (N >= 8192 && N % 64 == 0) { *cb = 4; *rb = 4; return; }
+    *rb = 1;
+    if (K >= 4096) *cb = N % 64 == 0 && M > 16 ? 4 : N % 32 == 0 ? 2 : 1;
+    else *cb = N % 32 == 0 && (M > 16 || N <= DEC_D) ? 2 : 1;
+}
 
 extern "C" long ctk_gemv_read_floor_blocks(const CtGemv *g) {
-    const int ksplit = g->ksplit < 1 ? 1 : g->ksplit, cb = gv_cb(g->N, g->K);
-    return (long)ksplit * (g->N / (16 * cb)) * ((g->M + 63) / 64);
+    const int ksplit = g->ksplit < 1 ? 1 : g->ksplit;
+    int cb, rb;
+    gv_tile(g->N, g->K, g->M, &cb, &rb);
+    return (long)ksplit * (g->N / (16 * cb)) * ((g->M + 16 * rb - 1) / (16 * rb));
 }
 
 extern "C" void ctk_gemv_read_floor(const CtGemv *g, float *sink, hipStream_t s) {
     if (g->M <= 0) return;
-    const int ksplit = g->ksplit < 1 ? 1 : g->ksplit, cb = gv_cb(g->N, g->K);
+    const int ksplit = g->ksplit < 1 ? 1 : g->ksplit;
+    int cb, rb;
+    gv_tile(g->N, g->K, g->M, &cb, &rb);
     if (!g->wtile || g->K % (256 * ksplit) != 0 || g->N % (16 * cb) != 0 || ((uintptr_t)g->W & 15))
         gv_fatal("read floor needs tiled, 16-byte aligned weights of a supported shape", g);
-    const dim3 grid(ksplit, g->N / (16 * cb),
-                    (g->M + 63) / 64);
+    const dim3 grid(ksplit, g->N / (16 * cb), (g->M + 16 * rb - 1) / (16 * rb));
     if (cb == 1) hipLaunchKernelGGL(read_floor_kernel<1>, grid, dim3(64 * GV_WAVES), 0, s, *g, ksplit, sink);
     else if (cb == 2) hipLaunchKernelGGL(read_floor_kernel<2>, grid, dim3(64 * GV_WAVES), 0, s, *g, ksplit, sink);
     else hipLaunchKernelGGL(read_floor_kernel<4>, grid, dim3(64 * GV_WAVES), 0, s, *g, ksplit, sink);
@@ -242,7 +259,9 @@ extern "C" void ctk_gemv_read_floor(const CtGemv *g, float *sink, hipStream_t s)
 
 
 extern "C" void ctk_gemv_warm(const CtGemv *g, CtWarm *w) {
-    const int ksplit = g->ksplit < 1 ? 1 : g->ksplit, cb = gv_cb(g->N, g->K);
+    const int ksplit = g->ksplit < 1 ? 1 : g->ksplit;
+    int cb, rb;
+    gv_tile(g->N, g->K, g->M, &cb, &rb);
     w->W = g->W;
     w->gx = g->wtile ? g->N / (16 * cb) : 0;
     w->gy = ksplit; w->cb = cb;
@@ -260,17 +279,17 @@ extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
         (g->out == CT_GV_FRAG && ((uintptr_t)g->F & 15)))
         gv_fatal("operands must be 16-byte aligned", g);
     const int spw = g->K / ksplit / 256;
-    const int cb = gv_cb(g->N, g->K);
-    const dim3 grid(ksplit, g->N / (16 * cb),
-                    (g->M + 63) / 64);
+    int cb, rb;
+    gv_tile(g->N, g->K, g->M, &cb, &rb);
+    const dim3 grid(ksplit, g->N / (16 * cb), (g->M + 16 * rb - 1) / (16 * rb));
     const dim3 block(64 * GV_WAVES);
-#define GV_CASE(CB, SPW)                                                          \
-    if (cb == CB && spw == SPW) {                                                 \
-        hipLaunchKernelGGL((gemv_kernel<CB, SPW>), grid, block, 0, s, *g);        \
+#define GV_CASE(CB, SPW, RB)                                                      \
+    if (cb == CB && spw == SPW && rb == RB) {                                     \
+        hipLaunchKernelGGL((gemv_kernel<CB, SPW, RB>), grid, block, 0, s, *g);    \
         return;                                                                   \
     }
-    GV_CASE(1, 1) GV_CASE(1, 2) GV_CASE(1, 4) GV_CASE(2, 1) GV_CASE(2, 2) GV_CASE(2, 4)
-    GV_CASE(4, 1) GV_CASE(4, 2) GV_CASE(4, 4)
+    GV_CASE(1, 1, 1) GV_CASE(1, 2, 1) GV_CASE(1, 4, 1) GV_CASE(2, 1, 1) GV_CASE(2, 2, 1) GV_CASE(2, 4, 1)
+    GV_CASE(4, 1, 1) GV_CASE(4, 2, 1) GV_CASE(4, 4, 1) GV_CASE(4, 1, 4) GV_CASE(4, 2, 4) GV_CASE(4, 4, 4)
 #undef GV_CASE
     gv_fatal("no kernel for this K slice", g);
 }

@@ -66,36 +66,59 @@ def test_kernel_struct_mirrors_match():
 def test_gemv_read_ahead_descriptor_covers_each_tile_once():
     """ctk_gemv_warm (host code) describes the tiles each decode-GEMM
     workgroup reads: workgroup i (K-slice i % gy, column position i / gy)
-    reads cb column blocks x per K-steps.  For every decoder shape the
-    workgroups' tiles together are each weight tile exactly once, and the
-    split matches ctk_gemv_ksplit."""
+    reads cb column blocks x per K-steps.  For every decoder shape and row
+    count the workgroups' tiles together are each weight tile exactly once,
+    the split matches ctk_gemv_ksplit, and a QKV launch's head-h tiles sit on
+    XCD h."""
     import numpy as np
     from structs import CtGemv, CtWarm
     lib = C.CDLL(cb.HIP_LIB)
     lib.ctk_gemv_warm.argtypes = [C.POINTER(CtGemv), C.POINTER(CtWarm)]
     lib.ctk_gemv_ksplit.argtypes = [C.c_int, C.c_int]
     lib.ctk_gemv_ksplit.restype = C.c_int
-    def qkv_col(p):          # ct_qkv_col: head-by-head positions of a QKV launch
-        j = p >> 3
-        return (j >> 3) * 64 + (p & 7) * 8 + (j & 7)
-    for N, K, partial, out in ((3072, 1024, False, 3), (3072, 1024, False, 1), (1024, 1024, True, 0),
-                               (4096, 1024, False, 2), (1024, 4096, True, 0), (16384, 1024, False, 1)):
-        ks = lib.ctk_gemv_ksplit(N, K) if partial else 1
-        g = CtGemv(W=1 << 20, N=N, K=K, ksplit=ks, wtile=1, out=out)
-        w = CtWarm()
-        lib.ctk_gemv_warm(C.byref(g), C.byref(w))
-        assert (w.gy, w.nsteps, w.per * w.gy, w.gx * w.cb * 16) == (ks, K // 32, K // 32, N), (N, K)
-        seen = np.zeros((N // 16) * (K // 32), np.int32)
-        assert w.heads == (out == 3)
-        for i in range(w.gx * w.gy):
-            cx, k = (qkv_col(i // w.gy) if w.heads else i // w.gy), i % w.gy
-            for c in range(w.cb):
-                t0 = (cx * w.cb + c) * w.nsteps + k * w.per
-                seen[t0:t0 + w.per] += 1
-        assert np.all(seen == 1), (N, K)
-        g.wtile = 0
-        lib.ctk_gemv_warm(C.byref(g), C.byref(w))
-        assert w.gx == 0
+    def qkv_col(p, cb):      # ct_qkv_col: head-by-head positions of a QKV launch
+        j, bph = p >> 3, 8 // cb
+        return (j // bph) * (64 // cb) + (p & 7) * bph + j % bph
+    widths = set()
+    for M in (8, 64, 80):
+        for N, K, partial, out in ((3072, 1024, False, 3), (3072, 1024, False, 1), (1024, 1024, True, 0),
+                                   (4096, 1024, False, 2), (1024, 4096, True, 0), (16384, 1024, False, 1)):
+            ks = lib.ctk_gemv_ksplit(N, K) if partial else 1
+            g = CtGemv(W=1 << 20, M=M, N=N, K=K, ksplit=ks, wtile=1, out=out)
+            w = CtWarm()
+            lib.ctk_gemv_warm(C.byref(g), C.byref(w))
+            assert (w.gy, w.nsteps, w.per * w.gy, w.gx * w.cb * 16) == (ks, K // 32, K // 32, N), (N, K)
+            assert (w.gx * w.gy) % 8 == 0    # later row groups land on the same XCDs
+            widths.add((N, K, w.cb))
+            seen = np.zeros((N // 16) * (K // 32), np.int32)
+            assert w.heads == (out == 3)
+            for i in range(w.gx * w.gy):
+                cx, k = (qkv_col(i // w.gy, w.cb) if w.heads else i // w.gy), i % w.gy
+                if w.heads:   # the attention's head h runs on XCD h
+                    assert (cx * w.cb * 16 % 1024) // 128 == i % 8
+                for c in range(w.cb):
+                    t0 = (cx * w.cb + c) * w.nsteps + k * w.per
+                    seen[t0:t0 + w.per] += 1
+            assert np.all(seen == 1), (M, N, K)
+            # the read-ahead's dealing (ct_warm_tiles, 32 rows per XCD): unit u = k*cb + c of
+            # XCD x is GEMM workgroup x + 8k's column block c; every tile once, on the GEMM
+            # workgroup's XCD, and each read-ahead workgroup's share set by N, K alone
+            rows, seen[:] = 32, 0
+            for x in range(8):
+                U = (w.gx * w.gy - x + 7) // 8 * w.cb
+                share = [len(range(j, U, rows)) for j in range(rows)]
+                assert max(share) == -(-(N // 16) * ks // 8 // rows), (M, N, K)
+                for u in range(U):
+                    i, c = x + 8 * (u // w.cb), u % w.cb
+                    cx, k = (qkv_col(i // w.gy, w.cb) if w.heads else i // w.gy), i % w.gy
+                    t0 = (cx * w.cb + c) * w.nsteps + k * w.per
+                    seen[t0:t0 + w.per] += 1
+            assert np.all(seen == 1), (M, N, K)
+            g.wtile = 0
+            lib.ctk_gemv_warm(C.byref(g), C.byref(w))
+            assert w.gx == 0
+    # both tile widths of the QKV launch are covered
+    assert {(3072, 1024, 1), (3072, 1024, 2)} <= widths
 
 
 def test_noalloc_variant_rejects_long_clips():
