@@ -225,15 +225,18 @@ extern "C" int ctk_gemv_ksplit(int N, int K) {
 // Tiling: 16-column blocks (cb) and 16-row blocks (rb) per workgroup.  A
 // workgroup pulls 16*rb*K*4 bytes of activations and 16*cb*K*2 of weights
 // through its CU's L2 port (≈ 64 B/clk), so the all-rows, 16-column tile
-// moved 8x more activation than weight bytes.  Measured over M = 16..80 with
-// weights streamed from HBM: one row block per workgroup and 32 columns (64
-// for the long-K projection) take 15-25% off the 64-row launches; 16 columns
-// stay best for the wide projections at M <= 16, and the LM head (32 MB of
-// weights, 256 workgroups) keeps all rows and 64 columns.
+// moved 8x more activation than weight bytes.  Measured over M = 16..80,
+// weights streamed from HBM and resident in L2: one row block per workgroup
+// and 32 columns take 15-25% off the 64-row launches, 64 columns for the
+// long-K projection and (above 32 rows, weights in L2 as the decode step's
+// read-ahead leaves them) for the wide ones; 16 columns stay best for the
+// wide projections at M <= 16, and the LM head (32 MB of weights, 256
+// workgroups) keeps all rows and 64 columns.
 static void gv_tile(int N, int K, int M, int *cb, int *rb) {
     if (N >= 8192 && N % 64 == 0) { *cb = 4; *rb = 4; return; }
     *rb = 1;
     if (K >= 4096) *cb = N % 64 == 0 && M > 16 ? 4 : N % 32 == 0 ? 2 : 1;
+    else if (N > DEC_D && N % 64 == 0 && M > 32) *cb = 4;
     else *cb = N % 32 == 0 && (M > 16 || N <= DEC_D) ? 2 : 1;
 }
 

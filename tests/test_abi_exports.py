@@ -80,7 +80,7 @@ def test_gemv_read_ahead_descriptor_covers_each_tile_once():
         j, bph = p >> 3, 8 // cb
         return (j // bph) * (64 // cb) + (p & 7) * bph + j % bph
     widths = set()
-    for M in (8, 64, 80):
+    for M in (8, 24, 64, 80):
         for N, K, partial, out in ((3072, 1024, False, 3), (3072, 1024, False, 1), (1024, 1024, True, 0),
                                    (4096, 1024, False, 2), (1024, 4096, True, 0), (16384, 1024, False, 1)):
             ks = lib.ctk_gemv_ksplit(N, K) if partial else 1
@@ -117,8 +117,8 @@ def test_gemv_read_ahead_descriptor_covers_each_tile_once():
             g.wtile = 0
             lib.ctk_gemv_warm(C.byref(g), C.byref(w))
             assert w.gx == 0
-    # both tile widths of the QKV launch are covered
-    assert {(3072, 1024, 1), (3072, 1024, 2)} <= widths
+    # every tile width of the QKV launch is covered
+    assert {(3072, 1024, 1), (3072, 1024, 2), (3072, 1024, 4)} <= widths
 
 
 def test_noalloc_variant_rejects_long_clips():
