@@ -42,11 +42,26 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u16x8 v) {
     return __builtin_bit_cast(bf16x8, v);
 }
 
+// v from the lane DPP control CTRL names (row_ror, row_bcast); lanes of rows
+// outside ROWS get 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+
 // Sum / max over the 64 lanes of a wavefront (every lane gets the result).
+// The sum stays in the VALU: rotations by 8, 4, 2 and 1 within each 16-lane
+// row (every lane then holds its row's sum), row 15's lane added into rows 1
+// and 3, lane 31 into rows 2 and 3, and lane 63's total read back for all.
+// Call with the whole wavefront active.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, CT_WAVE);
-    return v;
+    v += dpp_f<0x128, 0xF>(v);
+    v += dpp_f<0x124, 0xF>(v);
+    v += dpp_f<0x122, 0xF>(v);
+    v += dpp_f<0x121, 0xF>(v);
+    v += dpp_f<0x142, 0xA>(v);
+    v += dpp_f<0x143, 0xC>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -94,9 +94,13 @@ enum {
     CT_GV_PARTIAL = 0,  /* Y[(ks*M + m)*N + n] = partial sum over K-slice ks (no bias)  */
     CT_GV_DENSE   = 1,  /* Y[m*ldy + n] = act(s + b)                                    */
     CT_GV_FRAG    = 2,  /* F (frag layout, K' = N) = act(s + b), split hi/lo           */
-    CT_GV_QKV     = 3   /* n < 1024: Y[m*ldy + n] (query); n in [1024, 3072): key/value */
+    CT_GV_QKV     = 3,  /* n < 1024: Y[m*ldy + n] (query); n in [1024, 3072): key/value */
                         /* rows of the head-major caches kc/vc at rowoff[m] (< 0: skip) */
+    CT_GV_RESID   = 4   /* residual update Y[m*ldy + n] += s + b (N = DEC_D, no K split), */
+                        /* and each row's LayerNorm statistics per 32-column block b:     */
+                        /* lnstat[m*32 + b] = (mean, sum of squared deviations)          */
 };
+#define CT_LN_BLOCKS 32 /* 32-column blocks of a DEC_D row in lnstat                    */
 typedef struct {
     const uint16_t *A;        /* frag-ordered activations [M][K]                      */
     const uint16_t *W;        /* [N][K] bf16, or tiled (wtile)                         */
@@ -114,6 +118,13 @@ typedef struct {
     const int *m_active;      /* device int or NULL: rows at or past *m_active are
                                  unused this launch (workgroups of only such rows
                                  exit, their row blocks are not computed)           */
+    float *lnstat;            /* CT_GV_RESID output; with X the LayerNorm input      */
+    const float *X;           /* NULL, or A = LayerNorm(X) (K = DEC_D): rows X[m*ldx]
+                                 whose statistics a CT_GV_RESID launch left in lnstat,
+                                 normalised with lnw / lnb (bf16) and split hi/lo in
+                                 registers instead of read from frag A             */
+    long ldx;
+    const uint16_t *lnw, *lnb;
 } CtGemv;
 /* Requires N % 16 == 0 (N % 64 == 0 when N >= 8192), K % (256 * steps) == 0. */
 void ctk_gemv(const CtGemv *g, hipStream_t s);

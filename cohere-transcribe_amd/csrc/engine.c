@@ -77,8 +77,10 @@ struct HipbEngine {
     atomic_int n_assigned;     /* requests [0, n_assigned) have entries */
     atomic_int stop;           /* hipb_process ends: the encoder thread quits its wait */
     /* step activations: h residual rows (fp32); lnf/attf/midf the decode
-     * GEMMs' inputs in frag layout; parts K-slice partial sums */
-    float *h, *q, *parts, *logits;
+     * GEMMs' inputs in frag layout; parts K-slice partial sums; lnstat the
+     * rows' LayerNorm statistics per 32-column block, left by the residual
+     * projections for the next GEMM's LayerNorm input */
+    float *h, *q, *parts, *logits, *lnstat;
     int M;                     /* rows of the step being launched */
     /* decode GEMMs whose weight tiles the next attention launch reads ahead
      * into the L2 their workgroups will read from */
@@ -384,7 +386,9 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->attf = dmalloc(ct_frag_elems(NR, DEC_D) * 2);
     e->midf = dmalloc(ct_frag_elems(NR, DEC_FF) * 2);
     e->logits = dmalloc((size_t)S * VOCAB * 4);
+    e->lnstat = dmalloc((size_t)NR * CT_LN_BLOCKS * 2 * 4);
     ECHK(hipMemsetAsync(e->h, 0, (size_t)NR * DEC_D * 4, e->s));
+    ECHK(hipMemsetAsync(e->lnstat, 0, (size_t)NR * CT_LN_BLOCKS * 2 * 4, e->s));
     ECHK(hipMemsetAsync(d->act, 0, NR * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->tok, 0, NR * sizeof(int), e->s));
     ECHK(hipMemsetAsync(d->pos_len, 0, NR * sizeof(int), e->s));
@@ -446,7 +450,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.req_score, e->d.q,
                     e->d.req_next, e->d.rq, e->d.pend, e->d.fq,
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->ew_qkv, e->eb_qkv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
-                    e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits,
+                    e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits, e->lnstat,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep_all,
                     e->esub, e->emel, e->e_subtab, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
                     e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
@@ -1324,6 +1328,37 @@ static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint1
     launch_gemv(e, &g);
 }
 
+/* Output projection of an attention block onto the residual rows (h += attf
+ * W^T + b), leaving the rows' LayerNorm statistics for gv_ln: replaces the
+ * K-split projection plus the residual LayerNorm launch. */
+static void gv_resid(HipbEngine *e, const uint16_t *Wd, const uint16_t *bd) {
+    CtGemv g;
+    memset(&g, 0, sizeof g);
+    g.A = e->attf; g.W = Wd; g.bias = bd; g.wtile = CT_ENG_WTILE;
+    g.M = e->M; g.N = DEC_D; g.K = DEC_D; g.ksplit = 1;
+    g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
+    g.out = CT_GV_RESID;
+    g.Y = e->h; g.ldy = DEC_D; g.lnstat = e->lnstat;
+    launch_gemv(e, &g);
+}
+
+/* A decode GEMM on LayerNorm(h) (lnw, lnb), normalised in the GEMM from the
+ * statistics gv_resid left. */
+static void gv_ln(HipbEngine *e, const uint16_t *lnw, const uint16_t *lnb, const uint16_t *Wd,
+                  const uint16_t *bd, int N, int out, int relu, uint16_t *F) {
+    CtGemv g;
+    memset(&g, 0, sizeof g);
+    g.X = e->h; g.ldx = DEC_D; g.lnstat = e->lnstat; g.lnw = lnw; g.lnb = lnb;
+    g.W = Wd; g.bias = bd; g.wtile = CT_ENG_WTILE;
+    g.M = e->M; g.N = N; g.K = DEC_D;
+    g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
+    g.out = out; g.relu = relu;
+    g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, DEC_D) : 1;
+    g.Y = out == CT_GV_PARTIAL ? e->parts : NULL;
+    g.F = F;
+    launch_gemv(e, &g);
+}
+
 /* One decode step over slots rows, or (wide) over slots + prefill_rows rows
  * whose spare rows feed prompts several tokens a step.  full == 0 launches
  * only its GEMMs (timing support). */
@@ -1366,18 +1401,20 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)e->d.kv_rows * DEC_DK;
         g.kv_bf16 = e->esz == 2;
         launch_gemv(e, &g);
-        if (full && CT_WARM && e->read_ahead) warm_add(e, w_o, DEC_D, DEC_D, CT_GV_PARTIAL);
+        if (full && CT_WARM && e->read_ahead) warm_add(e, w_o, DEC_D, DEC_D, CT_GV_RESID);
         if (full && CT_WARM && e->read_ahead) warm_add(e, w_cq, DEC_D, DEC_D, CT_GV_PARTIAL);
         if (full) step_attention(e, l, 0);
-        gv(e, e->attf, w_o, NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
-
-        if (full) ln_frag(e, ks_o, DW(L->sa_ob), DW(L->ca_lnw), DW(L->ca_lnb));
-        gv(e, e->lnf, w_cq, NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
+        /* h += self-attention out-projection, then the cross-attention query
+         * from LayerNorm(h) normalised inside its GEMM */
+        gv_resid(e, w_o, DW(L->sa_ob));
+        gv_ln(e, DW(L->ca_lnw), DW(L->ca_lnb), w_cq, NULL, DEC_D, CT_GV_PARTIAL, 0, NULL);
         if (full && CT_WARM && e->read_ahead) warm_add(e, w_f1, DEC_FF, DEC_D, CT_GV_FRAG);
         if (full && CT_WARM && e->read_ahead) warm_add(e, w_f2, DEC_D, DEC_FF, CT_GV_PARTIAL);
         if (full) step_attention(e, l, 1);
+        /* the FFN's LayerNorm stays a launch of its own: normalising inside the
+         * FFN-up GEMM would repeat each row's LayerNorm over the full K in all
+         * 64 of its column-block workgroups (measured 2-5 us slower per launch) */
         gv(e, e->attf, w_co, NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
-
         if (full) ln_frag(e, ks_o, DW(L->ca_ob), DW(L->ffn_lnw), DW(L->ffn_lnb));
         gv(e, e->lnf, w_f1, DW(L->ffn_b1), DEC_FF, DEC_D, CT_GV_FRAG, 1, NULL, 0, e->midf);
         gv(e, e->midf, w_f2, NULL, DEC_D, DEC_FF, CT_GV_PARTIAL, 0, NULL, 0, NULL);

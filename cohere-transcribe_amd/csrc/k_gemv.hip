@@ -31,8 +31,32 @@ constexpr int GV_WAVES = 8;
 // XCDs (ct_qkv_col) so that head h's blocks run where the attention's head-h
 // workgroups read them.
 
-template <int CB, int SPW, int RB>
+// Sum over each 32-lane half of a wavefront, every lane getting the same
+// bits: rotations by 8, 4, 2 and 1 within each 16-lane row (DPP row_ror, no
+// LDS round trip), then the two rows swapped (ds_swizzle, XOR 16 within 32
+// lanes).  At every step the two lanes being combined hold equal values in
+// the step before, so each lane adds the same two numbers.
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float half_wave_sum(float v) {
+    v += row_ror<8>(v);
+    v += row_ror<4>(v);
+    v += row_ror<2>(v);
+    v += row_ror<1>(v);
+    return v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+
+// LNA: the A operand is LayerNorm(X) (backends/cpu/backend.c layernorm, eps
+// 1e-5) computed in registers: the row statistics merge the producer's 32
+// per-block (mean, squared deviations) pairs in a fixed order (Chan et al.'s
+// pairwise update with equal block sizes: mean of the means, then the
+// blocks' sums plus 32 (mean_b - mean)^2 each), and each input is
+// normalised, scaled and split hi/lo exactly as the LayerNorm kernels do.
+template <int CB, int SPW, int RB, bool LNA>
 __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
+    static_assert(!LNA || RB == 1, "the LayerNorm prologue covers one 16-row block");
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int r = lane & 15, kg = lane >> 4;
     const int pos = blockIdx.y;
@@ -48,11 +72,27 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
         nrb = min(nrb, (ma - m0 + 15) >> 4);
     }
     u16x8 ah[SPW][RB], al[SPW][RB], wv[SPW][CB];
+    float2 lst = make_float2(0.f, 0.f);
+    float4 xr[LNA ? SPW : 1][2];
+    u16x8 lw[LNA ? SPW : 1], lb[LNA ? SPW : 1];
+    if (LNA) {
+        // this thread's block statistics first, so their wait leaves the row loads in flight
+        const int m = min(m0 + (tid >> 5), g.M - 1);
+        lst = reinterpret_cast<const float2 *>(g.lnstat)[(long)m * CT_LN_BLOCKS + (tid & 31)];
+    }
 #pragma unroll
     for (int j = 0; j < SPW; j++) {
         const int st = s0 + w + GV_WAVES * j;
+        if (LNA) {
+            // the lane's 8 inputs of K-step st (rows past M read row M-1, never stored)
+            const int k = st * 32 + kg * 8;
+            const float4 *p = reinterpret_cast<const float4 *>(g.X + (long)min(m0 + r, g.M - 1) * g.ldx + k);
+            xr[j][0] = p[0]; xr[j][1] = p[1];
+            lw[j] = *reinterpret_cast<const u16x8 *>(g.lnw + k);
+            lb[j] = *reinterpret_cast<const u16x8 *>(g.lnb + k);
+        }
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++) {
+        for (int rb = 0; rb < RB && !LNA; rb++) {
             if (rb < nrb) {
                 // frag layout: per 64 rows and K-step, four 16-row pieces of 1 KB hi + 1 KB lo
                 const int q = q0 + rb;
@@ -68,6 +108,29 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
             wv[j][cb] = *reinterpret_cast<const u16x8 *>(
                 g.wtile ? g.W + ((((long)(c0 >> 4) + cb) * nsteps + st) << 9) + lane * 8
                         : g.W + (long)(c0 + cb * 16 + r) * g.K + st * 32 + kg * 8);
+    }
+    if (LNA) {
+        __shared__ float2 lnrow[16];
+        // half-wavefront h holds row h's 32 blocks (512 threads = 16 rows x 32 blocks)
+        const float mu = half_wave_sum(lst.x) / (float)CT_LN_BLOCKS;
+        const float d = lst.x - mu;
+        const float m2 = half_wave_sum(lst.y + (float)(DEC_D / CT_LN_BLOCKS) * d * d);
+        if ((tid & 31) == 0) lnrow[tid >> 5] = make_float2(mu, 1.0f / sqrtf(m2 / (float)DEC_D + 1e-5f));
+        __syncthreads();
+        const float2 mr = lnrow[r];
+#pragma unroll
+        for (int j = 0; j < SPW; j++) {
+            const float x[8] = {xr[j][0].x, xr[j][0].y, xr[j][0].z, xr[j][0].w,
+                                xr[j][1].x, xr[j][1].y, xr[j][1].z, xr[j][1].w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float o = (x[i] - mr.x) * mr.y * bf2f(lw[j][i]) + bf2f(lb[j][i]);
+                uint16_t hh, ll;
+                split_bf16(o, hh, ll);
+                ah[j][0][i] = hh;
+                al[j][0][i] = ll;
+            }
+        }
     }
     f32x4 acc[RB][CB];
 #pragma unroll
@@ -95,6 +158,27 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
             for (int j = 0; j < 4; j++) part[w][rb * 16 + kg * 4 + j][cb * 16 + r] = acc[rb][cb][j];
     __syncthreads();
 
+    if (CB == 2 && RB == 1 && g.out == CT_GV_RESID) {
+        // thread: row m0 + tid / 32, column c0 + tid % 32; a half-wavefront holds
+        // one row of this 32-column block
+        const int row = tid >> 5, cc = tid & 31, m = m0 + row, col = c0 + cc;
+        const bool ok = m < g.M && row < 16 * nrb;
+        float s = part[0][row][cc];
+#pragma unroll
+        for (int ww = 1; ww < GV_WAVES; ww++) s += part[ww][row][cc];
+        float x = 0.0f;
+        if (ok) {
+            float *hp = g.Y + (long)m * g.ldy + col;
+            x = *hp + (s + (g.bias ? bf2f(g.bias[col]) : 0.0f));
+            *hp = x;
+        }
+        const float mean = half_wave_sum(x) / 32.0f;
+        const float d = x - mean;
+        const float m2 = half_wave_sum(d * d);
+        if (ok && cc == 0)
+            reinterpret_cast<float2 *>(g.lnstat)[(long)m * CT_LN_BLOCKS + (col >> 5)] = make_float2(mean, m2);
+        return;
+    }
     if (g.out == CT_GV_FRAG) {
         // one thread per (row, 8 consecutive columns): a 16-byte piece per plane
         for (int e = tid; e < 16 * RB * 2 * CB; e += 64 * GV_WAVES) {
@@ -284,12 +368,20 @@ extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
     const int spw = g->K / ksplit / 256;
     int cb, rb;
     gv_tile(g->N, g->K, g->M, &cb, &rb);
+    const bool lna = g->X != NULL;
+    if (g->out == CT_GV_RESID &&
+        (g->N != DEC_D || ksplit != 1 || cb != 2 || rb != 1 || !g->lnstat || ((uintptr_t)g->lnstat & 7)))
+        gv_fatal("residual output needs N = DEC_D, no K split and an 8-byte aligned lnstat", g);
+    if (lna && (g->K != DEC_D || rb != 1 || !g->lnstat || !g->lnw || !g->lnb || g->ldx % 4 ||
+                ((uintptr_t)g->X & 15) || ((uintptr_t)g->lnw & 15) || ((uintptr_t)g->lnb & 15)))
+        gv_fatal("a LayerNorm input needs K = DEC_D, 16-byte aligned rows and vectors, and lnstat", g);
     const dim3 grid(ksplit, g->N / (16 * cb), (g->M + 16 * rb - 1) / (16 * rb));
     const dim3 block(64 * GV_WAVES);
-#define GV_CASE(CB, SPW, RB)                                                      \
-    if (cb == CB && spw == SPW && rb == RB) {                                     \
-        hipLaunchKernelGGL((gemv_kernel<CB, SPW, RB>), grid, block, 0, s, *g);    \
-        return;                                                                   \
+#define GV_CASE(CB, SPW, RB)                                                                \
+    if (cb == CB && spw == SPW && rb == RB) {                                               \
+        if (lna) hipLaunchKernelGGL((gemv_kernel<CB, SPW, RB, (RB == 1)>), grid, block, 0, s, *g); \
+        else hipLaunchKernelGGL((gemv_kernel<CB, SPW, RB, false>), grid, block, 0, s, *g);  \
+        return;                                                                             \
     }
     GV_CASE(1, 1, 1) GV_CASE(1, 2, 1) GV_CASE(1, 4, 1) GV_CASE(2, 1, 1) GV_CASE(2, 2, 1) GV_CASE(2, 4, 1)
     GV_CASE(4, 1, 1) GV_CASE(4, 2, 1) GV_CASE(4, 4, 1) GV_CASE(4, 1, 4) GV_CASE(4, 2, 4) GV_CASE(4, 4, 4)

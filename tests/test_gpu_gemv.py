@@ -367,3 +367,75 @@ def test_gemv_tiled_weights(lib, hip, N, K, out):
             assert np.array_equal(a[0], t[0]) and np.array_equal(a[1], t[1]), M
         else:
             assert np.array_equal(a.view(np.uint32), t.view(np.uint32)), M
+
+
+def test_gemv_residual_stats_and_layernorm_input(lib, hip):
+    """The residual projection (out CT_GV_RESID): h += x W^T + b on the
+    residual rows, leaving each row's (mean, squared deviations) per 32-column
+    block, against float64; then a GEMM whose A is LayerNorm(h) normalised in
+    the kernel from those statistics (CtGemv.X), against the float64 LayerNorm
+    (backends/cpu/backend.c layernorm, eps 1e-5) and product.  Rows must not
+    depend on the launch's row count or on the tile width it takes (M = 8, 24,
+    64 and 80 use 16-, 32- and 64-column tiles): bit-exact; rows past M stay
+    untouched."""
+    rng = np.random.default_rng(11)
+    dev = Dev(hip)
+    D, M, N2 = 1024, 80, 4096
+    h0 = (2.0 + rng.standard_normal((M, D))).astype(np.float32)      # rows with a nonzero mean
+    hi, lo = split(rng.standard_normal((M, D)).astype(np.float32))
+    Wo = f32_to_bf16(rng.standard_normal((D, D)).astype(np.float32) / 32)
+    bo = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
+    lnw = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32))
+    lnb = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
+    W2 = f32_to_bf16(rng.standard_normal((N2, D)).astype(np.float32) / 32)
+    b2 = f32_to_bf16(0.1 * rng.standard_normal(N2).astype(np.float32))
+
+    def tiled(W):
+        N, K = W.shape
+        praw, pt = dev.put(W), dev.zeros(N * K * 2)
+        lib.ctk_tile_w(praw, pt, N, K, None)
+        return pt
+
+    pWo, pW2 = tiled(Wo), tiled(W2)
+    pa, pbo = dev.put(to_frag(hi, lo)), dev.put(bo)
+    plnw, plnb, pb2 = dev.put(lnw), dev.put(lnb), dev.put(b2)
+    res = {}
+    for m in (80, 64, 24, 8):
+        print(f"case: residual projection + LayerNorm-input GEMM, M={m}", flush=True)
+        ph, pst, py = dev.put(h0), dev.zeros(M * 32 * 8), dev.zeros(M * N2 * 4)
+        dev.ev.sync()
+        g = CtGemv(A=pa, W=pWo, bias=pbo, M=m, N=D, K=D, ksplit=1, out=4, Y=ph, ldy=D, wtile=1,
+                   lnstat=pst)
+        lib.ctk_gemv(C.byref(g), None)
+        g2 = CtGemv(X=ph, ldx=D, lnstat=pst, lnw=plnw, lnb=plnb, W=pW2, bias=pb2, M=m, N=N2, K=D,
+                    ksplit=1, out=DENSE, Y=py, ldy=N2, wtile=1)
+        lib.ctk_gemv(C.byref(g2), None)
+        res[m] = (dev.get(ph, np.float32, M * D).reshape(M, D),
+                  dev.get(pst, np.float32, M * 64).reshape(M, 32, 2),
+                  dev.get(py, np.float32, M * N2).reshape(M, N2))
+    h, st, y = res[M]
+    x64 = bf16_to_f32(hi).astype(np.float64) + bf16_to_f32(lo)
+    href = h0 + x64 @ bf16_to_f32(Wo).astype(np.float64).T + bf16_to_f32(bo)
+    e = np.abs(h - href).max() / np.abs(href).max()
+    print(f"  residual relerr {e:.2e}")
+    assert e <= TOL
+    blk = h.astype(np.float64).reshape(M, 32, 32)
+    mean = blk.mean(2)
+    m2 = ((blk - mean[:, :, None]) ** 2).sum(2)
+    assert np.abs(st[:, :, 0] - mean).max() <= 1e-6 * np.abs(mean).max()
+    assert np.all(np.abs(st[:, :, 1] - m2) <= 1e-5 * m2 + 1e-6 * m2.max())
+    hd = h.astype(np.float64)
+    mu = hd.mean(1, keepdims=True)
+    var = ((hd - mu) ** 2).mean(1, keepdims=True)
+    ln = (hd - mu) / np.sqrt(var + 1e-5) * bf16_to_f32(lnw) + bf16_to_f32(lnb)
+    yref = ln @ bf16_to_f32(W2).astype(np.float64).T + bf16_to_f32(b2)
+    e = np.abs(y - yref).max() / np.abs(yref).max()
+    print(f"  LayerNorm-input GEMM relerr {e:.2e}")
+    assert e <= TOL
+    for m in (64, 24, 8):
+        hm, sm, ym = res[m]
+        assert np.array_equal(hm[:m].view(np.uint32), h[:m].view(np.uint32)), m
+        assert np.array_equal(sm[:m].view(np.uint32), st[:m].view(np.uint32)), m
+        assert np.array_equal(ym[:m].view(np.uint32), y[:m].view(np.uint32)), m
+        assert np.array_equal(hm[m:].view(np.uint32), h0[m:].view(np.uint32)), m
+        assert not sm[m:].any() and not ym[m:].any(), m
