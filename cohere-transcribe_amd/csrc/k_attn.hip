@@ -129,8 +129,10 @@ __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
     auto load_key = [&](int k, int v, Raw &kr, Raw &vr) {
         const long off = base + (long)k * a.kv_st + 8 * v;
         if constexpr (BF16 && VEC) {
-            kr = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.K) + off);
-            vr = *reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.V) + off);
+            // non-temporal: a step reads each cache row once, so the rows do not
+            // displace the weight tiles the launch's read-ahead rows bring into L2
+            kr = __builtin_nontemporal_load(reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.K) + off));
+            vr = __builtin_nontemporal_load(reinterpret_cast<const u16x8 *>(reinterpret_cast<const uint16_t *>(a.V) + off));
         } else {
             load8<BF16, VEC>(a.K, off, kr);
             load8<BF16, VEC>(a.V, off, vr);

@@ -105,9 +105,11 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
         }
 #pragma unroll
         for (int cb = 0; cb < CB; cb++)
-            wv[j][cb] = *reinterpret_cast<const u16x8 *>(
+            // non-temporal: a launch's weight tiles are dead after it, so they do not
+            // displace tiles the read-ahead brought in for the next GEMMs
+            wv[j][cb] = __builtin_nontemporal_load(reinterpret_cast<const u16x8 *>(
                 g.wtile ? g.W + ((((long)(c0 >> 4) + cb) * nsteps + st) << 9) + lane * 8
-                        : g.W + (long)(c0 + cb * 16 + r) * g.K + st * 32 + kg * 8);
+                        : g.W + (long)(c0 + cb * 16 + r) * g.K + st * 32 + kg * 8));
     }
     if (LNA) {
         __shared__ float2 lnrow[16];
