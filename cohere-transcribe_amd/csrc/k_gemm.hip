@@ -819,6 +819,10 @@ template <bool LO> struct Split256Cfg {
     static constexpr int STAGES = LO ? 3 : 4;                 // 144 KB, 128 KB of LDS
 };
 
+// GLU: the tile's 256 weight rows are 128 value columns c0.. and their 128
+// gate columns glu_half + c0..; waves with wn = 128 hold the gates and hand
+// them to the value waves through LDS (as gemm_split_kernel<true, LO> does).
+template <bool GLU>
 __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, int n_nt, int vepi) {
     constexpr bool LO = true;
     constexpr int T_STAGE = Split256Cfg<LO>::STAGE, T_PER_WAVE = Split256Cfg<LO>::PER_WAVE;
@@ -834,7 +838,8 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
     const int grp = t / gsize, rem = t % gsize;
     const int gm = min(SGM, n_mt - grp * SGM);
     const int tn = rem / gm, tm = grp * SGM + rem % gm;
-    const int m0 = tm * TBM, c0 = tn * SBN;
+    const int m0 = tm * TBM, c0 = tn * (GLU ? SBN / 2 : SBN);
+    const int nlim = GLU ? 2 * g.glu_half : g.N;
 
     // instruction i = wv + 8*j: i < 16 A-hi rows 16i.., then (LO) i < 32
     // A-lo, then W
@@ -852,7 +857,7 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
             dst[j] = (i < 16 ? 0 : T_A) + (i & 15) * 16 * SBK;
         } else {
             const int R = (i - NA) * 16 + Rl;
-            const int n = min(c0 + R, g.N - 1);
+            const int n = min(GLU ? (R < SBN / 2 ? c0 + R : g.glu_half + c0 + R - SBN / 2) : c0 + R, nlim - 1);
             src[j] = g.W + (long)n * g.K + swz(R, ch) * 8;
             dst[j] = (LO ? 2 : 1) * T_A + (i - NA) * 16 * SBK;
         }
@@ -907,6 +912,40 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
+    if (GLU) {
+        // value column lc (< 128) of row m: (s + b) * sigmoid(gate s + gate b)
+        float *sx = reinterpret_cast<float *>(smem);     // 256 x 128 gate sums = 128 KB
+        if (wn >= SBN / 2) {
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                for (int cb = 0; cb < 8; cb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        sx[(wm + rb * 16 + kg * 4 + j) * (SBN / 2) + cb * 16 + r] = acc[rb][cb][j];
+        }
+        __syncthreads();
+        if (wn < SBN / 2) {
+#pragma unroll
+            for (int cb = 0; cb < 8; cb++) {
+                const int lc = cb * 16 + r, col = c0 + lc;
+                if (col >= g.glu_half) continue;
+                const float ba = g.bias ? bf2f(g.bias[col]) : 0.0f;
+                const float bg = g.bias ? bf2f(g.bias[g.glu_half + col]) : 0.0f;
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int lrow = wm + rb * 16 + kg * 4 + j, m = m0 + lrow;
+                        if (m >= g.M) continue;
+                        const float a = acc[rb][cb][j] + ba;
+                        const float gt = sx[lrow * (SBN / 2) + lc] + bg;
+                        g.Y[(long)m * g.ldy + col] = a * sigmoid_hw(gt);
+                    }
+            }
+        }
+        return;
+    }
     // epilogue in two 128-row halves through the LDS ring (128 KB each); rows
     // finish 8 columns per thread (16-byte stores when vepi allows)
     float *sc = reinterpret_cast<float *>(smem);
@@ -1390,9 +1429,10 @@ extern "C" void ctk_gemm(const CtGemm *g, hipStream_t s) {
         const bool lo = g->Alo != NULL;     /* no lo plane: single-pass bf16 A */
         const bool t256 = g_force_tile ? g_force_tile == 256
                                        : g->M >= CT_SPLIT256_MIN_M && prefer_256(g->M, n_nt);
-        if (!glu && t256 && (lo || g->K % 64 == 0)) {
+        if (t256 && (glu ? lo : (lo || g->K % 64 == 0))) {
             const int n_mt2 = (g->M + TBM - 1) / TBM, nt2 = n_mt2 * n_nt, per2 = (nt2 + 7) / 8;
-            if (lo) hipLaunchKernelGGL(gemm_split256_kernel, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
+            if (glu) hipLaunchKernelGGL(gemm_split256_kernel<true>, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, 0);
+            else if (lo) hipLaunchKernelGGL(gemm_split256_kernel<false>, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
             else hipLaunchKernelGGL(gemm_split256_sp_kernel, dim3(per2 * 8), dim3(512), 0, s, *g, n_mt2, n_nt, vepi);
             return;
         }

@@ -12,8 +12,10 @@ through libct_hip.so's C entry point.
   float64 product of those values the fp32 sums agree to 1e-5, and an output
   rounded to bf16 lies within one bf16 step of the float64 value.
 * A row's bits do not depend on how many rows the launch has.
+* GLU (the conv module's first pointwise projection): value column j times
+  the sigmoid of gate column j + N/2, both with their bias.
 
-Semantics per output: backends/cpu/backend.c:124-182 (y = x W^T + b, SiLU,
+Semantics per output: backends/cpu/backend.c:124-182, 309 (y = x W^T + b, SiLU, GLU,
 ReLU, fmadd), with the encoder's output layouts (split planes, three dense
 segments, head-major cache rows with skipped rows).
 """
@@ -28,7 +30,7 @@ from test_gpu_gemv import Dev, bf16_to_f32, f32_to_bf16, split
 
 pytestmark = pytest.mark.gpu
 
-EPI_STORE, EPI_SILU, EPI_RELU, EPI_FMADD = 0, 1, 2, 3
+EPI_STORE, EPI_SILU, EPI_RELU, EPI_FMADD, EPI_GLU = 0, 1, 2, 3, 4
 OUT_DENSE, OUT_HEADS_BF16, OUT_SPLIT = 0, 2, 3
 M_FULL, M_PART = 1100, 300          # 4 full 256-row tiles and a partial one; a prefix of it
 KV_HSTRIDE = 64 * 128                # head stride of the head-major cache rows
@@ -73,6 +75,8 @@ class Case:
             self.pout = [dev.zeros(self.kv_elems * 2), dev.zeros(self.kv_elems * 2)]
         elif mode == "split":
             self.pout = [dev.zeros(M_FULL * N * 2), dev.zeros(M_FULL * N * 2)]
+        elif mode == "glu":
+            self.pout = [dev.zeros(M_FULL * (N // 2) * 4)]
         else:
             self.pout = [dev.zeros(M_FULL * N * 4)]
 
@@ -100,6 +104,8 @@ class Case:
                                  hstride=KV_HSTRIDE)
         elif self.mode == "fmadd":
             g.epi, g.Y, g.ldy = EPI_FMADD, self.pout[0], self.N
+        elif self.mode == "glu":
+            g.epi, g.glu_half, g.Y, g.ldy = EPI_GLU, self.N // 2, self.pout[0], self.N // 2
         else:
             g.epi, g.Y, g.ldy = EPI_RELU, self.pout[0], self.N
         return g
@@ -108,7 +114,8 @@ class Case:
         """Clears (or, for FMADD, re-seeds) the outputs, launches, returns the output bytes."""
         d = self.dev
         for p in self.pout:
-            nb = self.kv_elems * 2 if self.mode == "heads" else (M_FULL * self.N * (2 if self.mode == "split" else 4))
+            nb = (self.kv_elems * 2 if self.mode == "heads" else M_FULL * self.N * 2 if self.mode in ("split", "glu")
+                  else M_FULL * self.N * 4)
             # the host array must outlive the copy (a temporary's buffer is freed at once)
             src = self.y0 if self.mode == "fmadd" else np.full(nb // 4, -7.0, np.float32)
             d.hip.backend_htod(p, src.ctypes.data, src.size)
@@ -123,6 +130,8 @@ class Case:
                 outs.append(d.get(p, np.uint16, self.kv_elems))
             elif self.mode == "split":
                 outs.append(d.get(p, np.uint16, M_FULL * self.N).reshape(M_FULL, self.N))
+            elif self.mode == "glu":
+                outs.append(d.get(p, np.float32, M_FULL * self.N // 2).reshape(M_FULL, self.N // 2))
             elif self.mode == "qkv":
                 # three [M][N/3] segments back to back -> the logical [M][N] rows
                 w = self.N // 3
@@ -140,7 +149,7 @@ class Case:
 
 
 MODES = [("split", 5120, 1280), ("qkv", 3840, 1280), ("heads", 2048, 1024), ("fmadd", 1280, 2560),
-         ("relu", 1000, 1312)]
+         ("relu", 1000, 1312), ("glu", 2560, 1280)]
 
 
 @pytest.mark.parametrize("lo", [True, False], ids=["hilo", "single"])
@@ -216,6 +225,12 @@ def test_split_gemm_tiles_modes_and_float64(lib, hip, mode, N, K, lo):
         for seg in range(2):
             for hh in range(8):
                 assert np.array_equal(o256[seg][o + hh * KV_HSTRIDE:o + hh * KV_HSTRIDE + 128], fill)
+    elif mode == "glu":
+        h = N // 2
+        v = s[:, :h] / (1.0 + np.exp(-s[:, h:]))
+        e = np.abs(o256[0][rows].astype(np.float64) - v).max() / np.abs(v).max()
+        print(f"  relerr {e:.2e}")
+        assert e <= 2e-5
     elif mode == "fmadd":
         got = o256[0][rows].astype(np.float64)
         ref = case.y0[rows].astype(np.float64) + 0.5 * s
