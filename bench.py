@@ -61,9 +61,14 @@ TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 DOMINANT = "decode_gemm"
 BF16_PEAK_TFLOPS = 2500.0
 # Encoder frames per batch of the overlapped encode/decode (0: encode all,
-# then decode).  Measured on the stream: 4096 -> 3664 RTFx, 6144 -> 3770,
-# 9216 -> 3827, 12288 -> 3845, 16384 -> 3702, 20480 -> 3684, 0 -> 3708.
-OVERLAP_BATCH_FRAMES = int(os.environ.get("CT_BENCH_OVERLAP", "12288"))
+# then decode).  51 row tiles of 256 frames: every encoder GEMM's width is a
+# multiple of 1280 = 5 column tiles of 256, so a batch of 51 row tiles gives
+# 255, 510, 765 or 1020 tiles, each just under a whole number of rounds on
+# 256 CUs (52 row tiles would start a fifth round of the FFN-up GEMM for 16
+# of its 1040 tiles).  Measured on the stream: 10240 -> 4209 RTFx, 11264 ->
+# 4295, 12288 -> 4306, 12800 -> 4361, 13056 -> 4364, 13312 -> 4108, 14336 ->
+# 4130, 16384 -> 4134, 22528 (one batch) -> 4174.
+OVERLAP_BATCH_FRAMES = int(os.environ.get("CT_BENCH_OVERLAP", str(51 * 256)))
 METRIC = "audio-sec/sec (RTFx) + decode tokens/s at ragged batch 64; % HBM/MFMA peak"
 
 
