@@ -14,6 +14,10 @@
 // then the wave sum), so a row's bits never depend on how many rows the step
 // has or on the tiling chosen for them.
 //
+// Two fused forms: the residual projection (CT_GV_RESID) adds its sums into
+// the residual rows and leaves per-block LayerNorm statistics, and a GEMM with
+// CtGemv.X normalises those rows itself instead of reading frag activations.
+//
 // Semantics per output: backends/cpu/backend.c:124-182 (y = x W^T + b, ReLU,
 // fmadd), with x = hi + lo exactly representable to 2^-17 relative.
 #include "ct_dev.h"
@@ -29,7 +33,9 @@ constexpr int GV_WAVES = 8;
 // (its own L2) serves one slice and fetches only that slice's activations;
 // column blocks follow (grid y), a QKV launch's dealt head by head over the
 // XCDs (ct_qkv_col) so that head h's blocks run where the attention's head-h
-// workgroups read them.
+// workgroups read them; row groups come last (grid z), and since a launch's
+// K-slices x column blocks are a multiple of 8, every row group of a column
+// block runs on the same XCD and finds its weight tiles in that L2.
 
 // Sum over each 32-lane half of a wavefront, every lane getting the same
 // bits: rotations by 8, 4, 2 and 1 within each 16-lane row (DPP row_ror, no
