@@ -309,7 +309,7 @@ extern "C" int ctk_gemv_sizeof(void) { return (int)sizeof(CtGemv); }
 extern "C" int ctk_warmset_sizeof(void) { return (int)sizeof(CtWarmSet); }
 
 extern "C" int ctk_gemv_ksplit(int N, int K) {
-    if (N <= DEC_D && K == DEC_D) return 4;       // 256-column slices, one K-step per wave
+    if (N <= DEC_D && K == DEC_D) return 2;       // 512-column slices, two K-steps per wave
     if (N <= DEC_D && K == DEC_FF) return 8;      // 512-column slices
     return 1;
 }
