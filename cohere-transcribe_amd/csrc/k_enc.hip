@@ -42,23 +42,29 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
                                                           const int *blk_q0, int ldS,
                                                           uint16_t *Oh, uint16_t *Ol) {
     extern __shared__ float S[];      // [RQ][ldS]
+    // Dispatch order: workgroup L = x + y * gridDim.x runs on XCD L mod 8, so
+    // L is taken as (block L / 8, head L mod 8): every block of head h runs on
+    // XCD h, in block order, and a clip-head's consecutive query blocks share
+    // that XCD's L2 for its K, P and V rows.
+    const int lin = blockIdx.x + blockIdx.y * gridDim.x;
+    const int bi = lin / ENC_H, h = lin % ENC_H;
     int T, q0;
     long off = 0;
     if (PACKED) {
-        const int sq = blk_seq[blockIdx.x];
-        q0 = blk_q0[blockIdx.x];
+        const int sq = blk_seq[bi];
+        q0 = blk_q0[bi];
         T = seq_T[sq];
         off = seq_off[sq];
         P += (long)(T_max - T) * ENC_D;     // this clip's window of the T_max table
     } else {
         T = T_arg;
-        q0 = blockIdx.x * RQ;
+        q0 = bi * RQ;
     }
     Q += off * ENC_D; K += off * ENC_D; V += off * ENC_D;
     // the output goes to O, or split hi/lo to the planes Oh/Ol
     if (Oh) { Oh += off * ENC_D; Ol += off * ENC_D; }
     else O += off * ENC_D;
-    const int h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lk = lane >> 4;
     const int nq = min(RQ, T - q0);
     const long hc = (long)h * ENC_DK;
