@@ -195,6 +195,89 @@ def attention_roofline(hip, model, ev, reps=20, step_reps=0):
     }, micro
 
 
+def stream_rows(samples, limits, n_slots, n_prompt, seed):
+    """Self and cross lengths of the rows of one decode step of the stream:
+    n_slots slots each holding a random request of the stream part-way
+    through its decode (the 10 prompt ids fed, U[0, limit) tokens generated),
+    and n_prompt spare rows each feeding a prompt id (position U[1, 10]) of a
+    random request.  Returns (S, T_enc): keys before this step's append, and
+    encoder frames."""
+    rng = np.random.default_rng(seed)
+    T_all = np.asarray([cb.t_enc(cb.t_mel(int(n))) for n in samples], np.int64)
+    r = rng.integers(0, len(samples), n_slots + n_prompt)
+    S = np.empty(n_slots + n_prompt, np.int64)
+    S[:n_slots] = len(cb.PROMPT) + rng.integers(0, limits[r[:n_slots]])
+    S[n_slots:] = rng.integers(1, len(cb.PROMPT) + 1, n_prompt)
+    return S, T_all[r]
+
+
+def decode_b64(model, ev, samples, limits, reps=20):
+    """The decode step at the stream's shape (64 slots, 16 spare prompt
+    rows, bf16 K/V, lengths drawn from the stream's requests):
+      attention_b64    the 16 decode-attention launches of a step over the
+                       64 slots' rows plus 16 prompt rows (80 items, the
+                       widest step of the stream), algorithmic K+V bytes per
+                       launch / average launch time;
+      decode_step_b64  whole decode steps as the stream launches them (the
+                       captured wide-step graph, spare rows idle) over the
+                       64 slots: weight bytes + K/V bytes per step / step
+                       time, against 8 TB/s."""
+    smax = len(cb.PROMPT) + 256 + 64           # lengths up to 266 plus the timed steps
+    S, T = stream_rows(samples, limits, 64, 16, seed=21)
+    eng = cb.Engine(model, slots=80, max_requests=80, max_frames=376, kv_bf16=True, max_tokens=smax)
+    try:
+        eng.bench_fill(S, T, seed=9)
+        eng.step()                             # lengths now S + 1
+        s = eng.stream()
+        eng.attention_only()
+        a, b = ev.event(), ev.event()
+        ev.record(a, s)
+        for _ in range(reps):
+            eng.attention_only()
+        ev.record(b, s)
+        att_us = ev.ms(a, b) * 1e3 / (reps * 16)
+    finally:
+        eng.close()
+    att_bytes = float(np.sum(2 * (S + 1 + T) * cb.DEC_D * 2))      # K+V of one layer's items
+    att_gbs = att_bytes / (att_us * 1e-6) / 1e9
+    attention = {"bound": "hbm", "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                 "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                 "kernel": "attn_kernel<true, true> (decode self + cross attention, bf16 KV)",
+                 "avg_launch_us": round(att_us, 3), "bytes_per_launch": int(att_bytes),
+                 "workload": "80 items = 64 slots (S = 10 + U[0, limit) of a random stream request) "
+                             "+ 16 prompt rows (S ~ U[1,10]), T_enc of random stream requests "
+                             f"(mean S {np.mean(S + 1):.1f}, mean T_enc {np.mean(T):.1f}), bf16 KV, "
+                             "8 layers x (self, cross)"}
+    S, T = S[:64], T[:64]
+    warm = 3
+    eng = cb.Engine(model, slots=64, max_requests=64, max_frames=376, kv_bf16=True, max_tokens=smax,
+                    prefill_rows=16)
+    try:
+        eng.bench_fill(S, T, seed=9)
+        s = eng.stream()
+        eng.bench_steps(warm)
+        a, b = ev.event(), ev.event()
+        ev.record(a, s)
+        eng.bench_steps(reps)
+        ev.record(b, s)
+        step_us = ev.ms(a, b) * 1e3 / reps
+    finally:
+        eng.close()
+    w_bytes = float(sum(N * K * 2 for N, K in DEC_GEMMS))
+    # step i (0-based, counting the warm steps) attends over S + 1 + i self keys
+    s_mean = np.mean(S) + 1 + warm + (reps - 1) / 2.0
+    kv_bytes = cb.DEC_N * float(np.sum(2 * (s_mean + T) * cb.DEC_D * 2))
+    gbs = (w_bytes + kv_bytes) / (step_us * 1e-6) / 1e9
+    step = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "whole decode step (captured graph of the wide step)",
+            "step_us": round(step_us, 2), "bytes_per_step": int(w_bytes + kv_bytes),
+            "weight_bytes": int(w_bytes), "kv_bytes": int(kv_bytes),
+            "workload": "64 slots (S = 10 + U[0, limit) of a random stream request, T_enc of that "
+                        "request), 16 spare prompt rows idle, bf16 KV"}
+    return attention, step
+
+
 DEC_GEMMS = ([(3 * cb.DEC_D, cb.DEC_D), (cb.DEC_D, cb.DEC_D), (cb.DEC_D, cb.DEC_D), (cb.DEC_D, cb.DEC_D),
               (cb.DEC_FF, cb.DEC_D), (cb.DEC_D, cb.DEC_FF)] * cb.DEC_N + [(cb.VOCAB, cb.DEC_D)])
 
@@ -379,7 +462,9 @@ def cpu_baseline(samples, limits, procs=None):
     where the reference library is not built."""
     global _CPU_MODEL
     import multiprocessing as mp
-    procs = procs or min(16, len(os.sched_getaffinity(0)))
+    affine = len(os.sched_getaffinity(0))
+    # at most 16 processes: a one-GPU share of the host's cores
+    procs = procs or min(16, affine)
     audio = float(np.sum(samples)) / cb.SR
     T_enc = np.asarray([cb.t_enc(cb.t_mel(int(n))) for n in samples], np.float64)
     rows = float(np.sum(limits)) + len(cb.PROMPT) * len(limits)
@@ -387,25 +472,35 @@ def cpu_baseline(samples, limits, procs=None):
         return cpu_baseline_port(samples, limits)
     _CPU_MODEL = cb.SynthModel(seed=1234, variant=0)
     job = ("sample", CPU_LAYER_T, 1, CPU_DEC_T, CPU_DEC_S0, CPU_DEC_STEPS)
+
+    def rate(res):
+        t_layer = float(np.mean([r[0] for r in res]))
+        t_step = float(np.mean([r[1] for r in res])) / CPU_DEC_STEPS
+        per_frame = t_layer * cb.ENC_N / CPU_LAYER_T          # s of one process per encoder frame
+        return audio / (float(np.sum(T_enc)) * per_frame + rows * t_step), t_layer, t_step
+
+    # one process alone (the 1-thread figure), then one per core at once
+    with mp.get_context("fork").Pool(1) as pool:
+        alone, _, _ = rate(pool.map(_ref_worker, [job]))
     t0 = time.perf_counter()
     with mp.get_context("fork").Pool(procs) as pool:
         res = pool.map(_ref_worker, [job] * procs)
     wall = time.perf_counter() - t0
     _CPU_MODEL = None
-    t_layer = float(np.mean([r[0] for r in res]))
-    t_step = float(np.mean([r[1] for r in res])) / CPU_DEC_STEPS
-    per_frame = t_layer * cb.ENC_N / CPU_LAYER_T          # s of one process per encoder frame
-    t_proc = float(np.sum(T_enc)) * per_frame + rows * t_step
-    per_proc = audio / t_proc
+    per_proc, t_layer, t_step = rate(res)
     return {"value": round(per_proc * procs, 4), "unit": "audio-sec/sec", "cores": procs,
-            "kind": "reference",
+            "kind": "reference", "one_thread_value": round(alone, 5),
+            "nproc": os.cpu_count(), "affinity_cores": affine,
             "sample": f"{procs} processes at once, one per core (the reference's thread-per-device "
                       f"pool), each running the reference's model.h on its CPU backend: one "
                       f"Conformer layer over {CPU_LAYER_T} frames ({t_layer:.2f} s) and "
                       f"{CPU_DEC_STEPS} decode steps at S={CPU_DEC_S0}, T_enc={CPU_DEC_T} "
                       f"({t_step:.3f} s/step); extrapolated to the stream's {audio:.0f} audio-s "
                       f"({int(np.sum(T_enc))} encoder frames) and {int(rows)} token rows: "
-                      f"{per_proc:.4f} audio-s/s per process; {wall:.1f} s wall",
+                      f"{per_proc:.4f} audio-s/s per process; {wall:.1f} s wall; one process "
+                      f"alone {alone:.4f} audio-s/s (one_thread_value). {procs} of the "
+                      f"{affine} cores this process may run on (nproc {os.cpu_count()}): a "
+                      f"one-GPU share of the host",
             "cpu_model": cpu_model_name(), "extrapolated": True}
 
 
@@ -497,12 +592,15 @@ def _ref_clip(job):
     return time.perf_counter() - t0
 
 
-def measure_rooflines(hip, model, ev, ffn_bf16, step_reps=5):
+def measure_rooflines(hip, model, ev, ffn_bf16, samples, limits, step_reps=5):
     """Per-kernel rooflines; encoder_gemm is the FFN GEMM in the stream's
     precision mode, encoder_gemm_split the fp32-accurate form beside it
-    when the stream runs the single-pass one."""
+    when the stream runs the single-pass one; attention_b64 and
+    decode_step_b64 at the stream's own step shape."""
     att, micro = attention_roofline(hip, model, ev, step_reps=step_reps)
-    roofs = {"attention": att, "decode_gemm": decode_gemm_roofline(model, ev),
+    att64, step64 = decode_b64(model, ev, samples, limits)
+    roofs = {"attention": att, "attention_b64": att64, "decode_step_b64": step64,
+             "decode_gemm": decode_gemm_roofline(model, ev),
              "encoder_gemm": encoder_gemm_roofline(model, ev, ffn_bf16)}
     if ffn_bf16:
         roofs["encoder_gemm_split"] = encoder_gemm_roofline(model, ev, 0)
@@ -559,7 +657,7 @@ def main():
     ev = cb.HipEvents()
 
     if args.roofline_only:
-        roofs, micro = measure_rooflines(hip, model, ev, args.enc_ffn_bf16, step_reps=0)
+        roofs, micro = measure_rooflines(hip, model, ev, args.enc_ffn_bf16, samples, limits, step_reps=0)
         print(json.dumps({"rooflines": roofs, "decode_microbench": micro}))
         return
 
@@ -598,8 +696,25 @@ def main():
         dec_tps = gen_tokens / (float(np.sum(dec_times)) / args.steps)
     eng.close()
 
+    # the same stream with the other encoder FFN precision (one warm and one
+    # timed pass on an engine of its own), so the precision trade is visible
+    other = None
+    if not args.no_rooflines:
+        eng2 = cb.Engine(model, slots=args.slots, max_requests=args.requests, max_frames=376,
+                         kv_bf16=True, max_tokens=len(cb.PROMPT) + 256, prefill_rows=args.prefill_rows,
+                         admit_order=args.admit_order, enc_ffn_bf16=1 - args.enc_ffn_bf16)
+        try:
+            run_stream(hip, eng2, ev, dev_pcm, offs, samples, limits)
+            t2, _, st2 = run_stream(hip, eng2, ev, dev_pcm, offs, samples, limits)
+            if [len(eng2.tokens(r)) for r in range(len(limits))] != [int(x) for x in limits]:
+                raise RuntimeError("a request did not produce its forced number of tokens")
+        finally:
+            eng2.close()
+        other = {"encoder_ffn": "hi+lo split" if args.enc_ffn_bf16 else "single-pass bf16",
+                 "value": round(audio / t2, 2), "unit": "audio-sec/sec", "ms_per_pass": round(t2 * 1e3, 2),
+                 "decode_steps": int(st2), "passes": 1, "warmup": 1}
     roofs, micro = ({}, {}) if args.no_rooflines else measure_rooflines(hip, model, ev,
-                                                                         args.enc_ffn_bf16)
+                                                                         args.enc_ffn_bf16, samples, limits)
     configs = None if args.no_rooflines else config_latency(hip, model, ev, args.enc_ffn_bf16)
 
     out = {
@@ -620,6 +735,7 @@ def main():
         "decode_steps": int(np.mean(steps)),
         "roofline": dict(roofs[DOMINANT], name=DOMINANT) if roofs else None, "rooflines": roofs,
         "decode_microbench": micro,
+        "stream_other_ffn_precision": other,
         "config_runs": configs,
         "cpu_baseline": cpu,
     }

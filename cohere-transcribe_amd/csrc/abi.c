@@ -180,6 +180,7 @@ void backend_destroy(void) {
 /* Memory                                                              */
 /* ------------------------------------------------------------------ */
 float *backend_arena_alloc(size_t floats) {
+    if (floats > ((size_t)1 << 40)) CT_FATAL("backend_arena_alloc: request above 2^40 floats");
     require_init();
     const size_t need = (floats ? floats : 1) * sizeof(float);
     if (ct_t.arena) graphs_drop();
@@ -375,8 +376,8 @@ void backend_sdp_attn(float *out, const float *q, const float *k, const float *v
 void backend_embed(float *h, const int *tokens, int S, int pos_start,
                    const uint16_t *etw, const uint16_t *epw,
                    const uint16_t *elnw, const uint16_t *elnb) {
+    if (S < 0 || S > MAX_SEQ) CT_FATAL("embed: S outside [0, MAX_SEQ]");
     require_init();
-    if (S > MAX_SEQ) CT_FATAL("embed: S exceeds MAX_SEQ");
     /* Inside a captured region the tokens must already be staged
      * (backend_upload_tokens, model.h:466); outside, stage them here. */
     if (!capturing() && tokens) {
@@ -400,8 +401,8 @@ void backend_lm_head(float *logits_out, const float *last, const uint16_t *etw, 
 /* Graphs                                                              */
 /* ------------------------------------------------------------------ */
 void backend_upload_tokens(const int *host_tokens, int S) {
+    if (S < 0 || S > MAX_SEQ) CT_FATAL("upload_tokens: S outside [0, MAX_SEQ]");
     require_init();
-    if (S > MAX_SEQ) CT_FATAL("upload_tokens: S exceeds MAX_SEQ");
     put_ints(ct_t.d_tokens, host_tokens, S, 4);
     CHK(hipStreamSynchronize(ct_t.stream));
 }
@@ -503,8 +504,8 @@ static void check_batch(int B) {
 void backend_embed_decode_batch(float *h, const int *tokens, const int *S_dev, const int *active,
                                 int B, const uint16_t *etw, const uint16_t *epw,
                                 const uint16_t *elnw, const uint16_t *elnb) {
-    require_init();
     check_batch(B);
+    require_init();
     put_ints(ct_t.d_out, tokens, B, 0);
     put_ints(ct_t.d_S_batch, S_dev, B, 1);
     put_ints(ct_t.d_active, active, B, 2);
@@ -515,8 +516,8 @@ void backend_embed_decode_batch(float *h, const int *tokens, const int *S_dev, c
 
 void backend_lm_head_batch(float *logits, const float *h, const uint16_t *etw, const uint16_t *hdb,
                            const int *active, int B) {
-    require_init();
     check_batch(B);
+    require_init();
     put_ints(ct_t.d_active, active, B, 2);
     CtGemm g;
     memset(&g, 0, sizeof g);
@@ -528,8 +529,8 @@ void backend_lm_head_batch(float *logits, const float *h, const uint16_t *etw, c
 }
 
 void backend_argmax_batch(int *out, const float *logits, const int *active, int B) {
-    require_init();
     check_batch(B);
+    require_init();
     put_ints(ct_t.d_active, active, B, 2);
     ctk_argmax(ct_t.d_out, logits, B, VOCAB, ct_t.d_active, ct_t.stream);
     int *res = ct_t.h_stage + 3 * CT_MAX_BATCH;
@@ -540,8 +541,8 @@ void backend_argmax_batch(int *out, const float *logits, const int *active, int 
 }
 
 void backend_upload_T_enc(const int *T_enc, int B) {
-    require_init();
     check_batch(B);
+    require_init();
     put_ints(ct_t.d_T_enc, T_enc, B, 3);
     CHK(hipStreamSynchronize(ct_t.stream));
 }
@@ -549,8 +550,8 @@ void backend_upload_T_enc(const int *T_enc, int B) {
 void backend_linear_to_kvcache_batch(float *cache, const float *x, const uint16_t *W,
                                      const uint16_t *b, int B, int cache_seq_stride,
                                      int in_d, int out_d) {
-    require_init();
     check_batch(B);
+    require_init();
     CtGemm g;
     memset(&g, 0, sizeof g);
     g.A = x; g.lda = in_d; g.W = CT_W(W); g.bias = CT_W(b);
@@ -561,8 +562,8 @@ void backend_linear_to_kvcache_batch(float *cache, const float *x, const uint16_
 
 static void batch_attn(float *out, const float *Q, const float *K, const float *V,
                        int T_k_stride, int B, const int *lens) {
-    require_init();
     check_batch(B);
+    require_init();
     CtAttn a;
     attn_common(&a, out, Q);
     a.K = K; a.V = V; a.kv_sb = (long)T_k_stride * DEC_D;

@@ -272,6 +272,15 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
      * room for the retirements of 8 steps over all slots 4 times over (the
      * host reads the retirement ring at least every ring / 4 of them) */
     int ring = 1024;
+    {
+        /* HIPB_RING_MIN (a power of two >= 16): a smaller lower bound, so that
+         * tests reach the ring's wraparound with few requests */
+        const char *rmin = getenv("HIPB_RING_MIN");
+        if (rmin && rmin[0]) {
+            ring = atoi(rmin);
+            if (ring < 16 || (ring & (ring - 1))) CT_FATAL("hipb_create: HIPB_RING_MIN must be a power of two >= 16");
+        }
+    }
     while (ring < 4 * R || ring < 32 * S) ring <<= 1;
     e->ring = ring;
     d->ring_mask = ring - 1;
@@ -1207,30 +1216,20 @@ void hipb_encode(HipbEngine *e, int max_batch_frames) {
  * layout) for the out-projection.  The query is q (self) or the Q
  * projection's K-slice partials plus bias (cross). */
 /* Decode GEMMs read the tiled weight copies (one contiguous 1 KB per
- * wavefront load); CT_ENG_WTILE=0 builds the row-major reads instead. */
-#ifndef CT_ENG_WTILE
-#define CT_ENG_WTILE 1
-#endif
-#define WT(tiled, rowmajor) (CT_ENG_WTILE ? (tiled) : (rowmajor))
-
-/* Launches that read the next decode GEMMs' weight tiles ahead into the L2
- * their workgroups read from (CT_WARM_ROWS read-ahead workgroups per XCD):
- * the LayerNorm before each layer's QKV projection reads that projection's;
- * the self attention the out- and cross-query projections'; the cross
- * attention the FFN's.  CT_WARM=0 turns it off. */
-#ifndef CT_WARM
-#define CT_WARM 1
-#endif
-#ifndef CT_WARM_ROWS
+ * wavefront load).  Launches that read the next decode GEMMs' weight tiles
+ * ahead into the L2 their workgroups read from (CT_WARM_ROWS read-ahead
+ * workgroups per XCD): the LayerNorm before each layer's QKV projection
+ * reads that projection's; the self attention the out- and cross-query
+ * projections'; the cross attention the FFN's.  HIPB_READ_AHEAD=0 at engine
+ * creation turns it off. */
 #define CT_WARM_ROWS 32
-#endif
 /* Queues the weight tiles of the launch gv() makes for (Wd, N, K, out) for
  * the next attention or LayerNorm launch to read ahead. */
 static void warm_add(HipbEngine *e, const uint16_t *Wd, int N, int K, int out) {
     if (e->warm.n >= 4) return;
     CtGemv g;
     memset(&g, 0, sizeof g);
-    g.W = Wd; g.wtile = CT_ENG_WTILE; g.M = e->M; g.N = N; g.K = K; g.out = out;
+    g.W = Wd; g.wtile = 1; g.M = e->M; g.N = N; g.K = K; g.out = out;
     g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, K) : 1;
     ctk_gemv_warm(&g, &e->warm.t[e->warm.n++]);
 }
@@ -1318,7 +1317,7 @@ static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint1
                int out, int relu, float *Y, long ldy, uint16_t *F) {
     CtGemv g;
     memset(&g, 0, sizeof g);
-    g.A = A; g.W = Wd; g.bias = bd; g.wtile = CT_ENG_WTILE;
+    g.A = A; g.W = Wd; g.bias = bd; g.wtile = 1;
     g.M = e->M; g.N = N; g.K = K;
     g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
     g.out = out; g.relu = relu;
@@ -1334,7 +1333,7 @@ static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint1
 static void gv_resid(HipbEngine *e, const uint16_t *Wd, const uint16_t *bd) {
     CtGemv g;
     memset(&g, 0, sizeof g);
-    g.A = e->attf; g.W = Wd; g.bias = bd; g.wtile = CT_ENG_WTILE;
+    g.A = e->attf; g.W = Wd; g.bias = bd; g.wtile = 1;
     g.M = e->M; g.N = DEC_D; g.K = DEC_D; g.ksplit = 1;
     g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
     g.out = CT_GV_RESID;
@@ -1349,7 +1348,7 @@ static void gv_ln(HipbEngine *e, const uint16_t *lnw, const uint16_t *lnb, const
     CtGemv g;
     memset(&g, 0, sizeof g);
     g.X = e->h; g.ldx = DEC_D; g.lnstat = e->lnstat; g.lnw = lnw; g.lnb = lnb;
-    g.W = Wd; g.bias = bd; g.wtile = CT_ENG_WTILE;
+    g.W = Wd; g.bias = bd; g.wtile = 1;
     g.M = e->M; g.N = N; g.K = DEC_D;
     g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
     g.out = out; g.relu = relu;
@@ -1376,11 +1375,9 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         const DLayer *L = &W->dec[l];
         void *ks, *vs;
         self_kv(e, l, &ks, &vs);
-        const uint16_t *w_qkv = WT(e->wt_qkv[l], e->wqkv + (size_t)3 * l * DEC_D * DEC_D);
-        const uint16_t *w_o = WT(e->wt_o[l], DW(L->sa_ow)), *w_cq = WT(e->wt_cq[l], DW(L->ca_qw));
-        const uint16_t *w_co = WT(e->wt_co[l], DW(L->ca_ow)), *w_f1 = WT(e->wt_f1[l], DW(L->ffn_w1));
-        const uint16_t *w_f2 = WT(e->wt_f2[l], DW(L->ffn_w2));
-        if (full && CT_WARM && e->read_ahead) warm_add(e, w_qkv, 3 * DEC_D, DEC_D, CT_GV_QKV);
+        const uint16_t *w_qkv = e->wt_qkv[l], *w_o = e->wt_o[l], *w_cq = e->wt_cq[l];
+        const uint16_t *w_co = e->wt_co[l], *w_f1 = e->wt_f1[l], *w_f2 = e->wt_f2[l];
+        if (full && e->read_ahead) warm_add(e, w_qkv, 3 * DEC_D, DEC_D, CT_GV_QKV);
         if (full && l == 0) {
             /* the embedding LayerNorm and this one in one launch */
             CtWarmSet ws;
@@ -1393,7 +1390,7 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         CtGemv g;
         memset(&g, 0, sizeof g);
         g.A = e->lnf;
-        g.W = w_qkv; g.wtile = CT_ENG_WTILE;
+        g.W = w_qkv; g.wtile = 1;
         g.bias = e->bqkv + (size_t)3 * l * DEC_D;
         g.M = B; g.N = 3 * DEC_D; g.K = DEC_D; g.ksplit = 1; g.out = CT_GV_QKV;
         g.m_active = B > e->d.slots ? e->d.q + 6 : NULL;
@@ -1401,15 +1398,15 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)e->d.kv_rows * DEC_DK;
         g.kv_bf16 = e->esz == 2;
         launch_gemv(e, &g);
-        if (full && CT_WARM && e->read_ahead) warm_add(e, w_o, DEC_D, DEC_D, CT_GV_RESID);
-        if (full && CT_WARM && e->read_ahead) warm_add(e, w_cq, DEC_D, DEC_D, CT_GV_PARTIAL);
+        if (full && e->read_ahead) warm_add(e, w_o, DEC_D, DEC_D, CT_GV_RESID);
+        if (full && e->read_ahead) warm_add(e, w_cq, DEC_D, DEC_D, CT_GV_PARTIAL);
         if (full) step_attention(e, l, 0);
         /* h += self-attention out-projection, then the cross-attention query
          * from LayerNorm(h) normalised inside its GEMM */
         gv_resid(e, w_o, DW(L->sa_ob));
         gv_ln(e, DW(L->ca_lnw), DW(L->ca_lnb), w_cq, NULL, DEC_D, CT_GV_PARTIAL, 0, NULL);
-        if (full && CT_WARM && e->read_ahead) warm_add(e, w_f1, DEC_FF, DEC_D, CT_GV_FRAG);
-        if (full && CT_WARM && e->read_ahead) warm_add(e, w_f2, DEC_D, DEC_FF, CT_GV_PARTIAL);
+        if (full && e->read_ahead) warm_add(e, w_f1, DEC_FF, DEC_D, CT_GV_FRAG);
+        if (full && e->read_ahead) warm_add(e, w_f2, DEC_D, DEC_FF, CT_GV_PARTIAL);
         if (full) step_attention(e, l, 1);
         /* the FFN's LayerNorm stays a launch of its own: normalising inside the
          * FFN-up GEMM would repeat each row's LayerNorm over the full K in all
@@ -1424,7 +1421,7 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
     if (full) ln_frag(e, np, pb, DW(W->dlnw), DW(W->dlnb));
     /* logits only for the slots' own rows */
     e->M = e->d.slots;
-    gv(e, e->lnf, WT(e->wt_lm, DW(W->etw)), DW(W->hdb), VOCAB, DEC_D, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);
+    gv(e, e->lnf, e->wt_lm, DW(W->hdb), VOCAB, DEC_D, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);
     if (full) ctk_eng_end(&e->d, e->logits, s);
     e->M = e->d.slots;
 }
@@ -1488,8 +1485,9 @@ static void launch_step(HipbEngine *e, int wide) {
 }
 
 void hipb_bench_steps(HipbEngine *e, int n) {
-    ensure_graph(e, 0);
-    for (int i = 0; i < n; i++) launch_step(e, 0);
+    const int wide = want_wide(e);
+    ensure_graph(e, wide);
+    for (int i = 0; i < n; i++) launch_step(e, wide);
 }
 
 long hipb_run(HipbEngine *e, int chunk) {
@@ -1655,6 +1653,9 @@ static int req_results(HipbEngine *e, int req, void *out, int cap, int what) {
         if (n > 0) memcpy(out, what ? (const void *)q->score : (const void *)q->out, (size_t)n * 4);
         return n;
     }
+    /* fields not uploaded yet: the ring slot may still hold the results of
+     * request req - ring */
+    if (req >= e->meta_lo) return 0;
     const size_t slot = (size_t)(req & (e->ring - 1));
     ECHK(hipStreamSynchronize(e->s));
     ECHK(hipMemcpy(&n, e->d.req_ngen + slot, sizeof(int), hipMemcpyDeviceToHost));
@@ -1685,9 +1686,12 @@ void hipb_logits(HipbEngine *e, int slot, float *out) {
 }
 
 void hipb_enc_out(HipbEngine *e, int req, float *out) {
-    if (req < 0 || req >= e->n_enc) CT_FATAL("hipb_enc_out: request not encoded");
-    const int ent = e->req[req].entry;
-    if (ent < 0 || e->ent_owner[ent] != req)
+    if (req < 0 || req >= e->n_req) CT_FATAL("hipb_enc_out: no such request");
+    pthread_mutex_lock(&e->mu);
+    const int ent = e->req[req].entry, owner = ent >= 0 ? e->ent_owner[ent] : -1;
+    pthread_mutex_unlock(&e->mu);
+    if (ent < 0) CT_FATAL("hipb_enc_out: request not encoded");
+    if (owner != req)
         CT_FATAL("hipb_enc_out: the request's encoder entry was recycled for a later request");
     ECHK(hipStreamSynchronize(e->s));
     ECHK(hipMemcpy(out, e->enc_pool + (size_t)ent * e->d.tmax * DEC_D,
@@ -1753,7 +1757,6 @@ void hipb_bench_fill(HipbEngine *e, const int *S, const int *T_enc, uint64_t see
 void hipb_bench_decode_gemms(HipbEngine *e) { step_kernels(e, 0, 0); }
 
 void hipb_bench_read_floor(HipbEngine *e) {
-    if (!CT_ENG_WTILE) CT_FATAL("hipb_bench_read_floor: needs the tiled decode weights");
     const long cap = 256L * ((e->d.rows + 15) / 16);     /* <= 256 workgroups per 16 rows */
     if (e->floor_cap < cap) {
         if (e->floor_sink) ECHK(hipFree(e->floor_sink));

@@ -24,18 +24,13 @@
 namespace {
 
 constexpr int CT_ATTN_QPARTS = 4;   // most query partial slices a launch may pass
-// lanes per key (16: 8 head dims a lane, 8: 16 a lane)
-#ifndef CT_ATTN_LPK
-#define CT_ATTN_LPK 16
-#endif
+// lanes per key: 16, each owning 8 of the 128 head dimensions (one 16-byte
+// bf16 piece); 8 lanes per key (16 dimensions a lane) measured slower
+constexpr int CT_ATTN_LPK = 16;
 // threads per workgroup (NT / LPK lane groups)
-#ifndef CT_ATTN_NT
-#define CT_ATTN_NT 256
-#endif
+constexpr int CT_ATTN_NT = 256;
 // keys per lane group per trip (bf16; fp32 caches use 4)
-#ifndef CT_ATTN_KPI
-#define CT_ATTN_KPI 2
-#endif
+constexpr int CT_ATTN_KPI = 2;
 // rows per item (CtAttn.kv_rows) from which the first key trip (of bf16
 // caches) is issued ahead of the item's length: one trip's keys
 constexpr int CT_ATTN_EARLY_ROWS = CT_ATTN_NT / CT_ATTN_LPK * CT_ATTN_KPI;
@@ -78,14 +73,13 @@ __device__ __forceinline__ void store_out(const CtAttn &a, int bq, int col, long
 constexpr float LOG2E = 1.4426950408889634f;
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Sum over aligned groups of LPK lanes (16 or 8), every lane gets the result.
-template <int LPK>
-__device__ __forceinline__ float group_sum(float v) {
+// Sum over aligned groups of 16 lanes (one DPP row), every lane gets the
+// result.
+__device__ __forceinline__ float group_sum16(float v) {
     v += dpp_row<0xB1>(v);
     v += dpp_row<0x4E>(v);
     v += dpp_row<0x141>(v);
-    if (LPK == 16) v += dpp_row<0x140>(v);
-    return v;
+    return v + dpp_row<0x140>(v);
 }
 
 // LPK lanes per key: lane s of a group owns head dims [s*DPL, s*DPL + DPL),
@@ -93,6 +87,7 @@ __device__ __forceinline__ float group_sum(float v) {
 // stream keys g, g + NG, ... (KPI of them per trip, loads first).
 template <bool BF16, bool VEC, int LPK, bool MASK, int NT, bool EARLY>
 __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
+    static_assert(LPK == 16, "one 16-lane DPP row per key");
     constexpr int DPL = DEC_DK / LPK, NV = DPL / 8, NG = NT / LPK;
     if ((int)blockIdx.y >= a.B * a.T_q) {
         // read-ahead rows: launch position h + H * row runs on XCD h (H % 8 == 0)
@@ -225,7 +220,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
 #pragma unroll
         for (int j = 0; j < KPI; j++) {
             const int k = k0 + NG * j;
-            sc[j] = k < ke ? group_sum<LPK>(sc[j]) * scale2 + (MASK ? mrow[k] * LOG2E : 0.0f) : -INFINITY;
+            sc[j] = k < ke ? group_sum16(sc[j]) * scale2 + (MASK ? mrow[k] * LOG2E : 0.0f) : -INFINITY;
         }
         float mx = sc[0];
 #pragma unroll

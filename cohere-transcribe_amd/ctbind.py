@@ -13,7 +13,9 @@ import os
 import numpy as np
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-HOST_LIB = os.path.join(PKG_DIR, "libct_host.so")
+# CT_HOST_LIB / CT_CHUNK_LIB name sanitizer builds of the host C to load
+# instead (tests/test_sanitize.py)
+HOST_LIB = os.environ.get("CT_HOST_LIB") or os.path.join(PKG_DIR, "libct_host.so")
 HIP_LIB = os.path.join(PKG_DIR, "libct_hip.so")
 
 # Model constants (include/model_types.h).
@@ -379,7 +381,11 @@ _ENGINE_SIGS.update({
 def chunk_bounds(samples, silence_db=float("nan"), silence_dur=0.2, target_sec=20.0):
     """Chunk boundaries of a long recording, [(start, end), ...] in samples
     (hipb_chunk_bounds, host code of libct_hip.so)."""
-    lib = engine_lib()
+    if os.environ.get("CT_CHUNK_LIB"):
+        lib = C.CDLL(os.environ["CT_CHUNK_LIB"])
+        lib.hipb_chunk_bounds.argtypes, lib.hipb_chunk_bounds.restype = _ENGINE_SIGS["hipb_chunk_bounds"]
+    else:
+        lib = engine_lib()
     samples = np.ascontiguousarray(samples, np.float32)
     cap = len(samples) // HOP_LEN + 1
     b = np.zeros(2 * cap, np.int32)

@@ -42,7 +42,10 @@ typedef struct {
                            encoded and recycled after it finishes, so any
                            number of requests flows through.  Up to
                            max(4 x max_requests, 32 x slots, 1024) may be
-                           outstanding (submitted, not finished)          */
+                           outstanding (submitted, not finished).  The host
+                           keeps each request's record and results (8 bytes
+                           a token) until hipb_reset, which a long-running
+                           serving loop calls between batches of requests */
     int max_frames;     /* largest encoder length a request may have (<= 2048) */
     int kv_bf16;        /* 1: bf16 KV caches, 0: fp32                           */
     int max_tokens;     /* longest prompt + limit of any request (sizes the self
@@ -189,7 +192,9 @@ void hipb_bench_encoder_gemm(HipbEngine *e, int M);
 
 /* Launches n decode steps (graph replays, or eager steps under HIPB_EAGER=1)
  * on the engine's stream without waiting and without checking for finished
- * requests: the step-time benchmark over slots filled by hipb_bench_fill. */
+ * requests: the step-time benchmark over slots filled by hipb_bench_fill.
+ * With spare prompt rows configured these are the wide steps hipb_run
+ * launches (spare rows idle: no slot is feeding a prompt). */
 void hipb_bench_steps(HipbEngine *e, int n);
 /* The engine's HIP stream (hipStream_t), for events and profiling. */
 void *hipb_stream(HipbEngine *e);

@@ -5,6 +5,8 @@ import os
 import re
 import subprocess
 
+import pytest
+
 import ctbind as cb
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -131,3 +133,36 @@ def test_noalloc_variant_rejects_long_clips():
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert r.returncode == 1
     assert "T=377 outside [1, 376]" in r.stderr
+
+
+FATAL_CASES = {
+    # weight pointer translated before the blob was uploaded (abi.c ct_dev_w)
+    "weight_before_upload": ("L.backend_device_ptr(C.c_void_p(4096))",
+                             "weight pointer used before backend_weights_upload_blob"),
+    # S beyond MAX_SEQ (the reference's token buffer size)
+    "embed_long": ("L.backend_embed(None, None, 1025, 0, None, None, None, None)",
+                   "embed: S outside [0, MAX_SEQ]"),
+    "upload_tokens_long": ("L.backend_upload_tokens(None, 1025)", "upload_tokens: S outside [0, MAX_SEQ]"),
+    # batch beyond the 256 slots the batched entry points stage
+    "batch_257": ("L.backend_embed_decode_batch(None, None, None, None, 257, None, None, None, None)",
+                  "batch size outside [0, 256]"),
+    "batch_negative": ("L.backend_argmax_batch(None, None, None, -1)", "batch size outside [0, 256]"),
+    # arena request no device can hold (and whose byte count would overflow)
+    "arena_huge": ("L.backend_arena_alloc(C.c_size_t(1 << 62))", "request above 2^40 floats"),
+}
+
+
+@pytest.mark.parametrize("case", sorted(FATAL_CASES))
+def test_fatal_paths_before_device_work(case):
+    """The backend's error convention is the reference's: print what went
+    wrong and exit(1) (backends/cuda/backend.cu:26-33, backends/cpu/
+    backend.c:43-46).  Argument checks run before any device work, so each
+    of these fires on a host without a GPU: run in a child process, the call
+    exits with status 1 and names the problem on stderr."""
+    import sys
+    call, msg = FATAL_CASES[case]
+    code = f"import ctypes as C; L = C.CDLL({cb.HIP_LIB!r}); {call}; print('returned')"
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1, (r.returncode, r.stdout, r.stderr)
+    assert msg in r.stderr, r.stderr
+    assert "returned" not in r.stdout

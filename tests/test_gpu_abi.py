@@ -297,3 +297,26 @@ def test_encoder_ops_long_T_vs_oracle(hip, kmodel, T):
         e = relerr(dev.get(x), want)
         print(f"case: conformer_conv T={T} layer {layer}: relerr {e:.2e}", flush=True)
         assert e <= TOL, (T, layer, e)
+
+
+@pytest.mark.parametrize("case", ["weight_outside_blob", "arena_beyond_device"])
+def test_fatal_paths_after_init(case):
+    """Fatal exits that need an uploaded blob and an initialised device, in
+    a child process (the reference's convention: print and exit(1),
+    backends/cuda/backend.cu:26-33): a weight pointer past the end of the
+    uploaded blob, and an arena larger than the device's memory (1 TiB: the
+    allocation fails and the backend exits instead of returning NULL).  No
+    kernel is launched in either case."""
+    import sys
+    calls = {"weight_outside_blob": ("L.backend_device_ptr(C.c_void_p(C.addressof(b) + 8192))",
+                                     "weight pointer outside the uploaded blob"),
+             "arena_beyond_device": ("L.backend_arena_alloc(C.c_size_t(1 << 38))", "HIP error")}
+    call, msg = calls[case]
+    code = (f"import ctypes as C; L = C.CDLL({cb.HIP_LIB!r}); b = (C.c_char * 4096)(); "
+            "L.backend_weights_upload_blob(b, C.c_size_t(4096)); L.backend_init(0); "
+            f"print('case {case}', flush=True); {call}; print('returned')")
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert f"case {case}" in r.stdout, r.stderr
+    assert r.returncode == 1, (r.returncode, r.stdout, r.stderr)
+    assert msg in r.stderr, r.stderr
+    assert "returned" not in r.stdout

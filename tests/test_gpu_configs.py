@@ -303,16 +303,17 @@ def test_ragged_batch32_vs_single(hip):
                       f"request {r} ({secs[r]:.1f} s, {limits[r]} tokens) alone vs batch of 32")
 
 
-@pytest.mark.parametrize("admit_order,ffn_bf16,batch_frames", [(0, 0, 6144), (1, 1, 12288)])
+@pytest.mark.parametrize("admit_order,ffn_bf16,batch_frames", [(0, 0, 6144), (1, 1, 13056)])
 def test_stream256_counts_and_samples_alone(hip, admit_order, ffn_bf16, batch_frames):
     """The continuous-batching stream: 256 requests (clips lognormal, median
     6 s, in [1, 30] s; limits U[8, 256]), 64 slots, 16 spare prompt rows,
-    encoding overlapped with decoding in batches of 6144 or 12288 frames.  Every
+    encoding overlapped with decoding in batches of 6144 or 13056 frames.  Every
     request yields exactly its limit; four requests (the longest clip, the
     longest limit, the last submitted, one more) rerun alone give the same
     tokens and chosen-logit bits.  In submission order with the fp32-accurate
-    encoder, and largest token budget first with the single-pass FFN encoder
-    in batches of 12288 frames (the benchmark's settings)."""
+    encoder, and with the benchmark's own settings: largest token budget
+    first, the single-pass FFN encoder, batches of 13056 frames (51 row tiles
+    of 256)."""
     m = model(hip, 2)
     rng = np.random.default_rng(3)
     secs = np.clip(np.exp(rng.normal(np.log(6.0), 0.5, 256)), 1.0, 30.0)

@@ -585,3 +585,53 @@ def test_engine_entry_pool_recycles(hip, hot):
             assert np.array_equal(alone.scores(0).view(np.uint32), runs["process"][3][c].view(np.uint32)), c
         finally:
             alone.close()
+
+
+def test_engine_request_ring_wraps(hip, hot, monkeypatch):
+    """The request ring (per-request device fields indexed by id & mask)
+    wraps around: with HIPB_RING_MIN=16 the ring of a 2-slot engine holds
+    64 requests, and 120 requests flow through it in three waves, so ids
+    64..119 reuse the slots of 0..55, whose results move to the host first.
+    Every request yields its limit; sampled requests (results collected to
+    the host, and still in their slot) give the tokens and chosen-logit bits
+    of the same audio alone; a request submitted but not yet uploaded reports
+    no tokens (its slot still holds request id - 64's)."""
+    monkeypatch.setenv("HIPB_RING_MIN", "16")
+    rng = np.random.default_rng(91)
+    n, wave = 120, 40
+    pcms = [cb.synth_audio(int(rng.integers(2400, 6000)), 7000 + i) for i in range(n)]
+    limits = [int(x) for x in rng.integers(2, 7, n)]
+    kw = dict(slots=2, max_requests=4, max_frames=40, kv_bf16=True,
+              max_tokens=len(cb.PROMPT) + 6, prefill_rows=2)
+    eng = cb.Engine(hot, **kw)
+    try:
+        for w0 in range(0, n, wave):
+            ids = [eng.submit_pcm(p, lim, FLAGS) for p, lim in zip(pcms[w0:w0 + wave], limits[w0:w0 + wave])]
+            assert ids == list(range(w0, w0 + wave))
+            print(f"case: request ring of 64, wave of ids {w0}..{w0 + wave - 1}", flush=True)
+            eng.encode(max_batch_frames=64)
+            eng.run(chunk=2)
+            assert eng.finished() == w0 + wave
+        toks = [eng.tokens(r) for r in range(n)]
+        sample = (3, 50, 60, 70, 119)
+        scores = {r: eng.scores(r) for r in sample}
+        extra = eng.submit_pcm(pcms[0], limits[0], FLAGS)
+        assert extra == n
+        assert len(eng.tokens(extra)) == 0
+        assert np.array_equal(eng.tokens(n - 64), toks[n - 64])
+    finally:
+        eng.close()
+    assert [len(t) for t in toks] == limits
+    assert all(t[-1] == cb.EOS for t in toks)
+    monkeypatch.delenv("HIPB_RING_MIN")
+    for r in sample:
+        alone = cb.Engine(hot, slots=1, max_requests=1, max_frames=40, kv_bf16=True,
+                          max_tokens=len(cb.PROMPT) + 6)
+        try:
+            alone.submit_pcm(pcms[r], limits[r], FLAGS)
+            alone.encode()
+            alone.run(chunk=4)
+            assert np.array_equal(alone.tokens(0), toks[r]), r
+            assert np.array_equal(alone.scores(0).view(np.uint32), scores[r].view(np.uint32)), r
+        finally:
+            alone.close()
