@@ -238,7 +238,8 @@ def decode_b64(model, ev, samples, limits, reps=20):
         att_us = ev.ms(a, b) * 1e3 / (reps * 16)
     finally:
         eng.close()
-    att_bytes = float(np.sum(2 * (S + 1 + T) * cb.DEC_D * 2))      # K+V of one layer's items
+    # K+V bytes per launch: a layer's self (S + 1 keys) and cross (T_enc) launches
+    att_bytes = float(np.sum(2 * (S + 1 + T) * cb.DEC_D * 2)) / 2
     att_gbs = att_bytes / (att_us * 1e-6) / 1e9
     attention = {"bound": "hbm", "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                  "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": None,

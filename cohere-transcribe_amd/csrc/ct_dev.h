@@ -31,6 +31,13 @@ __device__ __forceinline__ float sigmoid_hw(float x) {
     return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
 }
 
+// a * b rounded to fp32 on its own: never contracted into a later add or
+// subtract (hipcc contracts across statements, __fmul_rn included)
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+
 // x = hi + lo + r with hi, lo bf16 and |r| <= 2^-17 |x|: the two-term split
 // that lets bf16 MFMA multiply an fp32 activation by an exact bf16 weight.
 __device__ __forceinline__ void split_bf16(float x, uint16_t &hi, uint16_t &lo) {

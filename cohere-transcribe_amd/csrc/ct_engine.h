@@ -23,7 +23,6 @@ extern "C" {
 #ifndef CT_RANK_MIN_ROWS
 #define CT_RANK_MIN_ROWS 96
 #endif
-#define CT_MAX_KSPLIT 8    /* largest ctk_gemv_ksplit() of a decoder weight */
 /* Spare rows per (slot, head) of the self caches: without them every
  * (slot, head) block starts on the same 256-KB boundary and the workgroups
  * of a step stream from the same memory channels at the same time (16 rows:

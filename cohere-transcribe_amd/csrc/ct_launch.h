@@ -118,16 +118,26 @@ typedef struct {
     const int *m_active;      /* device int or NULL: rows at or past *m_active are
                                  unused this launch (workgroups of only such rows
                                  exit, their row blocks are not computed)           */
-    float *lnstat;            /* CT_GV_RESID output; with X the LayerNorm input      */
-    const float *X;           /* NULL, or A = LayerNorm(X) (K = DEC_D): rows X[m*ldx]
-                                 whose statistics a CT_GV_RESID launch left in lnstat,
-                                 normalised with lnw / lnb (bf16) and split hi/lo in
-                                 registers instead of read from frag A             */
-    long ldx;
-    const uint16_t *lnw, *lnb;
+    float *lnstat;            /* CT_GV_RESID output; with fold_c1 the row statistics */
+    const uint16_t *fold_w;   /* CT_GV_RESID with F: F = frag(h_new * fold_w), the A
+                                 of a GEMM on LayerNorm(h_new) with gain fold_w     */
+    const float *fold_c1, *fold_c2;
+                              /* NULL, or the GEMM's A is frag(h * w) of rows h whose
+                                 statistics a CT_GV_RESID launch left in lnstat, and
+                                 each output is rstd (s - mu c1[n]) + c2[n]: the GEMM
+                                 of LayerNorm(h) (gain w, bias b) plus bias, with
+                                 c1 = W w and c2 = W b + bias (ctk_fold_cols); bias
+                                 is then ignored                                    */
 } CtGemv;
 /* Requires N % 16 == 0 (N % 64 == 0 when N >= 8192), K % (256 * steps) == 0. */
 void ctk_gemv(const CtGemv *g, hipStream_t s);
+/* Column constants of a GEMM on a folded LayerNorm (CtGemv.fold_c1/c2) for a
+ * row-major W[N][K], LayerNorm gain w and bias b (bf16, K entries) and the
+ * GEMM's bias (bf16, N entries, or NULL): c1[n] = sum_k w_k W_nk and c2[n] =
+ * sum_k b_k W_nk + bias_n, each summed in double over k in order and rounded
+ * to fp32 once. */
+void ctk_fold_cols(const uint16_t *W, const uint16_t *w, const uint16_t *b, const uint16_t *bias,
+                   int N, int K, float *c1, float *c2, hipStream_t s);
 /* The GEMM's weight reads alone (tiled weights, same grid as ctk_gemv for
  * g): one value per workgroup to sink (ctk_gemv_read_floor_blocks(g)
  * floats).  A floor for the GEMM's duration, for benchmarking. */
@@ -183,23 +193,24 @@ void ctk_tile_w(const uint16_t *W, uint16_t *Wt, int N, int K, hipStream_t s);
  * only, so every row's result is independent of M). */
 int  ctk_gemv_ksplit(int N, int K);
 
-/* Decoder residual + LayerNorm (D = DEC_D): h[m] += sum_{p<nparts} parts[p][m]
- * + pbias (in that order; skipped when nparts == 0), then frag = LN(h[m]) in
- * frag layout (K = DEC_D). */
-/* The decode step's embedding + first LayerNorm: for active rows r < M,
- * h[r] = LN_e(etw[tokens[r]] + epw[pos_len[r] - 1]) (as ctk_embed_ln); then
- * every row's LN(h[r]) with (w, b) into frag (as ctk_ln_frag with no
- * slices), carrying the read-ahead warm (NULL: none). */
-void ctk_embed_ln_frag(float *h, uint16_t *frag, const int *tokens, const int *pos_len,
-                       const int *active, const uint16_t *etw, const uint16_t *epw,
-                       const uint16_t *elnw, const uint16_t *elnb, const uint16_t *w,
-                       const uint16_t *b, int M, const CtWarmSet *warm, hipStream_t s);
-/* ctk_ln_frag plus the read-ahead warm (NULL or warm->n == 0: none). */
-void ctk_ln_frag_warm(float *h, uint16_t *frag, const float *parts, int nparts,
-                      const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,
-                      const CtWarmSet *warm, hipStream_t s);
-void ctk_ln_frag(float *h, uint16_t *frag, const float *parts, int nparts,
-                 const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M, hipStream_t s);
+/* Residual update after a K-split projection (rows r < M): h[r] += ((parts[0][r]
+ * + parts[1][r]) + ...) + pbias, the nparts slices (1, 2, 4 or 8) M * DEC_D
+ * floats apart; then the folded input of the next GEMM's LayerNorm with gain
+ * w (CtGemv.fold_c1): each 32-column block's (mean, squared deviations) of
+ * h[r] into lnstat[r*32 + b] and frag(h[r] * w); carrying the read-ahead warm
+ * (NULL: none). */
+void ctk_resid_fold(float *h, float *lnstat, uint16_t *frag, const float *parts, int nparts,
+                    const uint16_t *pbias, const uint16_t *w, int M, const CtWarmSet *warm,
+                    hipStream_t s);
+/* The decode step's embedding: for active rows r < M, h[r] = LN_e(etw[tokens[r]]
+ * + epw[pos_len[r] - 1]) (as ctk_embed_ln); then for every row the folded
+ * input of the first layer's LayerNorm with gain w (CtGemv.fold_c1): each
+ * 32-column block's (mean, squared deviations) of h[r] into lnstat[r*32 + b]
+ * and frag(h[r] * w), carrying the read-ahead warm (NULL: none). */
+void ctk_embed_fold(float *h, float *lnstat, uint16_t *frag, const int *tokens, const int *pos_len,
+                    const int *active, const uint16_t *etw, const uint16_t *epw,
+                    const uint16_t *elnw, const uint16_t *elnb, const uint16_t *w, int M,
+                    const CtWarmSet *warm, hipStream_t s);
 
 /* fp32 -> (hi, lo) bf16 pair, the split every GEMM applies to activations. */
 void ctk_split(uint16_t *hi, uint16_t *lo, const float *x, long n, hipStream_t s);
@@ -249,12 +260,6 @@ typedef struct {
     const float *mask;        /* optional additive [T_q][T_k] mask (B == 1)            */
     int   T_q, B, H;
     float scale;
-    /* optional: the query is the sum of q_nparts partial rows q_parts[p][b]
-     * (p-major, q_pstride floats apart) plus q_bias, instead of Q */
-    const float    *q_parts;
-    int             q_nparts;
-    long            q_pstride;
-    const uint16_t *q_bias;
     /* optional: write the output split hi/lo in frag layout (K = H*128),
      * row b*T_q + qi, instead of out */
     uint16_t       *out_frag;

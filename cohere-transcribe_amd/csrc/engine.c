@@ -77,10 +77,15 @@ struct HipbEngine {
     atomic_int n_assigned;     /* requests [0, n_assigned) have entries */
     atomic_int stop;           /* hipb_process ends: the encoder thread quits its wait */
     /* step activations: h residual rows (fp32); lnf/attf/midf the decode
-     * GEMMs' inputs in frag layout; parts K-slice partial sums; lnstat the
-     * rows' LayerNorm statistics per 32-column block, left by the residual
-     * projections for the next GEMM's LayerNorm input */
+     * GEMMs' inputs in frag layout (lnf holds h * w, the input of the next
+     * GEMM with its LayerNorm folded in); parts the FFN down projection's
+     * K-slice partial sums; lnstat the rows' statistics per 32-column block,
+     * left with lnf for that GEMM */
     float *h, *q, *parts, *logits, *lnstat;
+    /* folded LayerNorms: per layer the c1 / c2 column constants of the QKV,
+     * cross-query and FFN-up GEMMs, then the LM head's (ctk_fold_cols) */
+    float *fold;
+    const float *fc_qkv[DEC_N][2], *fc_cq[DEC_N][2], *fc_f1[DEC_N][2], *fc_lm[2];
     int M;                     /* rows of the step being launched */
     /* decode GEMMs whose weight tiles the next attention launch reads ahead
      * into the L2 their workgroups will read from */
@@ -381,6 +386,26 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
         ctk_tile_w(DW(W->etw), p, VOCAB, DEC_D, e->s);
         e->wt_lm = p;
     }
+    {
+        /* column constants of the GEMMs whose LayerNorm is folded in */
+        const size_t per = 2 * (3 * DEC_D + DEC_D + DEC_FF);
+        e->fold = dmalloc((DEC_N * per + 2 * (size_t)VOCAB) * sizeof(float));
+        float *p = e->fold;
+        for (int l = 0; l < DEC_N; l++) {
+            const DLayer *L = &W->dec[l];
+            ctk_fold_cols(e->wqkv + (size_t)3 * l * DEC_D * DEC_D, DW(L->sa_lnw), DW(L->sa_lnb),
+                          e->bqkv + (size_t)3 * l * DEC_D, 3 * DEC_D, DEC_D, p, p + 3 * DEC_D, e->s);
+            e->fc_qkv[l][0] = p; e->fc_qkv[l][1] = p + 3 * DEC_D; p += 6 * DEC_D;
+            ctk_fold_cols(DW(L->ca_qw), DW(L->ca_lnw), DW(L->ca_lnb), DW(L->ca_qb), DEC_D, DEC_D, p,
+                          p + DEC_D, e->s);
+            e->fc_cq[l][0] = p; e->fc_cq[l][1] = p + DEC_D; p += 2 * DEC_D;
+            ctk_fold_cols(DW(L->ffn_w1), DW(L->ffn_lnw), DW(L->ffn_lnb), DW(L->ffn_b1), DEC_FF, DEC_D, p,
+                          p + DEC_FF, e->s);
+            e->fc_f1[l][0] = p; e->fc_f1[l][1] = p + DEC_FF; p += 2 * DEC_FF;
+        }
+        ctk_fold_cols(DW(W->etw), DW(W->dlnw), DW(W->dlnb), DW(W->hdb), VOCAB, DEC_D, p, p + VOCAB, e->s);
+        e->fc_lm[0] = p; e->fc_lm[1] = p + VOCAB;
+    }
     const size_t self_el = (size_t)DEC_N * S * DEC_H * d->kv_rows * DEC_DK;
     const size_t cross_el = (size_t)DEC_N * R * DEC_H * tmax * DEC_DK;
     e->kself = dmalloc(self_el * e->esz);
@@ -390,7 +415,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->enc_pool = dmalloc((size_t)R * tmax * DEC_D * sizeof(float));
     e->h = dmalloc((size_t)NR * DEC_D * 4);
     e->q = dmalloc((size_t)NR * DEC_D * 4);
-    e->parts = dmalloc((size_t)CT_MAX_KSPLIT * NR * DEC_D * 4);
+    e->parts = dmalloc((size_t)ctk_gemv_ksplit(DEC_D, DEC_FF) * NR * DEC_D * 4);
     e->lnf = dmalloc(ct_frag_elems(NR, DEC_D) * 2);
     e->attf = dmalloc(ct_frag_elems(NR, DEC_D) * 2);
     e->midf = dmalloc(ct_frag_elems(NR, DEC_FF) * 2);
@@ -459,7 +484,7 @@ void hipb_destroy(HipbEngine *e) {
                     e->d.req_np, e->d.req_ngen, e->d.req_prompt, e->d.req_out, e->d.req_score, e->d.q,
                     e->d.req_next, e->d.rq, e->d.pend, e->d.fq,
                     e->wqkv, e->bqkv, e->wckv, e->bckv, e->ew_qkv, e->eb_qkv, e->wtile, e->kself, e->vself, e->kcross, e->vcross,
-                    e->enc_pool, e->h, e->q, e->parts, e->lnf, e->attf, e->midf, e->logits, e->lnstat,
+                    e->enc_pool, e->h, e->q, e->parts, e->fold, e->lnf, e->attf, e->midf, e->logits, e->lnstat,
                     e->ex, e->eln, e->emid, e->eq, e->ek, e->ev, e->eo, e->eg, e->edw, e->epe, e->ep_all,
                     e->esub, e->emel, e->e_subtab, e->e_row_start, e->e_row_len, e->e_seq_off, e->e_seq_T,
                     e->e_blk_seq, e->e_blk_q0, e->e_rowoff, e->d_hann, e->d_twr, e->d_twi, e->d_fb,
@@ -1245,15 +1270,8 @@ static void warm_take(HipbEngine *e, CtWarmSet *ws) {
     e->warm.n = 0;
 }
 
-/* Residual LayerNorm into frag, carrying the queued read-ahead. */
-static void ln_frag(HipbEngine *e, int np, const uint16_t *pb, const uint16_t *w, const uint16_t *b) {
-    CtWarmSet ws;
-    warm_take(e, &ws);
-    ctk_ln_frag_warm(e->h, e->lnf, e->parts, np, pb, w, b, e->M, &ws, e->s);
-}
-
 static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, long head_stride,
-                 int rows, const int *lens, const int *kv_index, const int *rank, const uint16_t *q_bias) {
+                 int rows, const int *lens, const int *kv_index, const int *rank) {
     CtAttn a;
     memset(&a, 0, sizeof a);
     a.Q = e->q; a.q_sb = DEC_D; a.q_st = DEC_D;
@@ -1263,12 +1281,6 @@ static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, 
     a.rank = e->M >= e->d.rank_min ? rank : NULL;
     a.T_q = 1; a.B = e->M; a.H = DEC_H;
     a.scale = 0.08838834764831845f;   /* 1/sqrt(128) */
-    if (q_bias) {
-        a.q_parts = e->parts;
-        a.q_nparts = ctk_gemv_ksplit(DEC_D, DEC_D);
-        a.q_pstride = (long)e->M * DEC_D;
-        a.q_bias = q_bias;
-    }
     a.out_frag = e->attf;
     warm_take(e, &a.warm);
     ctk_attn(&a, e->s);
@@ -1293,11 +1305,11 @@ static void step_attention(HipbEngine *e, int l, int cross) {
         /* row s is slot s's own row: only the spare rows of a wide step
          * need the row -> slot table */
         attn(e, k, v, (long)DEC_H * e->d.kv_rows * DEC_DK, (long)e->d.kv_rows * DEC_DK, e->d.kv_rows,
-             e->d.pos_len, e->M > e->d.slots ? e->d.row_slot : NULL, e->d.rank_self, NULL);
+             e->d.pos_len, e->M > e->d.slots ? e->d.row_slot : NULL, e->d.rank_self);
     } else {
         cross_kv(e, l, &k, &v);
         attn(e, k, v, (long)DEC_H * e->d.tmax * DEC_DK, (long)e->d.tmax * DEC_DK, e->d.tmax,
-             e->d.cross_len, e->d.cross_idx, e->d.rank_cross, DW(e->W.dec[l].ca_qb));
+             e->d.cross_len, e->d.cross_idx, e->d.rank_cross);
     }
 }
 
@@ -1311,66 +1323,68 @@ static void launch_gemv(HipbEngine *e, const CtGemv *g) {
     ctk_gemv_read_floor(g, e->floor_sink, e->s);
 }
 
-/* Decode GEMM over all slots; CT_GV_PARTIAL outputs go to parts. */
+/* A decode GEMM over all rows on LayerNorm(h), the LayerNorm folded in: A
+ * is lnf = frag(h * w), written with the row statistics by the residual
+ * projection (or the embedding) before it; c = the GEMM's (c1, c2). */
+static void gv_fold(HipbEngine *e, const uint16_t *Wd, const float *const c[2], int N, int out, int relu,
+                    float *Y, long ldy, uint16_t *F) {
+    CtGemv g;
+    memset(&g, 0, sizeof g);
+    g.A = e->lnf; g.W = Wd; g.wtile = 1;
+    g.M = e->M; g.N = N; g.K = DEC_D; g.ksplit = 1;
+    g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
+    g.out = out; g.relu = relu;
+    g.lnstat = e->lnstat; g.fold_c1 = c[0]; g.fold_c2 = c[1];
+    g.Y = Y; g.ldy = ldy; g.F = F;
+    launch_gemv(e, &g);
+}
 
-static void gv(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint16_t *bd, int N, int K,
-               int out, int relu, float *Y, long ldy, uint16_t *F) {
+/* A K-split decode GEMM: its slices' partial sums go to parts. */
+static void gv_partial(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, int N, int K) {
+    CtGemv g;
+    memset(&g, 0, sizeof g);
+    g.A = A; g.W = Wd; g.wtile = 1;
+    g.M = e->M; g.N = N; g.K = K; g.ksplit = ctk_gemv_ksplit(N, K);
+    g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
+    g.out = CT_GV_PARTIAL;
+    g.Y = e->parts;
+    launch_gemv(e, &g);
+}
+
+/* Output projection onto the residual rows (h += A W^T + b) that leaves the
+ * input of the next GEMM with its LayerNorm (gain lnw) folded in: the rows'
+ * statistics per 32-column block in lnstat and lnf = frag(h * lnw). */
+static void gv_resid(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint16_t *bd, int K,
+                     const uint16_t *lnw) {
     CtGemv g;
     memset(&g, 0, sizeof g);
     g.A = A; g.W = Wd; g.bias = bd; g.wtile = 1;
-    g.M = e->M; g.N = N; g.K = K;
-    g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
-    g.out = out; g.relu = relu;
-    g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, K) : 1;
-    g.Y = out == CT_GV_PARTIAL ? e->parts : Y;
-    g.ldy = ldy; g.F = F;
-    launch_gemv(e, &g);
-}
-
-/* Output projection of an attention block onto the residual rows (h += attf
- * W^T + b), leaving the rows' LayerNorm statistics for gv_ln: replaces the
- * K-split projection plus the residual LayerNorm launch. */
-static void gv_resid(HipbEngine *e, const uint16_t *Wd, const uint16_t *bd) {
-    CtGemv g;
-    memset(&g, 0, sizeof g);
-    g.A = e->attf; g.W = Wd; g.bias = bd; g.wtile = 1;
-    g.M = e->M; g.N = DEC_D; g.K = DEC_D; g.ksplit = 1;
+    g.M = e->M; g.N = DEC_D; g.K = K; g.ksplit = 1;
     g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
     g.out = CT_GV_RESID;
     g.Y = e->h; g.ldy = DEC_D; g.lnstat = e->lnstat;
-    launch_gemv(e, &g);
-}
-
-/* A decode GEMM on LayerNorm(h) (lnw, lnb), normalised in the GEMM from the
- * statistics gv_resid left. */
-static void gv_ln(HipbEngine *e, const uint16_t *lnw, const uint16_t *lnb, const uint16_t *Wd,
-                  const uint16_t *bd, int N, int out, int relu, uint16_t *F) {
-    CtGemv g;
-    memset(&g, 0, sizeof g);
-    g.X = e->h; g.ldx = DEC_D; g.lnstat = e->lnstat; g.lnw = lnw; g.lnb = lnb;
-    g.W = Wd; g.bias = bd; g.wtile = 1;
-    g.M = e->M; g.N = N; g.K = DEC_D;
-    g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
-    g.out = out; g.relu = relu;
-    g.ksplit = out == CT_GV_PARTIAL ? ctk_gemv_ksplit(N, DEC_D) : 1;
-    g.Y = out == CT_GV_PARTIAL ? e->parts : NULL;
-    g.F = F;
+    g.F = e->lnf; g.fold_w = lnw;
     launch_gemv(e, &g);
 }
 
 /* One decode step over slots rows, or (wide) over slots + prefill_rows rows
  * whose spare rows feed prompts several tokens a step.  full == 0 launches
- * only its GEMMs (timing support). */
+ * only its GEMMs (timing support).
+ *
+ * Every LayerNorm of the decoder runs inside the GEMM that consumes it: the
+ * residual projections of the attention outputs, the residual update after
+ * the K-split FFN down projection and the embedding leave h, its block
+ * statistics and frag(h * w) of the next LayerNorm's gain, and the next GEMM
+ * corrects each row in its epilogue (gemv_kernel FOLD).  A layer is 9
+ * launches: QKV, self attention, out projection, cross query, cross
+ * attention, cross out projection, FFN up, FFN down (8 K-slices), residual
+ * update. */
 static void step_kernels(HipbEngine *e, int full, int wide) {
     const Weights *W = &e->W;
     const int B = wide ? e->d.rows : e->d.slots;
     hipStream_t s = e->s;
-    const int ks_o = ctk_gemv_ksplit(DEC_D, DEC_D), ks_ff = ctk_gemv_ksplit(DEC_D, DEC_FF);
     e->M = B;
     if (full) ctk_eng_begin(&e->d, B - e->d.slots, s);
-    /* each LayerNorm first adds the previous projection's K-slices + bias to h */
-    int np = 0;
-    const uint16_t *pb = NULL;
     for (int l = 0; l < DEC_N; l++) {
         const DLayer *L = &W->dec[l];
         void *ks, *vs;
@@ -1379,49 +1393,53 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         const uint16_t *w_co = e->wt_co[l], *w_f1 = e->wt_f1[l], *w_f2 = e->wt_f2[l];
         if (full && e->read_ahead) warm_add(e, w_qkv, 3 * DEC_D, DEC_D, CT_GV_QKV);
         if (full && l == 0) {
-            /* the embedding LayerNorm and this one in one launch */
+            /* h = the embedding LayerNorm, with the first layer's folded input */
             CtWarmSet ws;
             warm_take(e, &ws);
-            ctk_embed_ln_frag(e->h, e->lnf, e->d.tok, e->d.pos_len, e->d.act, DW(W->etw), DW(W->epw),
-                              DW(W->elnw), DW(W->elnb), DW(L->sa_lnw), DW(L->sa_lnb), B, &ws, s);
+            ctk_embed_fold(e->h, e->lnstat, e->lnf, e->d.tok, e->d.pos_len, e->d.act, DW(W->etw),
+                           DW(W->epw), DW(W->elnw), DW(W->elnb), DW(L->sa_lnw), B, &ws, s);
         } else if (full) {
-            ln_frag(e, np, pb, DW(L->sa_lnw), DW(L->sa_lnb));
+            /* h += the previous layer's FFN (its K-slices and bias), with this
+             * layer's folded input */
+            CtWarmSet ws;
+            warm_take(e, &ws);
+            ctk_resid_fold(e->h, e->lnstat, e->lnf, e->parts, ctk_gemv_ksplit(DEC_D, DEC_FF),
+                           DW(W->dec[l - 1].ffn_b2), DW(L->sa_lnw), B, &ws, s);
         }
         CtGemv g;
         memset(&g, 0, sizeof g);
         g.A = e->lnf;
         g.W = w_qkv; g.wtile = 1;
-        g.bias = e->bqkv + (size_t)3 * l * DEC_D;
         g.M = B; g.N = 3 * DEC_D; g.K = DEC_D; g.ksplit = 1; g.out = CT_GV_QKV;
         g.m_active = B > e->d.slots ? e->d.q + 6 : NULL;
+        g.lnstat = e->lnstat; g.fold_c1 = e->fc_qkv[l][0]; g.fold_c2 = e->fc_qkv[l][1];
         g.Y = e->q; g.ldy = DEC_D;
         g.kc = ks; g.vc = vs; g.rowoff = e->d.kv_rowoff; g.hstride = (long)e->d.kv_rows * DEC_DK;
         g.kv_bf16 = e->esz == 2;
         launch_gemv(e, &g);
         if (full && e->read_ahead) warm_add(e, w_o, DEC_D, DEC_D, CT_GV_RESID);
-        if (full && e->read_ahead) warm_add(e, w_cq, DEC_D, DEC_D, CT_GV_PARTIAL);
+        if (full && e->read_ahead) warm_add(e, w_cq, DEC_D, DEC_D, CT_GV_DENSE);
         if (full) step_attention(e, l, 0);
-        /* h += self-attention out-projection, then the cross-attention query
-         * from LayerNorm(h) normalised inside its GEMM */
-        gv_resid(e, w_o, DW(L->sa_ob));
-        gv_ln(e, DW(L->ca_lnw), DW(L->ca_lnb), w_cq, NULL, DEC_D, CT_GV_PARTIAL, 0, NULL);
+        /* h += self-attention out-projection; the cross-attention query from
+         * LayerNorm(h) */
+        gv_resid(e, e->attf, w_o, DW(L->sa_ob), DEC_D, DW(L->ca_lnw));
+        gv_fold(e, w_cq, e->fc_cq[l], DEC_D, CT_GV_DENSE, 0, e->q, DEC_D, NULL);
         if (full && e->read_ahead) warm_add(e, w_f1, DEC_FF, DEC_D, CT_GV_FRAG);
         if (full && e->read_ahead) warm_add(e, w_f2, DEC_D, DEC_FF, CT_GV_PARTIAL);
         if (full) step_attention(e, l, 1);
-        /* the FFN's LayerNorm stays a launch of its own: normalising inside the
-         * FFN-up GEMM would repeat each row's LayerNorm over the full K in all
-         * 64 of its column-block workgroups (measured 2-5 us slower per launch) */
-        gv(e, e->attf, w_co, NULL, DEC_D, DEC_D, CT_GV_PARTIAL, 0, NULL, 0, NULL);
-        if (full) ln_frag(e, ks_o, DW(L->ca_ob), DW(L->ffn_lnw), DW(L->ffn_lnb));
-        gv(e, e->lnf, w_f1, DW(L->ffn_b1), DEC_FF, DEC_D, CT_GV_FRAG, 1, NULL, 0, e->midf);
-        gv(e, e->midf, w_f2, NULL, DEC_D, DEC_FF, CT_GV_PARTIAL, 0, NULL, 0, NULL);
-        np = ks_ff;
-        pb = DW(L->ffn_b2);
+        /* h += cross-attention out-projection; the FFN on LayerNorm(h), its
+         * down projection in K-slices summed into h by the next launch */
+        gv_resid(e, e->attf, w_co, DW(L->ca_ob), DEC_D, DW(L->ffn_lnw));
+        gv_fold(e, w_f1, e->fc_f1[l], DEC_FF, CT_GV_FRAG, 1, NULL, 0, e->midf);
+        gv_partial(e, e->midf, w_f2, DEC_D, DEC_FF);
     }
-    if (full) ln_frag(e, np, pb, DW(W->dlnw), DW(W->dlnb));
+    /* h += the last FFN, with the final LayerNorm's folded input */
+    if (full)
+        ctk_resid_fold(e->h, e->lnstat, e->lnf, e->parts, ctk_gemv_ksplit(DEC_D, DEC_FF),
+                       DW(W->dec[DEC_N - 1].ffn_b2), DW(W->dlnw), B, NULL, s);
     /* logits only for the slots' own rows */
     e->M = e->d.slots;
-    gv(e, e->lnf, e->wt_lm, DW(W->hdb), VOCAB, DEC_D, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);
+    gv_fold(e, e->wt_lm, e->fc_lm, VOCAB, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);
     if (full) ctk_eng_end(&e->d, e->logits, s);
     e->M = e->d.slots;
 }

@@ -23,7 +23,6 @@
 
 namespace {
 
-constexpr int CT_ATTN_QPARTS = 4;   // most query partial slices a launch may pass
 // lanes per key: 16, each owning 8 of the 128 head dimensions (one 16-byte
 // bf16 piece); 8 lanes per key (16 dimensions a lane) measured slower
 constexpr int CT_ATTN_LPK = 16;
@@ -143,34 +142,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
             for (int v = 0; v < NV; v++) load_key(g + NG * j, v, kA[j][v], vA[j][v]);
     }
     float q[DPL];
-    if (a.q_parts) {
-        // query = ((part 0 + part 1) + ...) + bias, the decode GEMM's K-slices
-        const float *qp = a.q_parts + qoff + ls * DPL;
-        float4 pr[CT_ATTN_QPARTS][DPL / 4];
-#pragma unroll
-        for (int p = 0; p < CT_ATTN_QPARTS; p++)
-            if (p < a.q_nparts) {
-#pragma unroll
-                for (int c = 0; c < DPL / 4; c++)
-                    pr[p][c] = *reinterpret_cast<const float4 *>(qp + p * a.q_pstride + 4 * c);
-            }
-#pragma unroll
-        for (int c = 0; c < DPL / 4; c++) {
-            q[4 * c] = pr[0][c].x; q[4 * c + 1] = pr[0][c].y; q[4 * c + 2] = pr[0][c].z; q[4 * c + 3] = pr[0][c].w;
-        }
-#pragma unroll
-        for (int p = 1; p < CT_ATTN_QPARTS; p++)
-            if (p < a.q_nparts) {
-#pragma unroll
-                for (int c = 0; c < DPL / 4; c++) {
-                    q[4 * c] += pr[p][c].x; q[4 * c + 1] += pr[p][c].y;
-                    q[4 * c + 2] += pr[p][c].z; q[4 * c + 3] += pr[p][c].w;
-                }
-            }
-        if (a.q_bias)
-#pragma unroll
-            for (int i = 0; i < DPL; i++) q[i] += bf2f(a.q_bias[h * DEC_DK + ls * DPL + i]);
-    } else {
+    {
         const float *qp = a.Q + qoff + ls * DPL;
 #pragma unroll
         for (int i = 0; i < DPL; i++) q[i] = qp[i];
@@ -292,12 +264,6 @@ extern "C" void ctk_attn(const CtAttn *a, hipStream_t s) {
     if (a->B <= 0 || a->T_q <= 0) return;
     if (a->rank && a->T_q != 1) {
         fprintf(stderr, "ctk_attn: a rank permutation needs one query per item\n");
-        exit(1);
-    }
-    if (a->q_parts && (a->q_nparts < 1 || a->q_nparts > CT_ATTN_QPARTS || a->q_pstride % 4 ||
-                       ((uintptr_t)a->q_parts & 15) || (a->q_bias && ((uintptr_t)a->q_bias & 15)) ||
-                       a->q_sb % 4 || a->q_st % 4)) {
-        fprintf(stderr, "ctk_attn: query partials need 1..4 slices and 16-byte aligned rows\n");
         exit(1);
     }
     const int wrows = ct_warm_rows(&a->warm, "ctk_attn");

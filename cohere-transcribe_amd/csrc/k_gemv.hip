@@ -54,15 +54,18 @@ __device__ __forceinline__ float half_wave_sum(float v) {
     return v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
 }
 
-// LNA: the A operand is LayerNorm(X) (backends/cpu/backend.c layernorm, eps
-// 1e-5) computed in registers: the row statistics merge the producer's 32
-// per-block (mean, squared deviations) pairs in a fixed order (Chan et al.'s
-// pairwise update with equal block sizes: mean of the means, then the
-// blocks' sums plus 32 (mean_b - mean)^2 each), and each input is
-// normalised, scaled and split hi/lo exactly as the LayerNorm kernels do.
-template <int CB, int SPW, int RB, bool LNA>
+// FOLD: the GEMM consumes LayerNorm(h) without a normalised copy of h.  With
+// LN(h)_k = (h_k - mu) * rstd * w_k + b_k (backends/cpu/backend.c layernorm,
+// eps 1e-5), a product row is
+//     y_n = sum_k LN(h)_k W_nk + bias_n = rstd * (s_n - mu * c1_n) + c2_n,
+//     s_n = sum_k (h_k w_k) W_nk,  c1_n = sum_k w_k W_nk,  c2_n = sum_k b_k W_nk + bias_n,
+// so A is frag(h * w) (written by the residual projection that produced h),
+// c1 / c2 are per-column constants (ctk_fold_cols), and each row's (mu, rstd)
+// merges the producer's 32 per-block (mean, squared deviations) pairs in a
+// fixed order (Chan et al.'s pairwise update with equal block sizes: mean of
+// the means, then the blocks' sums plus 32 (mean_b - mean)^2 each).
+template <int CB, int SPW, int RB, bool FOLD>
 __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
-    static_assert(!LNA || RB == 1, "the LayerNorm prologue covers one 16-row block");
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int r = lane & 15, kg = lane >> 4;
     const int pos = blockIdx.y;
@@ -77,28 +80,49 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
         if (m0 >= ma) return;
         nrb = min(nrb, (ma - m0 + 15) >> 4);
     }
-    u16x8 ah[SPW][RB], al[SPW][RB], wv[SPW][CB];
-    float2 lst = make_float2(0.f, 0.f);
-    float4 xr[LNA ? SPW : 1][2];
-    u16x8 lw[LNA ? SPW : 1], lb[LNA ? SPW : 1];
-    if (LNA) {
+    const bool resid = CB == 2 && RB == 1 && g.out == CT_GV_RESID;
+    float2 lst[FOLD ? RB : 1];
+    float h_in = 0.0f, b_in = 0.0f, fw = 0.0f;
+    if (FOLD) {
         // this thread's block statistics first, so their wait leaves the row loads in flight
-        const int m = min(m0 + (tid >> 5), g.M - 1);
-        lst = reinterpret_cast<const float2 *>(g.lnstat)[(long)m * CT_LN_BLOCKS + (tid & 31)];
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            const int m = min(m0 + 16 * rb + (tid >> 5), g.M - 1);
+            lst[rb] = reinterpret_cast<const float2 *>(g.lnstat)[(long)m * CT_LN_BLOCKS + (tid & 31)];
+        }
     }
+    // the folded LayerNorm's column constants of the columns this thread
+    // finishes (its column is the same in every epilogue round: 512 threads
+    // are a multiple of the tile width), loaded before the MFMAs
+    constexpr int NFC = FOLD ? 8 : 1;
+    float fc1[NFC], fc2[NFC];
+    if (FOLD) {
+        if (g.out == CT_GV_FRAG) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int col = c0 + (tid % (2 * CB)) * 8 + i;
+                fc1[i] = g.fold_c1[col];
+                fc2[i] = g.fold_c2[col];
+            }
+        } else {
+            fc1[0] = g.fold_c1[c0 + tid % (16 * CB)];
+            fc2[0] = g.fold_c2[c0 + tid % (16 * CB)];
+        }
+    }
+    if (resid) {
+        // the residual row element, bias and next LayerNorm gain this thread's epilogue needs
+        const int m = m0 + (tid >> 5), col = c0 + (tid & 31);
+        if (m < g.M) h_in = g.Y[(long)m * g.ldy + col];
+        if (g.bias) b_in = bf2f(g.bias[col]);
+        if (g.F) fw = bf2f(g.fold_w[col]);
+    }
+    // every load before the first MFMA: wavefront w takes K-steps w, w + 8, ...
+    u16x8 ah[SPW][RB], al[SPW][RB], wv[SPW][CB];
 #pragma unroll
     for (int j = 0; j < SPW; j++) {
         const int st = s0 + w + GV_WAVES * j;
-        if (LNA) {
-            // the lane's 8 inputs of K-step st (rows past M read row M-1, never stored)
-            const int k = st * 32 + kg * 8;
-            const float4 *p = reinterpret_cast<const float4 *>(g.X + (long)min(m0 + r, g.M - 1) * g.ldx + k);
-            xr[j][0] = p[0]; xr[j][1] = p[1];
-            lw[j] = *reinterpret_cast<const u16x8 *>(g.lnw + k);
-            lb[j] = *reinterpret_cast<const u16x8 *>(g.lnb + k);
-        }
 #pragma unroll
-        for (int rb = 0; rb < RB && !LNA; rb++) {
+        for (int rb = 0; rb < RB; rb++) {
             if (rb < nrb) {
                 // frag layout: per 64 rows and K-step, four 16-row pieces of 1 KB hi + 1 KB lo
                 const int q = q0 + rb;
@@ -117,27 +141,16 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
                 g.wtile ? g.W + ((((long)(c0 >> 4) + cb) * nsteps + st) << 9) + lane * 8
                         : g.W + (long)(c0 + cb * 16 + r) * g.K + st * 32 + kg * 8));
     }
-    if (LNA) {
-        __shared__ float2 lnrow[16];
+    __shared__ float2 lnrow[FOLD ? 16 * RB : 1];
+    if (FOLD) {
         // half-wavefront h holds row h's 32 blocks (512 threads = 16 rows x 32 blocks)
-        const float mu = half_wave_sum(lst.x) / (float)CT_LN_BLOCKS;
-        const float d = lst.x - mu;
-        const float m2 = half_wave_sum(lst.y + (float)(DEC_D / CT_LN_BLOCKS) * d * d);
-        if ((tid & 31) == 0) lnrow[tid >> 5] = make_float2(mu, 1.0f / sqrtf(m2 / (float)DEC_D + 1e-5f));
-        __syncthreads();
-        const float2 mr = lnrow[r];
 #pragma unroll
-        for (int j = 0; j < SPW; j++) {
-            const float x[8] = {xr[j][0].x, xr[j][0].y, xr[j][0].z, xr[j][0].w,
-                                xr[j][1].x, xr[j][1].y, xr[j][1].z, xr[j][1].w};
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float o = (x[i] - mr.x) * mr.y * bf2f(lw[j][i]) + bf2f(lb[j][i]);
-                uint16_t hh, ll;
-                split_bf16(o, hh, ll);
-                ah[j][0][i] = hh;
-                al[j][0][i] = ll;
-            }
+        for (int rb = 0; rb < RB; rb++) {
+            const float mu = half_wave_sum(lst[rb].x) / (float)CT_LN_BLOCKS;
+            const float d = lst[rb].x - mu;
+            const float m2 = half_wave_sum(lst[rb].y + (float)(DEC_D / CT_LN_BLOCKS) * d * d);
+            if ((tid & 31) == 0)
+                lnrow[16 * rb + (tid >> 5)] = make_float2(mu, 1.0f / sqrtf(m2 / (float)DEC_D + 1e-5f));
         }
     }
     f32x4 acc[RB][CB];
@@ -166,7 +179,17 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
             for (int j = 0; j < 4; j++) part[w][rb * 16 + kg * 4 + j][cb * 16 + r] = acc[rb][cb][j];
     __syncthreads();
 
-    if (CB == 2 && RB == 1 && g.out == CT_GV_RESID) {
+    // bias, or the folded LayerNorm's row correction and column constants
+    // (fc1 / fc2 entry i)
+    auto finish = [&](float s, int row, int col, int i) {
+        if (FOLD) {
+            const float2 mr = lnrow[row];
+            return mr.y * (s - mr.x * fc1[i]) + fc2[i];
+        }
+        return g.bias ? s + bf2f(g.bias[col]) : s;
+    };
+
+    if (resid) {
         // thread: row m0 + tid / 32, column c0 + tid % 32; a half-wavefront holds
         // one row of this 32-column block
         const int row = tid >> 5, cc = tid & 31, m = m0 + row, col = c0 + cc;
@@ -176,15 +199,35 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
         for (int ww = 1; ww < GV_WAVES; ww++) s += part[ww][row][cc];
         float x = 0.0f;
         if (ok) {
-            float *hp = g.Y + (long)m * g.ldy + col;
-            x = *hp + (s + (g.bias ? bf2f(g.bias[col]) : 0.0f));
-            *hp = x;
+            x = h_in + (s + b_in);
+            g.Y[(long)m * g.ldy + col] = x;
         }
         const float mean = half_wave_sum(x) / 32.0f;
         const float d = x - mean;
         const float m2 = half_wave_sum(d * d);
         if (ok && cc == 0)
             reinterpret_cast<float2 *>(g.lnstat)[(long)m * CT_LN_BLOCKS + (col >> 5)] = make_float2(mean, m2);
+        if (g.F) {
+            // frag(h * w) for the next GEMM's folded LayerNorm: lane cc of a
+            // half-wavefront gathers columns cc..cc+7 of its row by lane
+            // exchange, and every eighth lane stores the 16-byte pieces
+            uint16_t hh, ll;
+            // the product rounded on its own (no contraction into the split's subtraction)
+            split_bf16(mul_rn(x, fw), hh, ll);
+            const int v = (int)((uint32_t)hh | ((uint32_t)ll << 16));
+            u16x8 hv, lv;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t u = (uint32_t)__shfl(v, (lane & ~7) + i);
+                hv[i] = (uint16_t)(u & 0xFFFFu);
+                lv[i] = (uint16_t)(u >> 16);
+            }
+            if (ok && (cc & 7) == 0) {
+                const long o = ct_frag_off(m, col, DEC_D);
+                *reinterpret_cast<u16x8 *>(g.F + o) = hv;
+                *reinterpret_cast<u16x8 *>(g.F + o + 512) = lv;
+            }
+        }
         return;
     }
     if (g.out == CT_GV_FRAG) {
@@ -199,7 +242,7 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
                 float s = part[0][row][cc];
 #pragma unroll
                 for (int ww = 1; ww < GV_WAVES; ww++) s += part[ww][row][cc];
-                if (g.bias) s += bf2f(g.bias[c0 + cc]);
+                s = finish(s, row, c0 + cc, i);
                 if (g.relu) s = s > 0.0f ? s : 0.0f;
                 uint16_t hh, ll;
                 split_bf16(s, hh, ll);
@@ -221,7 +264,7 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_kernel(CtGemv g) {
             g.Y[((long)ks * g.M + m) * g.N + col] = s;
             continue;
         }
-        if (g.bias) s += bf2f(g.bias[col]);
+        s = finish(s, row, col, 0);
         if (g.relu) s = s > 0.0f ? s : 0.0f;
         if (g.out == CT_GV_DENSE || col < DEC_D) {
             g.Y[(long)m * g.ldy + col] = s;
@@ -288,6 +331,25 @@ __global__ __launch_bounds__(256) void tile_w_kernel(const uint16_t *W, uint16_t
     *reinterpret_cast<u16x8 *>(Wt + piece * 8) = *reinterpret_cast<const u16x8 *>(W + (long)n * K + k);
 }
 
+// One thread per output column n of W[N][K] (row-major bf16): c1[n] =
+// sum_k w_k W_nk, c2[n] = sum_k b_k W_nk + bias_n, in double, k in order.
+__global__ __launch_bounds__(256) void fold_cols_kernel(const uint16_t *W, const uint16_t *w,
+                                                        const uint16_t *b, const uint16_t *bias, int N,
+                                                        int K, float *c1, float *c2) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= N) return;
+    double s1 = 0.0, s2 = 0.0;
+    const uint16_t *row = W + (long)n * K;
+    for (int k = 0; k < K; k++) {
+        const double x = (double)bf2f(row[k]);
+        s1 += (double)bf2f(w[k]) * x;
+        s2 += (double)bf2f(b[k]) * x;
+    }
+    if (bias) s2 += (double)bf2f(bias[n]);
+    c1[n] = (float)s1;
+    c2[n] = (float)s2;
+}
+
 [[noreturn]] void gv_fatal(const char *msg, const CtGemv *g) {
     fprintf(stderr, "ctk_gemv: %s (M=%d N=%d K=%d ksplit=%d out=%d)\n", msg, g->M, g->N, g->K,
             g->ksplit, g->out);
@@ -303,6 +365,15 @@ extern "C" void ctk_tile_w(const uint16_t *W, uint16_t *Wt, int N, int K, hipStr
     }
     const long pieces = (long)N * K / 8;
     hipLaunchKernelGGL(tile_w_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, W, Wt, N, K);
+}
+
+extern "C" void ctk_fold_cols(const uint16_t *W, const uint16_t *w, const uint16_t *b, const uint16_t *bias,
+                              int N, int K, float *c1, float *c2, hipStream_t s) {
+    if (N <= 0 || K <= 0 || !W || !w || !b || !c1 || !c2) {
+        fprintf(stderr, "ctk_fold_cols: needs W, w, b, c1, c2 and N, K > 0\n");
+        exit(1);
+    }
+    hipLaunchKernelGGL(fold_cols_kernel, dim3((N + 255) / 256), dim3(256), 0, s, W, w, b, bias, N, K, c1, c2);
 }
 
 extern "C" int ctk_gemv_sizeof(void) { return (int)sizeof(CtGemv); }
@@ -324,7 +395,10 @@ extern "C" int ctk_gemv_ksplit(int N, int K) {
 // read-ahead leaves them) for the wide ones; 16 columns stay best for the
 // wide projections at M <= 16, and the LM head (32 MB of weights, 256
 // workgroups) keeps all rows and 64 columns.
-static void gv_tile(int N, int K, int M, int *cb, int *rb) {
+// The residual projection always takes 32 columns and one row block (its
+// epilogue holds a row's 32-column block in a half-wavefront; K = DEC_D).
+static void gv_tile(int N, int K, int M, int out, int *cb, int *rb) {
+    if (out == CT_GV_RESID) { *cb = 2; *rb = 1; return; }
     if (N >= 8192 && N % 64 == 0) { *cb = 4; *rb = 4; return; }
     *rb = 1;
     if (K >= 4096) *cb = N % 64 == 0 && M > 16 ? 4 : N % 32 == 0 ? 2 : 1;
@@ -335,7 +409,7 @@ static void gv_tile(int N, int K, int M, int *cb, int *rb) {
 extern "C" long ctk_gemv_read_floor_blocks(const CtGemv *g) {
     const int ksplit = g->ksplit < 1 ? 1 : g->ksplit;
     int cb, rb;
-    gv_tile(g->N, g->K, g->M, &cb, &rb);
+    gv_tile(g->N, g->K, g->M, g->out, &cb, &rb);
     return (long)ksplit * (g->N / (16 * cb)) * ((g->M + 16 * rb - 1) / (16 * rb));
 }
 
@@ -343,7 +417,7 @@ extern "C" void ctk_gemv_read_floor(const CtGemv *g, float *sink, hipStream_t s)
     if (g->M <= 0) return;
     const int ksplit = g->ksplit < 1 ? 1 : g->ksplit;
     int cb, rb;
-    gv_tile(g->N, g->K, g->M, &cb, &rb);
+    gv_tile(g->N, g->K, g->M, g->out, &cb, &rb);
     if (!g->wtile || g->K % (256 * ksplit) != 0 || g->N % (16 * cb) != 0 || ((uintptr_t)g->W & 15))
         gv_fatal("read floor needs tiled, 16-byte aligned weights of a supported shape", g);
     const dim3 grid(ksplit, g->N / (16 * cb), (g->M + 16 * rb - 1) / (16 * rb));
@@ -356,7 +430,7 @@ extern "C" void ctk_gemv_read_floor(const CtGemv *g, float *sink, hipStream_t s)
 extern "C" void ctk_gemv_warm(const CtGemv *g, CtWarm *w) {
     const int ksplit = g->ksplit < 1 ? 1 : g->ksplit;
     int cb, rb;
-    gv_tile(g->N, g->K, g->M, &cb, &rb);
+    gv_tile(g->N, g->K, g->M, g->out, &cb, &rb);
     w->W = g->W;
     w->gx = g->wtile ? g->N / (16 * cb) : 0;
     w->gy = ksplit; w->cb = cb;
@@ -375,24 +449,32 @@ extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
         gv_fatal("operands must be 16-byte aligned", g);
     const int spw = g->K / ksplit / 256;
     int cb, rb;
-    gv_tile(g->N, g->K, g->M, &cb, &rb);
-    const bool lna = g->X != NULL;
+    gv_tile(g->N, g->K, g->M, g->out, &cb, &rb);
+    const bool fold = g->fold_c1 != NULL;
     if (g->out == CT_GV_RESID &&
-        (g->N != DEC_D || ksplit != 1 || cb != 2 || rb != 1 || !g->lnstat || ((uintptr_t)g->lnstat & 7)))
-        gv_fatal("residual output needs N = DEC_D, no K split and an 8-byte aligned lnstat", g);
-    if (lna && (g->K != DEC_D || rb != 1 || !g->lnstat || !g->lnw || !g->lnb || g->ldx % 4 ||
-                ((uintptr_t)g->X & 15) || ((uintptr_t)g->lnw & 15) || ((uintptr_t)g->lnb & 15)))
-        gv_fatal("a LayerNorm input needs K = DEC_D, 16-byte aligned rows and vectors, and lnstat", g);
+        (g->N != DEC_D || g->K != DEC_D || ksplit != 1 || !g->lnstat || ((uintptr_t)g->lnstat & 7) ||
+         (g->F && (!g->fold_w || ((uintptr_t)g->F & 15)))))
+        gv_fatal("residual output needs N = K = DEC_D, no K split, an 8-byte aligned lnstat, and with F "
+                 "a 16-byte aligned F and its LayerNorm gain fold_w", g);
+    if (fold && (g->K != DEC_D || !g->fold_c2 || !g->lnstat || ((uintptr_t)g->lnstat & 7) ||
+                 g->out == CT_GV_PARTIAL || g->out == CT_GV_RESID))
+        gv_fatal("a folded LayerNorm needs K = DEC_D, c1, c2 and lnstat, and a dense, frag or QKV output", g);
     const dim3 grid(ksplit, g->N / (16 * cb), (g->M + 16 * rb - 1) / (16 * rb));
     const dim3 block(64 * GV_WAVES);
 #define GV_CASE(CB, SPW, RB)                                                                \
-    if (cb == CB && spw == SPW && rb == RB) {                                               \
-        if (lna) hipLaunchKernelGGL((gemv_kernel<CB, SPW, RB, (RB == 1)>), grid, block, 0, s, *g); \
-        else hipLaunchKernelGGL((gemv_kernel<CB, SPW, RB, false>), grid, block, 0, s, *g);  \
+    if (cb == CB && spw == SPW && rb == RB && !fold) {                                      \
+        hipLaunchKernelGGL((gemv_kernel<CB, SPW, RB, false>), grid, block, 0, s, *g);       \
+        return;                                                                             \
+    }
+#define GV_FOLD(CB, RB)                                                                     \
+    if (cb == CB && spw == 4 && rb == RB && fold) {                                         \
+        hipLaunchKernelGGL((gemv_kernel<CB, 4, RB, true>), grid, block, 0, s, *g);          \
         return;                                                                             \
     }
     GV_CASE(1, 1, 1) GV_CASE(1, 2, 1) GV_CASE(1, 4, 1) GV_CASE(2, 1, 1) GV_CASE(2, 2, 1) GV_CASE(2, 4, 1)
     GV_CASE(4, 1, 1) GV_CASE(4, 2, 1) GV_CASE(4, 4, 1) GV_CASE(4, 1, 4) GV_CASE(4, 2, 4) GV_CASE(4, 4, 4)
+    GV_FOLD(1, 1) GV_FOLD(2, 1) GV_FOLD(4, 1) GV_FOLD(4, 4)
 #undef GV_CASE
+#undef GV_FOLD
     gv_fatal("no kernel for this K slice", g);
 }

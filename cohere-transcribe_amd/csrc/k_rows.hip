@@ -259,93 +259,44 @@ __global__ void inc_kernel(int *p) {
     if (threadIdx.x == 0) *p += 1;
 }
 
-// Decoder residual update + LayerNorm into frag layout (D = DEC_D), one
-// 256-thread workgroup per row, a float4 per thread: h += ((parts[0] +
-// parts[1]) + ...) + pbias (the K-slice sums of the previous projection, in
-// slice order, then its bias), then the two-pass LayerNorm (mean, then the
-// variance of the centred values, eps 1e-5), each output split hi/lo and
-// stored where the decode GEMM's lanes read it.  NP (the number of slices)
-// is a template parameter so every load is issued before the first add.
-// The two-pass LayerNorm of one row held as one float4 per thread (thread t:
-// elements 4t..4t+3; 256 threads), then split hi/lo into frag rows.
-__device__ __forceinline__ void ln_frag_tail(float4 v, ushort4 w4, ushort4 b4, uint16_t *frag, int row) {
-    constexpr int D = DEC_D;
-    const int t = threadIdx.x, wv = t >> 6, lane = t & 63, d0 = 4 * t;
-    __shared__ float red[2][4];
-    const float s = wave_sum((v.x + v.y) + (v.z + v.w));
-    if (lane == 0) red[0][wv] = s;
-    __syncthreads();
-    const float mu = ((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])) / (float)D;
-    const float c0 = v.x - mu, c1 = v.y - mu, c2 = v.z - mu, c3 = v.w - mu;
-    const float q = wave_sum((c0 * c0 + c1 * c1) + (c2 * c2 + c3 * c3));
-    if (lane == 0) red[1][wv] = q;
-    __syncthreads();
-    const float var = ((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) / (float)D;
-    const float rs = 1.0f / sqrtf(var + 1e-5f);
-    const float o[4] = {c0 * rs * bf2f(w4.x) + bf2f(b4.x),
-                        c1 * rs * bf2f(w4.y) + bf2f(b4.y),
-                        c2 * rs * bf2f(w4.z) + bf2f(b4.z),
-                        c3 * rs * bf2f(w4.w) + bf2f(b4.w)};
-    ushort4 h4, l4;
+// The folded input of a GEMM on LayerNorm(h) (gemv_kernel FOLD) from one row
+// of h held as a float4 per thread (256 threads, thread t: columns 4t..4t+3):
+// each 32-column block's (mean, squared deviations) into lnstat (a block is 8
+// consecutive lanes), and frag(h * w), each product rounded on its own.
+__device__ __forceinline__ void fold_tail(float4 v, ushort4 w4, float *lnstat, uint16_t *frag, int row) {
+    const int t = threadIdx.x;
+    float sum = (v.x + v.y) + (v.z + v.w);
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    const float mean = sum / 32.0f;
+    const float c0 = v.x - mean, c1 = v.y - mean, c2 = v.z - mean, c3 = v.w - mean;
+    float m2 = (c0 * c0 + c1 * c1) + (c2 * c2 + c3 * c3);
+    m2 += __shfl_xor(m2, 1);
+    m2 += __shfl_xor(m2, 2);
+    m2 += __shfl_xor(m2, 4);
+    if ((t & 7) == 0)
+        reinterpret_cast<float2 *>(lnstat)[(long)row * CT_LN_BLOCKS + (t >> 3)] = make_float2(mean, m2);
+    const float o[4] = {mul_rn(v.x, bf2f(w4.x)), mul_rn(v.y, bf2f(w4.y)), mul_rn(v.z, bf2f(w4.z)),
+                        mul_rn(v.w, bf2f(w4.w))};
     uint16_t hh[4], ll[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) split_bf16(o[j], hh[j], ll[j]);
-    h4.x = hh[0]; h4.y = hh[1]; h4.z = hh[2]; h4.w = hh[3];
-    l4.x = ll[0]; l4.y = ll[1]; l4.z = ll[2]; l4.w = ll[3];
-    const long off = ct_frag_off(row, d0, D);
-    *reinterpret_cast<ushort4 *>(frag + off) = h4;
-    *reinterpret_cast<ushort4 *>(frag + off + 512) = l4;
+    const long off = ct_frag_off(row, 4 * t, DEC_D);
+    *reinterpret_cast<ushort4 *>(frag + off) = make_ushort4(hh[0], hh[1], hh[2], hh[3]);
+    *reinterpret_cast<ushort4 *>(frag + off + 512) = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
 }
 
-template <int NP>
-__global__ __launch_bounds__(256) void ln_frag_kernel(float *h, uint16_t *frag, const float *parts,
-                                                      long pstride, const uint16_t *pbias,
-                                                      const uint16_t *w, const uint16_t *b, int M,
-                                                      CtWarmSet warm) {
-    constexpr int D = DEC_D;
-    if ((int)blockIdx.x >= M) {
-        // read-ahead workgroups: launch position q runs on XCD q % 8
-        ct_warm_tiles<256>(warm, blockIdx.x & 7, (blockIdx.x - M) >> 3);
-        return;
-    }
-    const int row = blockIdx.x, t = threadIdx.x;
-    float4 *x = reinterpret_cast<float4 *>(h + (long)row * D);
-    // every load first: the row, its partial slices, then the three bf16
-    // vectors (4 entries = 8 bytes each)
-    float4 v = x[t];
-    float4 pr[NP > 0 ? NP : 1];
-#pragma unroll
-    for (int p = 0; p < NP; p++)
-        pr[p] = reinterpret_cast<const float4 *>(parts + p * pstride + (long)row * D)[t];
-    const ushort4 pb4 = (NP > 0 && pbias) ? reinterpret_cast<const ushort4 *>(pbias)[t] : make_ushort4(0, 0, 0, 0);
-    const ushort4 w4 = reinterpret_cast<const ushort4 *>(w)[t];
-    const ushort4 b4 = reinterpret_cast<const ushort4 *>(b)[t];
-    if (NP > 0) {
-        float4 a = pr[0];
-#pragma unroll
-        for (int p = 1; p < NP; p++) {
-            a.x += pr[p].x; a.y += pr[p].y; a.z += pr[p].z; a.w += pr[p].w;
-        }
-        if (pbias) {
-            a.x += bf2f(pb4.x); a.y += bf2f(pb4.y);
-            a.z += bf2f(pb4.z); a.w += bf2f(pb4.w);
-        }
-        v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
-        x[t] = v;
-    }
-    ln_frag_tail(v, w4, b4, frag, row);
-}
-
-// The decode step's first two launches in one: row r's embedding LayerNorm
-// (wave 0, the arithmetic of embed_ln_kernel), written to h for active rows,
-// then the first layer's LayerNorm of h into frag (ln_frag_kernel<0>'s
-// arithmetic; inactive rows normalise their stale h, as there).
-__global__ __launch_bounds__(256) void embed_ln_frag_kernel(float *h, uint16_t *frag, const int *tokens,
-                                                            const int *pos_len, const int *active,
-                                                            const uint16_t *etw, const uint16_t *epw,
-                                                            const uint16_t *elnw, const uint16_t *elnb,
-                                                            const uint16_t *w, const uint16_t *b, int M,
-                                                            CtWarmSet warm) {
+// The decode step's first launch: row r's embedding LayerNorm (wave 0, the
+// arithmetic of embed_ln_kernel), written to h for active rows (inactive rows
+// keep their stale h), then the folded input of the first layer's QKV
+// projection (fold_tail).
+__global__ __launch_bounds__(256) void embed_fold_kernel(float *h, float *lnstat, uint16_t *frag,
+                                                         const int *tokens, const int *pos_len,
+                                                         const int *active, const uint16_t *etw,
+                                                         const uint16_t *epw, const uint16_t *elnw,
+                                                         const uint16_t *elnb, const uint16_t *w, int M,
+                                                         CtWarmSet warm) {
     if ((int)blockIdx.x >= M) {
         ct_warm_tiles<256>(warm, blockIdx.x & 7, (blockIdx.x - M) >> 3);
         return;
@@ -353,7 +304,6 @@ __global__ __launch_bounds__(256) void embed_ln_frag_kernel(float *h, uint16_t *
     const int row = blockIdx.x, t = threadIdx.x;
     __shared__ float4 s_h[DEC_D / 4];
     const ushort4 w4 = reinterpret_cast<const ushort4 *>(w)[t];
-    const ushort4 b4 = reinterpret_cast<const ushort4 *>(b)[t];
     const bool act = active[row] != 0;
     float4 *x = reinterpret_cast<float4 *>(h + (long)row * DEC_D);
     if (!act) {
@@ -371,7 +321,45 @@ __global__ __launch_bounds__(256) void embed_ln_frag_kernel(float *h, uint16_t *
     __syncthreads();
     const float4 v = s_h[t];
     if (act) x[t] = v;
-    ln_frag_tail(v, w4, b4, frag, row);
+    fold_tail(v, w4, lnstat, frag, row);
+}
+
+// Residual update after a K-split projection, one 256-thread workgroup per
+// row: h += ((parts[0] + parts[1]) + ...) + pbias (the slices in order, then
+// the bias), then the folded input of the next GEMM's LayerNorm (fold_tail).
+// NP (the number of slices) is a template parameter so every load is issued
+// before the first add.
+template <int NP>
+__global__ __launch_bounds__(256) void resid_fold_kernel(float *h, float *lnstat, uint16_t *frag,
+                                                         const float *parts, long pstride,
+                                                         const uint16_t *pbias, const uint16_t *w, int M,
+                                                         CtWarmSet warm) {
+    if ((int)blockIdx.x >= M) {
+        // read-ahead workgroups: launch position q runs on XCD q % 8
+        ct_warm_tiles<256>(warm, blockIdx.x & 7, (blockIdx.x - M) >> 3);
+        return;
+    }
+    const int row = blockIdx.x, t = threadIdx.x;
+    float4 *x = reinterpret_cast<float4 *>(h + (long)row * DEC_D);
+    float4 v = x[t];
+    float4 pr[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+        pr[p] = reinterpret_cast<const float4 *>(parts + p * pstride + (long)row * DEC_D)[t];
+    const ushort4 pb4 = pbias ? reinterpret_cast<const ushort4 *>(pbias)[t] : make_ushort4(0, 0, 0, 0);
+    const ushort4 w4 = reinterpret_cast<const ushort4 *>(w)[t];
+    float4 a = pr[0];
+#pragma unroll
+    for (int p = 1; p < NP; p++) {
+        a.x += pr[p].x; a.y += pr[p].y; a.z += pr[p].z; a.w += pr[p].w;
+    }
+    if (pbias) {
+        a.x += bf2f(pb4.x); a.y += bf2f(pb4.y);
+        a.z += bf2f(pb4.z); a.w += bf2f(pb4.w);
+    }
+    v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+    x[t] = v;
+    fold_tail(v, w4, lnstat, frag, row);
 }
 
 }  // namespace
@@ -405,41 +393,6 @@ extern "C" void ctk_layernorm_split(uint16_t *hi, uint16_t *lo, const float *src
         hipLaunchKernelGGL(layernorm_split_kernel<5>, dim3((T + 3) / 4), dim3(256), 0, s, hi, lo, src, w, b, T);
 }
 
-extern "C" void ctk_ln_frag_warm(float *h, uint16_t *frag, const float *parts, int nparts,
-                                 const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,
-                                 const CtWarmSet *warm, hipStream_t s) {
-    if (M <= 0) return;
-    CtWarmSet ws;
-    memset(&ws, 0, sizeof ws);
-    if (warm) ws = *warm;
-    const int G = M + 8 * ct_warm_rows(&ws, "ctk_ln_frag");
-    if ((uintptr_t)h % 16 || (uintptr_t)frag % 16 || (nparts > 0 && (uintptr_t)parts % 16)) {
-        fprintf(stderr, "ctk_ln_frag: needs 16-byte aligned buffers\n");
-        exit(1);
-    }
-    if ((uintptr_t)w % 8 || (uintptr_t)b % 8 || (pbias && (uintptr_t)pbias % 8)) {
-        fprintf(stderr, "ctk_ln_frag: LayerNorm gain/bias and the partials' bias need 8-byte alignment\n");
-        exit(1);
-    }
-    const long ps = (long)M * DEC_D;
-    switch (nparts) {
-    case 0: hipLaunchKernelGGL(ln_frag_kernel<0>, dim3(G), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b, M, ws); break;
-    case 1: hipLaunchKernelGGL(ln_frag_kernel<1>, dim3(G), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b, M, ws); break;
-    case 2: hipLaunchKernelGGL(ln_frag_kernel<2>, dim3(G), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b, M, ws); break;
-    case 4: hipLaunchKernelGGL(ln_frag_kernel<4>, dim3(G), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b, M, ws); break;
-    case 8: hipLaunchKernelGGL(ln_frag_kernel<8>, dim3(G), dim3(256), 0, s, h, frag, parts, ps, pbias, w, b, M, ws); break;
-    default:
-        fprintf(stderr, "ctk_ln_frag: %d partial slices not supported (0, 1, 2, 4, 8)\n", nparts);
-        exit(1);
-    }
-}
-
-extern "C" void ctk_ln_frag(float *h, uint16_t *frag, const float *parts, int nparts,
-                            const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,
-                            hipStream_t s) {
-    ctk_ln_frag_warm(h, frag, parts, nparts, pbias, w, b, M, NULL, s);
-}
-
 extern "C" void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, const int *pos_len,
                              const int *active, const uint16_t *etw, const uint16_t *epw,
                              const uint16_t *lnw, const uint16_t *lnb, hipStream_t s) {
@@ -448,21 +401,47 @@ extern "C" void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, 
                        pos_len, active, etw, epw, lnw, lnb);
 }
 
-extern "C" void ctk_embed_ln_frag(float *h, uint16_t *frag, const int *tokens, const int *pos_len,
-                                  const int *active, const uint16_t *etw, const uint16_t *epw,
-                                  const uint16_t *elnw, const uint16_t *elnb, const uint16_t *w,
-                                  const uint16_t *b, int M, const CtWarmSet *warm, hipStream_t s) {
+extern "C" void ctk_resid_fold(float *h, float *lnstat, uint16_t *frag, const float *parts, int nparts,
+                               const uint16_t *pbias, const uint16_t *w, int M, const CtWarmSet *warm,
+                               hipStream_t s) {
     if (M <= 0) return;
-    if ((uintptr_t)h % 16 || (uintptr_t)frag % 16 || (uintptr_t)w % 8 || (uintptr_t)b % 8) {
-        fprintf(stderr, "ctk_embed_ln_frag: needs 16-byte aligned rows and 8-byte aligned gain/bias\n");
+    if ((uintptr_t)h % 16 || (uintptr_t)frag % 16 || (uintptr_t)parts % 16 || (uintptr_t)lnstat % 8 ||
+        (uintptr_t)w % 8 || (pbias && (uintptr_t)pbias % 8)) {
+        fprintf(stderr, "ctk_resid_fold: needs 16-byte aligned rows and partials, 8-byte aligned lnstat, "
+                        "gain and bias\n");
         exit(1);
     }
     CtWarmSet ws;
     memset(&ws, 0, sizeof ws);
     if (warm) ws = *warm;
-    const int G = M + 8 * ct_warm_rows(&ws, "ctk_embed_ln_frag");
-    hipLaunchKernelGGL(embed_ln_frag_kernel, dim3(G), dim3(256), 0, s, h, frag, tokens, pos_len, active,
-                       etw, epw, elnw, elnb, w, b, M, ws);
+    const int G = M + 8 * ct_warm_rows(&ws, "ctk_resid_fold");
+    const long ps = (long)M * DEC_D;
+    switch (nparts) {
+    case 1: hipLaunchKernelGGL(resid_fold_kernel<1>, dim3(G), dim3(256), 0, s, h, lnstat, frag, parts, ps, pbias, w, M, ws); break;
+    case 2: hipLaunchKernelGGL(resid_fold_kernel<2>, dim3(G), dim3(256), 0, s, h, lnstat, frag, parts, ps, pbias, w, M, ws); break;
+    case 4: hipLaunchKernelGGL(resid_fold_kernel<4>, dim3(G), dim3(256), 0, s, h, lnstat, frag, parts, ps, pbias, w, M, ws); break;
+    case 8: hipLaunchKernelGGL(resid_fold_kernel<8>, dim3(G), dim3(256), 0, s, h, lnstat, frag, parts, ps, pbias, w, M, ws); break;
+    default:
+        fprintf(stderr, "ctk_resid_fold: %d partial slices not supported (1, 2, 4, 8)\n", nparts);
+        exit(1);
+    }
+}
+
+extern "C" void ctk_embed_fold(float *h, float *lnstat, uint16_t *frag, const int *tokens,
+                               const int *pos_len, const int *active, const uint16_t *etw,
+                               const uint16_t *epw, const uint16_t *elnw, const uint16_t *elnb,
+                               const uint16_t *w, int M, const CtWarmSet *warm, hipStream_t s) {
+    if (M <= 0) return;
+    if ((uintptr_t)h % 16 || (uintptr_t)frag % 16 || (uintptr_t)lnstat % 8 || (uintptr_t)w % 8) {
+        fprintf(stderr, "ctk_embed_fold: needs 16-byte aligned rows, 8-byte aligned lnstat and gain\n");
+        exit(1);
+    }
+    CtWarmSet ws;
+    memset(&ws, 0, sizeof ws);
+    if (warm) ws = *warm;
+    const int G = M + 8 * ct_warm_rows(&ws, "ctk_embed_fold");
+    hipLaunchKernelGGL(embed_fold_kernel, dim3(G), dim3(256), 0, s, h, lnstat, frag, tokens, pos_len, active,
+                       etw, epw, elnw, elnb, w, M, ws);
 }
 
 extern "C" void ctk_argmax(int *out, const float *logits, int R, int n, const int *active,

@@ -13,8 +13,8 @@ class CtGemv(C.Structure):
                 ("Y", C.c_void_p), ("ldy", C.c_long), ("F", C.c_void_p),
                 ("kc", C.c_void_p), ("vc", C.c_void_p), ("rowoff", C.c_void_p),
                 ("hstride", C.c_long), ("kv_bf16", C.c_int), ("wtile", C.c_int),
-                ("m_active", C.c_void_p), ("lnstat", C.c_void_p), ("X", C.c_void_p),
-                ("ldx", C.c_long), ("lnw", C.c_void_p), ("lnb", C.c_void_p)]
+                ("m_active", C.c_void_p), ("lnstat", C.c_void_p), ("fold_w", C.c_void_p),
+                ("fold_c1", C.c_void_p), ("fold_c2", C.c_void_p)]
 
 
 class CtWarm(C.Structure):

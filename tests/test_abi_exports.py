@@ -84,7 +84,8 @@ def test_gemv_read_ahead_descriptor_covers_each_tile_once():
     widths = set()
     for M in (8, 24, 64, 80):
         for N, K, partial, out in ((3072, 1024, False, 3), (3072, 1024, False, 1), (1024, 1024, True, 0),
-                                   (4096, 1024, False, 2), (1024, 4096, True, 0), (16384, 1024, False, 1)):
+                                   (4096, 1024, False, 2), (1024, 4096, True, 0), (16384, 1024, False, 1),
+                                   (1024, 1024, False, 4), (1024, 4096, False, 4), (1024, 1024, False, 1)):
             ks = lib.ctk_gemv_ksplit(N, K) if partial else 1
             g = CtGemv(W=1 << 20, M=M, N=N, K=K, ksplit=ks, wtile=1, out=out)
             w = CtWarm()

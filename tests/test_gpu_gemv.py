@@ -1,5 +1,7 @@
-"""GPU checks of the decode step's GEMM (ctk_gemv) and residual LayerNorm
-(ctk_ln_frag), called through libct_hip.so's C entry points.
+"""GPU checks of the decode step's GEMM (ctk_gemv), its folded LayerNorms
+(residual projections leaving frag(h * w) and block statistics, GEMMs that
+correct each row in the epilogue) and the step's embedding launch, called
+through libct_hip.so's C entry points.
 
 The activations are given directly as (hi, lo) bf16 pairs in the frag layout,
 so the exact operand is x = hi + lo and the float64 product x W^T is the
@@ -18,7 +20,7 @@ from structs import CtGemv, CtWarm, CtWarmSet
 
 pytestmark = pytest.mark.gpu
 
-PARTIAL, DENSE, FRAG, QKV = 0, 1, 2, 3
+PARTIAL, DENSE, FRAG, QKV, RESID = 0, 1, 2, 3, 4
 TOL = 1e-5
 
 
@@ -79,24 +81,26 @@ def lib(hip):
     assert C.sizeof(CtGemv) == L.ctk_gemv_sizeof()
     assert C.sizeof(CtWarmSet) == L.ctk_warmset_sizeof()
     L.ctk_gemv_warm.argtypes = [C.POINTER(CtGemv), C.POINTER(CtWarm)]
-    L.ctk_ln_frag_warm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
-                                   C.c_void_p, C.c_void_p, C.c_int, C.POINTER(CtWarmSet),
-                                   C.c_void_p]
+    L.ctk_embed_fold.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                 C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                 C.POINTER(CtWarmSet), C.c_void_p]
+    L.ctk_resid_fold.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                 C.c_void_p, C.c_int, C.POINTER(CtWarmSet), C.c_void_p]
+    L.ctk_fold_cols.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                C.c_void_p, C.c_void_p, C.c_void_p]
     L.ctk_gemv.argtypes = [C.POINTER(CtGemv), C.c_void_p]
     L.ctk_gemv_ksplit.argtypes = [C.c_int, C.c_int]
     L.ctk_gemv_ksplit.restype = C.c_int
     L.ctk_tile_w.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
-    L.ctk_ln_frag.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
-                              C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
     return L
 
 
 class Dev:
     """Arena-backed device buffers of raw bytes."""
 
-    def __init__(self, hip):
+    def __init__(self, hip, floats=1 << 25):
         self.hip = hip
-        self.ar = ks.ArenaDev(hip, floats=1 << 25)
+        self.ar = ks.ArenaDev(hip, floats=floats)
         self.ev = cb.HipEvents()
 
     def put(self, a):
@@ -249,84 +253,6 @@ def test_gemv_qkv_scatter(lib, hip):
             assert np.all(others == 0x3F80), (name, m)
 
 
-def test_ln_frag(lib, hip):
-    """h += ((p0 + p1) + ...) + bias in that order, then LayerNorm (two-pass
-    mean / variance, eps 1e-5, backends/cpu/backend.c:109-122) split into frag."""
-    dev = Dev(hip)
-    rng = np.random.default_rng(5)
-    D = 1024
-    for M, nparts in ((1, 0), (64, 4), (70, 8)):
-        print(f"case: ln_frag M={M} nparts={nparts}", flush=True)
-        h = rng.standard_normal((M, D)).astype(np.float32)
-        parts = rng.standard_normal((max(nparts, 1), M, D)).astype(np.float32)
-        pb = f32_to_bf16(rng.standard_normal(D).astype(np.float32) * 0.1)
-        w = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32))
-        bb = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
-        ph = dev.put(h)
-        pf = dev.zeros(frag_elems(M, D) * 2)
-        pp = dev.put(parts)
-        dev.ev.sync()
-        lib.ctk_ln_frag(ph, pf, pp, nparts, dev.put(pb), dev.put(w), dev.put(bb), M, None)
-        h_new = dev.get(ph, np.float32, M * D).reshape(M, D)
-        if nparts:
-            acc = parts[0].copy()
-            for p in range(1, nparts):
-                acc = acc + parts[p]
-            want_h = h + (acc + bf16_to_f32(pb))
-            assert np.array_equal(h_new.view(np.uint32), want_h.astype(np.float32).view(np.uint32))
-        else:
-            assert np.array_equal(h_new, h)
-        x = h_new.astype(np.float64)
-        mu = x.mean(1, keepdims=True)
-        var = ((x - mu) ** 2).mean(1, keepdims=True)
-        ref = (x - mu) / np.sqrt(var + 1e-5) * bf16_to_f32(w) + bf16_to_f32(bb)
-        hi, lo = from_frag(dev.get(pf, np.uint16, frag_elems(M, D)), M, D)
-        got = bf16_to_f32(hi).astype(np.float64) + bf16_to_f32(lo)
-        assert rel(got, ref) <= 1e-5
-
-
-def test_ln_frag_read_ahead_leaves_results(lib, hip):
-    """Read-ahead workgroups appended to the LayerNorm launch (the tiles of a
-    QKV-shaped and an FFN-down-shaped decode GEMM) change nothing it writes:
-    h and the frag output are bit-identical to the plain launch, and the GEMM
-    that follows on those weights gives the same bits as without."""
-    dev = Dev(hip)
-    rng = np.random.default_rng(11)
-    D, M, nparts = 1024, 80, 4
-    h = rng.standard_normal((M, D)).astype(np.float32)
-    parts = rng.standard_normal((nparts, M, D)).astype(np.float32)
-    pb = f32_to_bf16(rng.standard_normal(D).astype(np.float32) * 0.1)
-    w = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32))
-    bb = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
-    pp, ppb, pw, pbb = dev.put(parts), dev.put(pb), dev.put(w), dev.put(bb)
-    shapes = ((3 * D, D, 1), (D, 4 * D, lib.ctk_gemv_ksplit(D, 4 * D)))
-    ws = CtWarmSet()
-    tiled = []
-    for t, (N, K, ksplit) in enumerate(shapes):
-        wt = f32_to_bf16(0.05 * rng.standard_normal((N, K)).astype(np.float32))
-        praw, ptile = dev.put(wt), dev.zeros(N * K * 2)
-        lib.ctk_tile_w(praw, ptile, N, K, None)
-        g = CtGemv(W=ptile, N=N, K=K, ksplit=ksplit, wtile=1)
-        lib.ctk_gemv_warm(C.byref(g), C.byref(ws.t[t]))
-        assert (ws.t[t].gx * ws.t[t].gy, ws.t[t].per * ws.t[t].gy) == (256 if t else 192, K // 32)
-        tiled.append((ptile, N, K))
-    ws.n, ws.rows, ws.magic, ws.sink = 2, 32, 0x5BD1E995, dev.zeros(1024)
-    outs = []
-    for warm in (None, C.byref(ws)):
-        print(f"case: ln_frag M={M} read-ahead={warm is not None}", flush=True)
-        ph, pf = dev.put(h), dev.zeros(frag_elems(M, D) * 2)
-        dev.ev.sync()
-        lib.ctk_ln_frag_warm(ph, pf, pp, nparts, ppb, pw, pbb, M, warm, None)
-        ptile, N, K = tiled[0]
-        py = dev.zeros(M * N * 4)
-        g = CtGemv(A=pf, W=ptile, M=M, N=N, K=K, ksplit=1, out=1, Y=py, ldy=N, wtile=1)
-        lib.ctk_gemv(C.byref(g), None)
-        outs.append((dev.get(ph, np.uint32, M * D), dev.get(pf, np.uint16, frag_elems(M, D)),
-                     dev.get(py, np.uint32, M * N)))
-    for a, b in zip(*outs):
-        assert np.array_equal(a, b)
-
-
 def wtile_index(N, K):
     """uint16 offset of W[n][k] in the tile layout: one 1024-entry tile per
     (16 rows, K-step of 32), row-block major; lane 16*(k%32//8) + n%16 holds
@@ -369,73 +295,228 @@ def test_gemv_tiled_weights(lib, hip, N, K, out):
             assert np.array_equal(a.view(np.uint32), t.view(np.uint32)), M
 
 
-def test_gemv_residual_stats_and_layernorm_input(lib, hip):
-    """The residual projection (out CT_GV_RESID): h += x W^T + b on the
-    residual rows, leaving each row's (mean, squared deviations) per 32-column
-    block, against float64; then a GEMM whose A is LayerNorm(h) normalised in
-    the kernel from those statistics (CtGemv.X), against the float64 LayerNorm
-    (backends/cpu/backend.c layernorm, eps 1e-5) and product.  Rows must not
-    depend on the launch's row count or on the tile width it takes (M = 8, 24,
-    64 and 80 use 16-, 32- and 64-column tiles): bit-exact; rows past M stay
+def tiled(lib, dev, W):
+    N, K = W.shape
+    praw, pt = dev.put(W), dev.zeros(N * K * 2)
+    lib.ctk_tile_w(praw, pt, N, K, None)
+    return pt
+
+
+def ln64(h, w, b):
+    """The reference LayerNorm (backends/cpu/backend.c:109-122: two-pass
+    mean and variance, eps 1e-5) in float64."""
+    x = np.asarray(h, np.float64)
+    mu = x.mean(1, keepdims=True)
+    var = ((x - mu) ** 2).mean(1, keepdims=True)
+    return (x - mu) / np.sqrt(var + 1e-5) * bf16_to_f32(w) + bf16_to_f32(b)
+
+
+def block_stats64(h):
+    x = np.asarray(h, np.float64).reshape(h.shape[0], 32, 32)
+    mean = x.mean(2)
+    return mean, ((x - mean[..., None]) ** 2).sum(2)
+
+
+def check_fold_input(dev, h, pst, pf, w, rows, what):
+    """lnstat holds each row's (mean, squared deviations) per 32-column block
+    of h (float64, 1e-5), and the frag buffer frag(h * w): the fp32 product,
+    split hi/lo, bit for bit."""
+    M, D = h.shape
+    st = dev.get(pst, np.float32, M * 64).reshape(M, 32, 2)[:rows]
+    mean, m2 = block_stats64(h[:rows])
+    assert np.abs(st[..., 0] - mean).max() <= 1e-5 * max(np.abs(mean).max(), 1.0), what
+    assert np.abs(st[..., 1] - m2).max() <= 1e-5 * m2.max(), what
+    hi, lo = from_frag(dev.get(pf, np.uint16, frag_elems(M, D)), M, D)
+    x = h[:rows] * bf16_to_f32(w)
+    whi, wlo = split(x)
+    bad = np.argwhere((hi[:rows] != whi) | (lo[:rows] != wlo))
+    for m, k in bad[:6]:
+        print(f"  {what}: row {m} col {k}: x {x[m, k]!r} got hi/lo {hi[m, k]:#06x}/{lo[m, k]:#06x} "
+              f"want {whi[m, k]:#06x}/{wlo[m, k]:#06x}")
+    assert len(bad) == 0, (what, len(bad))
+
+
+def test_folded_layernorm_gemms(lib, hip):
+    """The decode step's LayerNorms run inside GEMMs.  A residual projection
+    (out CT_GV_RESID, the attention outputs' projections, K = 1024):
+    h += x W^T + b on the residual rows against float64, leaving each row's
+    block statistics and frag(h * w) of the next LayerNorm's gain.  Then the
+    GEMMs with that LayerNorm folded in (fold_c1 / fold_c2 from ctk_fold_cols,
+    checked against float64 sums): the cross-query shape (dense), FFN up
+    (frag, ReLU) and the LM head (all 64 rows a workgroup) against the float64
+    LayerNorm of h (backends/cpu/backend.c layernorm) times W plus bias,
+    within 2e-5 of the largest output: the rows here have mean 2 and unit
+    spread, so the subtraction of mu * c1 doubles the split's 2^-18 relative
+    error.  Every row's bits are independent of the launch's row count
+    (M = 80, 64, 24, 8: 16-, 32- and 64-column tiles); rows past M stay
     untouched."""
     rng = np.random.default_rng(11)
-    dev = Dev(hip)
-    D, M, N2 = 1024, 80, 4096
+    dev = Dev(hip, floats=1 << 27)
+    D, M = 1024, 80
     h0 = (2.0 + rng.standard_normal((M, D))).astype(np.float32)      # rows with a nonzero mean
-    hi, lo = split(rng.standard_normal((M, D)).astype(np.float32))
-    Wo = f32_to_bf16(rng.standard_normal((D, D)).astype(np.float32) / 32)
-    bo = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
     lnw = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32))
     lnb = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
-    W2 = f32_to_bf16(rng.standard_normal((N2, D)).astype(np.float32) / 32)
-    b2 = f32_to_bf16(0.1 * rng.standard_normal(N2).astype(np.float32))
-
-    def tiled(W):
-        N, K = W.shape
-        praw, pt = dev.put(W), dev.zeros(N * K * 2)
-        lib.ctk_tile_w(praw, pt, N, K, None)
-        return pt
-
-    pWo, pW2 = tiled(Wo), tiled(W2)
-    pa, pbo = dev.put(to_frag(hi, lo)), dev.put(bo)
-    plnw, plnb, pb2 = dev.put(lnw), dev.put(lnb), dev.put(b2)
-    res = {}
-    for m in (80, 64, 24, 8):
-        print(f"case: residual projection + LayerNorm-input GEMM, M={m}", flush=True)
-        ph, pst, py = dev.put(h0), dev.zeros(M * 32 * 8), dev.zeros(M * N2 * 4)
+    plnw, plnb = dev.put(lnw), dev.put(lnb)
+    for K in (1024,):
+        hi, lo = split(rng.standard_normal((M, K)).astype(np.float32))
+        Wo = f32_to_bf16(rng.standard_normal((D, K)).astype(np.float32) / np.sqrt(K))
+        bo = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
+        pWo, pa, pbo = tiled(lib, dev, Wo), dev.put(to_frag(hi, lo)), dev.put(bo)
+        res = {}
+        for m in (80, 64, 24, 8):
+            print(f"case: residual projection K={K} M={m} with the folded next input", flush=True)
+            ph, pst, pf = dev.put(h0), dev.zeros(M * 32 * 8), dev.zeros(frag_elems(M, D) * 2)
+            dev.ev.sync()
+            g = CtGemv(A=pa, W=pWo, bias=pbo, M=m, N=D, K=K, ksplit=1, out=RESID, Y=ph, ldy=D, wtile=1,
+                       lnstat=pst, F=pf, fold_w=plnw)
+            lib.ctk_gemv(C.byref(g), None)
+            res[m] = (dev.get(ph, np.uint32, M * D).reshape(M, D),
+                      dev.get(pst, np.uint32, M * 64).reshape(M, 64),
+                      dev.get(pf, np.uint16, frag_elems(M, D)), (ph, pst, pf))
+            if m == M:
+                h = res[m][0].view(np.float32)
+                x64 = bf16_to_f32(hi).astype(np.float64) + bf16_to_f32(lo)
+                href = h0 + x64 @ bf16_to_f32(Wo).astype(np.float64).T + bf16_to_f32(bo)
+                e = rel(h, href)
+                print(f"  residual relerr {e:.2e}")
+                assert e <= TOL
+                check_fold_input(dev, h, pst, pf, lnw, M, f"resid K={K}")
+        hM, sM, fM, ptrs = res[M]
+        for m in (64, 24, 8):
+            h, st, fr, _ = res[m]
+            assert np.array_equal(h[:m], hM[:m]) and np.array_equal(h[m:], h0[m:].view(np.uint32)), (K, m)
+            assert np.array_equal(st[:m], sM[:m]) and not st[m:].any(), (K, m)
+            fi = frag_index(M, D)
+            assert np.array_equal(fr[fi[:m]], fM[fi[:m]]) and np.array_equal(fr[fi[:m] + 512], fM[fi[:m] + 512])
+    # the GEMMs consuming the projection's output
+    h = hM.view(np.float32)
+    ph, pst, pf = ptrs
+    ln = ln64(h, lnw, lnb)
+    for N, out, relu in ((1024, DENSE, 0), (4096, FRAG, 1), (16384, DENSE, 0)):
+        W2 = f32_to_bf16(rng.standard_normal((N, D)).astype(np.float32) / 32)
+        b2 = f32_to_bf16(0.1 * rng.standard_normal(N).astype(np.float32))
+        praw, pb2 = dev.put(W2), dev.put(b2)
+        pc1, pc2 = dev.zeros(N * 4), dev.zeros(N * 4)
         dev.ev.sync()
-        g = CtGemv(A=pa, W=pWo, bias=pbo, M=m, N=D, K=D, ksplit=1, out=4, Y=ph, ldy=D, wtile=1,
-                   lnstat=pst)
+        lib.ctk_fold_cols(praw, plnw, plnb, pb2, N, D, pc1, pc2, None)
+        W64 = bf16_to_f32(W2).astype(np.float64)
+        c1 = dev.get(pc1, np.float32, N)
+        c2 = dev.get(pc2, np.float32, N)
+        assert np.abs(c1 - W64 @ bf16_to_f32(lnw)).max() <= 2 ** -23 * np.abs(c1).max()
+        assert np.abs(c2 - (W64 @ bf16_to_f32(lnb) + bf16_to_f32(b2))).max() <= 2 ** -23 * np.abs(c2).max()
+        pW2 = tiled(lib, dev, W2)
+        ref = ln @ W64.T + bf16_to_f32(b2)
+        if relu:
+            ref = np.maximum(ref, 0.0)
+        outs = {}
+        for m in ((80, 64, 24, 8) if N < 16384 else (64, 24)):
+            print(f"case: folded LayerNorm GEMM N={N} out={out} M={m}", flush=True)
+            g = CtGemv(A=pf, W=pW2, M=m, N=N, K=D, ksplit=1, out=out, relu=relu, wtile=1, lnstat=pst,
+                       fold_c1=pc1, fold_c2=pc2)
+            if out == DENSE:
+                g.Y, g.ldy = dev.zeros(M * N * 4), N
+            else:
+                g.F = dev.zeros(frag_elems(M, N) * 2)
+            dev.ev.sync()
+            lib.ctk_gemv(C.byref(g), None)
+            if out == DENSE:
+                y = dev.get(g.Y, np.float32, M * N).reshape(M, N)
+                assert not y[m:].any(), (N, m)
+                y = y[:m]
+            else:
+                yh, yl = from_frag(dev.get(g.F, np.uint16, frag_elems(M, N)), M, N)
+                y = (bf16_to_f32(yh).astype(np.float64) + bf16_to_f32(yl))[:m]
+            outs[m] = y
+            e = rel(y, ref[:m])
+            print(f"  relerr {e:.2e}")
+            assert e <= 2e-5, (N, m, e)
+        m0 = max(outs)
+        for m, y in outs.items():
+            assert np.array_equal(np.asarray(y).view(np.uint64 if y.dtype == np.float64 else np.uint32),
+                                  np.asarray(outs[m0][:m]).view(np.uint64 if y.dtype == np.float64 else np.uint32)), (N, m)
+
+
+def test_embed_fold_and_read_ahead(lib, hip):
+    """The step's embedding launch: h = LN_e(etw[token] + epw[pos - 1]) for
+    active rows (float64, 1e-5; inactive rows keep their h), then each row's
+    block statistics and frag(h * w) for the first layer's folded LayerNorm.
+    Read-ahead workgroups appended to it (the tiles of a QKV-shaped and an
+    FFN-down-shaped decode GEMM) change nothing it writes, bit for bit, nor
+    the bits of the GEMM that follows on those weights."""
+    dev = Dev(hip)
+    rng = np.random.default_rng(12)
+    D, M, V, P = 1024, 80, 40, 30
+    etw = f32_to_bf16(rng.standard_normal((V, D)).astype(np.float32))
+    epw = f32_to_bf16(0.5 * rng.standard_normal((P, D)).astype(np.float32))
+    elnw = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32))
+    elnb = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
+    w = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32))
+    tok = rng.integers(0, V, M).astype(np.int32)
+    pos = rng.integers(1, P + 1, M).astype(np.int32)
+    act = (rng.random(M) < 0.8).astype(np.int32)
+    h0 = rng.standard_normal((M, D)).astype(np.float32)
+    ptr = [dev.put(a) for a in (tok, pos, act, etw, epw, elnw, elnb, w)]
+    shapes = ((3 * D, D, QKV), (D, 4 * D, RESID))
+    ws = CtWarmSet()
+    tiles = []
+    for t, (N, K, out) in enumerate(shapes):
+        wt = f32_to_bf16(0.05 * rng.standard_normal((N, K)).astype(np.float32))
+        ptile = tiled(lib, dev, wt)
+        g = CtGemv(W=ptile, N=N, K=K, M=M, ksplit=1, out=out, wtile=1)
+        lib.ctk_gemv_warm(C.byref(g), C.byref(ws.t[t]))
+        tiles.append((ptile, N, K))
+    ws.n, ws.rows, ws.magic, ws.sink = 2, 32, 0x5BD1E995, dev.zeros(1024)
+    outs = []
+    for warm in (None, C.byref(ws)):
+        print(f"case: embedding fold M={M} read-ahead={warm is not None}", flush=True)
+        ph, pst, pf = dev.put(h0), dev.zeros(M * 32 * 8), dev.zeros(frag_elems(M, D) * 2)
+        dev.ev.sync()
+        lib.ctk_embed_fold(ph, pst, pf, *ptr, M, warm, None)
+        ptile, N, K = tiles[1]
+        py = dev.zeros(M * 4 * D * 4)
+        g = CtGemv(A=pf, W=tiles[0][0], M=M, N=D, K=D, ksplit=1, out=DENSE, Y=py, ldy=D, wtile=1)
         lib.ctk_gemv(C.byref(g), None)
-        g2 = CtGemv(X=ph, ldx=D, lnstat=pst, lnw=plnw, lnb=plnb, W=pW2, bias=pb2, M=m, N=N2, K=D,
-                    ksplit=1, out=DENSE, Y=py, ldy=N2, wtile=1)
-        lib.ctk_gemv(C.byref(g2), None)
-        res[m] = (dev.get(ph, np.float32, M * D).reshape(M, D),
-                  dev.get(pst, np.float32, M * 64).reshape(M, 32, 2),
-                  dev.get(py, np.float32, M * N2).reshape(M, N2))
-    h, st, y = res[M]
-    x64 = bf16_to_f32(hi).astype(np.float64) + bf16_to_f32(lo)
-    href = h0 + x64 @ bf16_to_f32(Wo).astype(np.float64).T + bf16_to_f32(bo)
-    e = np.abs(h - href).max() / np.abs(href).max()
-    print(f"  residual relerr {e:.2e}")
-    assert e <= TOL
-    blk = h.astype(np.float64).reshape(M, 32, 32)
-    mean = blk.mean(2)
-    m2 = ((blk - mean[:, :, None]) ** 2).sum(2)
-    assert np.abs(st[:, :, 0] - mean).max() <= 1e-6 * np.abs(mean).max()
-    assert np.all(np.abs(st[:, :, 1] - m2) <= 1e-5 * m2 + 1e-6 * m2.max())
-    hd = h.astype(np.float64)
-    mu = hd.mean(1, keepdims=True)
-    var = ((hd - mu) ** 2).mean(1, keepdims=True)
-    ln = (hd - mu) / np.sqrt(var + 1e-5) * bf16_to_f32(lnw) + bf16_to_f32(lnb)
-    yref = ln @ bf16_to_f32(W2).astype(np.float64).T + bf16_to_f32(b2)
-    e = np.abs(y - yref).max() / np.abs(yref).max()
-    print(f"  LayerNorm-input GEMM relerr {e:.2e}")
-    assert e <= TOL
-    for m in (64, 24, 8):
-        hm, sm, ym = res[m]
-        assert np.array_equal(hm[:m].view(np.uint32), h[:m].view(np.uint32)), m
-        assert np.array_equal(sm[:m].view(np.uint32), st[:m].view(np.uint32)), m
-        assert np.array_equal(ym[:m].view(np.uint32), y[:m].view(np.uint32)), m
-        assert np.array_equal(hm[m:].view(np.uint32), h0[m:].view(np.uint32)), m
-        assert not sm[m:].any() and not ym[m:].any(), m
+        outs.append((dev.get(ph, np.uint32, M * D), dev.get(pst, np.uint32, M * 64),
+                     dev.get(pf, np.uint16, frag_elems(M, D)), dev.get(py, np.uint32, M * D)))
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    h = outs[0][0].view(np.float32).reshape(M, D)
+    e = bf16_to_f32(etw)[tok].astype(np.float64) + bf16_to_f32(epw)[pos - 1]
+    want = ln64(e, elnw, elnb)
+    on = act != 0
+    assert rel(h[on], want[on]) <= 1e-5
+    assert np.array_equal(h[~on], h0[~on])
+    check_fold_input(dev, h, pst, pf, w, M, "embedding")
+
+
+def test_resid_fold_after_k_split(lib, hip):
+    """The residual update after the K-split FFN down projection:
+    h += ((p0 + p1) + ... + p7) + bias, the slices in order then the bias,
+    bit for bit against the same fp32 sums, then the next LayerNorm's folded
+    input (block statistics, frag(h * w)); rows independent of M."""
+    dev = Dev(hip)
+    rng = np.random.default_rng(13)
+    D, M, NP = 1024, 80, 8
+    h0 = (1.5 + rng.standard_normal((M, D))).astype(np.float32)
+    parts = (0.3 * rng.standard_normal((NP, M, D))).astype(np.float32)
+    pb = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
+    w = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32))
+    pp, ppb, pw = dev.put(parts), dev.put(pb), dev.put(w)
+    res = {}
+    for m in (80, 37):
+        print(f"case: residual update after a K split, M={m}", flush=True)
+        ph, pst, pf = dev.put(h0), dev.zeros(M * 32 * 8), dev.zeros(frag_elems(M, D) * 2)
+        dev.ev.sync()
+        pparts = pp if m == M else dev.put(np.ascontiguousarray(parts[:, :m]))
+        lib.ctk_resid_fold(ph, pst, pf, pparts, NP, ppb, pw, m, None, None)
+        res[m] = (dev.get(ph, np.uint32, M * D).reshape(M, D), dev.get(pst, np.uint32, M * 64).reshape(M, 64))
+        if m == M:
+            acc = parts[0].copy()
+            for p in range(1, NP):
+                acc = acc + parts[p]
+            want = h0 + (acc + bf16_to_f32(pb))
+            h = res[m][0].view(np.float32)
+            assert np.array_equal(h.view(np.uint32), want.astype(np.float32).view(np.uint32))
+            check_fold_input(dev, h, pst, pf, w, M, "resid fold")
+    assert np.array_equal(res[37][0][:37], res[M][0][:37]) and np.array_equal(res[37][0][37:], h0[37:].view(np.uint32))
+    assert np.array_equal(res[37][1][:37], res[M][1][:37])
