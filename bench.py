@@ -279,13 +279,21 @@ def decode_b64(model, ev, samples, limits, reps=20):
     return attention, step
 
 
+# The decode step's weights (N, K): per layer QKV, out, cross Q, cross out,
+# FFN up, FFN down, then the LM head.
 DEC_GEMMS = ([(3 * cb.DEC_D, cb.DEC_D), (cb.DEC_D, cb.DEC_D), (cb.DEC_D, cb.DEC_D), (cb.DEC_D, cb.DEC_D),
               (cb.DEC_FF, cb.DEC_D), (cb.DEC_D, cb.DEC_FF)] * cb.DEC_N + [(cb.VOCAB, cb.DEC_D)])
 
 
+def dec_gemm_launch_bytes(slots):
+    """Algorithmic bytes of the step's 49 GEMM launches: weights, input rows
+    (fp32-equivalent hi+lo) and output rows (fp32)."""
+    return [N * K * 2 + slots * K * 4 + slots * N * 4 for N, K in DEC_GEMMS]
+
+
 def decode_gemm_roofline(model, ev, slots=64, reps=20):
-    """The decode step's GEMMs alone (8 x QKV, out, cross Q, cross out, FFN up,
-    FFN down; LM head) at the stream's slot count."""
+    """The decode step's GEMM launches alone (8 x QKV, out, cross Q, cross
+    out, FFN up, FFN down; LM head: 49 launches) at the stream's slot count."""
     rng = np.random.default_rng(6)
     S = rng.integers(1, 201, slots)
     T = rng.integers(26, 377, slots)
@@ -312,18 +320,19 @@ def decode_gemm_roofline(model, ev, slots=64, reps=20):
         floor_us = ev.ms(a2, b2) * 1e3 / reps
     finally:
         eng.close()
-    n = len(DEC_GEMMS)
+    per = dec_gemm_launch_bytes(slots)
+    n = len(per)
     w_bytes = float(sum(N * K * 2 for N, K in DEC_GEMMS))
-    # weights once, activations in (fp32-equivalent hi+lo), outputs (fp32)
-    bytes_step = float(sum(N * K * 2 + slots * K * 4 + slots * N * 4 for N, K in DEC_GEMMS))
+    bytes_step = float(sum(per))
     per_launch_us = step_us / n
     achieved = bytes_step / (step_us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "gemv_kernel (decode GEMMs, all instances)", "avg_launch_us": round(per_launch_us, 3),
-            "bytes_per_launch": int(bytes_step / n), "launches_per_step": n,
-            "workload": f"{slots} slots, one step's 49 GEMMs (268.4 MB of bf16 weights)",
-            "read_floor": {"avg_launch_us": round(floor_us / n, 3),
+            "kernel": "gemv_kernel (decode GEMMs, all instances)",
+            "avg_launch_us": round(per_launch_us, 3),
+            "bytes_per_launch": int(bytes_step / n), "launches_per_step": n, "step_us": round(step_us, 2),
+            "workload": f"{slots} slots, one step's {n} GEMM launches (268.4 MB of bf16 weights)",
+            "read_floor": {"step_us": round(floor_us, 2),
                            "weight_GBs": round(w_bytes / (floor_us * 1e-6) / 1e9, 1),
                            "gemm_over_floor": round(step_us / floor_us, 3),
                            "what": "the same 49 launches (grids, weight tiles per workgroup) reading "

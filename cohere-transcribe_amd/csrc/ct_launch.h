@@ -194,14 +194,15 @@ void ctk_tile_w(const uint16_t *W, uint16_t *Wt, int N, int K, hipStream_t s);
 int  ctk_gemv_ksplit(int N, int K);
 
 /* Residual update after a K-split projection (rows r < M): h[r] += ((parts[0][r]
- * + parts[1][r]) + ...) + pbias, the nparts slices (1, 2, 4 or 8) M * DEC_D
- * floats apart; then the folded input of the next GEMM's LayerNorm with gain
- * w (CtGemv.fold_c1): each 32-column block's (mean, squared deviations) of
- * h[r] into lnstat[r*32 + b] and frag(h[r] * w); carrying the read-ahead warm
+ * + parts[1][r]) + ...) + pbias, the nparts = 8 slices M * DEC_D floats
+ * apart; then, with b NULL, the folded input of the next GEMM's LayerNorm
+ * with gain w (CtGemv.fold_c1): each 32-column block's (mean, squared
+ * deviations) of h[r] into lnstat[r*32 + b] and frag(h[r] * w); with b,
+ * frag(LayerNorm(h[r])) with gain w and bias b.  Carries the read-ahead warm
  * (NULL: none). */
 void ctk_resid_fold(float *h, float *lnstat, uint16_t *frag, const float *parts, int nparts,
-                    const uint16_t *pbias, const uint16_t *w, int M, const CtWarmSet *warm,
-                    hipStream_t s);
+                    const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,
+                    const CtWarmSet *warm, hipStream_t s);
 /* The decode step's embedding: for active rows r < M, h[r] = LN_e(etw[tokens[r]]
  * + epw[pos_len[r] - 1]) (as ctk_embed_ln); then for every row the folded
  * input of the first layer's LayerNorm with gain w (CtGemv.fold_c1): each

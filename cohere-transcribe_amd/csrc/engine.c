@@ -78,14 +78,14 @@ struct HipbEngine {
     atomic_int stop;           /* hipb_process ends: the encoder thread quits its wait */
     /* step activations: h residual rows (fp32); lnf/attf/midf the decode
      * GEMMs' inputs in frag layout (lnf holds h * w, the input of the next
-     * GEMM with its LayerNorm folded in); parts the FFN down projection's
-     * K-slice partial sums; lnstat the rows' statistics per 32-column block,
-     * left with lnf for that GEMM */
+     * GEMM with its LayerNorm folded in, or the final LayerNorm's output);
+     * parts the FFN down projection's K-slice partial sums; lnstat the rows'
+     * statistics per 32-column block, left with lnf for that GEMM */
     float *h, *q, *parts, *logits, *lnstat;
     /* folded LayerNorms: per layer the c1 / c2 column constants of the QKV,
-     * cross-query and FFN-up GEMMs, then the LM head's (ctk_fold_cols) */
+     * cross-query and FFN-up GEMMs (ctk_fold_cols) */
     float *fold;
-    const float *fc_qkv[DEC_N][2], *fc_cq[DEC_N][2], *fc_f1[DEC_N][2], *fc_lm[2];
+    const float *fc_qkv[DEC_N][2], *fc_cq[DEC_N][2], *fc_f1[DEC_N][2];
     int M;                     /* rows of the step being launched */
     /* decode GEMMs whose weight tiles the next attention launch reads ahead
      * into the L2 their workgroups will read from */
@@ -389,7 +389,7 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     {
         /* column constants of the GEMMs whose LayerNorm is folded in */
         const size_t per = 2 * (3 * DEC_D + DEC_D + DEC_FF);
-        e->fold = dmalloc((DEC_N * per + 2 * (size_t)VOCAB) * sizeof(float));
+        e->fold = dmalloc(DEC_N * per * sizeof(float));
         float *p = e->fold;
         for (int l = 0; l < DEC_N; l++) {
             const DLayer *L = &W->dec[l];
@@ -403,8 +403,6 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
                           p + DEC_FF, e->s);
             e->fc_f1[l][0] = p; e->fc_f1[l][1] = p + DEC_FF; p += 2 * DEC_FF;
         }
-        ctk_fold_cols(DW(W->etw), DW(W->dlnw), DW(W->dlnb), DW(W->hdb), VOCAB, DEC_D, p, p + VOCAB, e->s);
-        e->fc_lm[0] = p; e->fc_lm[1] = p + VOCAB;
     }
     const size_t self_el = (size_t)DEC_N * S * DEC_H * d->kv_rows * DEC_DK;
     const size_t cross_el = (size_t)DEC_N * R * DEC_H * tmax * DEC_DK;
@@ -416,9 +414,9 @@ HipbEngine *hipb_create(const HipbConfig *cfg, const Weights *W) {
     e->h = dmalloc((size_t)NR * DEC_D * 4);
     e->q = dmalloc((size_t)NR * DEC_D * 4);
     e->parts = dmalloc((size_t)ctk_gemv_ksplit(DEC_D, DEC_FF) * NR * DEC_D * 4);
+    e->midf = dmalloc(ct_frag_elems(NR, DEC_FF) * 2);
     e->lnf = dmalloc(ct_frag_elems(NR, DEC_D) * 2);
     e->attf = dmalloc(ct_frag_elems(NR, DEC_D) * 2);
-    e->midf = dmalloc(ct_frag_elems(NR, DEC_FF) * 2);
     e->logits = dmalloc((size_t)S * VOCAB * 4);
     e->lnstat = dmalloc((size_t)NR * CT_LN_BLOCKS * 2 * 4);
     ECHK(hipMemsetAsync(e->h, 0, (size_t)NR * DEC_D * 4, e->s));
@@ -1339,6 +1337,19 @@ static void gv_fold(HipbEngine *e, const uint16_t *Wd, const float *const c[2], 
     launch_gemv(e, &g);
 }
 
+/* A plain decode GEMM over all rows into a dense output (the LM head). */
+static void gv_dense(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const uint16_t *bd, int N, int K,
+                     float *Y, long ldy) {
+    CtGemv g;
+    memset(&g, 0, sizeof g);
+    g.A = A; g.W = Wd; g.bias = bd; g.wtile = 1;
+    g.M = e->M; g.N = N; g.K = K; g.ksplit = 1;
+    g.m_active = e->M > e->d.slots ? e->d.q + 6 : NULL;
+    g.out = CT_GV_DENSE;
+    g.Y = Y; g.ldy = ldy;
+    launch_gemv(e, &g);
+}
+
 /* A K-split decode GEMM: its slices' partial sums go to parts. */
 static void gv_partial(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, int N, int K) {
     CtGemv g;
@@ -1371,14 +1382,15 @@ static void gv_resid(HipbEngine *e, const uint16_t *A, const uint16_t *Wd, const
  * whose spare rows feed prompts several tokens a step.  full == 0 launches
  * only its GEMMs (timing support).
  *
- * Every LayerNorm of the decoder runs inside the GEMM that consumes it: the
- * residual projections of the attention outputs, the residual update after
- * the K-split FFN down projection and the embedding leave h, its block
+ * Every LayerNorm of the decoder but the last runs inside the GEMM that
+ * consumes it: the residual projections of the attention outputs, the
+ * residual update after the FFN and the embedding leave h, its block
  * statistics and frag(h * w) of the next LayerNorm's gain, and the next GEMM
  * corrects each row in its epilogue (gemv_kernel FOLD).  A layer is 9
  * launches: QKV, self attention, out projection, cross query, cross
  * attention, cross out projection, FFN up, FFN down (8 K-slices), residual
- * update. */
+ * update (the next layer's, or with the final LayerNorm before the LM
+ * head). */
 static void step_kernels(HipbEngine *e, int full, int wide) {
     const Weights *W = &e->W;
     const int B = wide ? e->d.rows : e->d.slots;
@@ -1404,7 +1416,7 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
             CtWarmSet ws;
             warm_take(e, &ws);
             ctk_resid_fold(e->h, e->lnstat, e->lnf, e->parts, ctk_gemv_ksplit(DEC_D, DEC_FF),
-                           DW(W->dec[l - 1].ffn_b2), DW(L->sa_lnw), B, &ws, s);
+                           DW(W->dec[l - 1].ffn_b2), DW(L->sa_lnw), NULL, B, &ws, s);
         }
         CtGemv g;
         memset(&g, 0, sizeof g);
@@ -1433,13 +1445,13 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         gv_fold(e, w_f1, e->fc_f1[l], DEC_FF, CT_GV_FRAG, 1, NULL, 0, e->midf);
         gv_partial(e, e->midf, w_f2, DEC_D, DEC_FF);
     }
-    /* h += the last FFN, with the final LayerNorm's folded input */
+    /* h += the last FFN, then the final LayerNorm */
     if (full)
         ctk_resid_fold(e->h, e->lnstat, e->lnf, e->parts, ctk_gemv_ksplit(DEC_D, DEC_FF),
-                       DW(W->dec[DEC_N - 1].ffn_b2), DW(W->dlnw), B, NULL, s);
+                       DW(W->dec[DEC_N - 1].ffn_b2), DW(W->dlnw), DW(W->dlnb), B, NULL, s);
     /* logits only for the slots' own rows */
     e->M = e->d.slots;
-    gv_fold(e, e->wt_lm, e->fc_lm, VOCAB, CT_GV_DENSE, 0, e->logits, VOCAB, NULL);
+    gv_dense(e, e->lnf, e->wt_lm, DW(W->hdb), VOCAB, DEC_D, e->logits, VOCAB);
     if (full) ctk_eng_end(&e->d, e->logits, s);
     e->M = e->d.slots;
 }

@@ -22,9 +22,11 @@
 // fmadd), with x = hi + lo exactly representable to 2^-17 relative.
 #include "ct_dev.h"
 #include "ct_launch.h"
+#include "ct_warm.h"
 #include "../../include/model_types.h"
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 namespace {
 
@@ -473,7 +475,7 @@ extern "C" void ctk_gemv(const CtGemv *g, hipStream_t s) {
     }
     GV_CASE(1, 1, 1) GV_CASE(1, 2, 1) GV_CASE(1, 4, 1) GV_CASE(2, 1, 1) GV_CASE(2, 2, 1) GV_CASE(2, 4, 1)
     GV_CASE(4, 1, 1) GV_CASE(4, 2, 1) GV_CASE(4, 4, 1) GV_CASE(4, 1, 4) GV_CASE(4, 2, 4) GV_CASE(4, 4, 4)
-    GV_FOLD(1, 1) GV_FOLD(2, 1) GV_FOLD(4, 1) GV_FOLD(4, 4)
+    GV_FOLD(1, 1) GV_FOLD(2, 1) GV_FOLD(4, 1)
 #undef GV_CASE
 #undef GV_FOLD
     gv_fatal("no kernel for this K slice", g);

@@ -287,6 +287,32 @@ __device__ __forceinline__ void fold_tail(float4 v, ushort4 w4, float *lnstat, u
     *reinterpret_cast<ushort4 *>(frag + off + 512) = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
 }
 
+// The two-pass LayerNorm of one row held as a float4 per thread (mean, then
+// the variance of the centred values, eps 1e-5; backends/cpu/backend.c:
+// 109-122), each output split hi/lo into frag.
+__device__ __forceinline__ void ln_tail(float4 v, ushort4 w4, ushort4 b4, uint16_t *frag, int row) {
+    const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
+    __shared__ float red[2][4];
+    const float s = wave_sum((v.x + v.y) + (v.z + v.w));
+    if (lane == 0) red[0][wv] = s;
+    __syncthreads();
+    const float mu = ((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])) / (float)DEC_D;
+    const float c0 = v.x - mu, c1 = v.y - mu, c2 = v.z - mu, c3 = v.w - mu;
+    const float q = wave_sum((c0 * c0 + c1 * c1) + (c2 * c2 + c3 * c3));
+    if (lane == 0) red[1][wv] = q;
+    __syncthreads();
+    const float var = ((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) / (float)DEC_D;
+    const float rs = 1.0f / sqrtf(var + 1e-5f);
+    const float o[4] = {c0 * rs * bf2f(w4.x) + bf2f(b4.x), c1 * rs * bf2f(w4.y) + bf2f(b4.y),
+                        c2 * rs * bf2f(w4.z) + bf2f(b4.z), c3 * rs * bf2f(w4.w) + bf2f(b4.w)};
+    uint16_t hh[4], ll[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) split_bf16(o[j], hh[j], ll[j]);
+    const long off = ct_frag_off(row, 4 * t, DEC_D);
+    *reinterpret_cast<ushort4 *>(frag + off) = make_ushort4(hh[0], hh[1], hh[2], hh[3]);
+    *reinterpret_cast<ushort4 *>(frag + off + 512) = make_ushort4(ll[0], ll[1], ll[2], ll[3]);
+}
+
 // The decode step's first launch: row r's embedding LayerNorm (wave 0, the
 // arithmetic of embed_ln_kernel), written to h for active rows (inactive rows
 // keep their stale h), then the folded input of the first layer's QKV
@@ -325,15 +351,15 @@ __global__ __launch_bounds__(256) void embed_fold_kernel(float *h, float *lnstat
 }
 
 // Residual update after a K-split projection, one 256-thread workgroup per
-// row: h += ((parts[0] + parts[1]) + ...) + pbias (the slices in order, then
-// the bias), then the folded input of the next GEMM's LayerNorm (fold_tail).
-// NP (the number of slices) is a template parameter so every load is issued
-// before the first add.
-template <int NP>
+// row, a float4 per thread: h += ((parts[0] + parts[1]) + ...) + pbias (the
+// slices in order, then the bias), every load issued before the first add;
+// then (NORM false) the folded input of the next GEMM's LayerNorm with gain w
+// (fold_tail), or (NORM) the LayerNorm itself with gain w and bias b (ln_tail).
+template <int NP, bool NORM>
 __global__ __launch_bounds__(256) void resid_fold_kernel(float *h, float *lnstat, uint16_t *frag,
                                                          const float *parts, long pstride,
-                                                         const uint16_t *pbias, const uint16_t *w, int M,
-                                                         CtWarmSet warm) {
+                                                         const uint16_t *pbias, const uint16_t *w,
+                                                         const uint16_t *b, int M, CtWarmSet warm) {
     if ((int)blockIdx.x >= M) {
         // read-ahead workgroups: launch position q runs on XCD q % 8
         ct_warm_tiles<256>(warm, blockIdx.x & 7, (blockIdx.x - M) >> 3);
@@ -348,6 +374,7 @@ __global__ __launch_bounds__(256) void resid_fold_kernel(float *h, float *lnstat
         pr[p] = reinterpret_cast<const float4 *>(parts + p * pstride + (long)row * DEC_D)[t];
     const ushort4 pb4 = pbias ? reinterpret_cast<const ushort4 *>(pbias)[t] : make_ushort4(0, 0, 0, 0);
     const ushort4 w4 = reinterpret_cast<const ushort4 *>(w)[t];
+    const ushort4 b4 = NORM ? reinterpret_cast<const ushort4 *>(b)[t] : make_ushort4(0, 0, 0, 0);
     float4 a = pr[0];
 #pragma unroll
     for (int p = 1; p < NP; p++) {
@@ -359,7 +386,8 @@ __global__ __launch_bounds__(256) void resid_fold_kernel(float *h, float *lnstat
     }
     v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
     x[t] = v;
-    fold_tail(v, w4, lnstat, frag, row);
+    if (NORM) ln_tail(v, w4, b4, frag, row);
+    else fold_tail(v, w4, lnstat, frag, row);
 }
 
 }  // namespace
@@ -402,13 +430,17 @@ extern "C" void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, 
 }
 
 extern "C" void ctk_resid_fold(float *h, float *lnstat, uint16_t *frag, const float *parts, int nparts,
-                               const uint16_t *pbias, const uint16_t *w, int M, const CtWarmSet *warm,
-                               hipStream_t s) {
+                               const uint16_t *pbias, const uint16_t *w, const uint16_t *b, int M,
+                               const CtWarmSet *warm, hipStream_t s) {
     if (M <= 0) return;
-    if ((uintptr_t)h % 16 || (uintptr_t)frag % 16 || (uintptr_t)parts % 16 || (uintptr_t)lnstat % 8 ||
-        (uintptr_t)w % 8 || (pbias && (uintptr_t)pbias % 8)) {
+    if ((uintptr_t)h % 16 || (uintptr_t)frag % 16 || (uintptr_t)parts % 16 || (!b && (uintptr_t)lnstat % 8) ||
+        (uintptr_t)w % 8 || (b && (uintptr_t)b % 8) || (pbias && (uintptr_t)pbias % 8)) {
         fprintf(stderr, "ctk_resid_fold: needs 16-byte aligned rows and partials, 8-byte aligned lnstat, "
-                        "gain and bias\n");
+                        "gain and biases\n");
+        exit(1);
+    }
+    if (nparts != 8) {
+        fprintf(stderr, "ctk_resid_fold: %d partial slices not supported (8)\n", nparts);
         exit(1);
     }
     CtWarmSet ws;
@@ -416,15 +448,12 @@ extern "C" void ctk_resid_fold(float *h, float *lnstat, uint16_t *frag, const fl
     if (warm) ws = *warm;
     const int G = M + 8 * ct_warm_rows(&ws, "ctk_resid_fold");
     const long ps = (long)M * DEC_D;
-    switch (nparts) {
-    case 1: hipLaunchKernelGGL(resid_fold_kernel<1>, dim3(G), dim3(256), 0, s, h, lnstat, frag, parts, ps, pbias, w, M, ws); break;
-    case 2: hipLaunchKernelGGL(resid_fold_kernel<2>, dim3(G), dim3(256), 0, s, h, lnstat, frag, parts, ps, pbias, w, M, ws); break;
-    case 4: hipLaunchKernelGGL(resid_fold_kernel<4>, dim3(G), dim3(256), 0, s, h, lnstat, frag, parts, ps, pbias, w, M, ws); break;
-    case 8: hipLaunchKernelGGL(resid_fold_kernel<8>, dim3(G), dim3(256), 0, s, h, lnstat, frag, parts, ps, pbias, w, M, ws); break;
-    default:
-        fprintf(stderr, "ctk_resid_fold: %d partial slices not supported (1, 2, 4, 8)\n", nparts);
-        exit(1);
-    }
+    if (b)
+        hipLaunchKernelGGL((resid_fold_kernel<8, true>), dim3(G), dim3(256), 0, s, h, lnstat, frag, parts, ps,
+                           pbias, w, b, M, ws);
+    else
+        hipLaunchKernelGGL((resid_fold_kernel<8, false>), dim3(G), dim3(256), 0, s, h, lnstat, frag, parts, ps,
+                           pbias, w, b, M, ws);
 }
 
 extern "C" void ctk_embed_fold(float *h, float *lnstat, uint16_t *frag, const int *tokens,

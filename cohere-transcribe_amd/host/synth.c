@@ -265,8 +265,8 @@ static uint16_t gen_value(const TInfo *t, int variant, uint64_t key, size_t i) {
     const float z = ct_normal16(ct_hash64(key, i));
     switch (t->kind) {
     case K_NORMAL:
-        if (variant == 2 && !strncmp(t->name, DEC_PFX, strlen(DEC_PFX)))
-            return to_bf16_rne(0.12f * z);
+        if ((variant == 2 || variant == 3) && !strncmp(t->name, DEC_PFX, strlen(DEC_PFX)))
+            return to_bf16_rne((variant == 2 ? 0.12f : 0.08f) * z);
         return to_bf16_rne(0.02f * z);
     case K_ONES:   return to_bf16_rne(1.0f);
     case K_ZEROS:  return 0;

@@ -22,10 +22,15 @@ extern "C" {
  *            aligned with the input token's embedding, so greedy decoding
  *            repeats the last prompt token; the larger decoder weights make
  *            the residual dominate and greedy decoding input-dependent, which
- *            gives token-id parity tests near-ties to survive. */
+ *            gives token-id parity tests near-ties to survive.
+ * variant 3: the spec init with decoder-layer linear weights N(0, 0.08): the
+ *            smallest of these scales whose greedy decoding is input-dependent
+ *            while the bf16 rounding of K/V moves the fp32 logits by less than
+ *            1e-2 (about 6e-3; 1-1.7% with 0.12). */
 #define CT_SYNTH_SPEC      0
 #define CT_SYNTH_PERTURBED 1
 #define CT_SYNTH_DEC_HOT   2
+#define CT_SYNTH_DEC_WARM  3
 
 /* Number of tensors and total file size (8-byte length + JSON header + data). */
 int    ct_synth_tensor_count(void);

@@ -39,3 +39,4 @@ class CtGemm(C.Structure):
                 ("row_len", C.c_void_p), ("row_len_step", C.c_int), ("row_stride", C.c_long),
                 ("glu_half", C.c_int), ("row_mask", C.c_void_p), ("nseg", C.c_int), ("seg_w", C.c_int),
                 ("seg", CtSeg * 3)]
+

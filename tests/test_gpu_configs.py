@@ -47,11 +47,15 @@ FFN_LOGIT_SPEC = 5e-3
 # specified N(0, 0.02)): their large activations make the bf16 rounding of
 # K/V alone move the fp32 logits by 1-1.7% (the oracle in both KV modes
 # against each other, the reference's own arithmetic otherwise), so that
-# case is held to 2.5e-2.  The benchmark runs the specified weights.
-LOGIT_TOL = {(0, True): 1e-3, (0, False): 1e-5, (2, True): 2.5e-2, (2, False): 2e-4}
+# case is held to 2.5e-2.  The decoder-warm weights (linears N(0, 0.08)) keep
+# greedy decoding input-dependent with bf16 K/V inside the specified 1e-2.
+# The benchmark runs the specified weights.
+LOGIT_TOL = {(0, True): 1e-3, (0, False): 1e-5, (2, True): 2.5e-2, (2, False): 2e-4,
+             (3, True): SPEC_TOL, (3, False): 2e-4}
 # single-pass FFN mode: the encoder's bf16 rounding reaches the logits
 # (oracle emulation: 6e-4 on the specified weights, 4.7e-3 on the hot ones)
-LOGIT_TOL_FFN = {(0, True): 2e-3, (0, False): 2e-3, (2, True): 2.5e-2, (2, False): 1e-2}
+LOGIT_TOL_FFN = {(0, True): 2e-3, (0, False): 2e-3, (2, True): 2.5e-2, (2, False): 1e-2,
+                 (3, True): SPEC_TOL, (3, False): SPEC_TOL}
 
 
 def row_relerr(a, b):
@@ -91,7 +95,7 @@ def fixture_requests(g):
 
 
 @pytest.mark.parametrize("ffn_bf16", [False, True])
-@pytest.mark.parametrize("variant", [0, 2])
+@pytest.mark.parametrize("variant", [0, 2, 3])
 @pytest.mark.parametrize("kv_bf16", [True, False])
 def test_single_and_uniform_configs_vs_reference(hip, variant, kv_bf16, ffn_bf16):
     path = os.path.join(GOLD, f"config_c0c1_v{variant}.npz")
@@ -148,6 +152,11 @@ def test_single_and_uniform_configs_vs_reference(hip, variant, kv_bf16, ffn_bf16
         assert worst_enc <= ENC_REG[ffn_bf16], worst_enc
         if variant == 0:
             assert worst_lg <= (FFN_LOGIT_SPEC if ffn_bf16 else SPEC_TOL)
+        if variant == 3:
+            # input-dependent tokens and the specified bound in every mode,
+            # the benchmark's (bf16 K/V, single-pass FFN) included
+            assert worst_lg <= SPEC_TOL
+            assert max(len(set(g[f"{k}_tokens"].tolist())) for k, _ in reqs) >= 10
     finally:
         eng.close()
 

@@ -85,7 +85,7 @@ def lib(hip):
                                  C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
                                  C.POINTER(CtWarmSet), C.c_void_p]
     L.ctk_resid_fold.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
-                                 C.c_void_p, C.c_int, C.POINTER(CtWarmSet), C.c_void_p]
+                                 C.c_void_p, C.c_void_p, C.c_int, C.POINTER(CtWarmSet), C.c_void_p]
     L.ctk_fold_cols.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
                                 C.c_void_p, C.c_void_p, C.c_void_p]
     L.ctk_gemv.argtypes = [C.POINTER(CtGemv), C.c_void_p]
@@ -342,8 +342,8 @@ def test_folded_layernorm_gemms(lib, hip):
     h += x W^T + b on the residual rows against float64, leaving each row's
     block statistics and frag(h * w) of the next LayerNorm's gain.  Then the
     GEMMs with that LayerNorm folded in (fold_c1 / fold_c2 from ctk_fold_cols,
-    checked against float64 sums): the cross-query shape (dense), FFN up
-    (frag, ReLU) and the LM head (all 64 rows a workgroup) against the float64
+    checked against float64 sums): the cross-query and QKV shapes (dense)
+    and FFN up (frag, ReLU) against the float64
     LayerNorm of h (backends/cpu/backend.c layernorm) times W plus bias,
     within 2e-5 of the largest output: the rows here have mean 2 and unit
     spread, so the subtraction of mu * c1 doubles the split's 2^-18 relative
@@ -392,7 +392,7 @@ def test_folded_layernorm_gemms(lib, hip):
     h = hM.view(np.float32)
     ph, pst, pf = ptrs
     ln = ln64(h, lnw, lnb)
-    for N, out, relu in ((1024, DENSE, 0), (4096, FRAG, 1), (16384, DENSE, 0)):
+    for N, out, relu in ((1024, DENSE, 0), (3072, DENSE, 0), (4096, FRAG, 1)):
         W2 = f32_to_bf16(rng.standard_normal((N, D)).astype(np.float32) / 32)
         b2 = f32_to_bf16(0.1 * rng.standard_normal(N).astype(np.float32))
         praw, pb2 = dev.put(W2), dev.put(b2)
@@ -409,7 +409,7 @@ def test_folded_layernorm_gemms(lib, hip):
         if relu:
             ref = np.maximum(ref, 0.0)
         outs = {}
-        for m in ((80, 64, 24, 8) if N < 16384 else (64, 24)):
+        for m in (80, 64, 24, 8):
             print(f"case: folded LayerNorm GEMM N={N} out={out} M={m}", flush=True)
             g = CtGemv(A=pf, W=pW2, M=m, N=N, K=D, ksplit=1, out=out, relu=relu, wtile=1, lnstat=pst,
                        fold_c1=pc1, fold_c2=pc2)
@@ -508,7 +508,7 @@ def test_resid_fold_after_k_split(lib, hip):
         ph, pst, pf = dev.put(h0), dev.zeros(M * 32 * 8), dev.zeros(frag_elems(M, D) * 2)
         dev.ev.sync()
         pparts = pp if m == M else dev.put(np.ascontiguousarray(parts[:, :m]))
-        lib.ctk_resid_fold(ph, pst, pf, pparts, NP, ppb, pw, m, None, None)
+        lib.ctk_resid_fold(ph, pst, pf, pparts, NP, ppb, pw, None, m, None, None)
         res[m] = (dev.get(ph, np.uint32, M * D).reshape(M, D), dev.get(pst, np.uint32, M * 64).reshape(M, 64))
         if m == M:
             acc = parts[0].copy()
@@ -520,3 +520,40 @@ def test_resid_fold_after_k_split(lib, hip):
             check_fold_input(dev, h, pst, pf, w, M, "resid fold")
     assert np.array_equal(res[37][0][:37], res[M][0][:37]) and np.array_equal(res[37][0][37:], h0[37:].view(np.uint32))
     assert np.array_equal(res[37][1][:37], res[M][1][:37])
+
+
+def test_resid_fold_final_layernorm(lib, hip):
+    """The residual update after the last FFN normalises the rows itself: h +=
+    ((p0 + ... + p7) + b2) bit for bit, then frag(LayerNorm(h)) with the final
+    gain and bias against the float64 LayerNorm (1e-5), the input of the LM
+    head; rows independent of M."""
+    dev = Dev(hip)
+    rng = np.random.default_rng(19)
+    D, M, NP = 1024, 80, 8
+    h0 = (2.0 + rng.standard_normal((M, D))).astype(np.float32)
+    parts = (0.3 * rng.standard_normal((NP, M, D))).astype(np.float32)
+    b2 = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
+    lnw = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32))
+    lnb = f32_to_bf16(0.1 * rng.standard_normal(D).astype(np.float32))
+    acc = parts[0].copy()
+    for p in range(1, NP):
+        acc = acc + parts[p]
+    want = (h0 + (acc + bf16_to_f32(b2))).astype(np.float32)
+    outs = {}
+    for m in (80, 37):
+        print(f"case: residual update with the final LayerNorm, M={m}", flush=True)
+        ph, pf = dev.put(h0), dev.zeros(frag_elems(M, D) * 2)
+        pp = dev.put(np.ascontiguousarray(parts[:, :m]))
+        dev.ev.sync()
+        lib.ctk_resid_fold(ph, dev.zeros(M * 32 * 8), pf, pp, NP, dev.put(b2), dev.put(lnw), dev.put(lnb), m,
+                           None, None)
+        h = dev.get(ph, np.float32, M * D).reshape(M, D)
+        assert np.array_equal(h[:m].view(np.uint32), want[:m].view(np.uint32))
+        assert np.array_equal(h[m:].view(np.uint32), h0[m:].view(np.uint32))
+        hi, lo = from_frag(dev.get(pf, np.uint16, frag_elems(M, D)), M, D)
+        outs[m] = (hi[:m], lo[:m])
+        y = bf16_to_f32(hi[:m]).astype(np.float64) + bf16_to_f32(lo[:m])
+        e = rel(y, ln64(want[:m], lnw, lnb))
+        print(f"  final LayerNorm relerr {e:.2e}")
+        assert e <= 1e-5
+    assert np.array_equal(outs[37][0], outs[80][0][:37]) and np.array_equal(outs[37][1], outs[80][1][:37])
