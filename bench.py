@@ -20,6 +20,13 @@ per-kernel averages of `bench.py --roofline-only` can be set beside them):
                           128-slot ragged microbench shape (S ~ U(1,448),
                           T_enc ~ U(25,375)): algorithmic K+V bytes per
                           launch / average launch time, against 8 TB/s;
+  rooflines.attention_b64 the same at the stream's own step shape: 64 slots
+                          and 16 prompt rows, lengths drawn from the stream's
+                          requests;
+  rooflines.decode_step_b64  whole decode steps at the stream's shape (64
+                          slots, 16 idle spare rows) replayed from the
+                          captured graph: weight + K/V bytes per step / step
+                          time, against 8 TB/s;
   rooflines.decode_gemm   the 49 decode GEMMs of one step at the stream's 64
                           slots: weight + activation-in + output bytes per
                           launch / average launch time, against 8 TB/s; with
@@ -33,9 +40,13 @@ per-kernel averages of `bench.py --roofline-only` can be set beside them):
                           share of the stream's GPU time;
   config_runs             the single-clip and uniform-batch configurations
                           end to end on the engine (wall seconds);
+  stream_other_ffn_precision  the same stream with the other encoder FFN
+                          precision (fp32-accurate hi+lo when the line runs
+                          single-pass bf16), one timed pass;
   cpu_baseline            the reference CPU path (its model.h on its CPU
                           backend, compiled from its sources) on the host's
-                          cores, one process per core, on a bounded sample
+                          cores (one process alone, then one per core of
+                          the host's one-GPU share, 16), on a bounded sample
                           extrapolated to this workload's audio/token mix.
 HBM traffic per launch (`traffic`) comes from rocprofv3 FETCH_SIZE and
 WRITE_SIZE counter runs recorded in profiles/traffic.json, when present.
@@ -57,7 +68,7 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 # The kernel family with the largest share of the stream's GPU time (from the
 # eager rocprofv3 profile of the stream, encoding not overlapped: decode GEMMs
-# 31.2%, the encoder's pre-split GEMMs 25.4%, decode attention 20.0%).
+# 32.8%, the encoder's pre-split GEMMs 26.7%, decode attention 21.6%).
 DOMINANT = "decode_gemm"
 BF16_PEAK_TFLOPS = 2500.0
 # Encoder frames per batch of the overlapped encode/decode (0: encode all,
