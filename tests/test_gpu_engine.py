@@ -162,6 +162,31 @@ def test_engine_scheduling_knobs_keep_bits(hip, hot, monkeypatch, slots, max_tok
     assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
 
 
+def test_engine_eager_launches_equal_graph_replay(hip, hot, mels, monkeypatch):
+    """HIPB_EAGER=1 (the mode every profile is taken in) launches each step's
+    kernels one by one instead of replaying the captured graphs; a run of
+    three requests on 2 slots with 2 spare prompt rows (the narrow and the
+    wide step both) gives the same tokens and chosen-logit bits either way."""
+    runs = []
+    for eager in ("0", "1"):
+        print(f"case: HIPB_EAGER={eager}", flush=True)
+        monkeypatch.setenv("HIPB_EAGER", eager)
+        eng = cb.Engine(hot, slots=2, max_requests=4, max_frames=64, kv_bf16=True,
+                        max_tokens=len(cb.PROMPT) + max(LIMITS), prefill_rows=2)
+        try:
+            for i, mel in enumerate(mels):
+                eng.submit(mel, LIMITS[i], FLAGS)
+            eng.encode()
+            eng.run(chunk=2)
+            assert eng.finished() == len(mels)
+            runs.append([(eng.tokens(r), eng.scores(r)) for r in range(len(mels))])
+        finally:
+            eng.close()
+    for (ta, sa), (tb, sb) in zip(*runs):
+        assert np.array_equal(ta, tb)
+        assert np.array_equal(sa.view(np.uint32), sb.view(np.uint32))
+
+
 def test_engine_batch_vs_single_bitexact(hip, hot, mels):
     packed = cb.Engine(hot, slots=4, max_requests=8, max_frames=64, kv_bf16=True)
     try:
