@@ -252,6 +252,8 @@ typedef struct {
     int   lens_step;
     int   len_const;          /* ... or this when lens == NULL                          */
     const int   *kv_index;    /* optional: item b reads K/V block kv_index[b]          */
+    int   kv_direct;          /* with kv_index: items b < kv_direct read block b itself
+                                 (no index load before their first keys)             */
     const int   *rank;        /* optional (T_q == 1): items by descending length; launch
                                  position p takes item rank[snake(p)], so the items that
                                  share a CU pair long with short                      */

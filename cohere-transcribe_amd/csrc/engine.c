@@ -1269,13 +1269,13 @@ static void warm_take(HipbEngine *e, CtWarmSet *ws) {
 }
 
 static void attn(HipbEngine *e, const void *K, const void *V, long item_stride, long head_stride,
-                 int rows, const int *lens, const int *kv_index, const int *rank) {
+                 int rows, const int *lens, const int *kv_index, int kv_direct, const int *rank) {
     CtAttn a;
     memset(&a, 0, sizeof a);
     a.Q = e->q; a.q_sb = DEC_D; a.q_st = DEC_D;
     a.K = K; a.V = V; a.kv_bf16 = e->esz == 2;
     a.kv_sb = item_stride; a.kv_st = DEC_DK; a.kv_sh = head_stride;
-    a.lens = lens; a.lens_step = 1; a.kv_index = kv_index; a.kv_rows = rows;
+    a.lens = lens; a.lens_step = 1; a.kv_index = kv_index; a.kv_direct = kv_direct; a.kv_rows = rows;
     a.rank = e->M >= e->d.rank_min ? rank : NULL;
     a.T_q = 1; a.B = e->M; a.H = DEC_H;
     a.scale = 0.08838834764831845f;   /* 1/sqrt(128) */
@@ -1301,13 +1301,13 @@ static void step_attention(HipbEngine *e, int l, int cross) {
     if (!cross) {
         self_kv(e, l, &k, &v);
         /* row s is slot s's own row: only the spare rows of a wide step
-         * need the row -> slot table */
+         * need the row -> slot table, and only they wait for it */
         attn(e, k, v, (long)DEC_H * e->d.kv_rows * DEC_DK, (long)e->d.kv_rows * DEC_DK, e->d.kv_rows,
-             e->d.pos_len, e->M > e->d.slots ? e->d.row_slot : NULL, e->d.rank_self);
+             e->d.pos_len, e->M > e->d.slots ? e->d.row_slot : NULL, e->d.slots, e->d.rank_self);
     } else {
         cross_kv(e, l, &k, &v);
         attn(e, k, v, (long)DEC_H * e->d.tmax * DEC_DK, (long)e->d.tmax * DEC_DK, e->d.tmax,
-             e->d.cross_len, e->d.cross_idx, e->d.rank_cross);
+             e->d.cross_len, e->d.cross_idx, 0, e->d.rank_cross);
     }
 }
 

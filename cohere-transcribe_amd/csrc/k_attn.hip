@@ -113,7 +113,7 @@ __global__ __launch_bounds__(NT) void attn_kernel(CtAttn a) {
     // the length, the cache index, (EARLY) the first key trip and the query
     // (or its K-slice partials).
     const int T = a.lens ? a.lens[(long)b * a.lens_step] : a.len_const;
-    const long item = a.kv_index ? (long)a.kv_index[b] : (long)b;
+    const long item = a.kv_index && b >= a.kv_direct ? (long)a.kv_index[b] : (long)b;
     const long base = item * a.kv_sb + (long)h * a.kv_sh + ls * DPL;
     constexpr int KPI = BF16 ? CT_ATTN_KPI : 4;
     constexpr int STEP = NG * KPI;
