@@ -1089,6 +1089,13 @@ __global__ __launch_bounds__(512) void gemm_split256_sp_kernel(CtGemm g, int n_m
         for (int cb = 0; cb < 8; cb++)
             f.v[cb] = as_bf16x8(*reinterpret_cast<const u16x8 *>(st + boff + cb * 16 * SBK));
     };
+    // W fragments c0, c0 + 1 of step kt
+    auto read_b2 = [&](int kt, int c0, BFr &f) {
+        const uint16_t *st = smem + (kt % TST) * T_STAGE;
+#pragma unroll
+        for (int cb = c0; cb < c0 + 2; cb++)
+            f.v[cb] = as_bf16x8(*reinterpret_cast<const u16x8 *>(st + boff + cb * 16 * SBK));
+    };
     auto read_a = [&](int kt, int rb, AFr &f) {
         const uint16_t *st = smem + (kt % TST) * T_STAGE + aoff + rb * 16 * SBK;
         f.h = as_bf16x8(*reinterpret_cast<const u16x8 *>(st));
@@ -1129,18 +1136,27 @@ __global__ __launch_bounds__(512) void gemm_split256_sp_kernel(CtGemm g, int n_m
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (kt + TST - 1 < nk) issue(kt + TST - 1);
-        read_b(kt + 1, bn);
+        // LDS reads complete in issue order, so each MFMA group's A fragment
+        // is read ahead of the two W fragments of step kt + 1 that ride under
+        // the same group: its wait leaves them in flight
         read_a(kt, 1, a1);
+        read_b2(kt + 1, 0, bn);
         __builtin_amdgcn_sched_barrier(0);
         mma_row(0, a0, bc);
         __builtin_amdgcn_sched_barrier(0);
         read_a(kt, 2, a0);
+        read_b2(kt + 1, 2, bn);
+        __builtin_amdgcn_sched_barrier(0);
         mma_row(1, a1, bc);
         __builtin_amdgcn_sched_barrier(0);
         read_a(kt, 3, a1);
+        read_b2(kt + 1, 4, bn);
+        __builtin_amdgcn_sched_barrier(0);
         mma_row(2, a0, bc);
         __builtin_amdgcn_sched_barrier(0);
         read_a(kt + 1, 0, a0);
+        read_b2(kt + 1, 6, bn);
+        __builtin_amdgcn_sched_barrier(0);
         mma_row(3, a1, bc);
         __builtin_amdgcn_sched_barrier(0);
     };
