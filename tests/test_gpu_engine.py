@@ -187,6 +187,44 @@ def test_engine_eager_launches_equal_graph_replay(hip, hot, mels, monkeypatch):
         assert np.array_equal(sa.view(np.uint32), sb.view(np.uint32))
 
 
+def test_engine_128_slot_step_rows_independent(hip, hot):
+    """The decode-step microbench shape: 128 slots, self lengths U(1, 448),
+    encoder lengths U(25, 375), bf16 K/V filled from a seeded hash of each
+    element's index (hipb_bench_fill), one step.  A slot's logits are the same
+    bits whatever lengths the other 127 slots have.  At 128 rows the
+    attention deals its items by length rank, so the launch position of the
+    probed items moves between the two runs.  The logits are finite and
+    differ from slot to slot."""
+    rng = np.random.default_rng(31)
+    B = 128
+    S, T = rng.integers(1, 449, B), rng.integers(25, 376, B)
+    S2, T2 = rng.integers(1, 449, B), rng.integers(25, 376, B)
+    probe = [0, 5, 63, 64, 100, 127]
+    S2[probe], T2[probe] = S[probe], T[probe]
+    runs = []
+    for run, (s_, t_) in enumerate(((S, T), (S2, T2))):
+        print(f"case: 128-slot step, lengths set {run}", flush=True)
+        eng = cb.Engine(hot, slots=B, max_requests=B, max_frames=376, kv_bf16=True, max_tokens=512)
+        try:
+            eng.bench_fill(s_, t_, seed=9)
+            eng.step()
+            runs.append(np.stack([eng.logits(slot) for slot in range(B)]))
+        finally:
+            eng.close()
+    a, b = runs
+    assert np.isfinite(a).all() and np.isfinite(b).all()
+    assert np.abs(a - a[0]).max() > 0.0
+    def rank(L):
+        # position in the device's ranking: descending length, ties by row
+        rows = np.arange(B)
+        return np.array([np.sum((L > L[r]) | ((L == L[r]) & (rows < r))) for r in rows])
+    moved = [p for p in probe if rank(S)[p] != rank(S2)[p]]
+    print(f"  probed slots {probe}, self-length rank moved for {moved}")
+    assert moved
+    for p in probe:
+        assert np.array_equal(a[p].view(np.uint32), b[p].view(np.uint32)), p
+
+
 def test_engine_batch_vs_single_bitexact(hip, hot, mels):
     packed = cb.Engine(hot, slots=4, max_requests=8, max_frames=64, kv_bf16=True)
     try:
