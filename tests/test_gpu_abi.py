@@ -167,6 +167,82 @@ def test_ragged_attention_batch_invariance(hip, kmodel):
     assert bits_equal(dev.get(o2), got[5])
 
 
+def test_empty_batches_and_edge_lengths(hip, kmodel):
+    """Edge cases of the batched ABI as the reference's loops treat them
+    (backends/cpu/backend.c:425-500): a batch of 0 items writes nothing; an
+    item of zero keys gets a zero attention row (a sum over no keys); and
+    the longest lengths, MAX_SEQ self keys and 1024 encoder frames, match
+    the oracle, ragged beside short items, with the item alone giving the
+    same bits."""
+    o = ob.oracle()
+    dev = ks.ArenaDev(hip, 1 << 26)
+    rng = np.random.default_rng(44)
+    DD, V = 1024, cb.VOCAB
+    ints = ks._ints
+    # B = 0: every output untouched
+    print("case: batch of 0 items", flush=True)
+    h0 = np.full((2, DD), 2.5, np.float32)
+    lg0 = np.full((2, V), -1.5, np.float32)
+    h, lg, od = dev.put(h0), dev.put(lg0), dev.put(h0)
+    kc = dev.put(np.full((2, 4, DD), 0.75, np.float32))
+    hip.backend_embed_decode_batch(h[0], ints([3, 4]).ctypes.data, ints([1, 1]).ctypes.data,
+                                   ints([1, 1]).ctypes.data, 0, kmodel.ptr("etw"), kmodel.ptr("epw"),
+                                   kmodel.ptr("elnw"), kmodel.ptr("elnb"))
+    hip.backend_lm_head_batch(lg[0], h[0], kmodel.ptr("etw"), kmodel.ptr("hdb"), ints([1, 1]).ctypes.data, 0)
+    am = ints([-7, -7])
+    hip.backend_argmax_batch(am.ctypes.data, lg[0], ints([1, 1]).ctypes.data, 0)
+    hip.backend_linear_to_kvcache_batch(kc[0], h[0], kmodel.ptr("dec2.sa_kw"), kmodel.ptr("dec2.sa_kb"),
+                                        0, 4, DD, DD)
+    hip.backend_upload_T_enc(ints([3, 3]).ctypes.data, 0)
+    hip.backend_sdp_attn_batch_decode_sa(od[0], h[0], kc[0], kc[0], 4, 0, dev.zeros(2 * 8 * 4)[0])
+    hip.backend_sdp_attn_batch_decode_ca(od[0], h[0], kc[0], kc[0], 4, 0, dev.zeros(2 * 8 * 4)[0])
+    assert bits_equal(dev.get(h), h0) and bits_equal(dev.get(lg), lg0) and bits_equal(dev.get(od), h0)
+    assert np.all(dev.get(kc) == 0.75) and np.all(am == -7)
+    # cross attention: 0, 1, 1024 and 517 frames in one ragged batch
+    stride = 1024
+    lens = np.array([0, 1, 1024, 517], np.int32)
+    B = len(lens)
+    print(f"case: ragged cross attention, lengths {lens.tolist()}", flush=True)
+    Q = (rng.standard_normal((B, DD)) * 0.3).astype(np.float32)
+    K = (rng.standard_normal((B, stride, DD)) * 0.3).astype(np.float32)
+    Vv = rng.standard_normal((B, stride, DD)).astype(np.float32)
+    qd, kd, vd, out = dev.put(Q), dev.put(K), dev.put(Vv), dev.put(np.full((B, DD), 9.0, np.float32))
+    hip.backend_upload_T_enc(lens.ctypes.data, B)
+    hip.backend_sdp_attn_batch_decode_ca(out[0], qd[0], kd[0], vd[0], stride, B, dev.zeros(B * 8 * stride)[0])
+    got = dev.get(out)
+    assert np.all(got[0] == 0.0)
+    for b in range(1, B):
+        ref = np.zeros(DD, np.float32)
+        o.orc_sdp_attn(ref.ctypes.data, Q[b].ctypes.data, K[b].ctypes.data, Vv[b].ctypes.data,
+                       None, 1, int(lens[b]), None)
+        assert relerr(got[b], ref) <= TOL, b
+    one = lens[2:3].copy()
+    hip.backend_upload_T_enc(one.ctypes.data, 1)
+    o1 = dev.zeros(1, DD)
+    hip.backend_sdp_attn_batch_decode_ca(o1[0], qd[0] + 2 * DD * 4, kd[0] + 2 * stride * DD * 4,
+                                         vd[0] + 2 * stride * DD * 4, stride, 1, dev.zeros(8 * stride)[0])
+    assert bits_equal(dev.get(o1)[0], got[2])
+    # self attention at S = MAX_SEQ beside S = 1, the lengths latched by the batched embedding
+    print("case: self attention at S = MAX_SEQ and S = 1", flush=True)
+    S = np.array([cb.MAX_SEQ, 1], np.int32)
+    B = len(S)
+    hs = dev.zeros(B, DD)
+    hip.backend_embed_decode_batch(hs[0], ints([11, 12]).ctypes.data, S.ctypes.data, ints([1, 1]).ctypes.data,
+                                   B, kmodel.ptr("etw"), kmodel.ptr("epw"), kmodel.ptr("elnw"), kmodel.ptr("elnb"))
+    stride = cb.MAX_SEQ
+    Ks = (rng.standard_normal((B, stride, DD)) * 0.3).astype(np.float32)
+    Vs = rng.standard_normal((B, stride, DD)).astype(np.float32)
+    Qs = (rng.standard_normal((B, DD)) * 0.3).astype(np.float32)
+    qd, kd, vd, out = dev.put(Qs), dev.put(Ks), dev.put(Vs), dev.zeros(B, DD)
+    hip.backend_sdp_attn_batch_decode_sa(out[0], qd[0], kd[0], vd[0], stride, B, dev.zeros(B * 8 * stride)[0])
+    got = dev.get(out)
+    for b in range(B):
+        ref = np.zeros(DD, np.float32)
+        o.orc_sdp_attn(ref.ctypes.data, Qs[b].ctypes.data, Ks[b].ctypes.data, Vs[b].ctypes.data,
+                       None, 1, int(S[b]), None)
+        assert relerr(got[b], ref) <= TOL, b
+
+
 def test_graph_capture_replay(hip, kmodel):
     """A captured region replays to the eager result, several times, with
     eager work and synchronisation in between."""
