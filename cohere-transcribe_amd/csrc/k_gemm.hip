@@ -1074,6 +1074,11 @@ __global__ __launch_bounds__(512) void gemm_split256_sp_kernel(CtGemm g, int n_m
 #pragma unroll
         for (int j = 0; j < T_PER_WAVE; j++) lds_dma16_asm(src[j] + kt * SBK, stage + dst[j]);
     };
+    // DMA instruction j of stage kt
+    static_assert(T_PER_WAVE == 4, "one DMA instruction per MFMA row group");
+    auto issue1 = [&](int kt, int j) {
+        lds_dma16_asm(src[j] + kt * SBK, smem + (kt % TST) * T_STAGE + dst[j]);
+    };
     const int wm = (wv >> 1) * 64, wn = (wv & 1) * 128;
     // fragment offsets within a stage: rows of one fragment share the swizzle
     const int aoff = (wm + r) * SBK + swz(r, kg) * 8;
@@ -1135,27 +1140,33 @@ __global__ __launch_bounds__(512) void gemm_split256_sp_kernel(CtGemm g, int n_m
         wait_stages(min(nk - 2 - kt, TST - 3));
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (kt + TST - 1 < nk) issue(kt + TST - 1);
-        // LDS reads complete in issue order, so each MFMA group's A fragment
-        // is read ahead of the two W fragments of step kt + 1 that ride under
-        // the same group: its wait leaves them in flight
+        // the refill of the freed slot (stage kt + TST - 1) goes out one DMA
+        // instruction per MFMA group; LDS reads complete in issue order, so
+        // each group's A fragment is read ahead of the two W fragments of
+        // step kt + 1 that ride under the same group: its wait leaves them in
+        // flight
+        const bool refill = kt + TST - 1 < nk;
         read_a(kt, 1, a1);
         read_b2(kt + 1, 0, bn);
+        if (refill) issue1(kt + TST - 1, 0);
         __builtin_amdgcn_sched_barrier(0);
         mma_row(0, a0, bc);
         __builtin_amdgcn_sched_barrier(0);
         read_a(kt, 2, a0);
         read_b2(kt + 1, 2, bn);
+        if (refill) issue1(kt + TST - 1, 1);
         __builtin_amdgcn_sched_barrier(0);
         mma_row(1, a1, bc);
         __builtin_amdgcn_sched_barrier(0);
         read_a(kt, 3, a1);
         read_b2(kt + 1, 4, bn);
+        if (refill) issue1(kt + TST - 1, 2);
         __builtin_amdgcn_sched_barrier(0);
         mma_row(2, a0, bc);
         __builtin_amdgcn_sched_barrier(0);
         read_a(kt + 1, 0, a0);
         read_b2(kt + 1, 6, bn);
+        if (refill) issue1(kt + TST - 1, 3);
         __builtin_amdgcn_sched_barrier(0);
         mma_row(3, a1, bc);
         __builtin_amdgcn_sched_barrier(0);
