@@ -498,6 +498,22 @@ __device__ __forceinline__ void lds_dma16(const void *g, uint16_t *lds_wave_base
     __builtin_amdgcn_global_load_lds((glb_ptr_t)g, (lds_ptr_t)lds_wave_base, 16, 0, 0);
 }
 
+// The same DMA as lds_dma16, issued from inline assembly.  The compiler counts
+// the builtin's LDS write as an LDS event of unknown order (it is not: the
+// hardware's lgkmcnt does not wait for the DMA's data), so with the builtin in
+// a loop every first use of an LDS fragment waits for all LDS reads in
+// flight.  Issued here, the DMA is invisible to that bookkeeping and the
+// fragment reads get in-order waits; the DMA itself is waited for explicitly
+// (vmcnt) before the barrier that publishes a stage.  M0 takes the wave's LDS
+// destination; one wait state separates its write from the load.  M0 is a
+// register the compiler reserves (an asm clobber of it is ignored): the kernels
+// that use this helper have no other instruction that reads M0 (no LDS-DMA
+// builtin, no register-indexed moves), so nothing relies on its old value.
+__device__ __forceinline__ void lds_dma16_asm(const void *g, uint16_t *lds_wave_base) {
+    const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_ptr_t)lds_wave_base);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(l) : "memory");
+}
+
 // 16-byte chunk c of a 64-byte LDS row R sits at chunk swz(R, c).  The 16 rows
 // a fragment read touches then cover every bank once whether the LDS serves
 // 16 lanes over 64 banks or 8 lanes over 32 banks per cycle.
@@ -862,10 +878,17 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
             dst[j] = (LO ? 2 : 1) * T_A + (i - NA) * 16 * SBK;
         }
     }
+    // the DMA from inline assembly (lds_dma16_asm: this kernel has no other
+    // M0 reader), so the fragment reads get exact LDS waits
     auto issue = [&](int kt) {
         uint16_t *stage = smem + (kt % TST) * T_STAGE;
 #pragma unroll
-        for (int j = 0; j < T_PER_WAVE; j++) lds_dma16(src[j] + kt * SBK, stage + dst[j]);
+        for (int j = 0; j < T_PER_WAVE; j++) lds_dma16_asm(src[j] + kt * SBK, stage + dst[j]);
+    };
+    // DMA instruction j of stage kt
+    static_assert(T_PER_WAVE == 6, "the refill is spread 2, 2, 1, 1 over the row groups");
+    auto issue1 = [&](int kt, int j) {
+        lds_dma16_asm(src[j] + kt * SBK, smem + (kt % TST) * T_STAGE + dst[j]);
     };
 
     f32x4 acc[4][8];
@@ -886,7 +909,9 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
         else __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (kt + TST - 1 < nk) issue(kt + TST - 1);
+        // the refill of the freed slot (stage kt + TST - 1) goes out beside the
+        // MFMAs: 2, 2, 1 and 1 DMA instructions after the row groups' reads
+        const bool refill = kt + TST - 1 < nk;
         const uint16_t *st = smem + (kt % TST) * T_STAGE;
         const uint16_t *sAh = st, *sAl = st + T_A, *sW = st + (LO ? 2 : 1) * T_A;
         bf16x8 bfr[8];
@@ -901,6 +926,14 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
             const int off = R * SBK + swz(R, kg) * 8;
             const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAh + off));
             const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
+            if (refill) {
+                if (rb < 2) {
+                    issue1(kt + TST - 1, 2 * rb);
+                    issue1(kt + TST - 1, 2 * rb + 1);
+                } else {
+                    issue1(kt + TST - 1, 2 + rb);
+                }
+            }
 #pragma unroll
             for (int cb = 0; cb < 8; cb++) {
                 acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
@@ -1006,21 +1039,6 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
     }
 }
 
-// The same DMA as lds_dma16, issued from inline assembly.  The compiler counts
-// the builtin's LDS write as an LDS event of unknown order (it is not: the
-// hardware's lgkmcnt does not wait for the DMA's data), so with the builtin in
-// a loop every first use of an LDS fragment waits for all LDS reads in
-// flight.  Issued here, the DMA is invisible to that bookkeeping and the
-// fragment reads get in-order waits; the DMA itself is waited for explicitly
-// (vmcnt) before the barrier that publishes a stage.  M0 takes the wave's LDS
-// destination; one wait state separates its write from the load.  M0 is a
-// register the compiler reserves (an asm clobber of it is ignored): the kernel
-// that uses this helper has no other instruction that reads M0 (no LDS-DMA
-// builtin, no register-indexed moves), so nothing relies on its old value.
-__device__ __forceinline__ void lds_dma16_asm(const void *g, uint16_t *lds_wave_base) {
-    const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_ptr_t)lds_wave_base);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(l) : "memory");
-}
 
 // ---------------------------------------------------------------------------
 // The 256 x 256 tile, single-pass form (A is bf16 alone: one MFMA per K-step
