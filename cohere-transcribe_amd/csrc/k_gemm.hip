@@ -560,6 +560,40 @@ __device__ __forceinline__ Epi8 epi8_setup(const CtGemm &g, int col) {
 // Local rows lr0 + 16*i (i < NI) of the staged tile sc = output rows m0 + those.
 template <int NI>
 __device__ __forceinline__ void epi8_rows(const CtGemm &g, const Epi8 &e, const float *sc, int lr0, int m0, int g8) {
+    if (e.mode == CT_OUT_SPLIT && !g.row_mask) {
+        // bf16 rows (the FFN's hidden activations): every row's staged sums
+        // are read first, then each row is finished and stored straight
+        // through, the store predicated on the row being in range, so no
+        // branch stands between one row's LDS reads and the next row's
+        float4 a[NI], b[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int row = lr0 + 16 * i;
+            const float4 *pv = reinterpret_cast<const float4 *>(sc + row * SBN + ((g8 * 8) ^ (((row >> 2) & 3) << 4)));
+            a[i] = pv[0]; b[i] = pv[1];
+        }
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int m = m0 + lr0 + 16 * i;
+            const long o = (long)m * e.ld + e.off;
+            float v[8] = {a[i].x, a[i].y, a[i].z, a[i].w, b[i].x, b[i].y, b[i].z, b[i].w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] += e.b[j];
+            act8(g, v);
+            u16x8 h8;
+#pragma unroll
+            for (int j = 0; j < 8; j++) h8[j] = f2bf(v[j]);
+            if (m < g.M) *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base) + o) = h8;
+            if (e.base_lo) {
+                // lo = the rounding remainder, as split_bf16
+                u16x8 l8;
+#pragma unroll
+                for (int j = 0; j < 8; j++) l8[j] = f2bf(v[j] - bf2f(h8[j]));
+                if (m < g.M) *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base_lo) + o) = l8;
+            }
+        }
+        return;
+    }
     const bool fmadd = e.mode < 0 && g.epi == CT_EPI_FMADD;
     const bool heads = e.mode == CT_OUT_HEADS_F32 || e.mode == CT_OUT_HEADS_BF16;
     bool ok[NI];
