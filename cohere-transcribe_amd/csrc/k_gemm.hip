@@ -560,11 +560,13 @@ __device__ __forceinline__ Epi8 epi8_setup(const CtGemm &g, int col) {
 // Local rows lr0 + 16*i (i < NI) of the staged tile sc = output rows m0 + those.
 template <int NI>
 __device__ __forceinline__ void epi8_rows(const CtGemm &g, const Epi8 &e, const float *sc, int lr0, int m0, int g8) {
-    if (e.mode == CT_OUT_SPLIT && !g.row_mask) {
-        // bf16 rows (the FFN's hidden activations): every row's staged sums
-        // are read first, then each row is finished and stored straight
-        // through, the store predicated on the row being in range, so no
-        // branch stands between one row's LDS reads and the next row's
+    if (!g.row_mask && (e.mode == CT_OUT_SPLIT || e.mode == CT_OUT_DENSE ||
+                        (e.mode < 0 && g.epi != CT_EPI_FMADD))) {
+        // rows that only store (bf16 planes, dense fp32 segments, plain rows
+        // with their activation): every row's staged sums are read first,
+        // then each row is finished and stored straight through, the store
+        // predicated on the row being in range, so no branch stands between
+        // one row's LDS reads and the next row's
         float4 a[NI], b[NI];
 #pragma unroll
         for (int i = 0; i < NI; i++) {
@@ -579,18 +581,57 @@ __device__ __forceinline__ void epi8_rows(const CtGemm &g, const Epi8 &e, const 
             float v[8] = {a[i].x, a[i].y, a[i].z, a[i].w, b[i].x, b[i].y, b[i].z, b[i].w};
 #pragma unroll
             for (int j = 0; j < 8; j++) v[j] += e.b[j];
-            act8(g, v);
-            u16x8 h8;
+            if (e.mode == CT_OUT_SPLIT) {
+                act8(g, v);
+                u16x8 h8;
 #pragma unroll
-            for (int j = 0; j < 8; j++) h8[j] = f2bf(v[j]);
-            if (m < g.M) *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base) + o) = h8;
-            if (e.base_lo) {
-                // lo = the rounding remainder, as split_bf16
-                u16x8 l8;
+                for (int j = 0; j < 8; j++) h8[j] = f2bf(v[j]);
+                if (m < g.M) *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base) + o) = h8;
+                if (e.base_lo) {
+                    // lo = the rounding remainder, as split_bf16
+                    u16x8 l8;
 #pragma unroll
-                for (int j = 0; j < 8; j++) l8[j] = f2bf(v[j] - bf2f(h8[j]));
-                if (m < g.M) *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base_lo) + o) = l8;
+                    for (int j = 0; j < 8; j++) l8[j] = f2bf(v[j] - bf2f(h8[j]));
+                    if (m < g.M) *reinterpret_cast<u16x8 *>(reinterpret_cast<uint16_t *>(e.base_lo) + o) = l8;
+                }
+            } else {
+                if (e.mode < 0) act8(g, v);      // plain rows take the activation; DENSE segments do not
+                float4 *y4 = reinterpret_cast<float4 *>(reinterpret_cast<float *>(e.base) + o);
+                if (m < g.M) {
+                    y4[0] = make_float4(v[0], v[1], v[2], v[3]);
+                    y4[1] = make_float4(v[4], v[5], v[6], v[7]);
+                }
             }
+        }
+        return;
+    }
+    if (!g.row_mask && e.mode < 0 && g.epi == CT_EPI_FMADD) {
+        // y += scale * (sum + bias) on plain fp32 rows: every row's residual
+        // load goes out first, then the rows straight through
+        float4 y0[NI], y1[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int m = m0 + lr0 + 16 * i;
+            if (m < g.M) {
+                const float4 *y4 = reinterpret_cast<const float4 *>(reinterpret_cast<float *>(e.base) + (long)m * e.ld + e.off);
+                y0[i] = y4[0]; y1[i] = y4[1];
+            } else {
+                y0[i] = y1[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int row = lr0 + 16 * i, m = m0 + row;
+            const float4 *pv = reinterpret_cast<const float4 *>(sc + row * SBN + ((g8 * 8) ^ (((row >> 2) & 3) << 4)));
+            const float4 a = pv[0], b = pv[1];
+            float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] += e.b[j];
+            float4 p = y0[i], q = y1[i];
+            p.x += g.scale * v[0]; p.y += g.scale * v[1]; p.z += g.scale * v[2]; p.w += g.scale * v[3];
+            q.x += g.scale * v[4]; q.y += g.scale * v[5]; q.z += g.scale * v[6]; q.w += g.scale * v[7];
+            float4 *y4 = reinterpret_cast<float4 *>(reinterpret_cast<float *>(e.base) + (long)m * e.ld + e.off);
+            if (m < g.M) { y4[0] = p; y4[1] = q; }
         }
         return;
     }
