@@ -492,17 +492,13 @@ template <bool LO> struct SplitCfg {
 };
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
-typedef const __attribute__((address_space(1))) void *glb_ptr_t;
 
-__device__ __forceinline__ void lds_dma16(const void *g, uint16_t *lds_wave_base) {
-    __builtin_amdgcn_global_load_lds((glb_ptr_t)g, (lds_ptr_t)lds_wave_base, 16, 0, 0);
-}
-
-// The same DMA as lds_dma16, issued from inline assembly.  The compiler counts
-// the builtin's LDS write as an LDS event of unknown order (it is not: the
-// hardware's lgkmcnt does not wait for the DMA's data), so with the builtin in
-// a loop every first use of an LDS fragment waits for all LDS reads in
-// flight.  Issued here, the DMA is invisible to that bookkeeping and the
+// One 16-byte-per-lane DMA from global memory into the wave's LDS range,
+// issued from inline assembly.  The compiler counts the builtin form's
+// (__builtin_amdgcn_global_load_lds) LDS write as an LDS event of unknown
+// order (it is not: the hardware's lgkmcnt does not wait for the DMA's data),
+// so with the builtin in a loop every first use of an LDS fragment waits for
+// all LDS reads in flight.  Issued here, the DMA is invisible to that bookkeeping and the
 // fragment reads get in-order waits; the DMA itself is waited for explicitly
 // (vmcnt) before the barrier that publishes a stage.  M0 takes the wave's LDS
 // destination; one wait state separates its write from the load.  M0 is a
@@ -750,11 +746,16 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
             dst[j] = (LO ? 2 : 1) * S_A + (i - NA) * 16 * SBK;
         }
     }
-    auto issue = [&](int kt) {
-        uint16_t *stage = smem + (kt % NST) * STAGE_ELEMS;
-#pragma unroll
-        for (int j = 0; j < S_PER_WAVE; j++) lds_dma16(src[j] + kt * SBK, stage + dst[j]);
+    // DMA instruction j of stage kt (inline assembly: the builtin makes the
+    // compiler wait for all LDS traffic before every fragment read)
+    auto issue1 = [&](int kt, int j) {
+        lds_dma16_asm(src[j] + kt * SBK, smem + (kt % NST) * STAGE_ELEMS + dst[j]);
     };
+    auto issue = [&](int kt) {
+#pragma unroll
+        for (int j = 0; j < S_PER_WAVE; j++) issue1(kt, j);
+    };
+    static_assert(S_PER_WAVE <= 4, "at most one refill DMA instruction per MFMA row group");
 
     f32x4 acc[4][4];
 #pragma unroll
@@ -775,7 +776,10 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
         else __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
         __builtin_amdgcn_s_barrier();            // stage kt landed for every wave, and every
         asm volatile("" ::: "memory");           // wave is done reading stage kt-1
-        if (kt + NST - 1 < nk) issue(kt + NST - 1);
+        // the refill of the freed slot (stage kt + NST - 1) goes out one DMA
+        // instruction per MFMA row group, after that group's fragment reads,
+        // rather than all at once ahead of the first MFMA
+        const bool refill = kt + NST - 1 < nk;
         const uint16_t *st = smem + (kt % NST) * STAGE_ELEMS;
         const uint16_t *sAh = st, *sAl = st + S_A, *sW = st + (LO ? 2 : 1) * S_A;
         bf16x8 bfr[4];
@@ -789,8 +793,11 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
             const int R = wm + rb * 16 + r;
             const int off = R * SBK + swz(R, kg) * 8;
             const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAh + off));
+            bf16x8 al;
+            if (LO) al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
+            if (refill && rb < S_PER_WAVE) issue1(kt + NST - 1, rb);
+            __builtin_amdgcn_sched_barrier(0);
             if (LO) {
-                const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8 *>(sAl + off));
 #pragma unroll
                 for (int cb = 0; cb < 4; cb++) {
                     acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
@@ -800,6 +807,7 @@ __global__ __launch_bounds__(512) void gemm_split_kernel(CtGemm g, int n_mt, int
 #pragma unroll
                 for (int cb = 0; cb < 4; cb++) acc[rb][cb] = mfma16(ah, bfr[cb], acc[rb][cb]);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);
