@@ -170,11 +170,20 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
 #pragma unroll
             for (int u = 0; u < 8; u++) acc = mfma4(a[u], bv[u], acc);
         }
-        for (; k0 < T; k0 += 4) {
-            const int k = k0 + lk;
-            const float a = k < T ? sr[k] : 0.0f;
-            const float bv = k < T ? vp[(long)k * ENC_D] : 0.0f;
-            acc = mfma4(a, bv, acc);
+        if (k0 < T) {
+            // the last T - k0 < 32 keys: every load of the batch goes out before
+            // the first MFMA (one round trip instead of one per step of 4
+            // keys); the MFMAs are the same steps as one at a time
+            float a[8], bv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int k = k0 + 4 * u + lk;
+                a[u] = k < T ? sr[k] : 0.0f;
+                bv[u] = k < T ? vp[(long)k * ENC_D] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (k0 + 4 * u < T) acc = mfma4(a[u], bv[u], acc);
         }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
