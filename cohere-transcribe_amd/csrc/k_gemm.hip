@@ -553,6 +553,9 @@ __device__ __forceinline__ Epi8 epi8_setup(const CtGemm &g, int col) {
     return e;
 }
 
+template <int NI>
+__device__ __forceinline__ void epi8_rows_any(const CtGemm &g, const Epi8 &e, const float *sc, int lr0, int m0, int g8);
+
 // Local rows lr0 + 16*i (i < NI) of the staged tile sc = output rows m0 + those.
 template <int NI>
 __device__ __forceinline__ void epi8_rows(const CtGemm &g, const Epi8 &e, const float *sc, int lr0, int m0, int g8) {
@@ -599,9 +602,7 @@ __device__ __forceinline__ void epi8_rows(const CtGemm &g, const Epi8 &e, const 
                 }
             }
         }
-        return;
-    }
-    if (!g.row_mask && e.mode < 0 && g.epi == CT_EPI_FMADD) {
+    } else if (!g.row_mask && e.mode < 0 && g.epi == CT_EPI_FMADD) {
         // y += scale * (sum + bias) on plain fp32 rows: every row's residual
         // load goes out first, then the rows straight through
         float4 y0[NI], y1[NI];
@@ -629,8 +630,14 @@ __device__ __forceinline__ void epi8_rows(const CtGemm &g, const Epi8 &e, const 
             float4 *y4 = reinterpret_cast<float4 *>(reinterpret_cast<float *>(e.base) + (long)m * e.ld + e.off);
             if (m < g.M) { y4[0] = p; y4[1] = q; }
         }
-        return;
+    } else {
+        epi8_rows_any<NI>(g, e, sc, lr0, m0, g8);
     }
+}
+
+// The general form of epi8_rows (row masks, cache rows by head), row by row.
+template <int NI>
+__device__ __forceinline__ void epi8_rows_any(const CtGemm &g, const Epi8 &e, const float *sc, int lr0, int m0, int g8) {
     const bool fmadd = e.mode < 0 && g.epi == CT_EPI_FMADD;
     const bool heads = e.mode == CT_OUT_HEADS_F32 || e.mode == CT_OUT_HEADS_BF16;
     bool ok[NI];
@@ -1068,7 +1075,6 @@ __global__ __launch_bounds__(512) void gemm_split256_kernel(CtGemm g, int n_mt, 
     const int eg8 = tid & 31, ecol = c0 + eg8 * 8;
     Epi8 ep;
     if (vepi == 2 && ecol < g.N) ep = epi8_setup(g, ecol);
-#pragma unroll
     for (int half = 0; half < 2; half++) {
         if ((wm >> 7) == half) {
 #pragma unroll
@@ -1297,7 +1303,6 @@ __global__ __launch_bounds__(512) void gemm_split256_sp_kernel(CtGemm g, int n_m
     const int eg8 = tid & 31, ecol = c0 + eg8 * 8;
     Epi8 ep;
     if (vepi == 2 && ecol < g.N) ep = epi8_setup(g, ecol);
-#pragma unroll
     for (int half = 0; half < 2; half++) {
         if ((wm >> 7) == half) {
 #pragma unroll
