@@ -1243,9 +1243,11 @@ void hipb_encode(HipbEngine *e, int max_batch_frames) {
  * ahead into the L2 their workgroups read from (CT_WARM_ROWS read-ahead
  * workgroups per XCD): the LayerNorm before each layer's QKV projection
  * reads that projection's; the self attention the out- and cross-query
- * projections'; the cross attention the FFN's.  HIPB_READ_AHEAD=0 at engine
- * creation turns it off. */
+ * projections'; the cross attention the FFN's; the final residual update
+ * half of the LM head's.  HIPB_READ_AHEAD=0 at engine creation turns it off. */
 #define CT_WARM_ROWS 32
+/* LM-head columns the final residual update reads ahead */
+#define CT_WARM_LM_COLS 8192
 /* Queues the weight tiles of the launch gv() makes for (Wd, N, K, out) for
  * the next attention or LayerNorm launch to read ahead. */
 static void warm_add(HipbEngine *e, const uint16_t *Wd, int N, int K, int out) {
@@ -1446,9 +1448,23 @@ static void step_kernels(HipbEngine *e, int full, int wide) {
         gv_partial(e, e->midf, w_f2, DEC_D, DEC_FF);
     }
     /* h += the last FFN, then the final LayerNorm */
-    if (full)
+    if (full) {
+        /* that launch reads the LM head's first CT_WARM_LM_COLS columns of
+         * weights ahead (16.8 MB: the whole head, 33.6 MB, does not stay in
+         * the L2s); workgroup i of the LM head keeps its XCD whatever the
+         * column count, so a prefix GEMM's tiles are the head's own */
+        CtWarmSet lws;
+        memset(&lws, 0, sizeof lws);
+        if (e->read_ahead) {
+            const int rows = e->M;
+            e->M = e->d.slots;
+            warm_add(e, e->wt_lm, CT_WARM_LM_COLS, DEC_D, CT_GV_DENSE);
+            e->M = rows;
+            warm_take(e, &lws);
+        }
         ctk_resid_fold(e->h, e->lnstat, e->lnf, e->parts, ctk_gemv_ksplit(DEC_D, DEC_FF),
-                       DW(W->dec[DEC_N - 1].ffn_b2), DW(W->dlnw), DW(W->dlnb), B, NULL, s);
+                       DW(W->dec[DEC_N - 1].ffn_b2), DW(W->dlnw), DW(W->dlnb), B, &lws, s);
+    }
     /* logits only for the slots' own rows */
     e->M = e->d.slots;
     gv_dense(e, e->lnf, e->wt_lm, DW(W->hdb), VOCAB, DEC_D, e->logits, VOCAB);
