@@ -20,6 +20,8 @@ per-kernel averages of `bench.py --roofline-only` can be set beside them):
                           128-slot ragged microbench shape (S ~ U(1,448),
                           T_enc ~ U(25,375)): algorithmic K+V bytes per
                           launch / average launch time, against 8 TB/s;
+  rooflines.attention_64  the same lengths over 64 slots (a ragged batch
+                          of 64);
   rooflines.attention_b64 the same at the stream's own step shape: 64 slots
                           and 16 prompt rows, lengths drawn from the stream's
                           requests;
@@ -159,11 +161,11 @@ def config_latency(hip, model, ev, ffn_bf16, reps=3):
     return out
 
 
-def attention_roofline(hip, model, ev, reps=20, step_reps=0):
-    """Decode-attention kernel at the 128-slot microbench shape; with
-    step_reps > 0 also the whole decode step at that shape (eager steps)."""
+def attention_roofline(hip, model, ev, reps=20, step_reps=0, B=128):
+    """Decode-attention kernel at the microbench's ragged lengths (S ~
+    U(1,448), T_enc ~ U(25,375)) over B slots; with step_reps > 0 also the
+    whole decode step at that shape (eager steps)."""
     rng = np.random.default_rng(4)
-    B = 128
     S = rng.integers(1, 449, B)
     T = rng.integers(25, 376, B)
     eng = cb.Engine(model, slots=B, max_requests=B, max_frames=376, kv_bf16=True, max_tokens=512)
@@ -202,7 +204,7 @@ def attention_roofline(hip, model, ev, reps=20, step_reps=0):
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
         "kernel": "attn_kernel<true, true> (decode self + cross attention, bf16 KV)",
         "avg_launch_us": round(per_launch_us, 3), "bytes_per_launch": int(bytes_launch),
-        "workload": "128 slots, S~U(1,448)+1, T_enc~U(25,375), bf16 KV, 8 layers x (self, cross)",
+        "workload": f"{B} slots, S~U(1,448)+1, T_enc~U(25,375), bf16 KV, 8 layers x (self, cross)",
     }, micro
 
 
@@ -619,8 +621,9 @@ def measure_rooflines(hip, model, ev, ffn_bf16, samples, limits, step_reps=5):
     when the stream runs the single-pass one; attention_b64 and
     decode_step_b64 at the stream's own step shape."""
     att, micro = attention_roofline(hip, model, ev, step_reps=step_reps)
+    att_64, _ = attention_roofline(hip, model, ev, B=64)
     att64, step64 = decode_b64(model, ev, samples, limits)
-    roofs = {"attention": att, "attention_b64": att64, "decode_step_b64": step64,
+    roofs = {"attention": att, "attention_64": att_64, "attention_b64": att64, "decode_step_b64": step64,
              "decode_gemm": decode_gemm_roofline(model, ev),
              "encoder_gemm": encoder_gemm_roofline(model, ev, ffn_bf16)}
     if ffn_bf16:
