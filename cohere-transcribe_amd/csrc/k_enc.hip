@@ -70,20 +70,23 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
     const long hc = (long)h * ENC_DK;
     const float sc = 1.0f / sqrtf((float)ENC_DK);
 
-    // The MFMA K index of step st in lane group lk is head dim 40*lk + st:
-    // every lane reads one contiguous 160-byte run of a row (10 float4).
+    // The MFMA K index of step st = 4c + e in lane group lk is head dim
+    // 16c + 4lk + e: a float4 load c of row li takes dims [16c, 16c + 16) of
+    // the row across the 4 lane groups, one 64-byte segment (a 160-byte run
+    // per lane would put each lane's piece in a segment of its own: 4x the
+    // L1 lookups per load).
     // A fragments of Q+u and Q+v: row li.
     float au[RKS], av[RKS];
     {
         const bool ok = li < nq;
-        const float4 *qp = reinterpret_cast<const float4 *>(Q + (long)(q0 + li) * ENC_D + hc + RKS * lk);
+        const float4 *qp = reinterpret_cast<const float4 *>(Q + (long)(q0 + li) * ENC_D + hc + 4 * lk);
 #pragma unroll
         for (int c = 0; c < RKS / 4; c++) {
-            const float4 x = ok ? qp[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 x = ok ? qp[4 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
             const float xs[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int st = 4 * c + e, d = RKS * lk + st;
+                const int st = 4 * c + e, d = 16 * c + 4 * lk + e;
                 au[st] = xs[e] + bf2f(pbu[hc + d]);
                 av[st] = xs[e] + bf2f(pbv[hc + d]);
             }
@@ -94,11 +97,11 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
     for (int kt = w; kt < nkt; kt += 4) {
         const int key = kt * 16 + li;
         const bool ok = key < T;
-        const float4 *kp = reinterpret_cast<const float4 *>(K + (long)key * ENC_D + hc + RKS * lk);
+        const float4 *kp = reinterpret_cast<const float4 *>(K + (long)key * ENC_D + hc + 4 * lk);
         float b[RKS];
 #pragma unroll
         for (int c = 0; c < RKS / 4; c++) {
-            const float4 x = ok ? kp[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 x = ok ? kp[4 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
             b[4 * c] = x.x; b[4 * c + 1] = x.y; b[4 * c + 2] = x.z; b[4 * c + 3] = x.w;
         }
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -116,11 +119,11 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
     for (int wt = w; wt < nwt; wt += 4) {
         const int win = wt * 16 + li, p = plo + win;
         const bool ok = win < T + RQ - 1 && p >= 0 && p <= 2 * T - 2;
-        const float4 *pp = reinterpret_cast<const float4 *>(P + (long)p * ENC_D + hc + RKS * lk);
+        const float4 *pp = reinterpret_cast<const float4 *>(P + (long)p * ENC_D + hc + 4 * lk);
         float b[RKS];
 #pragma unroll
         for (int c = 0; c < RKS / 4; c++) {
-            const float4 x = ok ? pp[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 x = ok ? pp[4 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
             b[4 * c] = x.x; b[4 * c + 1] = x.y; b[4 * c + 2] = x.z; b[4 * c + 3] = x.w;
         }
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
