@@ -70,7 +70,7 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 # The kernel family with the largest share of the stream's GPU time (from the
 # eager rocprofv3 profile of the stream, encoding not overlapped: decode GEMMs
-# 33.8%, the encoder's pre-split GEMMs 25.0%, decode attention 22.1%).
+# 33.8%, the encoder's pre-split GEMMs 25.4%, decode attention 22.2%).
 DOMINANT = "decode_gemm"
 BF16_PEAK_TFLOPS = 2500.0
 # Encoder frames per batch of the overlapped encode/decode (0: encode all,

@@ -72,9 +72,9 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
 
     // The MFMA K index of step st = 4c + e in lane group lk is head dim
     // 16c + 4lk + e: a float4 load c of row li takes dims [16c, 16c + 16) of
-    // the row across the 4 lane groups, one 64-byte segment (a 160-byte run
-    // per lane would put each lane's piece in a segment of its own: 4x the
-    // L1 lookups per load).
+    // the row across the 4 lane groups, one 64-byte segment.  (With a 160-
+    // byte run per lane, each segment is requested by 4 successive loads and
+    // the L1 does not keep it between them: twice the L1 -> L2 requests.)
     // A fragments of Q+u and Q+v: row li.
     float au[RKS], av[RKS];
     {
