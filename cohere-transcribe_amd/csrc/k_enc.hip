@@ -214,10 +214,7 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(float *O, const float 
 // in registers, so each input row is fetched about twice instead of once per
 // tap.  The arithmetic per element is the scalar form's (taps in order, taps
 // outside the row's sequence skipped, then BN and SiLU).
-#ifndef CT_DW_RB
-#define CT_DW_RB 8
-#endif
-constexpr int DW_RB = CT_DW_RB;
+constexpr int DW_RB = 8;
 __global__ __launch_bounds__(256) void dwconv_bn_silu_kernel(float *out, uint16_t *out_hi, uint16_t *out_lo,
                                                              const float *in, int M, const int *row_start,
                                                              const int *row_len, const uint16_t *dww,
