@@ -222,6 +222,12 @@ void ctk_layernorm_split(uint16_t *hi, uint16_t *lo, const float *src, const uin
                          const uint16_t *b, int T, int D, hipStream_t s);
 void ctk_layernorm(float *dst, const float *src, const uint16_t *w, const uint16_t *b,
                    int T, int D, hipStream_t s);
+/* x = LayerNorm(x; w1, b1) in place, then LayerNorm(x; w2, b2) pre-split
+ * (hi, lo bf16; lo may be NULL): the bits of ctk_layernorm followed by
+ * ctk_layernorm_split, in one pass over x. */
+void ctk_layernorm_pair_split(float *x, uint16_t *hi, uint16_t *lo, const uint16_t *w1,
+                              const uint16_t *b1, const uint16_t *w2, const uint16_t *b2, int T,
+                              int D, hipStream_t s);
 void ctk_add(float *dst, const float *src, long n, hipStream_t s);
 /* dst row dst_row[m] = src row m, M rows of D floats. */
 void ctk_copy_rows(float *dst, const float *src, const int *dst_row, int M, int D, hipStream_t s);

@@ -980,8 +980,9 @@ static void encode_batch(HipbEngine *e, const int *ids, int n) {
     uint16_t *const ffl = e->cfg.enc_ffn_bf16 ? NULL : e->eln_l, *const ffm = e->cfg.enc_ffn_bf16 ? NULL : e->emid_l;
     for (int l = 0; l < ENC_N; l++) {
         const ELayer *L = &W->enc[l];
-        /* x += 0.5 FFN1(LN x) */
-        ctk_layernorm_split(e->eln_h, ffl, e->ex, DW(L->ff1_lnw), DW(L->ff1_lnb), M, ENC_D, s);
+        /* x += 0.5 FFN1(LN x); past layer 0 the LayerNorm ran with the
+         * previous layer's output norm */
+        if (l == 0) ctk_layernorm_split(e->eln_h, ffl, e->ex, DW(L->ff1_lnw), DW(L->ff1_lnb), M, ENC_D, s);
         gemm_sp_silu_split(e, e->eln_h, ffl, M, L->ff1_w1, L->ff1_b1, e->emid_h, ffm);
         gemm_sp(e, e->emid_h, ffm, M, ENC_FF, L->ff1_w2, L->ff1_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
         /* x += MHSA(LN x) */
@@ -1017,11 +1018,16 @@ static void encode_batch(HipbEngine *e, const int *ids, int n) {
                                   DW(L->cv_dww), DW(L->cv_dwb), DW(L->cv_bnw), DW(L->cv_bnb),
                                   DW(L->cv_bnmean), DW(L->cv_bnvar), s);
         gemm_sp(e, e->edw_h, e->edw_l, M, ENC_D, L->cv_pw2w, L->cv_pw2b, e->ex, ENC_D, CT_EPI_FMADD, 1.0f);
-        /* x += 0.5 FFN2(LN x); x = LN(x) */
+        /* x += 0.5 FFN2(LN x); x = LN(x), with the next layer's first
+         * LayerNorm in the same pass */
         ctk_layernorm_split(e->eln_h, ffl, e->ex, DW(L->ff2_lnw), DW(L->ff2_lnb), M, ENC_D, s);
         gemm_sp_silu_split(e, e->eln_h, ffl, M, L->ff2_w1, L->ff2_b1, e->emid_h, ffm);
         gemm_sp(e, e->emid_h, ffm, M, ENC_FF, L->ff2_w2, L->ff2_b2, e->ex, ENC_D, CT_EPI_FMADD, 0.5f);
-        ctk_layernorm(e->ex, e->ex, DW(L->out_lnw), DW(L->out_lnb), M, ENC_D, s);
+        if (l + 1 < ENC_N)
+            ctk_layernorm_pair_split(e->ex, e->eln_h, ffl, DW(L->out_lnw), DW(L->out_lnb),
+                                     DW(W->enc[l + 1].ff1_lnw), DW(W->enc[l + 1].ff1_lnb), M, ENC_D, s);
+        else
+            ctk_layernorm(e->ex, e->ex, DW(L->out_lnw), DW(L->out_lnb), M, ENC_D, s);
     }
     /* the encoder output, packed (the Q workspace is free now), goes to
      * each request's entry of enc_pool; cross K/V go straight into the

@@ -64,8 +64,58 @@ __global__ __launch_bounds__(256) void layernorm_kernel(float *dst, const float 
     ln_row(v, D, lane, w, b, dst + (long)row * D);
 }
 
-// D = 256*V (the model's 1024 and 1280): each lane holds V float4 of the row,
-// all loaded before any arithmetic.
+// D = 256*V (the model's 1024 and 1280): each lane holds V float4 of the row
+// (elements 4(lane + 64i) .. + 3), all loaded before any arithmetic.
+
+// Mean, then 1/sqrt(mean squared deviation + 1e-5), of such a row.
+template <int V>
+__device__ __forceinline__ void ln_stats(const float4 (&v)[V], float &mu, float &rs) {
+    constexpr int D = 256 * V;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    mu = wave_sum(s) / (float)D;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const float a = v[i].x - mu, bb = v[i].y - mu, c = v[i].z - mu, d = v[i].w - mu;
+        q += (a * a + bb * bb) + (c * c + d * d);
+    }
+    rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
+}
+
+// (v - mu) * rs * gain + bias, elementwise (backends/cpu/backend.c:109-122).
+__device__ __forceinline__ float4 ln_apply(const float4 &v, float mu, float rs, ushort4 w, ushort4 b) {
+    float4 o;
+    o.x = (v.x - mu) * rs * bf2f(w.x) + bf2f(b.x);
+    o.y = (v.y - mu) * rs * bf2f(w.y) + bf2f(b.y);
+    o.z = (v.z - mu) * rs * bf2f(w.z) + bf2f(b.z);
+    o.w = (v.w - mu) * rs * bf2f(w.w) + bf2f(b.w);
+    return o;
+}
+
+template <int V>
+__device__ __forceinline__ void ln_params(const uint16_t *w, const uint16_t *b, int lane, ushort4 (&w4)[V],
+                                          ushort4 (&b4)[V]) {
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        w4[i] = reinterpret_cast<const ushort4 *>(w)[lane + 64 * i];
+        b4[i] = reinterpret_cast<const ushort4 *>(b)[lane + 64 * i];
+    }
+}
+
+// Element group lane + 64i of a row written as its hi/lo bf16 split (lo
+// plane optional).
+__device__ __forceinline__ void ln_store_split(uint16_t *hi, uint16_t *lo, long off, int idx, float4 o) {
+    ushort4 h4, l4;
+    split_bf16(o.x, h4.x, l4.x);
+    split_bf16(o.y, h4.y, l4.y);
+    split_bf16(o.z, h4.z, l4.z);
+    split_bf16(o.w, h4.w, l4.w);
+    reinterpret_cast<ushort4 *>(hi + off)[idx] = h4;
+    if (lo) reinterpret_cast<ushort4 *>(lo + off)[idx] = l4;
+}
+
 template <int V>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(float *dst, const float *src,
                                                             const uint16_t *w, const uint16_t *b, int T) {
@@ -78,32 +128,12 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(float *dst, const fl
     ushort4 w4[V], b4[V];
 #pragma unroll
     for (int i = 0; i < V; i++) v[i] = x[lane + 64 * i];
-#pragma unroll
-    for (int i = 0; i < V; i++) {
-        w4[i] = reinterpret_cast<const ushort4 *>(w)[lane + 64 * i];
-        b4[i] = reinterpret_cast<const ushort4 *>(b)[lane + 64 * i];
-    }
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < V; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    const float mu = wave_sum(s) / (float)D;
-    float q = 0.0f;
-#pragma unroll
-    for (int i = 0; i < V; i++) {
-        const float a = v[i].x - mu, bb = v[i].y - mu, c = v[i].z - mu, d = v[i].w - mu;
-        q += (a * a + bb * bb) + (c * c + d * d);
-    }
-    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
+    ln_params<V>(w, b, lane, w4, b4);
+    float mu, rs;
+    ln_stats<V>(v, mu, rs);
     float4 *y = reinterpret_cast<float4 *>(dst + (long)row * D);
 #pragma unroll
-    for (int i = 0; i < V; i++) {
-        float4 o;
-        o.x = (v[i].x - mu) * rs * bf2f(w4[i].x) + bf2f(b4[i].x);
-        o.y = (v[i].y - mu) * rs * bf2f(w4[i].y) + bf2f(b4[i].y);
-        o.z = (v[i].z - mu) * rs * bf2f(w4[i].z) + bf2f(b4[i].z);
-        o.w = (v[i].w - mu) * rs * bf2f(w4[i].w) + bf2f(b4[i].w);
-        y[lane + 64 * i] = o;
-    }
+    for (int i = 0; i < V; i++) y[lane + 64 * i] = ln_apply(v[i], mu, rs, w4[i], b4[i]);
 }
 
 // Same as layernorm_vec_kernel, writing each output as its hi/lo bf16 split.
@@ -120,37 +150,44 @@ __global__ __launch_bounds__(256) void layernorm_split_kernel(uint16_t *hi, uint
     ushort4 w4[V], b4[V];
 #pragma unroll
     for (int i = 0; i < V; i++) v[i] = x[lane + 64 * i];
+    ln_params<V>(w, b, lane, w4, b4);
+    float mu, rs;
+    ln_stats<V>(v, mu, rs);
+#pragma unroll
+    for (int i = 0; i < V; i++) ln_store_split(hi, lo, (long)row * D, lane + 64 * i, ln_apply(v[i], mu, rs, w4[i], b4[i]));
+}
+
+// Two LayerNorms in a row, as the encoder runs them from one layer's output
+// norm into the next layer's first FFN norm: x = LN1(x) in place, then
+// LN2(x) as its hi/lo split.  The second norm works on the first one's fp32
+// results in registers, the values a separate launch would read back, so the
+// bits are those of layernorm_vec_kernel followed by layernorm_split_kernel.
+template <int V>
+__global__ __launch_bounds__(256) void layernorm_pair_split_kernel(float *xio, uint16_t *hi, uint16_t *lo,
+                                                                   const uint16_t *w1, const uint16_t *b1,
+                                                                   const uint16_t *w2, const uint16_t *b2,
+                                                                   int T) {
+    constexpr int D = 256 * V;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= T) return;
+    float4 *x = reinterpret_cast<float4 *>(xio + (long)row * D);
+    float4 v[V];
+    ushort4 w4[V], b4[V], w4b[V], b4b[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) v[i] = x[lane + 64 * i];
+    ln_params<V>(w1, b1, lane, w4, b4);
+    ln_params<V>(w2, b2, lane, w4b, b4b);
+    float mu, rs;
+    ln_stats<V>(v, mu, rs);
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        w4[i] = reinterpret_cast<const ushort4 *>(w)[lane + 64 * i];
-        b4[i] = reinterpret_cast<const ushort4 *>(b)[lane + 64 * i];
+        v[i] = ln_apply(v[i], mu, rs, w4[i], b4[i]);
+        x[lane + 64 * i] = v[i];
     }
-    float s = 0.0f;
+    ln_stats<V>(v, mu, rs);
 #pragma unroll
-    for (int i = 0; i < V; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    const float mu = wave_sum(s) / (float)D;
-    float q = 0.0f;
-#pragma unroll
-    for (int i = 0; i < V; i++) {
-        const float a = v[i].x - mu, bb = v[i].y - mu, c = v[i].z - mu, d = v[i].w - mu;
-        q += (a * a + bb * bb) + (c * c + d * d);
-    }
-    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
-#pragma unroll
-    for (int i = 0; i < V; i++) {
-        const float o[4] = {(v[i].x - mu) * rs * bf2f(w4[i].x) + bf2f(b4[i].x),
-                            (v[i].y - mu) * rs * bf2f(w4[i].y) + bf2f(b4[i].y),
-                            (v[i].z - mu) * rs * bf2f(w4[i].z) + bf2f(b4[i].z),
-                            (v[i].w - mu) * rs * bf2f(w4[i].w) + bf2f(b4[i].w)};
-        ushort4 h4, l4;
-        uint16_t hh[4], ll[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) split_bf16(o[j], hh[j], ll[j]);
-        h4.x = hh[0]; h4.y = hh[1]; h4.z = hh[2]; h4.w = hh[3];
-        l4.x = ll[0]; l4.y = ll[1]; l4.z = ll[2]; l4.w = ll[3];
-        reinterpret_cast<ushort4 *>(hi + (long)row * D)[lane + 64 * i] = h4;
-        if (lo) reinterpret_cast<ushort4 *>(lo + (long)row * D)[lane + 64 * i] = l4;
-    }
+    for (int i = 0; i < V; i++) ln_store_split(hi, lo, (long)row * D, lane + 64 * i, ln_apply(v[i], mu, rs, w4b[i], b4b[i]));
 }
 
 // Rows longer than 2048: three passes over the (cache-resident) row.
@@ -419,6 +456,24 @@ extern "C" void ctk_layernorm_split(uint16_t *hi, uint16_t *lo, const float *src
         hipLaunchKernelGGL(layernorm_split_kernel<4>, dim3((T + 3) / 4), dim3(256), 0, s, hi, lo, src, w, b, T);
     else
         hipLaunchKernelGGL(layernorm_split_kernel<5>, dim3((T + 3) / 4), dim3(256), 0, s, hi, lo, src, w, b, T);
+}
+
+extern "C" void ctk_layernorm_pair_split(float *x, uint16_t *hi, uint16_t *lo, const uint16_t *w1,
+                                         const uint16_t *b1, const uint16_t *w2, const uint16_t *b2, int T,
+                                         int D, hipStream_t s) {
+    if (T <= 0) return;
+    if ((uintptr_t)x % 16 || (uintptr_t)hi % 8 || (uintptr_t)lo % 8 || (uintptr_t)w1 % 8 ||
+        (uintptr_t)b1 % 8 || (uintptr_t)w2 % 8 || (uintptr_t)b2 % 8 || (D != 1024 && D != 1280)) {
+        fprintf(stderr, "ctk_layernorm_pair_split: needs D in {1024, 1280}, aligned rows and 8-byte aligned "
+                        "gains and biases\n");
+        exit(1);
+    }
+    if (D == 1024)
+        hipLaunchKernelGGL(layernorm_pair_split_kernel<4>, dim3((T + 3) / 4), dim3(256), 0, s, x, hi, lo, w1, b1,
+                           w2, b2, T);
+    else
+        hipLaunchKernelGGL(layernorm_pair_split_kernel<5>, dim3((T + 3) / 4), dim3(256), 0, s, x, hi, lo, w1, b1,
+                           w2, b2, T);
 }
 
 extern "C" void ctk_embed_ln(float *h, const int *tokens, int R, int pos_start, const int *pos_len,
