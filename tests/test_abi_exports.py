@@ -167,3 +167,26 @@ def test_fatal_paths_before_device_work(case):
     assert r.returncode == 1, (r.returncode, r.stdout, r.stderr)
     assert msg in r.stderr, r.stderr
     assert "returned" not in r.stdout
+
+
+TRANSCRIBE_HIP = os.path.join(REPO, "oracle", "_ref", "transcribe_hip")
+
+
+@pytest.mark.skipif(not os.path.exists(TRANSCRIBE_HIP),
+                    reason="oracle/_ref/transcribe_hip is built only where the reference sources are")
+def test_reference_transcribe_links_against_hip_backend():
+    """The reference's CLI host (transcribe.c), unchanged, links against
+    libct_hip.so with the link line of the build.sh binding: every backend_*
+    symbol it needs is undefined in the binary and defined by the library,
+    the loader finds the library, and the program runs to its argument check
+    (usage and status 1, transcribe.c:1283-1293) without touching a device."""
+    und = subprocess.run(["nm", "-D", "--undefined-only", TRANSCRIBE_HIP], check=True,
+                         capture_output=True, text=True).stdout
+    needed = {ln.split()[-1] for ln in und.splitlines() if ln.split()[-1].startswith("backend_")}
+    assert len(needed) >= 20
+    assert needed <= exported(cb.HIP_LIB)
+    deps = subprocess.run(["ldd", TRANSCRIBE_HIP], capture_output=True, text=True).stdout
+    line = next(ln for ln in deps.splitlines() if "libct_hip.so" in ln)
+    assert os.path.realpath(line.split("=>")[1].split()[0]) == os.path.realpath(cb.HIP_LIB)
+    r = subprocess.run([TRANSCRIBE_HIP], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1 and "Usage:" in r.stderr
