@@ -45,8 +45,9 @@ static size_t work_floats(int T_mel) {
     return w;
 }
 
-static float *g_base;
-static size_t g_off, g_cap;
+/* per thread, as transcribe.c's workers each hold their own backend state */
+static _Thread_local float *g_base;
+static _Thread_local size_t g_off, g_cap;
 static void arena_begin(size_t floats) {
     g_base = backend_arena_alloc(floats);
     g_cap = floats;

@@ -328,6 +328,58 @@ def test_reference_host_on_hip(hip, variant, fname):
     assert np.array_equal(bt, g["batch_tokens"])
 
 
+
+def test_reference_host_threads_on_hip(hip):
+    """transcribe.c's worker pattern (transcribe.c:849-943): each thread calls
+    backend_init, runs the model.h single path on its own clip through its own
+    thread-local state (stream, arena, device S counter, graphs), then
+    backend_thread_cleanup.  Three threads at once give each clip the tokens
+    and logits bits of a run on the main thread."""
+    import threading
+    from golden.make_golden import SINGLE_LIMIT, MODEL_SEED
+    path = os.path.join(GOLD, "model_small_hot.npz")
+    if not os.path.exists(path):
+        pytest.skip("model fixture not generated")
+    g = np.load(path)
+    lib = ref_model_hip()
+    m = cb.SynthModel(seed=MODEL_SEED, variant=2)
+    hip.backend_weights_upload_blob(m.data_ptr, m.data_bytes)
+    lib.ref_set_weights(m.weights_ref())
+    prompt = np.asarray(cb.PROMPT, np.int32)
+    mels = [np.ascontiguousarray(g["mel0"]), np.ascontiguousarray(g["mel1"])]
+
+    def run(mel):
+        toks = np.zeros(SINGLE_LIMIT, np.int32)
+        lg = np.zeros((SINGLE_LIMIT, cb.VOCAB), np.float32)
+        n = lib.ref_transcribe_single(mel.ctypes.data, mel.shape[1], prompt.ctypes.data, len(prompt),
+                                      SINGLE_LIMIT, 1, 0, toks.ctypes.data, lg.ctypes.data, None)
+        return toks[:n], lg[:n]
+
+    print("case: model.h single path, main thread, clips 0 and 1", flush=True)
+    want = [run(mm) for mm in mels]
+    got, errs = [None] * 3, []
+
+    def worker(i):
+        try:
+            hip.backend_init(0)
+            got[i] = run(mels[i % 2])
+            hip.backend_thread_cleanup()
+        except BaseException as ex:   # surfaced below
+            errs.append(ex)
+
+    print("case: three worker threads, clips 0, 1, 0", flush=True)
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(3)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=240)
+    assert not errs and all(not t.is_alive() for t in ts)
+    for i in range(3):
+        wt, wl = want[i % 2]
+        assert np.array_equal(got[i][0], wt), i
+        assert bits_equal(got[i][1], wl), i
+
+
 ENC_T = [17, 37, 101, 376, 751, 2048]
 
 
