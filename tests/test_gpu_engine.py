@@ -698,3 +698,43 @@ def test_engine_request_ring_wraps(hip, hot, monkeypatch):
             assert np.array_equal(alone.scores(0).view(np.uint32), scores[r].view(np.uint32)), r
         finally:
             alone.close()
+
+
+def test_engine_from_c_host_matches_binding(hip):
+    """The engine driven from a plain C program (examples/engine_demo.c: its
+    own synthetic weights, backend_weights_upload_blob, backend_init,
+    hipb_create / hipb_submit_pcm / hipb_encode / hipb_run / hipb_tokens)
+    gives every request the tokens the same calls give through this binding
+    in this process."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(cb.HIP_LIB), "_build", "engine_demo")
+    if not os.path.exists(exe):
+        pytest.skip("cohere-transcribe_amd/_build/engine_demo not built")
+    seed, variant, n, slots = 4321, 3, 6, 3
+    print(f"case: C host, weights seed {seed} variant {variant}, {n} clips on {slots} slots", flush=True)
+    r = subprocess.run([exe, str(seed), str(variant), str(n), str(slots)], capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0, r.stderr[-2000:]
+    got = {}
+    for line in r.stdout.splitlines():
+        head, rest = line.split(":")
+        vals = [int(v) for v in rest.split()]
+        got[int(head.split()[1])] = vals[1:1 + vals[0]]
+    assert sorted(got) == list(range(n))
+    m = cb.SynthModel(seed=seed, variant=variant)
+    hip.backend_weights_upload_blob(m.data_ptr, m.data_bytes)
+    eng = cb.Engine(m, slots=slots, max_requests=n, max_frames=376, kv_bf16=True, max_tokens=32,
+                    admit_order=1, enc_ffn_bf16=1)
+    try:
+        flags = cb.HIPB_SUPPRESS_EOS | cb.HIPB_FORCE_EOS
+        for i in range(n):
+            eng.submit_pcm(cb.synth_audio(8000 + 3000 * i, 500 + i), 4 + 3 * (i % 5), flags)
+        eng.encode(max_batch_frames=4096)
+        eng.run(chunk=4)
+        for i in range(n):
+            want = list(eng.tokens(i))
+            assert len(want) == 4 + 3 * (i % 5), i
+            assert got[i] == want, i
+    finally:
+        eng.close()
